@@ -1,0 +1,317 @@
+"""Decode-GEMV benchmark for the MI355X k-quant path (BASELINE metric:
+"Q4_K GEMV HBM GB/s (% of peak) + batch-1 decode tok/s, Qwen3-8B shapes").
+
+One step = the quantized-projection work of one batch-1 Qwen3-8B decode token:
+for each of 36 layers, RMSNorm-fused q/k/v (Q4_K 4096->4096/1024/1024), o
+(Q4_K 4096->4096), RMSNorm-fused gate/up (Q4_K 4096->12288) and down (Q5_K
+12288->4096), then the RMSNorm-fused Q6_K lm_head (4096->151936). Every layer
+has its own synthetic weights (4.64 GB per step, far beyond the 256 MB
+Infinity Cache), resident in HBM before timing starts. Attention, SwiGLU and
+residual kernels are not part of this step (the activations are synthetic).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Prints one JSON line. `value` is achieved algorithmic GB/s over the timed
+steps (weights + f32 activations in + f32 outputs, each once per launch).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+HIDDEN, FFN, Q_OUT, KV_OUT, VOCAB = 4096, 12288, 4096, 1024, 151936
+EPS = 1e-6
+METRIC = "Q4_K GEMV HBM GB/s (% of peak) + batch-1 decode tok/s, Qwen3-8B shapes"
+
+# (name, value type, K, N, norm group) per layer, in decode order (decode.rs:544-696).
+LAYER = [
+    ("q", 12, HIDDEN, Q_OUT, "attn"),
+    ("k", 12, HIDDEN, KV_OUT, "attn"),
+    ("v", 12, HIDDEN, KV_OUT, "attn"),
+    ("o", 12, Q_OUT, HIDDEN, None),
+    ("gate", 12, HIDDEN, FFN, "ffn"),
+    ("up", 12, HIDDEN, FFN, "ffn"),
+    ("down", 13, FFN, HIDDEN, None),
+]
+BLOCK_BYTES = {12: 144, 13: 176, 14: 210}
+
+
+def launch_bytes(t, k, n):
+    return k // 256 * n * BLOCK_BYTES[t] + 4 * k + 4 * n
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_model(E, synth, torch, layers, seed):
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(seed)
+    dev = torch.device("cuda:0")
+    weights = []
+    for li in range(layers):
+        lw = {}
+        for name, t, k, n, _ in LAYER:
+            lw[name] = (t, k, n, synth.kquant_torch(t, k, n, gen, dev))
+        lw["attn_gamma"] = 1.0 + 0.02 * torch.randn(HIDDEN, device=dev, generator=gen)
+        lw["ffn_gamma"] = 1.0 + 0.02 * torch.randn(HIDDEN, device=dev, generator=gen)
+        weights.append(lw)
+    head = (14, HIDDEN, VOCAB, synth.kquant_torch(14, HIDDEN, VOCAB, gen, dev))
+    out_gamma = 1.0 + 0.02 * torch.randn(HIDDEN, device=dev, generator=gen)
+    acts = {
+        "hidden": torch.randn(HIDDEN, device=dev, generator=gen),
+        "attn_out": torch.randn(Q_OUT, device=dev, generator=gen),
+        "ffn_act": torch.randn(FFN, device=dev, generator=gen),
+    }
+    return weights, head, out_gamma, acts
+
+
+class DecodeGemvStep:
+    """Issues one step's launches through the C ABI on ctx's stream."""
+
+    def __init__(self, E, torch, ctx, weights, head, out_gamma, acts):
+        self.store = E.AmdWeightStore(ctx)
+        self.kern = {t: E.QwenGemvKernel.from_value_type(ctx, t) for t in (12, 13, 14)}
+        self.layers = []
+        for li, lw in enumerate(weights):
+            entry = {}
+            for name, t, k, n, norm in LAYER:
+                key = f"blk.{li}.{name}"
+                self.store.materialize_quantized(key, [k, n], t, lw[name][3])
+                entry[name] = (self.store.quantized_tensor(key), t, k, n, norm)
+            entry["attn_gamma"] = lw["attn_gamma"]
+            entry["ffn_gamma"] = lw["ffn_gamma"]
+            self.layers.append(entry)
+        self.store.materialize_quantized("output", [HIDDEN, VOCAB], 14, head[3])
+        self.head = self.store.quantized_tensor("output")
+        self.out_gamma = out_gamma
+        self.acts = acts
+        self.outs = {name: torch.empty(n, device="cuda:0") for name, _, _, n, _ in LAYER}
+        self.logits = torch.empty(VOCAB, device="cuda:0")
+        self.bytes_per_step = sum(launch_bytes(t, k, n) for _, t, k, n, _ in LAYER) * len(weights) \
+            + launch_bytes(14, HIDDEN, VOCAB)
+
+    def layer(self, entry):
+        for name, _, _, _, norm in LAYER:
+            w, t, k, n, _ = entry[name]
+            kern = self.kern[t]
+            if norm is not None:
+                kern.execute_rms_norm(w, self.acts["hidden"], entry[f"{norm}_gamma"], EPS, self.outs[name], 1)
+            elif name == "o":
+                kern.execute_warp(w, self.acts["attn_out"], self.outs[name])
+            else:
+                kern.execute_warp(w, self.acts["ffn_act"], self.outs[name])
+
+    def run(self):
+        for entry in self.layers:
+            self.layer(entry)
+        self.kern[14].execute_rms_norm(self.head, self.acts["hidden"], self.out_gamma, EPS, self.logits, 1)
+
+    def run_gate_up(self):
+        for entry in self.layers:
+            for name in ("gate", "up"):
+                w, t, k, n, norm = entry[name]
+                self.kern[t].execute_rms_norm(w, self.acts["hidden"], entry["ffn_gamma"], EPS, self.outs[name], 1)
+
+
+def capture(torch, stream, fn):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    return g
+
+
+def cpu_baseline(seconds_budget=12.0):
+    """Reference CPU path (dequantize_block + sequential f32 dot) on one Qwen3-8B layer."""
+    import numpy as np
+
+    from engine_amd import synth
+    from oracle import kquant_oracle as O
+
+    mats = [(t, k, n, synth.kquant_numpy(t, k, n, seed=500 + i)) for i, (_, t, k, n, _) in enumerate(LAYER)]
+    x = {k: synth.activations_numpy(k, 1, seed=k)[0] for k in (HIDDEN, FFN)}
+    gamma = synth.gamma_numpy(HIDDEN, seed=9)
+    layer_bytes = sum(launch_bytes(t, k, n) for t, k, n, _ in mats)
+
+    def one_layer(threads):
+        normed = O.rms_norm_raw(x[HIDDEN], gamma, EPS)
+        for t, k, n, enc in mats:
+            src = normed if k == HIDDEN else x[FFN]
+            O.quant_gemv(t, enc, k, n, src, threads=threads)
+
+    results = {}
+    for threads in (1, min(16, os.cpu_count() or 1)):
+        for _ in range(2):
+            one_layer(threads)
+        samples = []
+        t_end = time.perf_counter() + seconds_budget / 2
+        while len(samples) < 20 and (time.perf_counter() < t_end or len(samples) < 5):
+            t0 = time.perf_counter()
+            one_layer(threads)
+            samples.append(time.perf_counter() - t0)
+        samples.sort()
+        med = samples[len(samples) // 2]
+        results[threads] = (med, samples[0], len(samples))
+    med1, min1, n1 = results[1]
+    threads_all = max(results)
+    med_all, _, _ = results[threads_all]
+    return {
+        "value": layer_bytes / med1 / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"one Qwen3-8B layer (RMSNorm + q,k,v,o,gate,up Q4_K + down Q5_K, {layer_bytes} B), "
+                   f"oracle/kquant_oracle.c -O2 -ffp-contract=off, median of {n1} runs "
+                   f"(min {layer_bytes / min1 / 1e9:.3f} GB/s); {1.0 / (36 * med1):.3f} layer-stacks/s"),
+        "all_cores": {"value": layer_bytes / med_all / 1e9, "cores": threads_all},
+        "host_cpu": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--no-graph", action="store_true", help="issue launches eagerly instead of replaying a HIP graph")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU: the k-quant decode path runs on a single "
+                                   "MI355X; multi-GPU sharding is a design note only", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+
+    import engine_amd as E
+    from engine_amd import synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    log(f"bench: generating {args.layers} layers + lm_head of synthetic weights on the device")
+    weights, head, out_gamma, acts = build_model(E, synth, torch, args.layers, args.seed)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    ctx = E.AmdContext(0, stream=stream)
+    step = DecodeGemvStep(E, torch, ctx, weights, head, out_gamma, acts)
+    log(f"bench: {step.bytes_per_step / 1e9:.3f} GB of algorithmic traffic per step")
+
+    with torch.cuda.stream(stream):
+        step.run()  # eager warm-up (and validation of every launch)
+    torch.cuda.synchronize()
+    graph = None if args.no_graph else capture(torch, stream, step.run)
+    graph_gu = capture(torch, stream, step.run_gate_up)
+
+    def one():
+        if graph is not None:
+            graph.replay()
+        else:
+            step.run()
+
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            one()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(args.steps):
+            one()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(end)
+    ms_step = ms_total / args.steps
+    gbs = step.bytes_per_step / (ms_step * 1e-3) / 1e9
+    log(f"bench: {ms_step:.4f} ms/step, {gbs:.1f} GB/s")
+
+    # Dominant kernel: RMSNorm-fused Q4_K GEMV 4096->12288 (gate/up), timed live with
+    # HIP events over back-to-back launches on the stream it runs on.
+    reps = 5
+    with torch.cuda.stream(stream):
+        graph_gu.replay()
+        s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s2.record(stream)
+        for _ in range(reps):
+            graph_gu.replay()
+        e2.record(stream)
+    torch.cuda.synchronize()
+    launches = reps * 2 * args.layers
+    us_launch = s2.elapsed_time(e2) * 1e3 / launches
+    gu_bytes = launch_bytes(12, HIDDEN, FFN)
+    achieved = gu_bytes / (us_launch * 1e-6) / 1e9
+    roofline = {
+        "bound": "hbm",
+        "kernel": "gemv_wave_kernel<Q4_K, 1 member, fused RMSNorm> 4096->12288",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": None,
+        "avg_launch_us": round(us_launch, 3),
+        "bytes_per_launch": gu_bytes,
+    }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("bench: timing the CPU baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+        "decode_tok_s": round(1000.0 / ms_step, 2),
+        "config": {
+            "workload": "qwen3-8b-decode-gemv-b1",
+            "layers": args.layers,
+            "hidden": HIDDEN,
+            "ffn": FFN,
+            "projections": "q,k,v,o,gate,up Q4_K; down Q5_K; lm_head Q6_K 151936x4096",
+            "rmsnorm": "fused into q,k,v,gate,up,lm_head activation load, eps 1e-6",
+            "bytes_per_step": step.bytes_per_step,
+            "launches_per_step": 7 * args.layers + 1,
+            "hip_graph": graph is not None,
+            "batch": 1,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

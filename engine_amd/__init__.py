@@ -1,0 +1,20 @@
+"""engine_amd: MI355X-native (gfx950) k-quant decode path behind a C ABI.
+
+The product is libribn_amd.so (HIP kernels + C ABI, include/ribn_amd.h); this
+package holds its sources (csrc/), the build script, a ctypes binding and a
+host-side mirror of the reference's operator API (kquant.py).
+"""
+from . import _lib  # noqa: F401
+from .kquant import (  # noqa: F401
+    Q4_K, Q5_K, Q6_K, BLOCK_BYTES,
+    AmdContext, AmdWeightStore, AmdQuantizedWeight,
+    AmdQ4KGemv, AmdQ5KGemv, AmdQ6KGemv, QwenGemvKernel, AmdQwenOps,
+    AmdKernelError, AmdQuantizedKernelError, AmdModelKernelError, AmdWeightError,
+    validate_quantized_geometry,
+)
+
+__all__ = [
+    "Q4_K", "Q5_K", "Q6_K", "BLOCK_BYTES", "AmdContext", "AmdWeightStore", "AmdQuantizedWeight",
+    "AmdQ4KGemv", "AmdQ5KGemv", "AmdQ6KGemv", "QwenGemvKernel", "AmdQwenOps", "AmdKernelError",
+    "AmdQuantizedKernelError", "AmdModelKernelError", "AmdWeightError", "validate_quantized_geometry",
+]

@@ -1,0 +1,111 @@
+"""ctypes binding of libribn_amd.so (the C ABI in include/ribn_amd.h).
+
+The library is built in-tree by `python -m engine_amd.build` (or
+__graft_entry__.build()). Loading fails loudly when it is missing: there is no
+CPU fallback for any operation of this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libribn_amd.so")
+HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "ribn_amd.h")
+
+STATUS_NAMES = {
+    0: "Ok", 1: "Driver", 2: "Module", 3: "InvalidWeight", 4: "UnsupportedValueType",
+    5: "ShapeOverflow", 6: "InputLength", 7: "OutputLength", 8: "ContextMismatch",
+    9: "EmptyInput", 10: "WeightLength", 11: "InvalidEpsilon", 12: "InvalidArgument",
+    13: "EmptyEncoding", 14: "SourceIncomplete",
+}
+
+
+class RibnAmdError(ctypes.Structure):
+    _fields_ = [("status", ctypes.c_int32), ("expected", ctypes.c_uint64),
+                ("actual", ctypes.c_uint64), ("message", ctypes.c_char * 512)]
+
+
+READ_FN = ctypes.CFUNCTYPE(ctypes.c_int64, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint8), ctypes.c_size_t)
+
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+_pvp = ctypes.POINTER(ctypes.c_void_p)
+
+SIGNATURES = {
+    "ribn_amd_last_error": (_i32, [ctypes.POINTER(RibnAmdError)]),
+    "ribn_amd_status_name": (ctypes.c_char_p, [_i32]),
+    "ribn_amd_abi_version": (_i32, []),
+    "ribn_amd_context_create": (_i32, [_i32, _pvp]),
+    "ribn_amd_context_wrap_stream": (_i32, [_i32, _vp, _pvp]),
+    "ribn_amd_context_destroy": (None, [_vp]),
+    "ribn_amd_context_synchronize": (_i32, [_vp]),
+    "ribn_amd_context_stream": (_vp, [_vp]),
+    "ribn_amd_context_device": (_i32, [_vp]),
+    "ribn_amd_alloc": (_i32, [_vp, _sz, _pvp]),
+    "ribn_amd_free": (_i32, [_vp, _vp]),
+    "ribn_amd_memcpy_htod": (_i32, [_vp, _vp, _vp, _sz]),
+    "ribn_amd_memcpy_dtoh": (_i32, [_vp, _vp, _vp, _sz]),
+    "ribn_amd_weight_materialize": (_i32, [_vp, _u32, _u64, _u64, _vp, _u64, _pvp]),
+    "ribn_amd_weight_materialize_reader": (_i32, [_vp, _u32, _u64, _u64, _u64, READ_FN, _vp, _pvp]),
+    "ribn_amd_weight_wrap_device": (_i32, [_vp, _u32, _u64, _u64, _vp, _u64, _pvp]),
+    "ribn_amd_weight_copy_to_host": (_i32, [_vp, _vp, _vp, _u64]),
+    "ribn_amd_weight_destroy": (None, [_vp]),
+    "ribn_amd_weight_value_type": (_u32, [_vp]),
+    "ribn_amd_weight_encoded_bytes": (_u64, [_vp]),
+    "ribn_amd_weight_input_size": (_u64, [_vp]),
+    "ribn_amd_weight_output_size": (_u64, [_vp]),
+    "ribn_amd_weight_device_ptr": (_vp, [_vp]),
+    "ribn_amd_validate_quantized_geometry": (_i32, [_u32, _u32, ctypes.POINTER(_u64), _sz, _u64,
+                                                    ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "ribn_amd_gemv_create": (_i32, [_vp, _u32, _pvp]),
+    "ribn_amd_gemv_destroy": (None, [_vp]),
+    "ribn_amd_gemv_value_type": (_u32, [_vp]),
+    "ribn_amd_gemv_execute": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
+    "ribn_amd_gemv_execute_warp": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
+    "ribn_amd_gemv_execute_warp_batch": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz, _sz]),
+    "ribn_amd_gemv_execute_rms_norm": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz, _f32, _vp, _sz, _sz]),
+    "ribn_amd_dequantize": (_i32, [_vp, _vp, _vp, _sz]),
+    "ribn_amd_rms_norm": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _f32]),
+    "ribn_amd_rms_norm_batch": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _f32]),
+}
+
+_lib = None
+
+
+def declared_functions() -> list[str]:
+    """Function names declared in include/ribn_amd.h (typedefs excluded)."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set(re.findall(r"\b(ribn_amd_[a-z0-9_]+)\s*\(", text))
+    typedefs = set(re.findall(r"\(\s*\*\s*(ribn_amd_[a-z0-9_]+)\s*\)", text))
+    return sorted(names - typedefs)
+
+
+def load():
+    """Loads and types the library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m engine_amd.build` "
+            "(the k-quant path has no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error():
+    err = RibnAmdError()
+    load().ribn_amd_last_error(ctypes.byref(err))
+    return err

@@ -1,0 +1,639 @@
+// Host side of the C ABI declared in include/ribn_amd.h: contexts, the opaque
+// weight store, validation that mirrors the reference's operator wrappers
+// (crates/nvidia/src/quantized.rs, model_ops.rs, cuda.rs) and kernel dispatch.
+#include "ribn_amd.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <new>
+#include <vector>
+
+#include "kquant_launch.hpp"
+
+struct ribn_amd_context {
+    int device;
+    hipStream_t stream;
+    bool owns_stream;
+    int cu_count;
+};
+
+struct ribn_amd_quantized_weight {
+    ribn_amd_context* ctx;
+    uint32_t value_type;
+    uint64_t input_size;
+    uint64_t output_size;
+    uint64_t encoded_bytes;
+    uint8_t* data;
+    bool owns_data;
+};
+
+struct ribn_amd_gemv {
+    ribn_amd_context* ctx;
+    uint32_t value_type;
+};
+
+namespace {
+
+thread_local ribn_amd_error g_last_error = {RIBN_AMD_OK, 0, 0, {0}};
+
+ribn_amd_status fail(ribn_amd_status status, uint64_t expected, uint64_t actual, const char* fmt, ...) {
+    g_last_error.status = status;
+    g_last_error.expected = expected;
+    g_last_error.actual = actual;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error.message, sizeof g_last_error.message, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+ribn_amd_status ok() {
+    g_last_error.status = RIBN_AMD_OK;
+    g_last_error.expected = 0;
+    g_last_error.actual = 0;
+    g_last_error.message[0] = 0;
+    return RIBN_AMD_OK;
+}
+
+ribn_amd_status driver(hipError_t e, const char* what) {
+    if (e == hipErrorNoBinaryForGpu || e == hipErrorInvalidImage || e == hipErrorInvalidDeviceFunction) {
+        return fail(RIBN_AMD_MODULE, 0, 0, "%s: no gfx950 code object for this device (%s)", what,
+                    hipGetErrorString(e));
+    }
+    return fail(RIBN_AMD_DRIVER, 0, 0, "%s: %s", what, hipGetErrorString(e));
+}
+
+const char* type_label(uint32_t t) {
+    switch (t) {
+    case RIBN_AMD_Q4_K: return "Q4_K";
+    case RIBN_AMD_Q5_K: return "Q5_K";
+    case RIBN_AMD_Q6_K: return "Q6_K";
+    default: return "unsupported";
+    }
+}
+
+uint64_t block_bytes(uint32_t t) {
+    switch (t) {
+    case RIBN_AMD_Q4_K: return 144;
+    case RIBN_AMD_Q5_K: return 176;
+    case RIBN_AMD_Q6_K: return 210;
+    default: return 0;
+    }
+}
+
+bool supported(uint32_t t) { return block_bytes(t) != 0; }
+
+struct DeviceGuard {
+    int previous = -1;
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&previous) != hipSuccess) previous = -1;
+        if (previous != device) hipSetDevice(device);
+    }
+    ~DeviceGuard() {
+        if (previous >= 0) hipSetDevice(previous);
+    }
+};
+
+// The ContextMismatch check of quantized.rs:260-266 for raw device pointers:
+// the buffer must be device (or managed) memory of the context's device.
+ribn_amd_status check_device_ptr(const ribn_amd_context* ctx, const void* ptr, const char* what) {
+    if (ptr == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "%s is null", what);
+    if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, 16, reinterpret_cast<uintptr_t>(ptr) & 15u,
+                    "%s must be 16-byte aligned", what);
+    }
+    hipPointerAttribute_t attr;
+    hipError_t e = hipPointerGetAttributes(&attr, ptr);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "%s is not a device allocation (%s)", what,
+                    hipGetErrorString(e));
+    }
+    if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "%s is not device memory", what);
+    }
+    if (attr.device != ctx->device) {
+        return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)ctx->device, (uint64_t)attr.device,
+                    "%s belongs to device %d, the context to device %d", what, attr.device, ctx->device);
+    }
+    return RIBN_AMD_OK;
+}
+
+ribn_amd_status validate_geometry(uint32_t kernel_type, const ribn_amd_quantized_weight* w, uint64_t* k,
+                                  uint64_t* n) {
+    const uint64_t dims[2] = {w->input_size, w->output_size};
+    return ribn_amd_validate_quantized_geometry(kernel_type, w->value_type, dims, 2, w->encoded_bytes, k, n);
+}
+
+// quantized.rs:252-355 validate / validate_batch, in the reference's order:
+// contexts, geometry, input length, output length.
+ribn_amd_status validate_launch(const ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const float* in,
+                                size_t in_len, const float* out, size_t out_len, size_t members, uint64_t* k,
+                                uint64_t* n) {
+    if (g == nullptr || w == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null kernel or weight handle");
+    if (w->ctx->device != g->ctx->device) {
+        return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)g->ctx->device, (uint64_t)w->ctx->device,
+                    "weight and kernel belong to different devices");
+    }
+    ribn_amd_status st = check_device_ptr(g->ctx, in, "input");
+    if (st != RIBN_AMD_OK) return st;
+    st = check_device_ptr(g->ctx, out, "output");
+    if (st != RIBN_AMD_OK) return st;
+    st = validate_geometry(g->value_type, w, k, n);
+    if (st != RIBN_AMD_OK) return st;
+    if (members != 0 && *k > std::numeric_limits<size_t>::max() / members) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "input size overflows");
+    }
+    if (members != 0 && *n > std::numeric_limits<size_t>::max() / members) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "output size overflows");
+    }
+    const uint64_t expected_in = *k * members;
+    const uint64_t expected_out = *n * members;
+    if (in_len != expected_in) {
+        return fail(RIBN_AMD_INPUT_LENGTH, expected_in, in_len,
+                    "quantized GEMV input has %zu values, expected %llu", in_len,
+                    (unsigned long long)expected_in);
+    }
+    if (out_len != expected_out) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, expected_out, out_len,
+                    "quantized GEMV output has %zu values, expected %llu", out_len,
+                    (unsigned long long)expected_out);
+    }
+    if (members > (size_t)std::numeric_limits<int>::max()) return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "members overflow");
+    return RIBN_AMD_OK;
+}
+
+ribn_amd_status validate_members(const ribn_amd_gemv* g, size_t members) {
+    // quantized.rs:458-469: zero members is an input-length error, too many an
+    // invalid-weight error naming the family.
+    if (members == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "batched GEMV needs at least one member");
+    if (members > RIBN_AMD_MAX_BATCH_MEMBERS) {
+        return fail(RIBN_AMD_INVALID_WEIGHT, RIBN_AMD_MAX_BATCH_MEMBERS, members,
+                    "%s batched GEMV supports at most %u members", g ? type_label(g->value_type) : "?",
+                    RIBN_AMD_MAX_BATCH_MEMBERS);
+    }
+    return RIBN_AMD_OK;
+}
+
+ribn_amd_status launch_batched(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const float* in,
+                               const float* gamma, float eps, float* out, uint64_t k, uint64_t n,
+                               size_t members) {
+    DeviceGuard guard(g->ctx->device);
+    // Wave kernels accumulate up to kWaveMaxMembers members per launch; larger
+    // batches run as consecutive launch groups over the same weights.
+    for (size_t m0 = 0; m0 < members; m0 += ribn_amd::kWaveMaxMembers) {
+        const size_t mc = std::min<size_t>(ribn_amd::kWaveMaxMembers, members - m0);
+        hipError_t e = ribn_amd::launch_gemv_wave((int)g->value_type, w->data, (uint32_t)w->encoded_bytes,
+                                                  in + m0 * k, out + m0 * n, (int)k, (int)n, (int)mc, gamma, eps,
+                                                  g->ctx->cu_count, g->ctx->stream);
+        if (e != hipSuccess) return driver(e, "launch wave GEMV");
+    }
+    return ok();
+}
+
+ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_context** out) {
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return driver(e, "hipGetDeviceProperties");
+    auto* ctx = new (std::nothrow) ribn_amd_context{device, stream, owns, prop.multiProcessorCount};
+    if (!ctx) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    *out = ctx;
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+ribn_amd_status ribn_amd_last_error(ribn_amd_error* out) {
+    if (!out) return RIBN_AMD_INVALID_ARGUMENT;
+    *out = g_last_error;
+    return RIBN_AMD_OK;
+}
+
+const char* ribn_amd_status_name(int32_t status) {
+    switch (status) {
+    case RIBN_AMD_OK: return "Ok";
+    case RIBN_AMD_DRIVER: return "Driver";
+    case RIBN_AMD_MODULE: return "Module";
+    case RIBN_AMD_INVALID_WEIGHT: return "InvalidWeight";
+    case RIBN_AMD_UNSUPPORTED_VALUE_TYPE: return "UnsupportedValueType";
+    case RIBN_AMD_SHAPE_OVERFLOW: return "ShapeOverflow";
+    case RIBN_AMD_INPUT_LENGTH: return "InputLength";
+    case RIBN_AMD_OUTPUT_LENGTH: return "OutputLength";
+    case RIBN_AMD_CONTEXT_MISMATCH: return "ContextMismatch";
+    case RIBN_AMD_EMPTY_INPUT: return "EmptyInput";
+    case RIBN_AMD_WEIGHT_LENGTH: return "WeightLength";
+    case RIBN_AMD_INVALID_EPSILON: return "InvalidEpsilon";
+    case RIBN_AMD_INVALID_ARGUMENT: return "InvalidArgument";
+    case RIBN_AMD_EMPTY_ENCODING: return "EmptyEncoding";
+    case RIBN_AMD_SOURCE_INCOMPLETE: return "SourceIncomplete";
+    default: return "Unknown";
+    }
+}
+
+int32_t ribn_amd_abi_version(void) { return RIBN_AMD_ABI_VERSION; }
+
+ribn_amd_status ribn_amd_context_create(int32_t device, ribn_amd_context** out) {
+    if (!out) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "out is null");
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return driver(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count) {
+        return fail(RIBN_AMD_DRIVER, (uint64_t)count, (uint64_t)device, "device %d out of range (%d devices)",
+                    device, count);
+    }
+    DeviceGuard guard(device);
+    hipStream_t stream;
+    e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return driver(e, "hipStreamCreateWithFlags");
+    ribn_amd_status st = new_context(device, stream, true, out);
+    if (st != RIBN_AMD_OK) hipStreamDestroy(stream);
+    return st;
+}
+
+ribn_amd_status ribn_amd_context_wrap_stream(int32_t device, void* hip_stream, ribn_amd_context** out) {
+    if (!out) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "out is null");
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return driver(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count) {
+        return fail(RIBN_AMD_DRIVER, (uint64_t)count, (uint64_t)device, "device %d out of range", device);
+    }
+    hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+    if (stream != nullptr) {
+        hipDevice_t sdev;
+        e = hipStreamGetDevice(stream, &sdev);
+        if (e == hipSuccess && sdev != device) {
+            return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)device, (uint64_t)sdev,
+                        "stream belongs to device %d, not %d", sdev, device);
+        }
+    }
+    return new_context(device, stream, false, out);
+}
+
+void ribn_amd_context_destroy(ribn_amd_context* ctx) {
+    if (!ctx) return;
+    if (ctx->owns_stream) {
+        DeviceGuard guard(ctx->device);
+        hipStreamSynchronize(ctx->stream);
+        hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+}
+
+ribn_amd_status ribn_amd_context_synchronize(ribn_amd_context* ctx) {
+    if (!ctx) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null context");
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return driver(e, "hipStreamSynchronize");
+    return ok();
+}
+
+void* ribn_amd_context_stream(const ribn_amd_context* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+int32_t ribn_amd_context_device(const ribn_amd_context* ctx) { return ctx ? ctx->device : -1; }
+
+ribn_amd_status ribn_amd_alloc(ribn_amd_context* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    DeviceGuard guard(ctx->device);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) return driver(e, "hipMalloc");
+    e = hipMemsetAsync(p, 0, bytes ? bytes : 1, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        hipFree(p);
+        return driver(e, "zero-fill");
+    }
+    *out = p;
+    return ok();
+}
+
+ribn_amd_status ribn_amd_free(ribn_amd_context* ctx, void* ptr) {
+    if (!ctx) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null context");
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipFree(ptr);
+    if (e != hipSuccess) return driver(e, "hipFree");
+    return ok();
+}
+
+ribn_amd_status ribn_amd_memcpy_htod(ribn_amd_context* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return driver(e, "host-to-device copy");
+    return ok();
+}
+
+ribn_amd_status ribn_amd_memcpy_dtoh(ribn_amd_context* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return driver(e, "device-to-host copy");
+    return ok();
+}
+
+ribn_amd_status ribn_amd_validate_quantized_geometry(uint32_t kernel_value_type, uint32_t weight_value_type,
+                                                     const uint64_t* dims, size_t rank, uint64_t encoded_bytes,
+                                                     uint64_t* input_size, uint64_t* output_size) {
+    if (weight_value_type != kernel_value_type) {
+        return fail(RIBN_AMD_UNSUPPORTED_VALUE_TYPE, kernel_value_type, weight_value_type,
+                    "quantized GEMV requires GGML value type %u, got %u", kernel_value_type, weight_value_type);
+    }
+    if (!supported(kernel_value_type)) {
+        return fail(RIBN_AMD_UNSUPPORTED_VALUE_TYPE, RIBN_AMD_Q4_K, kernel_value_type,
+                    "GGML value type %u has no MI355X kernel", kernel_value_type);
+    }
+    if (rank != 2 || dims == nullptr) {
+        return fail(RIBN_AMD_INVALID_WEIGHT, 2, rank, "expected rank-2 tensor, got rank %zu", rank);
+    }
+    const uint64_t k = dims[0], n = dims[1];
+    const uint64_t bb = block_bytes(kernel_value_type);
+    if (k == 0 || n == 0 || k % 256 != 0) {
+        return fail(RIBN_AMD_INVALID_WEIGHT, 256, k,
+                    "%s shape is %llux%llu; input size must be a positive multiple of 256",
+                    type_label(kernel_value_type), (unsigned long long)k, (unsigned long long)n);
+    }
+    const uint64_t per_row = k / 256;
+    if (per_row > std::numeric_limits<uint64_t>::max() / n) return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "block count overflows");
+    const uint64_t blocks = per_row * n;
+    if (blocks > std::numeric_limits<uint64_t>::max() / bb) return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "byte count overflows");
+    const uint64_t expected = blocks * bb;
+    if (encoded_bytes != expected) {
+        return fail(RIBN_AMD_INVALID_WEIGHT, expected, encoded_bytes, "encoded length is %llu, expected %llu",
+                    (unsigned long long)encoded_bytes, (unsigned long long)expected);
+    }
+    // quantized.rs:1795-1800: every byte offset and dimension must fit i32.
+    // (Offsets are additionally bounded by the buffer resource's 32-bit range.)
+    if (blocks > (uint64_t)std::numeric_limits<int32_t>::max() / bb) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "encoded tensor exceeds the i32 byte-offset range");
+    }
+    if (k > (uint64_t)std::numeric_limits<int32_t>::max() || n > (uint64_t)std::numeric_limits<int32_t>::max()) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "dimension exceeds i32");
+    }
+    if (input_size) *input_size = k;
+    if (output_size) *output_size = n;
+    return ok();
+}
+
+static ribn_amd_status new_weight(ribn_amd_context* ctx, uint32_t value_type, uint64_t k, uint64_t n,
+                                  uint64_t encoded_bytes, ribn_amd_quantized_weight** out) {
+    if (!ctx || !out) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (encoded_bytes == 0) return fail(RIBN_AMD_EMPTY_ENCODING, 1, 0, "tensor has an empty encoding");
+    if (encoded_bytes > (uint64_t)std::numeric_limits<size_t>::max()) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "encoded length does not fit the host");
+    }
+    auto* w = new (std::nothrow) ribn_amd_quantized_weight{ctx, value_type, k, n, encoded_bytes, nullptr, true};
+    if (!w) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->data), encoded_bytes);
+    if (e != hipSuccess) {
+        delete w;
+        return driver(e, "hipMalloc weight");
+    }
+    *out = w;
+    return RIBN_AMD_OK;
+}
+
+ribn_amd_status ribn_amd_weight_materialize(ribn_amd_context* ctx, uint32_t value_type, uint64_t input_size,
+                                            uint64_t output_size, const uint8_t* encoded, uint64_t encoded_bytes,
+                                            ribn_amd_quantized_weight** out) {
+    if (!encoded && encoded_bytes) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "encoded is null");
+    ribn_amd_quantized_weight* w = nullptr;
+    ribn_amd_status st = new_weight(ctx, value_type, input_size, output_size, encoded_bytes, &w);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipMemcpyAsync(w->data, encoded, encoded_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        ribn_amd_weight_destroy(w);
+        return driver(e, "upload weight");
+    }
+    *out = w;
+    return ok();
+}
+
+ribn_amd_status ribn_amd_weight_materialize_reader(ribn_amd_context* ctx, uint32_t value_type,
+                                                   uint64_t input_size, uint64_t output_size,
+                                                   uint64_t encoded_bytes, ribn_amd_read_fn read, void* user,
+                                                   ribn_amd_quantized_weight** out) {
+    if (!read) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "read callback is null");
+    ribn_amd_quantized_weight* w = nullptr;
+    ribn_amd_status st = new_weight(ctx, value_type, input_size, output_size, encoded_bytes, &w);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(ctx->device);
+    const size_t chunk = (size_t)std::min<uint64_t>(encoded_bytes, 1u << 20);
+    std::vector<uint8_t> host(chunk);
+    uint64_t offset = 0;
+    while (offset < encoded_bytes) {
+        const size_t requested = (size_t)std::min<uint64_t>(encoded_bytes - offset, chunk);
+        size_t filled = 0;
+        while (filled < requested) {
+            const int64_t got = read(user, host.data() + filled, requested - filled);
+            if (got < 0) {
+                ribn_amd_weight_destroy(w);
+                return fail(RIBN_AMD_SOURCE_INCOMPLETE, encoded_bytes, offset + filled, "source read failed");
+            }
+            if (got == 0) {
+                ribn_amd_weight_destroy(w);
+                return fail(RIBN_AMD_SOURCE_INCOMPLETE, encoded_bytes, offset + filled,
+                            "source ended after %llu of %llu bytes", (unsigned long long)(offset + filled),
+                            (unsigned long long)encoded_bytes);
+            }
+            filled += (size_t)got;
+        }
+        hipError_t e = hipMemcpyAsync(w->data + offset, host.data(), requested, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            ribn_amd_weight_destroy(w);
+            return driver(e, "upload weight chunk");
+        }
+        offset += requested;
+    }
+    *out = w;
+    return ok();
+}
+
+ribn_amd_status ribn_amd_weight_wrap_device(ribn_amd_context* ctx, uint32_t value_type, uint64_t input_size,
+                                            uint64_t output_size, const void* device_bytes, uint64_t encoded_bytes,
+                                            ribn_amd_quantized_weight** out) {
+    if (!ctx || !out) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (encoded_bytes == 0) return fail(RIBN_AMD_EMPTY_ENCODING, 1, 0, "tensor has an empty encoding");
+    ribn_amd_status st = check_device_ptr(ctx, device_bytes, "weight bytes");
+    if (st != RIBN_AMD_OK) return st;
+    auto* w = new (std::nothrow) ribn_amd_quantized_weight{
+        ctx, value_type, input_size, output_size, encoded_bytes,
+        const_cast<uint8_t*>(static_cast<const uint8_t*>(device_bytes)), false};
+    if (!w) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    *out = w;
+    return ok();
+}
+
+ribn_amd_status ribn_amd_weight_copy_to_host(ribn_amd_context* ctx, const ribn_amd_quantized_weight* weight,
+                                             uint8_t* host, uint64_t capacity) {
+    if (!ctx || !weight || !host) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (capacity != weight->encoded_bytes) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, weight->encoded_bytes, capacity, "host buffer holds %llu bytes, need %llu",
+                    (unsigned long long)capacity, (unsigned long long)weight->encoded_bytes);
+    }
+    return ribn_amd_memcpy_dtoh(ctx, host, weight->data, (size_t)capacity);
+}
+
+void ribn_amd_weight_destroy(ribn_amd_quantized_weight* weight) {
+    if (!weight) return;
+    if (weight->owns_data && weight->data) {
+        DeviceGuard guard(weight->ctx->device);
+        hipStreamSynchronize(weight->ctx->stream);
+        hipFree(weight->data);
+    }
+    delete weight;
+}
+
+uint32_t ribn_amd_weight_value_type(const ribn_amd_quantized_weight* w) { return w ? w->value_type : 0; }
+uint64_t ribn_amd_weight_encoded_bytes(const ribn_amd_quantized_weight* w) { return w ? w->encoded_bytes : 0; }
+uint64_t ribn_amd_weight_input_size(const ribn_amd_quantized_weight* w) { return w ? w->input_size : 0; }
+uint64_t ribn_amd_weight_output_size(const ribn_amd_quantized_weight* w) { return w ? w->output_size : 0; }
+const void* ribn_amd_weight_device_ptr(const ribn_amd_quantized_weight* w) { return w ? w->data : nullptr; }
+
+ribn_amd_status ribn_amd_gemv_create(ribn_amd_context* ctx, uint32_t value_type, ribn_amd_gemv** out) {
+    if (!ctx || !out) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (!supported(value_type)) {
+        return fail(RIBN_AMD_UNSUPPORTED_VALUE_TYPE, RIBN_AMD_Q4_K, value_type,
+                    "GGML value type %u has no MI355X GEMV kernel", value_type);
+    }
+    auto* g = new (std::nothrow) ribn_amd_gemv{ctx, value_type};
+    if (!g) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    *out = g;
+    return ok();
+}
+
+void ribn_amd_gemv_destroy(ribn_amd_gemv* gemv) { delete gemv; }
+uint32_t ribn_amd_gemv_value_type(const ribn_amd_gemv* gemv) { return gemv ? gemv->value_type : 0; }
+
+ribn_amd_status ribn_amd_gemv_execute(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const float* input,
+                                      size_t input_len, float* output, size_t output_len) {
+    uint64_t k, n;
+    ribn_amd_status st = validate_launch(g, w, input, input_len, output, output_len, 1, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(g->ctx->device);
+    hipError_t e = ribn_amd::launch_gemv_exact((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, input,
+                                               output, (int)k, (int)n, 1, g->ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch exact GEMV");
+    return ok();
+}
+
+ribn_amd_status ribn_amd_gemv_execute_warp(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w,
+                                           const float* input, size_t input_len, float* output,
+                                           size_t output_len) {
+    uint64_t k, n;
+    ribn_amd_status st = validate_launch(g, w, input, input_len, output, output_len, 1, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    return launch_batched(g, w, input, nullptr, 0.f, output, k, n, 1);
+}
+
+ribn_amd_status ribn_amd_gemv_execute_warp_batch(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w,
+                                                 const float* input, size_t input_len, float* output,
+                                                 size_t output_len, size_t members) {
+    ribn_amd_status st = validate_members(g, members);
+    if (st != RIBN_AMD_OK) return st;
+    uint64_t k, n;
+    st = validate_launch(g, w, input, input_len, output, output_len, members, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    return launch_batched(g, w, input, nullptr, 0.f, output, k, n, members);
+}
+
+ribn_amd_status ribn_amd_gemv_execute_rms_norm(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w,
+                                               const float* input, size_t input_len, const float* gamma,
+                                               size_t gamma_len, float epsilon, float* output,
+                                               size_t output_len, size_t members) {
+    ribn_amd_status st = validate_members(g, members);
+    if (st != RIBN_AMD_OK) return st;
+    uint64_t k, n;
+    st = validate_launch(g, w, input, input_len, output, output_len, members, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    st = check_device_ptr(g->ctx, gamma, "gamma");
+    if (st != RIBN_AMD_OK) return st;
+    if (gamma_len != k) {
+        return fail(RIBN_AMD_WEIGHT_LENGTH, k, gamma_len, "RMSNorm weight has %zu values, expected %llu", gamma_len,
+                    (unsigned long long)k);
+    }
+    if (!(epsilon > 0.f) || epsilon == std::numeric_limits<float>::infinity()) {
+        return fail(RIBN_AMD_INVALID_EPSILON, 0, 0, "RMSNorm epsilon must be finite and positive");
+    }
+    return launch_batched(g, w, input, gamma, epsilon, output, k, n, members);
+}
+
+ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, float* output,
+                                    size_t output_len) {
+    if (!g || !w) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null kernel or weight handle");
+    ribn_amd_status st = check_device_ptr(g->ctx, output, "output");
+    if (st != RIBN_AMD_OK) return st;
+    uint64_t k, n;
+    st = validate_geometry(g->value_type, w, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    if (output_len != k * n) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, k * n, output_len, "dequantized output has %zu values, expected %llu",
+                    output_len, (unsigned long long)(k * n));
+    }
+    DeviceGuard guard(g->ctx->device);
+    hipError_t e = ribn_amd::launch_dequant((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, output,
+                                            (uint32_t)(k / 256 * n), g->ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch dequantize");
+    return ok();
+}
+
+static ribn_amd_status rms_common(ribn_amd_context* ctx, const float* input, size_t input_len, const float* weight,
+                                  size_t weight_len, float* output, size_t output_len, size_t length,
+                                  float epsilon) {
+    if (!ctx) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null context");
+    ribn_amd_status st = check_device_ptr(ctx, input, "input");
+    if (st == RIBN_AMD_OK) st = check_device_ptr(ctx, weight, "weight");
+    if (st == RIBN_AMD_OK) st = check_device_ptr(ctx, output, "output");
+    if (st != RIBN_AMD_OK) return st;
+    // model_ops.rs:1780-1806 order: empty, divisibility, weight, output, epsilon.
+    if (input_len == 0 || length == 0) return fail(RIBN_AMD_EMPTY_INPUT, 1, 0, "RMSNorm input is empty");
+    if (input_len % length != 0) {
+        return fail(RIBN_AMD_INPUT_LENGTH, input_len, length, "input of %zu values is not a multiple of %zu",
+                    input_len, length);
+    }
+    if (weight_len != length) {
+        return fail(RIBN_AMD_WEIGHT_LENGTH, length, weight_len, "RMSNorm weight has %zu values, expected %zu",
+                    weight_len, length);
+    }
+    if (output_len != input_len) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, input_len, output_len, "RMSNorm output has %zu values, expected %zu",
+                    output_len, input_len);
+    }
+    if (!(epsilon > 0.f) || epsilon == std::numeric_limits<float>::infinity()) {
+        return fail(RIBN_AMD_INVALID_EPSILON, 0, 0, "RMSNorm epsilon must be finite and positive");
+    }
+    const size_t members = input_len / length;
+    if (length > (size_t)std::numeric_limits<int>::max() || members > (size_t)std::numeric_limits<int>::max()) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "RMSNorm shape exceeds launch limits");
+    }
+    DeviceGuard guard(ctx->device);
+    hipError_t e = ribn_amd::launch_rms_norm(input, weight, output, (int)length, (int)members, epsilon, ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch RMSNorm");
+    return ok();
+}
+
+ribn_amd_status ribn_amd_rms_norm(ribn_amd_context* ctx, const float* input, size_t input_len, const float* weight,
+                                  size_t weight_len, float* output, size_t output_len, float epsilon) {
+    // model_ops.rs:1714-1760: one vector; weight and output lengths equal the input's.
+    return rms_common(ctx, input, input_len, weight, weight_len, output, output_len, input_len, epsilon);
+}
+
+ribn_amd_status ribn_amd_rms_norm_batch(ribn_amd_context* ctx, const float* input, size_t input_len,
+                                        const float* weight, size_t weight_len, float* output, size_t output_len,
+                                        size_t length, float epsilon) {
+    return rms_common(ctx, input, input_len, weight, weight_len, output, output_len, length, epsilon);
+}
+
+}  // extern "C"

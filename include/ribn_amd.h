@@ -1,0 +1,207 @@
+/*
+ * ribn_amd.h -- C ABI of the MI355X (gfx950) k-quant decode path.
+ *
+ * This is the drop-in boundary a Rust `crates/amd` backend binds in place of
+ * the reference's `crates/nvidia` operators. Every entry point below names the
+ * reference interface it replaces (paths relative to nijaru/engine). Device
+ * buffers are plain pointers plus element counts (the reference passes
+ * `CudaSlice<T>`, whose `len()` the C side receives explicitly); no torch or
+ * HIP C++ types appear in signatures. HIP streams are passed as `void*`.
+ *
+ * Conventions
+ *  - GGML dims are [K, N]: K is the contiguous input size, N the output rows
+ *    (crates/nvidia/src/quantized.rs:136-142). Encoded weights stay in GGML's
+ *    array-of-blocks layout on the device; nothing is repacked.
+ *  - Activations are f32 batch-major [members][K]; outputs [members][N].
+ *  - Launches are asynchronous on the context's stream; completion is observed
+ *    by ribn_amd_context_synchronize or a later stream-ordered copy
+ *    (quantized.rs:357-363). Execute calls never allocate device memory.
+ *  - Every call validates before launching and returns a status; details
+ *    (expected/actual values, message) are kept per thread and read with
+ *    ribn_amd_last_error (mirrors CudaQuantizedKernelError, quantized.rs:91-134,
+ *    and CudaModelKernelError, model_ops.rs:12-22).
+ *  - Device pointers handed to kernels must be 16-byte aligned (hipMalloc and
+ *    ribn_amd_alloc return 256-byte-aligned memory).
+ *  - Thread compatibility: a context and its kernel objects may be used from
+ *    one thread at a time; distinct contexts are independent.
+ */
+#ifndef RIBN_AMD_H
+#define RIBN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RIBN_AMD_ABI_VERSION 1
+
+/* GGML value types served by this library (quantized.rs:25-27). */
+#define RIBN_AMD_Q4_K 12u
+#define RIBN_AMD_Q5_K 13u
+#define RIBN_AMD_Q6_K 14u
+
+/* Members one batched launch accepts. The reference caps its weights-read-once
+ * kernels at 8 (quantized.rs:12); this library serves decode batches up to 64
+ * and prefill through ribn_amd_gemm_prefill. */
+#define RIBN_AMD_MAX_BATCH_MEMBERS 64u
+
+typedef enum ribn_amd_status {
+    RIBN_AMD_OK = 0,
+    RIBN_AMD_DRIVER = 1,                 /* Driver(String): a HIP runtime call failed */
+    RIBN_AMD_MODULE = 2,                 /* Nvrtc(String): no gfx950 code object for this device */
+    RIBN_AMD_INVALID_WEIGHT = 3,         /* InvalidWeight(String) */
+    RIBN_AMD_UNSUPPORTED_VALUE_TYPE = 4, /* UnsupportedValueType { expected, actual } */
+    RIBN_AMD_SHAPE_OVERFLOW = 5,         /* ShapeOverflow */
+    RIBN_AMD_INPUT_LENGTH = 6,           /* InputLength { expected, actual } */
+    RIBN_AMD_OUTPUT_LENGTH = 7,          /* OutputLength { expected, actual } */
+    RIBN_AMD_CONTEXT_MISMATCH = 8,       /* ContextMismatch: buffer on another device */
+    RIBN_AMD_EMPTY_INPUT = 9,            /* CudaModelKernelError::EmptyInput */
+    RIBN_AMD_WEIGHT_LENGTH = 10,         /* CudaModelKernelError::WeightLength { expected, actual } */
+    RIBN_AMD_INVALID_EPSILON = 11,       /* CudaModelKernelError::InvalidEpsilon */
+    RIBN_AMD_INVALID_ARGUMENT = 12,      /* null handle / misaligned pointer (no reference twin) */
+    RIBN_AMD_EMPTY_ENCODING = 13,        /* CudaWeightError::EmptyEncoding (cuda.rs:335-337) */
+    RIBN_AMD_SOURCE_INCOMPLETE = 14,     /* CudaWeightError::SourceIncomplete (cuda.rs:350-356) */
+} ribn_amd_status;
+
+typedef struct ribn_amd_error {
+    int32_t status;
+    uint64_t expected;
+    uint64_t actual;
+    char message[512];
+} ribn_amd_error;
+
+typedef struct ribn_amd_context ribn_amd_context;
+typedef struct ribn_amd_quantized_weight ribn_amd_quantized_weight;
+typedef struct ribn_amd_gemv ribn_amd_gemv;
+
+/* ---------------------------------------------------------------- errors */
+
+/* Copies the calling thread's last error record (status RIBN_AMD_OK if none). */
+ribn_amd_status ribn_amd_last_error(ribn_amd_error *out);
+/* Static, NUL-terminated name of a status ("InputLength", ...). */
+const char *ribn_amd_status_name(int32_t status);
+int32_t ribn_amd_abi_version(void);
+
+/* ------------------------------------------------------------- lifecycle */
+
+/* CudaContext::new(device) + context.default_stream() (quantized.rs:1487-1492):
+ * a context owning a fresh non-blocking stream on `device`. */
+ribn_amd_status ribn_amd_context_create(int32_t device, ribn_amd_context **out);
+/* from_context(&ctx, stream) (quantized.rs:1500-1516): wraps a caller-owned HIP
+ * stream; the caller keeps ownership and must outlive the context. */
+ribn_amd_status ribn_amd_context_wrap_stream(int32_t device, void *hip_stream, ribn_amd_context **out);
+void ribn_amd_context_destroy(ribn_amd_context *ctx);
+/* CudaStream::synchronize. */
+ribn_amd_status ribn_amd_context_synchronize(ribn_amd_context *ctx);
+void *ribn_amd_context_stream(const ribn_amd_context *ctx);
+int32_t ribn_amd_context_device(const ribn_amd_context *ctx);
+
+/* ---------------------------------------------------- device memory helpers */
+
+/* CudaStream::alloc_zeros::<u8>(bytes): zero-filled, 256-byte aligned. */
+ribn_amd_status ribn_amd_alloc(ribn_amd_context *ctx, size_t bytes, void **out);
+ribn_amd_status ribn_amd_free(ribn_amd_context *ctx, void *device_ptr);
+/* clone_htod / clone_dtoh: stream-ordered copies that return after completion. */
+ribn_amd_status ribn_amd_memcpy_htod(ribn_amd_context *ctx, void *dst, const void *src, size_t bytes);
+ribn_amd_status ribn_amd_memcpy_dtoh(ribn_amd_context *ctx, void *dst, const void *src, size_t bytes);
+
+/* ----------------------------------------------------------- weight store */
+
+/* Pull-style source for ribn_amd_weight_materialize_reader, mirroring
+ * `&mut impl Read`: returns bytes written to buf (0 = end of source), or a
+ * negative value on a source error. */
+typedef int64_t (*ribn_amd_read_fn)(void *user, uint8_t *buf, size_t capacity);
+
+/* CudaWeightStore::materialize_quantized (crates/nvidia/src/cuda.rs:321-387):
+ * uploads `encoded_bytes` opaque GGML bytes of a [input_size=K, output_size=N]
+ * tensor of `value_type`. The bytes are not interpreted or repacked; geometry
+ * is checked when a kernel uses the weight (validate_quantized_geometry). */
+ribn_amd_status ribn_amd_weight_materialize(ribn_amd_context *ctx, uint32_t value_type, uint64_t input_size,
+                                            uint64_t output_size, const uint8_t *encoded, uint64_t encoded_bytes,
+                                            ribn_amd_quantized_weight **out);
+/* Same, streaming from `read` in 1 MiB chunks (cuda.rs:340-377). */
+ribn_amd_status ribn_amd_weight_materialize_reader(ribn_amd_context *ctx, uint32_t value_type,
+                                                   uint64_t input_size, uint64_t output_size,
+                                                   uint64_t encoded_bytes, ribn_amd_read_fn read, void *user,
+                                                   ribn_amd_quantized_weight **out);
+/* Adopts `encoded_bytes` already resident on the context's device (no copy;
+ * the caller keeps ownership of the memory). */
+ribn_amd_status ribn_amd_weight_wrap_device(ribn_amd_context *ctx, uint32_t value_type, uint64_t input_size,
+                                            uint64_t output_size, const void *device_bytes, uint64_t encoded_bytes,
+                                            ribn_amd_quantized_weight **out);
+/* CudaWeightStore::copy_quantized_to_host (cuda.rs:451-458): exact bytes back. */
+ribn_amd_status ribn_amd_weight_copy_to_host(ribn_amd_context *ctx, const ribn_amd_quantized_weight *weight,
+                                             uint8_t *host, uint64_t capacity);
+void ribn_amd_weight_destroy(ribn_amd_quantized_weight *weight);
+/* CudaQuantizedWeight accessors (cuda.rs:164-183). */
+uint32_t ribn_amd_weight_value_type(const ribn_amd_quantized_weight *weight);
+uint64_t ribn_amd_weight_encoded_bytes(const ribn_amd_quantized_weight *weight);
+uint64_t ribn_amd_weight_input_size(const ribn_amd_quantized_weight *weight);
+uint64_t ribn_amd_weight_output_size(const ribn_amd_quantized_weight *weight);
+const void *ribn_amd_weight_device_ptr(const ribn_amd_quantized_weight *weight);
+
+/* validate_quantized_geometry (quantized.rs:1755-1804), host-only: checks the
+ * value type against the kernel's, rank 2, K a positive multiple of 256, the
+ * exact encoded length and i32 launch limits. Writes (K, N) on success. */
+ribn_amd_status ribn_amd_validate_quantized_geometry(uint32_t kernel_value_type, uint32_t weight_value_type,
+                                                     const uint64_t *dims, size_t rank, uint64_t encoded_bytes,
+                                                     uint64_t *input_size, uint64_t *output_size);
+
+/* ----------------------------------------------------------- GEMV kernels */
+
+/* CudaQ4KGemv / CudaQ5KGemv / CudaQ6KGemv ::from_context (quantized.rs:1465-1753),
+ * i.e. QwenGemvKernel::from_value_type (staging.rs:108-127): a kernel object
+ * for one GGML value type on a context. Unsupported types return
+ * UnsupportedValueType { expected: 12, actual }. */
+ribn_amd_status ribn_amd_gemv_create(ribn_amd_context *ctx, uint32_t value_type, ribn_amd_gemv **out);
+void ribn_amd_gemv_destroy(ribn_amd_gemv *gemv);
+uint32_t ribn_amd_gemv_value_type(const ribn_amd_gemv *gemv);
+
+/* execute (quantized.rs:356-388): y[N] = W x[K]. Exact-order kernel: per row,
+ * elements in K order, each product and sum rounded separately, so results
+ * equal the host decoder + sequential f32 dot bit for bit. Correctness oracle;
+ * slow. */
+ribn_amd_status ribn_amd_gemv_execute(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
+                                      const float *input, size_t input_len, float *output, size_t output_len);
+/* execute_warp (quantized.rs:401-435): the wave64 bandwidth kernel (default decode path). */
+ribn_amd_status ribn_amd_gemv_execute_warp(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
+                                           const float *input, size_t input_len, float *output,
+                                           size_t output_len);
+/* execute_warp_batch (quantized.rs:445-487): `members` batch-major rows,
+ * weights read once per launch group. input_len == members*K,
+ * output_len == members*N, 1 <= members <= RIBN_AMD_MAX_BATCH_MEMBERS.
+ * Per row bit-identical to execute_warp for members <= 4. */
+ribn_amd_status ribn_amd_gemv_execute_warp_batch(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
+                                                 const float *input, size_t input_len, float *output,
+                                                 size_t output_len, size_t members);
+/* RMSNorm fused into the activation load of execute_warp_batch: replaces the
+ * pair rms_norm_batch (model_ops.rs:1770-1824) + gemv_batch (decode.rs:1516-1558)
+ * with one launch computing y_m = W * (x_m * inv_rms(x_m) * gamma),
+ * inv_rms = 1/sqrt(sum(x^2)/K + eps). gamma has K values. */
+ribn_amd_status ribn_amd_gemv_execute_rms_norm(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
+                                               const float *input, size_t input_len, const float *gamma,
+                                               size_t gamma_len, float epsilon, float *output,
+                                               size_t output_len, size_t members);
+/* Bit-exact device dequantisation to f32 [N][K] (twin of lib.rs:596-661;
+ * the reference's device equivalent is the q4_k_embedding gather, q4_k.cu:1-67). */
+ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight, float *output,
+                                    size_t output_len);
+
+/* ------------------------------------------------------------- model ops */
+
+/* CudaQwen35Ops::rms_norm (model_ops.rs:1714-1760). */
+ribn_amd_status ribn_amd_rms_norm(ribn_amd_context *ctx, const float *input, size_t input_len,
+                                  const float *weight, size_t weight_len, float *output, size_t output_len,
+                                  float epsilon);
+/* CudaQwen35Ops::rms_norm_batch (model_ops.rs:1770-1824): [members][length]. */
+ribn_amd_status ribn_amd_rms_norm_batch(ribn_amd_context *ctx, const float *input, size_t input_len,
+                                        const float *weight, size_t weight_len, float *output,
+                                        size_t output_len, size_t length, float epsilon);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RIBN_AMD_H */

@@ -1,0 +1,34 @@
+"""Shared helpers for the GPU parity tests (device buffers via torch)."""
+import numpy as np
+
+# Max relative error bound for GEMV/GEMM outputs against the f32-accumulated
+# oracle, measured normwise: max|y - ref| <= RTOL * max|ref|.
+RTOL = 1e-3
+
+
+def max_rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = max(float(np.abs(ref).max()), 1e-30)
+    return float(np.abs(got - ref).max()) / scale
+
+
+def to_dev(a, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to("cuda:0")
+
+
+def empty_dev(n, dtype=None):
+    import torch
+    return torch.full((n,), float("nan"), dtype=dtype or torch.float32, device="cuda:0")
+
+
+def to_host(t, ctx=None):
+    import torch
+    if ctx is not None:
+        ctx.synchronize()
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()

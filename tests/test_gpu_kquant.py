@@ -1,0 +1,297 @@
+"""GPU parity tests for the k-quant path, called through the C ABI.
+
+Bars: dequantised weights bit-exact against the oracle; the exact-order GEMV
+bit-exact against the oracle's sequential f32 dot; the wave GEMV (default
+decode path), batched and RMSNorm-fused variants within max relative error
+1e-3 (normwise, gpu_helpers.RTOL) of the oracle. Full BASELINE shapes are
+checked against the oracle too (the C oracle runs them in well under a second
+each) and through size-independent properties (linearity, batch/single
+bit identity).
+"""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+from engine_amd import synth
+from oracle import kquant_oracle as O
+
+from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "kquant_golden.npz")
+TYPES = (12, 13, 14)
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    import engine_amd as E
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    ctx = E.AmdContext(0)
+    store = E.AmdWeightStore(ctx)
+    kernels = {t: E.QwenGemvKernel.from_value_type(ctx, t) for t in TYPES}
+    return {"E": E, "ctx": ctx, "store": store, "k": kernels, "n": [0]}
+
+
+def upload(env, t, k, n, enc):
+    env["n"][0] += 1
+    name = f"w{env['n'][0]}"
+    env["store"].materialize_quantized(name, [k, n], t, enc)
+    return env["store"].quantized_tensor(name)
+
+
+def print_case(**kw):
+    print("CASE", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_reference_fixture_bit_exact(env, t):
+    g = np.load(GOLDEN)
+    enc = g[f"fixture_{t}_encoded"]
+    w = upload(env, t, 512, 2, enc)
+    out = empty_dev(1024)
+    env["k"][t].dequantize(w, out)
+    got = to_host(out, env["ctx"])
+    assert np.array_equal(got.view(np.uint32), g[f"fixture_{t}_dequant"].view(np.uint32))
+
+
+@pytest.mark.parametrize("t,k,n", [(12, 4096, 4096), (13, 12288, 512), (14, 4096, 1024), (14, 512, 33),
+                                   (12, 256, 1), (13, 768, 7)])
+def test_dequant_bit_exact_random(env, t, k, n):
+    print_case(test="dequant", t=t, k=k, n=n)
+    enc = synth.kquant_numpy(t, k, n, seed=1000 + t + k + n)
+    w = upload(env, t, k, n, enc)
+    out = empty_dev(k * n)
+    env["k"][t].dequantize(w, out)
+    got = to_host(out, env["ctx"])
+    ref = O.dequantize_tensor(t, enc)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_golden_checksums(env):
+    g = np.load(GOLDEN)
+    i = 0
+    while f"random_{i}_meta" in g:
+        t, k, n, m, seed = (int(v) for v in g[f"random_{i}_meta"])
+        w = upload(env, t, k, n, g[f"random_{i}_encoded"])
+        out = empty_dev(k * n)
+        env["k"][t].dequantize(w, out)
+        got = to_host(out, env["ctx"])
+        assert hashlib.sha256(got.tobytes()).hexdigest() == bytes(g[f"random_{i}_dequant_sha256"]).decode()
+        i += 1
+
+
+# ------------------------------------------------------- reference fixtures
+
+@pytest.mark.parametrize("t", TYPES)
+def test_reference_device_fixture(env, t):
+    # cuda_reference.rs:858-960 (and the Q6_K twin): [512, 2], input (i%17)*0.125-1, |d| < 1e-3
+    g = np.load(GOLDEN)
+    w = upload(env, t, 512, 2, g[f"fixture_{t}_encoded"])
+    x = to_dev(g[f"fixture_{t}_input"])
+    expected = g[f"fixture_{t}_output"]
+    for variant in ("execute", "execute_warp"):
+        y = empty_dev(2)
+        getattr(env["k"][t], variant)(w, x, y)
+        got = to_host(y, env["ctx"])
+        assert np.all(np.abs(got - expected) < 1e-3), (variant, got, expected)
+    y = empty_dev(2)
+    env["k"][t].execute(w, x, y)
+    assert np.array_equal(to_host(y, env["ctx"]), expected)
+
+
+# ------------------------------------------------------------- exact GEMV
+
+@pytest.mark.parametrize("t,k,n", [(12, 1024, 64), (13, 768, 40), (14, 1280, 24), (12, 4096, 256)])
+def test_exact_gemv_bit_identical_to_oracle(env, t, k, n):
+    print_case(test="exact", t=t, k=k, n=n)
+    enc = synth.kquant_numpy(t, k, n, seed=7 * k + n + t)
+    x = synth.activations_numpy(k, 1, seed=n)[0]
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(n)
+    env["k"][t].execute(w, to_dev(x), y)
+    got = to_host(y, env["ctx"])
+    ref = O.quant_gemv(t, enc, k, n, x)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# --------------------------------------------------------------- wave GEMV
+
+def test_golden_random_cases_wave_and_batch(env):
+    g = np.load(GOLDEN)
+    i = 0
+    while f"random_{i}_meta" in g:
+        t, k, n, m, seed = (int(v) for v in g[f"random_{i}_meta"])
+        print_case(test="golden", i=i, t=t, k=k, n=n, m=m)
+        w = upload(env, t, k, n, g[f"random_{i}_encoded"])
+        x = to_dev(g[f"random_{i}_input"].reshape(-1))
+        y = empty_dev(m * n)
+        env["k"][t].execute_warp_batch(w, x, y, m)
+        got = to_host(y, env["ctx"]).reshape(m, n)
+        assert max_rel_err(got, g[f"random_{i}_output"]) <= RTOL
+        i += 1
+
+
+# Qwen3-8B projection shapes plus ragged / small edges.
+SHAPES = [
+    (12, 4096, 4096), (12, 4096, 1024), (12, 4096, 12288), (13, 12288, 4096), (14, 4096, 4096),
+    (14, 12288, 4096), (12, 256, 1), (13, 256, 3), (14, 256, 5), (12, 768, 333), (14, 2304, 77),
+    (12, 5120, 100), (13, 4352, 64),
+]
+
+
+@pytest.mark.parametrize("t,k,n", SHAPES)
+def test_wave_gemv_against_oracle(env, t, k, n):
+    print_case(test="wave", t=t, k=k, n=n)
+    enc = synth.kquant_numpy(t, k, n, seed=k + 3 * n + t)
+    x = synth.activations_numpy(k, 1, seed=n + 5)[0]
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(n)
+    env["k"][t].execute_warp(w, to_dev(x), y)
+    got = to_host(y, env["ctx"])
+    ref = O.quant_gemv(t, enc, k, n, x, threads=8)
+    err = max_rel_err(got, ref)
+    print(f"max_rel_err={err:.3e}", flush=True)
+    assert err <= RTOL
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("members", [1, 2, 3, 4, 5, 8, 13])
+def test_batch_matches_oracle_and_single_bitwise(env, t, members):
+    k, n = 1024, 96
+    print_case(test="batch", t=t, members=members)
+    enc = synth.kquant_numpy(t, k, n, seed=members + 31 * t)
+    x = synth.activations_numpy(k, members, seed=members)
+    w = upload(env, t, k, n, enc)
+    xd = to_dev(x.reshape(-1))
+    y = empty_dev(members * n)
+    env["k"][t].execute_warp_batch(w, xd, y, members)
+    got = to_host(y, env["ctx"]).reshape(members, n)
+    ref = O.quant_gemv(t, enc, k, n, x.reshape(-1), members=members).reshape(members, n)
+    assert max_rel_err(got, ref) <= RTOL
+    # weights-read-once batching keeps every row bit-identical to the single path
+    for m in range(members):
+        ys = empty_dev(n)
+        env["k"][t].execute_warp(w, to_dev(x[m]), ys)
+        assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
+
+
+@pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096), (14, 4096, 4096)])
+def test_linearity_full_size(env, t, k, n):
+    # W(a x1 + b x2) = a W x1 + b W x2 (size-independent property)
+    enc = synth.kquant_numpy(t, k, n, seed=99 + t)
+    x = synth.activations_numpy(k, 2, seed=17)
+    a, b = np.float32(0.75), np.float32(-1.25)
+    w = upload(env, t, k, n, enc)
+    outs = []
+    for v in (x[0], x[1], a * x[0] + b * x[1]):
+        y = empty_dev(n)
+        env["k"][t].execute_warp(w, to_dev(v.astype(np.float32)), y)
+        outs.append(to_host(y, env["ctx"]).astype(np.float64))
+    assert max_rel_err(outs[2], a * outs[0] + b * outs[1]) <= RTOL
+
+
+# -------------------------------------------------------------- RMSNorm
+
+def test_rms_norm_against_oracle(env):
+    import torch
+    g = np.load(GOLDEN)
+    ops = env["E"].AmdQwenOps.from_context(env["ctx"])
+    for name, eps in (("rms_small", 1e-5), ("rms_4096", 1e-6)):
+        x = to_dev(g[f"{name}_input"])
+        w = to_dev(g[f"{name}_weight"])
+        y = torch.empty_like(x)
+        ops.rms_norm(x, w, y, eps)
+        got = to_host(y, env["ctx"])
+        assert np.allclose(got, g[f"{name}_output"], rtol=1e-5, atol=1e-6)
+    xb = synth.activations_numpy(4096, 3, seed=2)
+    gam = synth.gamma_numpy(4096, seed=3)
+    yb = empty_dev(3 * 4096)
+    ops.rms_norm_batch(to_dev(xb.reshape(-1)), to_dev(gam), yb, 4096, 1e-6)
+    got = to_host(yb, env["ctx"]).reshape(3, 4096)
+    for m in range(3):
+        assert np.allclose(got[m], O.rms_norm_raw(xb[m], gam, 1e-6), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("t,k,n,members", [(12, 4096, 4096, 1), (12, 4096, 12288, 1), (12, 4096, 1024, 4),
+                                           (14, 4096, 512, 2), (13, 4096, 256, 3)])
+def test_fused_rms_norm_gemv(env, t, k, n, members):
+    print_case(test="fused", t=t, k=k, n=n, m=members)
+    enc = synth.kquant_numpy(t, k, n, seed=5 + n)
+    x = synth.activations_numpy(k, members, seed=6)
+    gam = synth.gamma_numpy(k, seed=7)
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(members * n)
+    env["k"][t].execute_rms_norm(w, to_dev(x.reshape(-1)), to_dev(gam), 1e-6, y, members)
+    got = to_host(y, env["ctx"]).reshape(members, n)
+    for m in range(members):
+        normed = O.rms_norm_raw(x[m], gam, 1e-6)
+        ref = O.quant_gemv(t, enc, k, n, normed, threads=8)
+        assert max_rel_err(got[m], ref) <= RTOL
+
+
+# ------------------------------------------------------ boundary behaviour
+
+def test_weight_bytes_round_trip(env):
+    # cuda_reference.rs:282-310: encoded bytes come back unchanged
+    import io
+    store = env["store"]
+    for t in TYPES:
+        enc = synth.kquant_numpy(t, 512, 9, seed=t)
+        store.materialize_quantized(f"rt{t}", [512, 9], t, enc)
+        assert store.copy_quantized_to_host(f"rt{t}") == enc.tobytes()
+        store.materialize_quantized_reader(f"rr{t}", [512, 9], t, enc.nbytes, io.BytesIO(enc.tobytes()))
+        assert store.copy_quantized_to_host(f"rr{t}") == enc.tobytes()
+    E = env["E"]
+    with pytest.raises(E.AmdWeightError) as e:
+        store.materialize_quantized_reader("short", [512, 9], 12, 144 * 18, io.BytesIO(b"\0" * 100))
+    assert e.value.kind == "SourceIncomplete" and e.value.actual == 100
+
+
+def test_validation_errors(env):
+    import torch
+    E = env["E"]
+    enc = synth.kquant_numpy(12, 512, 4, seed=1)
+    w = upload(env, 12, 512, 4, enc)
+    x = torch.zeros(512, device="cuda:0")
+    y = torch.zeros(4, device="cuda:0")
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][13].execute_warp(w, x, y)
+    assert e.value.kind == "UnsupportedValueType" and (e.value.expected, e.value.actual) == (13, 12)
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][12].execute_warp(w, torch.zeros(256, device="cuda:0"), y)
+    assert e.value.kind == "InputLength" and (e.value.expected, e.value.actual) == (512, 256)
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][12].execute_warp(w, x, torch.zeros(8, device="cuda:0"))
+    assert e.value.kind == "OutputLength" and (e.value.expected, e.value.actual) == (4, 8)
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][12].execute_warp_batch(w, x, y, 0)
+    assert e.value.kind == "InputLength" and (e.value.expected, e.value.actual) == (1, 0)
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][12].execute_warp_batch(w, x, y, 65)
+    assert e.value.kind == "InvalidWeight"
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][12].execute_warp(w, torch.zeros(520, device="cuda:0")[1:513], y)
+    assert e.value.kind == "InvalidArgument"  # misaligned device pointer
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][12].execute_warp(w, torch.zeros(512), y)
+    assert e.value.kind == "InvalidArgument"  # host memory
+    bad = upload(env, 12, 512, 3, synth.kquant_numpy(12, 512, 4, seed=1))  # 4 rows of bytes for 3
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][12].execute_warp(bad, x, torch.zeros(3, device="cuda:0"))
+    assert e.value.kind == "InvalidWeight" and e.value.expected == 3 * 2 * 144
+    ops = E.AmdQwenOps.from_context(env["ctx"])
+    with pytest.raises(E.AmdModelKernelError) as e:
+        ops.rms_norm(x, torch.zeros(511, device="cuda:0"), torch.zeros(512, device="cuda:0"), 1e-6)
+    assert e.value.kind == "WeightLength"
+    with pytest.raises(E.AmdModelKernelError) as e:
+        ops.rms_norm(x, x, torch.zeros(512, device="cuda:0"), 0.0)
+    assert e.value.kind == "InvalidEpsilon"
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        E.QwenGemvKernel.from_value_type(env["ctx"], 11)
+    assert e.value.kind == "UnsupportedValueType" and e.value.actual == 11
