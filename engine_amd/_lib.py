@@ -70,6 +70,8 @@ SIGNATURES = {
     "ribn_amd_gemv_execute_warp": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
     "ribn_amd_gemv_execute_warp_batch": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz, _sz]),
     "ribn_amd_gemv_execute_rms_norm": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz, _f32, _vp, _sz, _sz]),
+    "ribn_amd_gemv_execute_group": (_i32, [_vp, _pvp, _sz, _vp, _sz, _vp, _sz, _f32, _pvp,
+                                           ctypes.POINTER(_sz), _sz]),
     "ribn_amd_dequantize": (_i32, [_vp, _vp, _vp, _sz]),
     "ribn_amd_rms_norm": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _f32]),
     "ribn_amd_rms_norm_batch": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _f32]),

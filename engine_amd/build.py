@@ -24,11 +24,14 @@ ARCH = os.environ.get("RIBN_AMD_ARCH", "gfx950")
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Products and sums round separately unless a kernel asks for an FMA
+    # (__builtin_fmaf): keeps the exact-order kernels bit-identical to the host.
+    "-ffp-contract=off",
     "-I", os.path.join(ROOT, "include"), "-I", CSRC,
     "-Wall", "-Wno-unused-function",
 ]
 
-SOURCES = ["kquant_kernels.hip", "ribn_amd.cpp"]
+SOURCES = ["kquant_kernels.hip", "gemv_wave.hip", "ribn_amd.cpp"]
 
 
 def hipcc() -> str:

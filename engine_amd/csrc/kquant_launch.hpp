@@ -8,6 +8,27 @@ namespace ribn_amd {
 
 // Members one wave-GEMV launch accumulates; larger batches are split by the host.
 constexpr int kWaveMaxMembers = 4;
+// Weights one grouped wave-GEMV launch streams (they share one activation vector).
+constexpr int kMaxGroup = 4;
+// LDS the wave GEMV may use to stage [members][K] activations.
+constexpr long long kWaveMaxLdsBytes = 128 * 1024;
+
+struct WaveGemvArgs {
+    const uint8_t* w[kMaxGroup];
+    uint32_t wbytes[kMaxGroup];
+    float* y[kMaxGroup];      // y[i] is [members][N_i]
+    int rows_end[kMaxGroup];  // prefix sums of N_i
+    int count;
+    int total_rows;
+    const float* x;           // [members][K]
+    const float* gamma;       // RMSNorm weight [K], or null for a plain GEMV
+    float eps;
+    int K;
+    int members;
+};
+
+// Largest member count one wave launch can stage for this K (0 if none).
+int wave_max_members(int K);
 
 hipError_t launch_dequant(int value_type, const uint8_t* w, uint32_t wbytes, float* out, uint32_t nblocks,
                           hipStream_t stream);
@@ -15,9 +36,8 @@ hipError_t launch_dequant(int value_type, const uint8_t* w, uint32_t wbytes, flo
 hipError_t launch_gemv_exact(int value_type, const uint8_t* w, uint32_t wbytes, const float* x, float* y,
                              int K, int N, int members, hipStream_t stream);
 
-// gamma == nullptr: plain GEMV; otherwise RMSNorm(x; gamma, eps) is fused into the activation load.
-hipError_t launch_gemv_wave(int value_type, const uint8_t* w, uint32_t wbytes, const float* x, float* y, int K,
-                            int N, int members, const float* gamma, float eps, int cu_count, hipStream_t stream);
+// args.gamma == nullptr: plain GEMV; otherwise RMSNorm(x; gamma, eps) is fused into the activation load.
+hipError_t launch_gemv_wave(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* y, int length, int members, float eps,
                            hipStream_t stream);

@@ -24,6 +24,7 @@ struct ribn_amd_context {
 
 struct ribn_amd_quantized_weight {
     ribn_amd_context* ctx;
+    int device;  // kept so destruction never touches the (possibly destroyed) context
     uint32_t value_type;
     uint64_t input_size;
     uint64_t output_size;
@@ -180,20 +181,65 @@ ribn_amd_status validate_members(const ribn_amd_gemv* g, size_t members) {
     return RIBN_AMD_OK;
 }
 
-ribn_amd_status launch_batched(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const float* in,
-                               const float* gamma, float eps, float* out, uint64_t k, uint64_t n,
-                               size_t members) {
+// Runs a (grouped) wave GEMV over `count` weights sharing one activation
+// vector. Members are split into launch groups that fit the LDS staging of K.
+ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_weight* const* ws, size_t count,
+                                  const float* in, const float* gamma, float eps, float* const* outs, uint64_t k,
+                                  size_t members) {
     DeviceGuard guard(g->ctx->device);
-    // Wave kernels accumulate up to kWaveMaxMembers members per launch; larger
-    // batches run as consecutive launch groups over the same weights.
-    for (size_t m0 = 0; m0 < members; m0 += ribn_amd::kWaveMaxMembers) {
-        const size_t mc = std::min<size_t>(ribn_amd::kWaveMaxMembers, members - m0);
-        hipError_t e = ribn_amd::launch_gemv_wave((int)g->value_type, w->data, (uint32_t)w->encoded_bytes,
-                                                  in + m0 * k, out + m0 * n, (int)k, (int)n, (int)mc, gamma, eps,
-                                                  g->ctx->cu_count, g->ctx->stream);
+    const int per_launch = std::min(ribn_amd::wave_max_members((int)k), ribn_amd::kWaveMaxMembers);
+    if (per_launch <= 0) {
+        // K too large to stage in LDS: the exact-order kernel still serves it.
+        if (gamma != nullptr) {
+            return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)(ribn_amd::kWaveMaxLdsBytes / 4), k,
+                        "fused RMSNorm supports K up to %lld", ribn_amd::kWaveMaxLdsBytes / 4);
+        }
+        for (size_t i = 0; i < count; ++i) {
+            hipError_t e = ribn_amd::launch_gemv_exact((int)g->value_type, ws[i]->data,
+                                                       (uint32_t)ws[i]->encoded_bytes, in, outs[i], (int)k,
+                                                       (int)ws[i]->output_size, (int)members, g->ctx->stream);
+            if (e != hipSuccess) return driver(e, "launch exact GEMV");
+        }
+        return ok();
+    }
+    for (size_t m0 = 0; m0 < members; m0 += (size_t)per_launch) {
+        const size_t mc = std::min<size_t>((size_t)per_launch, members - m0);
+        ribn_amd::WaveGemvArgs a{};
+        int rows = 0;
+        for (size_t i = 0; i < count; ++i) {
+            const uint64_t n = ws[i]->output_size;
+            a.w[i] = ws[i]->data;
+            a.wbytes[i] = (uint32_t)ws[i]->encoded_bytes;
+            a.y[i] = outs[i] + m0 * n;
+            rows += (int)n;
+            a.rows_end[i] = rows;
+        }
+        a.count = (int)count;
+        a.total_rows = rows;
+        a.x = in + m0 * k;
+        a.gamma = gamma;
+        a.eps = eps;
+        a.K = (int)k;
+        a.members = (int)mc;
+        hipError_t e = ribn_amd::launch_gemv_wave((int)g->value_type, a, g->ctx->cu_count, g->ctx->stream);
         if (e != hipSuccess) return driver(e, "launch wave GEMV");
     }
     return ok();
+}
+
+ribn_amd_status launch_batched(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const float* in,
+                               const float* gamma, float eps, float* out, uint64_t k, uint64_t /*n*/,
+                               size_t members) {
+    const ribn_amd_quantized_weight* ws[1] = {w};
+    float* outs[1] = {out};
+    return launch_wave_group(g, ws, 1, in, gamma, eps, outs, k, members);
+}
+
+ribn_amd_status check_epsilon(float epsilon) {
+    if (!(epsilon > 0.f) || epsilon == std::numeric_limits<float>::infinity()) {
+        return fail(RIBN_AMD_INVALID_EPSILON, 0, 0, "RMSNorm epsilon must be finite and positive");
+    }
+    return RIBN_AMD_OK;
 }
 
 ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_context** out) {
@@ -390,7 +436,8 @@ static ribn_amd_status new_weight(ribn_amd_context* ctx, uint32_t value_type, ui
     if (encoded_bytes > (uint64_t)std::numeric_limits<size_t>::max()) {
         return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "encoded length does not fit the host");
     }
-    auto* w = new (std::nothrow) ribn_amd_quantized_weight{ctx, value_type, k, n, encoded_bytes, nullptr, true};
+    auto* w = new (std::nothrow)
+        ribn_amd_quantized_weight{ctx, ctx->device, value_type, k, n, encoded_bytes, nullptr, true};
     if (!w) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
     DeviceGuard guard(ctx->device);
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->data), encoded_bytes);
@@ -469,7 +516,7 @@ ribn_amd_status ribn_amd_weight_wrap_device(ribn_amd_context* ctx, uint32_t valu
     ribn_amd_status st = check_device_ptr(ctx, device_bytes, "weight bytes");
     if (st != RIBN_AMD_OK) return st;
     auto* w = new (std::nothrow) ribn_amd_quantized_weight{
-        ctx, value_type, input_size, output_size, encoded_bytes,
+        ctx, ctx->device, value_type, input_size, output_size, encoded_bytes,
         const_cast<uint8_t*>(static_cast<const uint8_t*>(device_bytes)), false};
     if (!w) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
     *out = w;
@@ -489,9 +536,8 @@ ribn_amd_status ribn_amd_weight_copy_to_host(ribn_amd_context* ctx, const ribn_a
 void ribn_amd_weight_destroy(ribn_amd_quantized_weight* weight) {
     if (!weight) return;
     if (weight->owns_data && weight->data) {
-        DeviceGuard guard(weight->ctx->device);
-        hipStreamSynchronize(weight->ctx->stream);
-        hipFree(weight->data);
+        DeviceGuard guard(weight->device);
+        hipFree(weight->data);  // synchronises with outstanding work on the device
     }
     delete weight;
 }
@@ -564,10 +610,45 @@ ribn_amd_status ribn_amd_gemv_execute_rms_norm(ribn_amd_gemv* g, const ribn_amd_
         return fail(RIBN_AMD_WEIGHT_LENGTH, k, gamma_len, "RMSNorm weight has %zu values, expected %llu", gamma_len,
                     (unsigned long long)k);
     }
-    if (!(epsilon > 0.f) || epsilon == std::numeric_limits<float>::infinity()) {
-        return fail(RIBN_AMD_INVALID_EPSILON, 0, 0, "RMSNorm epsilon must be finite and positive");
-    }
+    st = check_epsilon(epsilon);
+    if (st != RIBN_AMD_OK) return st;
     return launch_batched(g, w, input, gamma, epsilon, output, k, n, members);
+}
+
+ribn_amd_status ribn_amd_gemv_execute_group(ribn_amd_gemv* g, const ribn_amd_quantized_weight* const* weights,
+                                            size_t count, const float* input, size_t input_len,
+                                            const float* gamma, size_t gamma_len, float epsilon,
+                                            float* const* outputs, const size_t* output_lens, size_t members) {
+    ribn_amd_status st = validate_members(g, members);
+    if (st != RIBN_AMD_OK) return st;
+    if (!weights || !outputs || !output_lens) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null array argument");
+    if (count == 0 || count > (size_t)ribn_amd::kMaxGroup) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, ribn_amd::kMaxGroup, count, "a group holds 1..%d weights",
+                    ribn_amd::kMaxGroup);
+    }
+    uint64_t k0 = 0;
+    uint64_t total_rows = 0;
+    for (size_t i = 0; i < count; ++i) {
+        uint64_t k, n;
+        st = validate_launch(g, weights[i], input, input_len, outputs[i], output_lens[i], members, &k, &n);
+        if (st != RIBN_AMD_OK) return st;
+        if (i == 0) k0 = k;
+        total_rows += n;
+    }
+    if (total_rows > (uint64_t)std::numeric_limits<int32_t>::max()) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "grouped rows exceed i32");
+    }
+    if (gamma != nullptr) {
+        st = check_device_ptr(g->ctx, gamma, "gamma");
+        if (st != RIBN_AMD_OK) return st;
+        if (gamma_len != k0) {
+            return fail(RIBN_AMD_WEIGHT_LENGTH, k0, gamma_len, "RMSNorm weight has %zu values, expected %llu",
+                        gamma_len, (unsigned long long)k0);
+        }
+        st = check_epsilon(epsilon);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    return launch_wave_group(g, weights, count, input, gamma, epsilon, outputs, k0, members);
 }
 
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, float* output,
@@ -611,9 +692,8 @@ static ribn_amd_status rms_common(ribn_amd_context* ctx, const float* input, siz
         return fail(RIBN_AMD_OUTPUT_LENGTH, input_len, output_len, "RMSNorm output has %zu values, expected %zu",
                     output_len, input_len);
     }
-    if (!(epsilon > 0.f) || epsilon == std::numeric_limits<float>::infinity()) {
-        return fail(RIBN_AMD_INVALID_EPSILON, 0, 0, "RMSNorm epsilon must be finite and positive");
-    }
+    st = check_epsilon(epsilon);
+    if (st != RIBN_AMD_OK) return st;
     const size_t members = input_len / length;
     if (length > (size_t)std::numeric_limits<int>::max() || members > (size_t)std::numeric_limits<int>::max()) {
         return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "RMSNorm shape exceeds launch limits");

@@ -15,6 +15,7 @@ default is torch's current stream so torch-side copies order after them.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 
 from . import _lib
@@ -44,6 +45,22 @@ class AmdModelKernelError(AmdKernelError):
 
 class AmdWeightError(AmdKernelError):
     pass
+
+
+_SHUTTING_DOWN = [False]
+
+
+def _mark_shutdown():
+    # Handles still alive at interpreter exit are leaked on purpose: releasing
+    # them while the HIP runtime and torch tear down is not ordered.
+    _SHUTTING_DOWN[0] = True
+
+
+atexit.register(_mark_shutdown)
+
+
+def _live() -> bool:
+    return not _SHUTTING_DOWN[0]
 
 
 def _check(status: int, cls=AmdQuantizedKernelError):
@@ -78,7 +95,7 @@ class AmdContext:
         _check(self._lib.ribn_amd_context_synchronize(self.handle))
 
     def close(self):
-        if self.handle:
+        if self.handle and _live():
             self._lib.ribn_amd_context_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 
@@ -109,7 +126,7 @@ class AmdQuantizedWeight:
         return int(self.ctx._lib.ribn_amd_weight_device_ptr(self.handle) or 0)
 
     def close(self):
-        if self.handle:
+        if self.handle and _live():
             self.ctx._lib.ribn_amd_weight_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 
@@ -226,11 +243,22 @@ class _AmdQuantizedGemv:
                                                         _ptr(gamma), gamma.numel(), epsilon, _ptr(output),
                                                         output.numel(), members))
 
+    def execute_group(self, weights, input, outputs, members: int = 1, gamma=None, epsilon: float = 1e-6):
+        """One launch over weights sharing `input` (optionally RMSNorm-fused)."""
+        n = len(weights)
+        wh = (ctypes.c_void_p * n)(*[w.handle.value for w in weights])
+        oh = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outputs])
+        ol = (ctypes.c_size_t * n)(*[o.numel() for o in outputs])
+        g = _ptr(gamma) if gamma is not None else None
+        gl = gamma.numel() if gamma is not None else 0
+        _check(self._lib.ribn_amd_gemv_execute_group(self.handle, wh, n, _ptr(input), input.numel(), g, gl,
+                                                     epsilon, oh, ol, members))
+
     def dequantize(self, weight, output):
         _check(self._lib.ribn_amd_dequantize(self.handle, weight.handle, _ptr(output), output.numel()))
 
     def close(self):
-        if self.handle:
+        if self.handle and _live():
             self._lib.ribn_amd_gemv_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 

@@ -184,6 +184,16 @@ ribn_amd_status ribn_amd_gemv_execute_rms_norm(ribn_amd_gemv *gemv, const ribn_a
                                                const float *input, size_t input_len, const float *gamma,
                                                size_t gamma_len, float epsilon, float *output,
                                                size_t output_len, size_t members);
+/* Grouped form of execute_rms_norm / execute_warp_batch with no reference
+ * counterpart (the reference launches each projection separately,
+ * decode.rs:582-617): streams `count` (1..4) weights of this kernel's type and
+ * equal K that share one input in a single launch, e.g. q/k/v or gate/up of a
+ * decoder layer. outputs[i] holds members*N_i values (output_lens[i]).
+ * gamma == NULL skips the RMSNorm prologue (gamma_len and epsilon ignored). */
+ribn_amd_status ribn_amd_gemv_execute_group(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *const *weights,
+                                            size_t count, const float *input, size_t input_len,
+                                            const float *gamma, size_t gamma_len, float epsilon,
+                                            float *const *outputs, const size_t *output_lens, size_t members);
 /* Bit-exact device dequantisation to f32 [N][K] (twin of lib.rs:596-661;
  * the reference's device equivalent is the q4_k_embedding gather, q4_k.cu:1-67). */
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight, float *output,

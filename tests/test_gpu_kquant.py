@@ -295,3 +295,33 @@ def test_validation_errors(env):
     with pytest.raises(E.AmdQuantizedKernelError) as e:
         E.QwenGemvKernel.from_value_type(env["ctx"], 11)
     assert e.value.kind == "UnsupportedValueType" and e.value.actual == 11
+
+
+@pytest.mark.parametrize("t,k,ns,members,norm", [(12, 4096, (4096, 1024, 1024), 1, True),
+                                                 (12, 4096, (12288, 12288), 1, True),
+                                                 (12, 4096, (512, 96, 33), 3, True),
+                                                 (13, 12288, (256, 100), 2, False),
+                                                 (14, 2304, (77, 5, 64, 9), 1, False)])
+def test_grouped_launch_matches_separate(env, t, k, ns, members, norm):
+    # one launch over weights sharing the input equals the per-weight launches bit for bit
+    import torch
+    print_case(test="group", t=t, k=k, ns=ns, m=members, norm=norm)
+    encs = [synth.kquant_numpy(t, k, n, seed=n + i) for i, n in enumerate(ns)]
+    ws = [upload(env, t, k, n, e) for n, e in zip(ns, encs)]
+    x = synth.activations_numpy(k, members, seed=3)
+    gam = synth.gamma_numpy(k, seed=4)
+    xd, gd = to_dev(x.reshape(-1)), to_dev(gam)
+    outs = [empty_dev(members * n) for n in ns]
+    env["k"][t].execute_group(ws, xd, outs, members, gd if norm else None, 1e-6)
+    for w, n, o, e in zip(ws, ns, outs, encs):
+        single = empty_dev(members * n)
+        if norm:
+            env["k"][t].execute_rms_norm(w, xd, gd, 1e-6, single, members)
+        else:
+            env["k"][t].execute_warp_batch(w, xd, single, members)
+        got = to_host(o, env["ctx"])
+        assert np.array_equal(got.view(np.uint32), to_host(single, env["ctx"]).view(np.uint32))
+        for m in range(members):
+            src = O.rms_norm_raw(x[m], gam, 1e-6) if norm else x[m]
+            ref = O.quant_gemv(t, e, k, n, src, threads=8)
+            assert max_rel_err(got.reshape(members, n)[m], ref) <= RTOL
