@@ -96,8 +96,11 @@ class DecodeGemvStep:
         self.acts = acts
         self.outs = {name: torch.empty(n, device="cuda:0") for name, _, _, n, _ in LAYER}
         self.logits = torch.empty(VOCAB, device="cuda:0")
-        self.bytes_per_step = sum(launch_bytes(t, k, n) for _, t, k, n, _ in LAYER) * len(weights) \
-            + launch_bytes(14, HIDDEN, VOCAB)
+        # Algorithmic bytes per launch: encoded weights + f32 input once + f32 outputs.
+        qkv = sum(launch_bytes(12, HIDDEN, n) - 4 * HIDDEN for n in (Q_OUT, KV_OUT, KV_OUT)) + 4 * HIDDEN
+        gate_up = 2 * (launch_bytes(12, HIDDEN, FFN) - 4 * HIDDEN) + 4 * HIDDEN
+        per_layer = qkv + launch_bytes(12, Q_OUT, HIDDEN) + gate_up + launch_bytes(13, FFN, HIDDEN)
+        self.bytes_per_step = per_layer * len(weights) + launch_bytes(14, HIDDEN, VOCAB)
 
     def layer(self, entry):
         # q/k/v share the attention-normed input and gate/up the FFN-normed
@@ -290,7 +293,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        # products: 4..6-bit quants x 16-bit fixed-point activations (v_dot4, int32); scales and sums f32
+        "dtype": "i8dot4-f32",
         "data": "synthetic",
         "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
         "decode_tok_s": round(1000.0 / ms_step, 2),

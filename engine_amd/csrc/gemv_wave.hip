@@ -6,46 +6,102 @@
 // Layout and mapping
 //  - Weights are the encoded GGML array-of-blocks; row n of a [K, N] tensor is
 //    K/256 consecutive super-blocks (crates/nvidia/src/quantized.rs:136-142).
-//  - A workgroup is 8 waves. It stages the activations [members][K] once into
-//    LDS (scaled by inv_rms * gamma when RMSNorm is fused), then each wave
-//    streams a contiguous range of output rows.
-//  - A wave covers 16 consecutive super-blocks of a row per "slice"; lane l owns
-//    block (l >> 2) of the slice and quarter p = (l & 3), i.e. 64 elements:
+//  - A wave covers 16 consecutive super-blocks of a row per "slice" (K = 4096
+//    is one slice); lane l owns block (l >> 2) of the slice and quarter
+//    p = (l & 3), i.e. 64 elements:
 //      Q4_K / Q5_K: groups 2p and 2p+1 (payload bytes 32p..32p+31, low/high nibbles);
 //      Q6_K:        groups 4c..4c+3 at positions 16s..16s+15 (c = p >> 1, s = p & 1).
-//  - Per row a lane issues 128-bit buffer loads for its payload and header,
-//    forms sum(q*x) per scale group in f32 and applies (d*sc) and (dmin*m) once
-//    per group: y = sum_g (d*sc_g)*sum(q*x) - (dmin*m_g)*sum(x).
-//  - Weight loads for the next rows are issued before the current rows are
-//    reduced (one-deep software pipeline), and the first rows' loads are issued
-//    before the activation staging, so HBM latency overlaps the prologue.
+//  - Activations are quantized once per workgroup into 16-bit fixed point per
+//    k-quant scale group (v = round(x * 2^(15-e)), 2^e > max|x| of the group),
+//    stored as a signed high byte and an unsigned low byte, so the products
+//    with the 4..6-bit quants are v_dot4 integer dot products (exact, int32
+//    accumulation). Per group the row gains
+//        unscale_g * ((d*sc_g) * S_g - (dmin*m_g) * X_g)     (Q4_K / Q5_K)
+//        unscale_g * (d*sc_g) * (S_g - 32 X_g)               (Q6_K)
+//    with S_g = sum(q*v) and X_g = sum(v). The activation rounding is at most
+//    2^-16 of the group's maximum per element.
+//  - The quantized activations sit in LDS in lane order (one padded record
+//    per lane and slice), so each wave reads its lane's data with conflict-free
+//    128-bit LDS loads. A fused RMSNorm multiplies x by gamma before the
+//    quantization and applies 1/rms to each output, which keeps the only
+//    cross-wave dependency (the sum of squares) to one workgroup barrier.
+//  - Weight loads for a wave's first units are issued right after the
+//    activation loads, before the staging, so HBM latency overlaps the
+//    prologue. Each wave then keeps a ring of units (row x slice) in
+//    registers: a unit is reduced, then its slot is refilled with the unit a
+//    full ring ahead.
 // Arithmetic per member is independent of the member count, so every row of a
 // batched launch is bit-identical to the single-member launch.
 #include "kquant_device.hpp"
 #include "kquant_launch.hpp"
 
+#include <algorithm>
+#include <atomic>
+
 namespace ribn_amd {
 
-constexpr int kWaves = 8;          // waves per workgroup
+constexpr int kWaves = 8;  // waves per workgroup
 constexpr int kThreads = kWaves * 64;
-constexpr int kRows = 2;           // rows per pipeline stage
+constexpr uint32_t kOutOfRange = 0xffffff00u;  // buffer offset past any tensor: loads return 0, stores drop
+constexpr int kSliceElems = 16 * kQK;          // elements a wave covers per unit
 
-struct LaneX {
-    float v[64];
+template <int T> struct ActTraits {
+    static constexpr int group = (T == kQ6K) ? 16 : 32;  // elements per scale group
+    static constexpr int groups = 64 / group;            // scale groups per lane
+    // Dwords per lane record: 16 high-byte words, 16 low-byte words, then
+    // `groups` unscale factors and `groups` sums. The stride is odd in
+    // 16-byte units, so 16 lanes' 128-bit reads fall in distinct banks.
+    static constexpr int stride = (T == kQ6K) ? 44 : 36;
 };
 
-__device__ __forceinline__ float4 ld_f4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// One lane's quantized activations for one slice.
+template <int T> struct LaneAct {
+    uint32_t h[16];  // signed high bytes, four elements per word
+    uint32_t l[16];  // unsigned low bytes
+    float unscale[ActTraits<T>::groups];
+    float xsum[ActTraits<T>::groups];  // X_g as f32 (exact: |X_g| < 2^21)
+    int xsum32[ActTraits<T>::groups];  // -32 X_g (Q6_K)
+};
 
-__device__ __forceinline__ float ubyte_f(uint32_t w, int t) { return (float)((w >> (8 * t)) & 0xffu); }
-
-// Offset within a super-block of lane-local activation j (0..63).
+// Position of element e (a multiple of 4, within one slice) in the lane
+// records: lane, word, scale group.
 template <int T>
-__device__ __forceinline__ int lane_x_offset(int p, int j) {
+__device__ __forceinline__ void act_slot(int e, int& lane, int& word, int& group) {
     if constexpr (T == kQ6K) {
-        return 128 * (p >> 1) + 32 * (j >> 4) + 16 * (p & 1) + (j & 15);
+        const int bs = e >> 8, c = (e >> 7) & 1, v = (e >> 5) & 3, s = (e >> 4) & 1, j = (e >> 2) & 3;
+        lane = 4 * bs + 2 * c + s;
+        word = 4 * v + j;
+        group = v;
     } else {
-        return 64 * p + j;
+        lane = e >> 6;
+        word = (e >> 2) & 15;
+        group = word >> 3;
     }
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_sum_step_i(int v) {
+    return v + __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+// Max / sum over the lanes holding one scale group (4 or 8 consecutive lanes).
+template <int T>
+__device__ __forceinline__ float group_max(float v) {
+    v = dpp_max_step<0xb1>(v);  // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4e>(v);  // quad_perm [2,3,0,1]
+    if constexpr (ActTraits<T>::group == 32) v = dpp_max_step<0x141>(v);  // row_half_mirror
+    return v;
+}
+template <int T>
+__device__ __forceinline__ int group_sum(int v) {
+    v = dpp_sum_step_i<0xb1>(v);
+    v = dpp_sum_step_i<0x4e>(v);
+    if constexpr (ActTraits<T>::group == 32) v = dpp_sum_step_i<0x141>(v);
+    return v;
+}
+
+__device__ __forceinline__ float4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+    return __builtin_bit_cast(float4, load_b128(r, offset));
 }
 
 // ----------------------------------------------------------- raw row loads
@@ -54,15 +110,10 @@ template <int T> struct RowData;
 template <> struct RowData<kQ4K> { uint4 h, qa, qb; };
 template <> struct RowData<kQ5K> { uint4 h, ha, hb, qa, qb; };
 template <> struct RowData<kQ6K> {
-    uint4 la, lb, qh, sc;       // dword-aligned-down 16-byte windows
+    uint4 la, lb, qh, sc;             // dword-aligned-down 16-byte windows
     uint32_t la_t, lb_t, qh_t, sc_t;  // the dword after each window
     uint32_t d16, shift;
 };
-
-template <int T>
-__device__ __forceinline__ void zero_row(RowData<T>& d) {
-    d = RowData<T>{};
-}
 
 template <int T>
 __device__ __forceinline__ void load_row(RowData<T>& d, __amdgpu_buffer_rsrc_t r, uint32_t off, int p) {
@@ -109,11 +160,20 @@ __device__ __forceinline__ uint4 funnel(uint4 a, uint32_t t, uint32_t sh) {
     return o;
 }
 
-// --------------------------------------------------- per-row dot products
+// Four-way byte dot products: quants (0..63) against the signed high bytes
+// and the unsigned low bytes of the fixed-point activations.
+__device__ __forceinline__ int sdot4(uint32_t q, uint32_t x, int acc) {
+    return __builtin_amdgcn_sdot4((int)q, (int)x, acc, false);
+}
+__device__ __forceinline__ int udot4(uint32_t q, uint32_t x, int acc) {
+    return (int)__builtin_amdgcn_udot4(q, x, (uint32_t)acc, false);
+}
 
+// --------------------------------------------------- per-row dot products
+//
+// part[m] = this lane's share of row . x_m for one unit (already unscaled).
 template <int T, int MT>
-__device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneX (&xa)[MT],
-                                        const float (&gsum)[MT][4], float (&acc)[MT]) {
+__device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneAct<T> (&xa)[MT], float (&part)[MT]) {
     if constexpr (T == kQ4K || T == kQ5K) {
         const uint4 h = d.h;
         const float dd = half_bits_to_float(h.x & 0xffffu);
@@ -131,36 +191,34 @@ __device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneX 
         const float b0 = dmin * (float)((mnw >> sh) & 0xffu);
         const float b1 = dmin * (float)((mnw >> (sh + 8)) & 0xffu);
         const uint32_t qw[8] = {d.qa.x, d.qa.y, d.qa.z, d.qa.w, d.qb.x, d.qb.y, d.qb.z, d.qb.w};
-        float q0[32], q1[32];
+        int hA[MT], lA[MT], hB[MT], lB[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) hA[m] = lA[m] = hB[m] = lB[m] = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            uint32_t lo = qw[j] & 0x0f0f0f0fu;
-            uint32_t hi = (qw[j] >> 4) & 0x0f0f0f0fu;
+            // group A = 2p (low nibbles), group B = 2p+1 (high nibbles), 5th bit for Q5_K
+            uint32_t qa = qw[j] & 0x0f0f0f0fu;
+            uint32_t qb = (qw[j] >> 4) & 0x0f0f0f0fu;
             if constexpr (T == kQ5K) {
                 const uint32_t hw[8] = {d.ha.x, d.ha.y, d.ha.z, d.ha.w, d.hb.x, d.hb.y, d.hb.z, d.hb.w};
-                lo |= ((hw[j] >> (2 * p)) & 0x01010101u) << 4;
-                hi |= ((hw[j] >> (2 * p + 1)) & 0x01010101u) << 4;
+                qa |= ((hw[j] >> (2 * p)) & 0x01010101u) << 4;
+                qb |= ((hw[j] >> (2 * p + 1)) & 0x01010101u) << 4;
             }
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                q0[4 * j + t] = ubyte_f(lo, t);
-                q1[4 * j + t] = ubyte_f(hi, t);
+            for (int m = 0; m < MT; ++m) {
+                hA[m] = sdot4(qa, xa[m].h[j], hA[m]);
+                lA[m] = udot4(qa, xa[m].l[j], lA[m]);
+                hB[m] = sdot4(qb, xa[m].h[8 + j], hB[m]);
+                lB[m] = udot4(qb, xa[m].l[8 + j], lB[m]);
             }
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                s0 = __builtin_fmaf(q0[i], xa[m].v[i], s0);
-                s1 = __builtin_fmaf(q1[i], xa[m].v[32 + i], s1);
-            }
-            float a = acc[m];
-            a = __builtin_fmaf(a0, s0, a);
-            a = __builtin_fmaf(-b0, gsum[m][0], a);
-            a = __builtin_fmaf(a1, s1, a);
-            a = __builtin_fmaf(-b1, gsum[m][1], a);
-            acc[m] = a;
+            const float sA = (float)(hA[m] * 256 + lA[m]);
+            const float sB = (float)(hB[m] * 256 + lB[m]);
+            const float tA = __builtin_fmaf(a0, sA, -(b0 * xa[m].xsum[0]));
+            const float tB = __builtin_fmaf(a1, sB, -(b1 * xa[m].xsum[1]));
+            part[m] = __builtin_fmaf(tA, xa[m].unscale[0], tB * xa[m].unscale[1]);
         }
     } else {
         const int c = p >> 1, s = p & 1;
@@ -168,7 +226,7 @@ __device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneX 
         const uint4 la = funnel(d.la, d.la_t, sh);
         const uint4 lb = funnel(d.lb, d.lb_t, sh);
         const uint4 qh = funnel(d.qh, d.qh_t, sh);
-        const uint4 sc = funnel(d.sc, d.sc_t, sh);  // int8 scales 0..15
+        const uint4 sc = funnel(d.sc, d.sc_t, sh);  // int8 scales
         const float dd = half_bits_to_float(d.d16);
         const uint32_t w0 = c ? sc.z : sc.x;  // scales 8c+0..8c+3
         const uint32_t w1 = c ? sc.w : sc.y;  // scales 8c+4..8c+7
@@ -180,227 +238,380 @@ __device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneX 
         const uint32_t law[4] = {la.x, la.y, la.z, la.w};
         const uint32_t lbw[4] = {lb.x, lb.y, lb.z, lb.w};
         const uint32_t qhw[4] = {qh.x, qh.y, qh.z, qh.w};
-        float q[4][16];
+        int hs[MT][4], ls[MT][4];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) hs[m][v] = ls[m][v] = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t v0 = (law[j] & 0x0f0f0f0fu) | ((qhw[j] << 4) & 0x30303030u);
-            const uint32_t v1 = (lbw[j] & 0x0f0f0f0fu) | ((qhw[j] << 2) & 0x30303030u);
-            const uint32_t v2 = ((law[j] >> 4) & 0x0f0f0f0fu) | (qhw[j] & 0x30303030u);
-            const uint32_t v3 = ((lbw[j] >> 4) & 0x0f0f0f0fu) | ((qhw[j] >> 2) & 0x30303030u);
+            // quants 0..63 (the -32 offset is applied through X_g)
+            uint32_t q[4];
+            q[0] = (law[j] & 0x0f0f0f0fu) | ((qhw[j] << 4) & 0x30303030u);
+            q[1] = (lbw[j] & 0x0f0f0f0fu) | ((qhw[j] << 2) & 0x30303030u);
+            q[2] = ((law[j] >> 4) & 0x0f0f0f0fu) | (qhw[j] & 0x30303030u);
+            q[3] = ((lbw[j] >> 4) & 0x0f0f0f0fu) | ((qhw[j] >> 2) & 0x30303030u);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                q[0][4 * j + t] = ubyte_f(v0, t);
-                q[1][4 * j + t] = ubyte_f(v1, t);
-                q[2][4 * j + t] = ubyte_f(v2, t);
-                q[3][4 * j + t] = ubyte_f(v3, t);
+            for (int v = 0; v < 4; ++v) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    hs[m][v] = sdot4(q[v], xa[m].h[4 * v + j], hs[m][v]);
+                    ls[m][v] = udot4(q[v], xa[m].l[4 * v + j], ls[m][v]);
+                }
             }
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            float accm = acc[m];
+            float t = 0.f;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                float sv = 0.f;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) sv = __builtin_fmaf(q[v][i], xa[m].v[16 * v + i], sv);
-                // sum((q - 32) * x) = sum(q*x) - 32 * sum(x)
-                accm = __builtin_fmaf(a[v], sv, accm);
-                accm = __builtin_fmaf(-32.f * a[v], gsum[m][v], accm);
+                // sum((q - 32) v) = S - 32 X, exact in int32
+                const float sv = (float)(hs[m][v] * 256 + ls[m][v] + xa[m].xsum32[v]);
+                t = __builtin_fmaf(a[v], sv * xa[m].unscale[v], t);
             }
-            acc[m] = accm;
+            part[m] = t;
         }
     }
 }
 
 // ------------------------------------------------------------------ kernel
 
-template <int T, int MT, bool NORM, bool ONE_SLICE>
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF>
 __global__ __launch_bounds__(kThreads) void gemv_wave_kernel(WaveGemvArgs args) {
     constexpr int BB = BlockTraits<T>::bytes;
-    extern __shared__ float xs[];  // [MT][K] staged activations
+    constexpr int G = ActTraits<T>::groups;
+    constexpr int STRIDE = ActTraits<T>::stride;
+    constexpr int CH = ONE_SLICE ? kSliceElems / (4 * kThreads) : kWaveMaxK / (4 * kThreads);
+    extern __shared__ uint32_t xs[];  // [MT][slices][64 lanes][STRIDE]
     __shared__ float partial[MT][kWaves];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = args.K;
     const int nb = K >> 8;
-    const int slices = (nb + 15) >> 4;
+    const int slices = ONE_SLICE ? 1 : (nb + 15) >> 4;
+    const int members = args.members;
     const int p = lane & 3;
     const int bs = lane >> 2;
     const int nwaves = gridDim.x * kWaves;
     const int wg = blockIdx.x * kWaves + wave;
     const int r_begin = (int)((long long)args.total_rows * wg / nwaves);
     const int r_end = (int)((long long)args.total_rows * (wg + 1) / nwaves);
-    const int row_blocks = (r_end - r_begin + kRows - 1) / kRows;
-    const int items = row_blocks * slices;
     const uint32_t row_bytes = (uint32_t)nb * BB;
 
-    // Row -> (matrix, local row); the row index is wave-uniform.
+    // Row -> (matrix, local row); the row index is wave-uniform. Fields of
+    // the argument arrays are picked by selects, not by a dynamic index
+    // (which would reload them from the argument segment every unit).
     auto locate = [&](int row, int& mat, int& local) {
         mat = 0;
+        int start = 0;
 #pragma unroll
         for (int i = 0; i < kMaxGroup - 1; ++i) {
-            if (i + 1 < args.count && row >= args.rows_end[i]) mat = i + 1;
-        }
-        local = row - (mat ? args.rows_end[mat - 1] : 0);
-    };
-
-    auto load_item = [&](RowData<T> (&dst)[kRows], int it) {
-        const int rb = it / slices;
-        const int s = it - rb * slices;
-        const int b = s * 16 + bs;
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-            const int row = r_begin + rb * kRows + r;
-            zero_row<T>(dst[r]);
-            if (row < r_end) {
-                int mat, local;
-                locate(row, mat, local);
-                const __amdgpu_buffer_rsrc_t rs = make_rsrc(args.w[mat], args.wbytes[mat]);
-                if (b < nb) load_row<T>(dst[r], rs, (uint32_t)local * row_bytes + (uint32_t)b * BB, p);
+            if (i + 1 < args.count && row >= args.rows_end[i]) {
+                mat = i + 1;
+                start = args.rows_end[i];
             }
         }
+        local = row - start;
+    };
+    auto pick_w = [&](int mat) {
+        const uint8_t* w = args.w[0];
+        uint32_t bytes = args.wbytes[0];
+#pragma unroll
+        for (int i = 1; i < kMaxGroup; ++i) {
+            if (mat == i) {
+                w = args.w[i];
+                bytes = args.wbytes[i];
+            }
+        }
+        return make_rsrc(w, bytes);
+    };
+    auto pick_y = [&](int mat, int& rows_mat) {
+        float* y = args.y[0];
+        int begin = 0, end = args.rows_end[0];
+#pragma unroll
+        for (int i = 1; i < kMaxGroup; ++i) {
+            if (mat == i) {
+                y = args.y[i];
+                begin = args.rows_end[i - 1];
+                end = args.rows_end[i];
+            }
+        }
+        rows_mat = end - begin;
+        return make_rsrc(y, (uint32_t)members * (uint32_t)rows_mat * 4u);
     };
 
-    RowData<T> cur[kRows];
-    if (items > 0) load_item(cur, 0);
-
-    // ---- stage activations [members][K] into LDS (normalised when fused)
-    const int members = args.members;
+    // ---- activation loads first: vector memory returns in order, so the
+    // staging below waits for these and not for the weight loads after them.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(args.x, (uint32_t)members * (uint32_t)K * 4u);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(args.gamma, NORM ? (uint32_t)K * 4u : 0u);
+    float4 xv[MT][CH];
+    float4 gv[CH];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        float ssq = 0.f;
-        for (int k = threadIdx.x * 4; k < K; k += kThreads * 4) {
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m < members) v = ld_f4(args.x + (size_t)m * K + k);
-            *reinterpret_cast<float4*>(&xs[m * K + k]) = v;
-            if constexpr (NORM) ssq += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    for (int c = 0; c < CH; ++c) {
+        const int e = 4 * ((int)threadIdx.x + kThreads * c);
+        const bool in = e < K;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            xv[m][c] = load_f4(xr, (in && m < members) ? (uint32_t)(m * K + e) * 4u : kOutOfRange);
         }
-        if constexpr (NORM) {
-            ssq = wave_sum(ssq);
-            if (lane == 0) partial[m][wave] = ssq;
+        if constexpr (NORM) gv[c] = load_f4(gr, in ? (uint32_t)e * 4u : kOutOfRange);
+    }
+    asm volatile("" ::: "memory");
+
+    // ---- weight ring, primed now. Loads are issued unconditionally (units
+    // past the wave's range and blocks past K read from an out-of-range
+    // offset, which returns zeros), so each stays where it is issued and the
+    // wave waits for exactly the unit it reduces next.
+    RowData<T> ring[NBUF];
+    int lrow = r_begin, lslice = 0;  // next unit to load
+    auto load_next = [&](RowData<T>& dst) {
+        const bool live_row = lrow < r_end;
+        int mat, local;
+        locate(live_row ? lrow : r_begin, mat, local);
+        const __amdgpu_buffer_rsrc_t rs = pick_w(mat);
+        const int b = lslice * 16 + bs;
+        const bool live = live_row && b < nb;
+        load_row<T>(dst, rs, live ? (uint32_t)local * row_bytes + (uint32_t)b * BB : kOutOfRange, p);
+        if (ONE_SLICE || ++lslice == slices) {
+            lslice = 0;
+            ++lrow;
+        }
+    };
+#pragma unroll
+    for (int r = 0; r < NBUF; ++r) load_next(ring[r]);
+
+    // ---- staging: x (times gamma) into per-group fixed point, in lane order.
+    float ssq[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) ssq[m] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int e = 4 * ((int)threadIdx.x + kThreads * c);
+        const int slice = e / kSliceElems;
+        int al, aw, ag;
+        act_slot<T>(e - slice * kSliceElems, al, aw, ag);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float4 v = xv[m][c];
+            if constexpr (NORM) {
+                ssq[m] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                v.x *= gv[c].x;
+                v.y *= gv[c].y;
+                v.z *= gv[c].z;
+                v.w *= gv[c].w;
+            }
+            const float gmax = group_max<T>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            // gmax < 2^ex; groups below 2^-100 quantize to zero.
+            int ex = gmax > 0.f ? __builtin_amdgcn_frexp_expf(gmax) : 0;
+            ex = ex < -100 ? -100 : ex;
+            const int sh = 15 - ex;
+            int q[4];
+            q[0] = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v.x, sh));
+            q[1] = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v.y, sh));
+            q[2] = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v.z, sh));
+            q[3] = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v.w, sh));
+            uint32_t hw = 0, lw = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                q[t] = q[t] > 32767 ? 32767 : q[t];  // rounding can reach 2^15
+                hw |= ((uint32_t)(q[t] >> 8) & 0xffu) << (8 * t);
+                lw |= ((uint32_t)q[t] & 0xffu) << (8 * t);
+            }
+            const int xsum = group_sum<T>(q[0] + q[1] + q[2] + q[3]);
+            if (slice < slices) {
+                uint32_t* dst = xs + ((m * slices + slice) * 64 + al) * STRIDE;
+                dst[aw] = hw;
+                dst[16 + aw] = lw;
+                if ((lane & (ActTraits<T>::group / 4 - 1)) == 0) {
+                    dst[32 + ag] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_ldexpf(1.0f, ex - 15));
+                    dst[32 + G + ag] = (uint32_t)xsum;
+                }
+            }
         }
     }
     if constexpr (NORM) {
-        __syncthreads();
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            float total = 0.f;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) total += partial[m][w];
-            // RMSNorm (qwen_reference.rs:550-556): x * (1/sqrt(sum(x^2)/K + eps)) * gamma
-            const float inv = 1.0f / sqrtf(total / (float)K + args.eps);
-            for (int k = threadIdx.x * 4; k < K; k += kThreads * 4) {
-                float4 v = *reinterpret_cast<float4*>(&xs[m * K + k]);
-                const float4 g = ld_f4(args.gamma + k);
-                v.x = v.x * inv * g.x;
-                v.y = v.y * inv * g.y;
-                v.z = v.z * inv * g.z;
-                v.w = v.w * inv * g.w;
-                *reinterpret_cast<float4*>(&xs[m * K + k]) = v;
-            }
+            const float wsum = wave_sum_uniform(ssq[m]);
+            if (lane == 0) partial[m][wave] = wsum;
         }
     }
     __syncthreads();
 
-    LaneX xa[MT];
-    float gsum[MT][4];
-    auto load_x = [&](int s) {
-        const int b = s * 16 + bs;
-        const bool valid = b < nb;
+    float inv[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        inv[m] = 1.f;
+        if constexpr (NORM) {
+            float total = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) total += partial[m][w];
+            // RMSNorm (qwen_reference.rs:550-556): x * (1/sqrt(sum(x^2)/K + eps)) * gamma
+            inv[m] = 1.0f / sqrtf(total / (float)K + args.eps);
+        }
+    }
+
+    LaneAct<T> xa[MT];
+    auto read_act = [&](int slice) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const float* src = xs + m * K + b * 256;
+            const uint32_t* src = xs + ((m * slices + slice) * 64 + lane) * STRIDE;
 #pragma unroll
-            for (int j = 0; j < 64; j += 4) {
-                const float4 v = valid ? *reinterpret_cast<const float4*>(src + lane_x_offset<T>(p, j))
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-                xa[m].v[j] = v.x;
-                xa[m].v[j + 1] = v.y;
-                xa[m].v[j + 2] = v.z;
-                xa[m].v[j + 3] = v.w;
+            for (int i = 0; i < 4; ++i) {
+                const uint4 a = *reinterpret_cast<const uint4*>(src + 4 * i);
+                const uint4 b = *reinterpret_cast<const uint4*>(src + 16 + 4 * i);
+                xa[m].h[4 * i + 0] = a.x;
+                xa[m].h[4 * i + 1] = a.y;
+                xa[m].h[4 * i + 2] = a.z;
+                xa[m].h[4 * i + 3] = a.w;
+                xa[m].l[4 * i + 0] = b.x;
+                xa[m].l[4 * i + 1] = b.y;
+                xa[m].l[4 * i + 2] = b.z;
+                xa[m].l[4 * i + 3] = b.w;
             }
-            constexpr int NG = (T == kQ6K) ? 4 : 2;
-            constexpr int GS = 64 / NG;
+            uint32_t prm[2 * G];
 #pragma unroll
-            for (int g = 0; g < NG; ++g) {
-                float sum = 0.f;
+            for (int i = 0; i < 2 * G; i += 4) {
+                const uint4 a = *reinterpret_cast<const uint4*>(src + 32 + i);
+                prm[i] = a.x;
+                prm[i + 1] = a.y;
+                prm[i + 2] = a.z;
+                prm[i + 3] = a.w;
+            }
 #pragma unroll
-                for (int j = 0; j < GS; ++j) sum += xa[m].v[g * GS + j];
-                gsum[m][g] = sum;
+            for (int g = 0; g < G; ++g) {
+                xa[m].unscale[g] = __builtin_bit_cast(float, prm[g]);
+                xa[m].xsum[g] = (float)(int)prm[G + g];
+                xa[m].xsum32[g] = -32 * (int)prm[G + g];
             }
         }
     };
-    if constexpr (ONE_SLICE) load_x(0);
+    if constexpr (ONE_SLICE) read_act(0);
 
-    float acc[kRows][MT];
-    for (int it = 0; it < items; ++it) {
-        RowData<T> nxt[kRows];
-        if (it + 1 < items) load_item(nxt, it + 1);
-        const int rb = it / slices;
-        const int s = it - rb * slices;
-        if constexpr (!ONE_SLICE) load_x(s);
-        if (s == 0) {
+    // ---- ring: reduce a unit, store its row when the unit completes it
+    // (other stores go to an out-of-range offset and are dropped), refill the
+    // slot with the unit NBUF ahead.
+    int crow = r_begin, cslice = 0;  // unit being reduced
+    float acc[MT];
 #pragma unroll
-            for (int r = 0; r < kRows; ++r)
+    for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+    auto consume = [&](const RowData<T>& d) {
+        if constexpr (!ONE_SLICE) read_act(cslice);
+        float part[MT];
+        row_dot<T, MT>(d, p, xa, part);
+        const bool last = ONE_SLICE || cslice == slices - 1;
+        int mat, local;
+        locate(crow, mat, local);
+        int rows_mat;
+        const __amdgpu_buffer_rsrc_t yr = pick_y(mat, rows_mat);
 #pragma unroll
-                for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
+        for (int m = 0; m < MT; ++m) {
+            acc[m] = (ONE_SLICE || cslice == 0) ? part[m] : acc[m] + part[m];
+            const float total = wave_sum_uniform(acc[m]) * inv[m];
+            const uint32_t off =
+                (last && lane == 0 && m < members) ? (uint32_t)(m * rows_mat + local) * 4u : kOutOfRange;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, total), yr, (int)off, 0, 0);
         }
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) row_dot<T, MT>(cur[r], p, xa, gsum, acc[r]);
-        if (s == slices - 1) {
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const int row = r_begin + rb * kRows + r;
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const float total = wave_sum(acc[r][m]);
-                    if (row < r_end && m < members && lane == 0) {
-                        int mat, local;
-                        locate(row, mat, local);
-                        const int rows_mat = args.rows_end[mat] - (mat ? args.rows_end[mat - 1] : 0);
-                        args.y[mat][(size_t)m * rows_mat + local] = total;
-                    }
-                }
-            }
+        if (ONE_SLICE || ++cslice == slices) {
+            cslice = 0;
+            ++crow;
         }
+    };
+
+    const int units = (r_end - r_begin) * slices;
+    const int passes = (units + NBUF - 1) / NBUF;
+    for (int pass = 0; pass + 1 < passes; ++pass) {
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) cur[r] = nxt[r];
+        for (int r = 0; r < NBUF; ++r) {
+            consume(ring[r]);
+            load_next(ring[r]);
+        }
+    }
+    if (passes > 0) {
+        const int left = units - (passes - 1) * NBUF;
+#pragma unroll
+        for (int r = 0; r < NBUF; ++r) {
+            if (r < left) consume(ring[r]);
+        }
     }
 }
 
 // ---------------------------------------------------------------- launcher
 
+template <int T> constexpr int max_ring() { return T == kQ4K ? 8 : 4; }
+
+// LDS of the activation records: [members][slices][64][stride] dwords.
+template <int T>
+static size_t act_lds_bytes(int members, int K) {
+    const int slices = ((K >> 8) + 15) >> 4;
+    return (size_t)members * slices * 64 * ActTraits<T>::stride * sizeof(uint32_t);
+}
+
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF>
+struct WaveInstance {
+    static std::atomic<int> per_cu;  // resident workgroups per CU at the largest LDS size (0: not queried)
+    static hipError_t launch(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
+        auto kern = gemv_wave_kernel<T, MT, NORM, ONE_SLICE, NBUF>;
+        const size_t lds = act_lds_bytes<T>(MT, a.K);
+        int occ = per_cu.load(std::memory_order_relaxed);
+        if (occ == 0) {
+            const int max_lds = (int)act_lds_bytes<T>(MT, ONE_SLICE ? kSliceElems : kWaveMaxK);
+            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)kern, kThreads, max_lds) !=
+                    hipSuccess ||
+                occ < 1) {
+                occ = 1;
+            }
+            per_cu.store(occ, std::memory_order_relaxed);
+        }
+        // One resident round of workgroups; each wave streams a contiguous
+        // row range of at least a couple of units.
+        const int slices = ONE_SLICE ? 1 : ((a.K >> 8) + 15) >> 4;
+        const long long units = (long long)a.total_rows * slices;
+        const long long want = (units + 2 * kWaves - 1) / (2 * kWaves);
+        int grid = (int)std::min<long long>(want, (long long)cu_count * occ);
+        if (grid < 1) grid = 1;
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, a);
+        return hipGetLastError();
+    }
+};
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF>
+std::atomic<int> WaveInstance<T, MT, NORM, ONE_SLICE, NBUF>::per_cu{0};
+
+template <int T, int MT, bool NORM, bool ONE_SLICE>
+static hipError_t launch_ring(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
+    // Ring depth: deep enough to keep several units in flight, no deeper than
+    // the units a wave gets (extra slots only issue out-of-range loads).
+    const int slices = ONE_SLICE ? 1 : ((a.K >> 8) + 15) >> 4;
+    const long long units = (long long)a.total_rows * slices;
+    const long long waves = (long long)cu_count * kWaves;
+    const long long per_wave = (units + waves - 1) / waves;
+    if constexpr (MT == 1 && max_ring<T>() >= 8) {
+        if (per_wave >= 8) return WaveInstance<T, MT, NORM, ONE_SLICE, 8>::launch(a, cu_count, stream);
+    }
+    if constexpr (MT == 1) {
+        if (per_wave >= 4) return WaveInstance<T, MT, NORM, ONE_SLICE, 4>::launch(a, cu_count, stream);
+    }
+    return WaveInstance<T, MT, NORM, ONE_SLICE, 2>::launch(a, cu_count, stream);
+}
+
 template <int T, int MT, bool NORM>
 static hipError_t launch_tm(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
-    const size_t lds = (size_t)MT * a.K * sizeof(float);
-    const int min_rows_per_wave = 2;
-    int grid = (a.total_rows + kWaves * min_rows_per_wave - 1) / (kWaves * min_rows_per_wave);
-    const int max_grid = cu_count * 2;
-    if (grid > max_grid) grid = max_grid;
-    if (grid < 1) grid = 1;
-    if ((a.K >> 8) <= 16) {
-        auto kern = gemv_wave_kernel<T, MT, NORM, true>;
-        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, a);
-    } else {
-        auto kern = gemv_wave_kernel<T, MT, NORM, false>;
-        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, a);
-    }
-    return hipGetLastError();
+    if (a.K <= kSliceElems) return launch_ring<T, MT, NORM, true>(a, cu_count, stream);
+    return launch_ring<T, MT, NORM, false>(a, cu_count, stream);
 }
 
 template <int T, bool NORM>
 static hipError_t launch_t(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
     if (a.members <= 1) return launch_tm<T, 1, NORM>(a, cu_count, stream);
-    if (a.members <= 2) return launch_tm<T, 2, NORM>(a, cu_count, stream);
-    return launch_tm<T, 4, NORM>(a, cu_count, stream);
+    return launch_tm<T, 2, NORM>(a, cu_count, stream);
 }
 
 int wave_max_members(int K) {
-    const long long fit = kWaveMaxLdsBytes / ((long long)K * (long long)sizeof(float));
-    if (fit >= 4) return 4;
+    if (K > kWaveMaxK) return 0;
+    const long long per_member = (long long)act_lds_bytes<kQ6K>(1, K);
+    const long long fit = kWaveMaxLdsBytes / per_member;
     if (fit >= 2) return 2;
     return fit >= 1 ? 1 : 0;
 }

@@ -78,6 +78,33 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
+// DPP row-local reduction (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror) leaves each 16-lane row's sum in all its lanes; four readlanes
+// add the rows. The result is wave-uniform and needs no LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp_step(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
+    return v + __builtin_bit_cast(float, moved);
+}
+
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+    v = dpp_step<0xb1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_step<0x4e>(v);   // quad_perm [2,3,0,1]
+    v = dpp_step<0x141>(v);  // row_half_mirror
+    v = dpp_step<0x140>(v);  // row_mirror
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
+    return fmaxf(v, __builtin_bit_cast(float, moved));
+}
+
 // Sum across the 64 lanes of a wave; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

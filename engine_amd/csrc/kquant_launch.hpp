@@ -6,12 +6,15 @@
 
 namespace ribn_amd {
 
-// Members one wave-GEMV launch accumulates; larger batches are split by the host.
-constexpr int kWaveMaxMembers = 4;
+// Members one wave-GEMV launch accumulates (their activations live in registers);
+// larger batches are split by the host into launch groups.
+constexpr int kWaveMaxMembers = 2;
 // Weights one grouped wave-GEMV launch streams (they share one activation vector).
 constexpr int kMaxGroup = 4;
-// LDS the wave GEMV may use to stage [members][K] activations.
+// LDS the wave GEMV may use for its quantized [members][K] activation
+// records, and the largest K its staging covers.
 constexpr long long kWaveMaxLdsBytes = 128 * 1024;
+constexpr int kWaveMaxK = 16384;
 
 struct WaveGemvArgs {
     const uint8_t* w[kMaxGroup];

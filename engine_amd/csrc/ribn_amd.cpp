@@ -191,8 +191,8 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
     if (per_launch <= 0) {
         // K too large to stage in LDS: the exact-order kernel still serves it.
         if (gamma != nullptr) {
-            return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)(ribn_amd::kWaveMaxLdsBytes / 4), k,
-                        "fused RMSNorm supports K up to %lld", ribn_amd::kWaveMaxLdsBytes / 4);
+            return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kWaveMaxK, k, "fused RMSNorm supports K up to %d",
+                        ribn_amd::kWaveMaxK);
         }
         for (size_t i = 0; i < count; ++i) {
             hipError_t e = ribn_amd::launch_gemv_exact((int)g->value_type, ws[i]->data,
