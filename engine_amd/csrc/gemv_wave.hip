@@ -40,8 +40,6 @@
 
 namespace ribn_amd {
 
-constexpr int kWaves = 8;  // waves per workgroup
-constexpr int kThreads = kWaves * 64;
 constexpr uint32_t kOutOfRange = 0xffffff00u;  // buffer offset past any tensor: loads return 0, stores drop
 constexpr int kSliceElems = 16 * kQK;          // elements a wave covers per unit
 
@@ -100,8 +98,9 @@ __device__ __forceinline__ int group_sum(int v) {
     return v;
 }
 
+// Activations are read by every workgroup: default cache policy, so they stay in L2.
 __device__ __forceinline__ float4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
-    return __builtin_bit_cast(float4, load_b128(r, offset));
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)offset, 0, 0));
 }
 
 // ----------------------------------------------------------- raw row loads
@@ -276,8 +275,10 @@ __device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneAc
 
 // ------------------------------------------------------------------ kernel
 
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF>
-__global__ __launch_bounds__(kThreads) void gemv_wave_kernel(WaveGemvArgs args) {
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args) {
+    constexpr int kWaves = WAVES;
+    constexpr int kThreads = WAVES * 64;
     constexpr int BB = BlockTraits<T>::bytes;
     constexpr int G = ActTraits<T>::groups;
     constexpr int STRIDE = ActTraits<T>::stride;
@@ -539,8 +540,6 @@ __global__ __launch_bounds__(kThreads) void gemv_wave_kernel(WaveGemvArgs args) 
 
 // ---------------------------------------------------------------- launcher
 
-template <int T> constexpr int max_ring() { return T == kQ4K ? 8 : 4; }
-
 // LDS of the activation records: [members][slices][64][stride] dwords.
 template <int T>
 static size_t act_lds_bytes(int members, int K) {
@@ -548,52 +547,57 @@ static size_t act_lds_bytes(int members, int K) {
     return (size_t)members * slices * 64 * ActTraits<T>::stride * sizeof(uint32_t);
 }
 
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF>
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES>
 struct WaveInstance {
-    static std::atomic<int> per_cu;  // resident workgroups per CU at the largest LDS size (0: not queried)
-    static hipError_t launch(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
-        auto kern = gemv_wave_kernel<T, MT, NORM, ONE_SLICE, NBUF>;
+    static std::atomic<int> occupancy;  // resident workgroups per CU at the largest LDS size (0: not queried)
+    // Launches `per_cu` workgroups on every CU (capped by occupancy; fewer
+    // when the problem has fewer than two units per wave).
+    static hipError_t launch(const WaveGemvArgs& a, int cu_count, int per_cu, hipStream_t stream) {
+        auto kern = gemv_wave_kernel<T, MT, NORM, ONE_SLICE, NBUF, WAVES>;
         const size_t lds = act_lds_bytes<T>(MT, a.K);
-        int occ = per_cu.load(std::memory_order_relaxed);
+        int occ = occupancy.load(std::memory_order_relaxed);
         if (occ == 0) {
             const int max_lds = (int)act_lds_bytes<T>(MT, ONE_SLICE ? kSliceElems : kWaveMaxK);
             hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)kern, kThreads, max_lds) !=
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)kern, WAVES * 64, max_lds) !=
                     hipSuccess ||
                 occ < 1) {
                 occ = 1;
             }
-            per_cu.store(occ, std::memory_order_relaxed);
+            occupancy.store(occ, std::memory_order_relaxed);
         }
-        // One resident round of workgroups; each wave streams a contiguous
-        // row range of at least a couple of units.
         const int slices = ONE_SLICE ? 1 : ((a.K >> 8) + 15) >> 4;
         const long long units = (long long)a.total_rows * slices;
-        const long long want = (units + 2 * kWaves - 1) / (2 * kWaves);
-        int grid = (int)std::min<long long>(want, (long long)cu_count * occ);
+        const long long want = (units + 2 * WAVES - 1) / (2 * WAVES);
+        long long grid = want;
+        if (want >= cu_count) {
+            grid = (long long)cu_count * std::min<long long>({(want + cu_count - 1) / cu_count, (long long)occ,
+                                                               (long long)per_cu});
+        }
         if (grid < 1) grid = 1;
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, a);
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WAVES * 64), lds, stream, a);
         return hipGetLastError();
     }
 };
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF>
-std::atomic<int> WaveInstance<T, MT, NORM, ONE_SLICE, NBUF>::per_cu{0};
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES>
+std::atomic<int> WaveInstance<T, MT, NORM, ONE_SLICE, NBUF, WAVES>::occupancy{0};
 
+// Launch shape by units (row x slice) per CU, from sweeps on MI355X over
+// workgroup size {2,4,8,16} waves x ring depth {2,4,8} x workgroups per CU
+// {1,2,4}: short launches want every wave started at once with a shallow
+// ring; long streams want fewer, deeper streams per CU.
 template <int T, int MT, bool NORM, bool ONE_SLICE>
 static hipError_t launch_ring(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
-    // Ring depth: deep enough to keep several units in flight, no deeper than
-    // the units a wave gets (extra slots only issue out-of-range loads).
     const int slices = ONE_SLICE ? 1 : ((a.K >> 8) + 15) >> 4;
     const long long units = (long long)a.total_rows * slices;
-    const long long waves = (long long)cu_count * kWaves;
-    const long long per_wave = (units + waves - 1) / waves;
-    if constexpr (MT == 1 && max_ring<T>() >= 8) {
-        if (per_wave >= 8) return WaveInstance<T, MT, NORM, ONE_SLICE, 8>::launch(a, cu_count, stream);
+    const long long per_cu = (units + cu_count - 1) / cu_count;
+    if constexpr (MT == 1 && ONE_SLICE) {
+        if (per_cu >= 128) {
+            if constexpr (T == kQ6K) return WaveInstance<T, MT, NORM, ONE_SLICE, 8, 4>::launch(a, cu_count, 1, stream);
+            return WaveInstance<T, MT, NORM, ONE_SLICE, 4, 8>::launch(a, cu_count, 4, stream);
+        }
     }
-    if constexpr (MT == 1) {
-        if (per_wave >= 4) return WaveInstance<T, MT, NORM, ONE_SLICE, 4>::launch(a, cu_count, stream);
-    }
-    return WaveInstance<T, MT, NORM, ONE_SLICE, 2>::launch(a, cu_count, stream);
+    return WaveInstance<T, MT, NORM, ONE_SLICE, 2, 8>::launch(a, cu_count, per_cu > 48 ? 2 : 1, stream);
 }
 
 template <int T, int MT, bool NORM>

@@ -34,7 +34,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Cache-policy bits for streamed weights (read once per launch).
+// Cache-policy bits for streamed weights. The non-temporal hint (nt = 2)
+// speeds up a purely contiguous stream, but the GEMV's block-strided loads
+// touch each 128-byte line from several instructions and lose those re-hits
+// under it, so weights use the default policy.
 constexpr int kStreamPolicy = 0;
 
 __device__ __forceinline__ uint4 load_b128(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
