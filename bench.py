@@ -178,6 +178,27 @@ def cpu_baseline(seconds_budget=12.0):
     }
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_wave_q4k_gate_up_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per gate+up launch from the committed rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes, when they were taken on the current kernel sources."""
+    try:
+        from engine_amd.profiling import source_hash
+        fields = {}
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if "=" in line and line.strip().startswith(("traffic_bytes_per_launch", "source_hash")):
+                    k, v = line.split("=", 1)
+                    fields[k.strip()] = v.strip().strip("`")
+        if fields.get("source_hash") != source_hash():
+            return None
+        return int(fields["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -199,6 +220,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="issue launches eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="after the timed work, copy a MIB-MiB device buffer three times: a kernel of known "
+                         "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE onto bytes")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -226,7 +250,7 @@ def main():
         step.run()  # eager warm-up (and validation of every launch)
     torch.cuda.synchronize()
     graph = None if args.no_graph else capture(torch, stream, step.run)
-    graph_gu = capture(torch, stream, step.run_gate_up)
+    graph_gu = None if args.no_graph else capture(torch, stream, step.run_gate_up)
 
     def one():
         if graph is not None:
@@ -253,12 +277,13 @@ def main():
     # Dominant kernel: the RMSNorm-fused Q4_K gate+up group launch (4096 -> 2x12288),
     # timed live with HIP events over back-to-back launches on the stream it runs on.
     reps = 5
+    gate_up = graph_gu.replay if graph_gu is not None else step.run_gate_up
     with torch.cuda.stream(stream):
-        graph_gu.replay()
+        gate_up()
         s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s2.record(stream)
         for _ in range(reps):
-            graph_gu.replay()
+            gate_up()
         e2.record(stream)
     torch.cuda.synchronize()
     launches = reps * args.layers
@@ -272,10 +297,17 @@ def main():
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
-        "traffic": None,
+        "traffic": measured_traffic(),
         "avg_launch_us": round(us_launch, 3),
         "bytes_per_launch": gu_bytes,
     }
+
+    if args.calibrate_copy > 0:
+        src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
     cpu = None
     if not args.no_cpu_baseline:

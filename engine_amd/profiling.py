@@ -1,0 +1,130 @@
+"""Summaries of rocprofv3 CSV output for the k-quant kernels.
+
+    python -m engine_amd.profiling trace <dir-or-kernel_trace.csv>
+    python -m engine_amd.profiling pmc <dir-or-counter_collection.csv> [--copy-bytes N]
+    python -m engine_amd.profiling source-hash
+
+`trace` groups dispatches by (kernel, grid size), since one kernel instance can
+serve launches of different shapes (the q/k/v and gate/up groups share one),
+and prints count / mean / median / min duration in microseconds.
+
+`pmc` groups counter values the same way and prints the mean per dispatch.
+FETCH_SIZE and WRITE_SIZE are reported by rocprofv3 in KiB; with
+`--copy-bytes N` the summary also reads the counter on the largest copy kernel
+in the run (a device-to-device copy of N bytes reads N and writes N bytes) and
+prints the scale factor that maps the counter onto true bytes.
+
+`source-hash` prints the hash of the kernel sources, recorded in profile
+summaries so a stale measurement is recognisable.
+"""
+from __future__ import annotations
+
+import csv
+import glob
+import hashlib
+import os
+import statistics
+import sys
+from collections import defaultdict
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KERNEL_SOURCES = ("csrc/gemv_wave.hip", "csrc/kquant_kernels.hip", "csrc/kquant_device.hpp",
+                  "csrc/kquant_launch.hpp")
+
+
+def source_hash() -> str:
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(HERE, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def _find(path: str, suffix: str) -> list[str]:
+    if os.path.isfile(path):
+        return [path]
+    return sorted(glob.glob(os.path.join(path, "**", f"*{suffix}"), recursive=True))
+
+
+def short_name(name: str) -> str:
+    name = name.replace("void ", "", 1).replace("ribn_amd::", "")
+    depth, out = 0, []
+    for ch in name:  # drop the argument list, keep template arguments
+        if ch == "(" and depth == 0:
+            break
+        depth += ch == "<"
+        depth -= ch == ">"
+        out.append(ch)
+    return "".join(out)[:90]
+
+
+def trace_summary(path: str, match: str = "") -> list[tuple]:
+    """[(kernel, grid, count, mean_us, median_us, min_us)] sorted by total time."""
+    groups: dict[tuple, list[int]] = defaultdict(list)
+    for f in _find(path, "kernel_trace.csv"):
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                name = short_name(row["Kernel_Name"])
+                if match and match not in name:
+                    continue
+                grid = int(row.get("Grid_Size_X") or row.get("Grid_Size") or 0)
+                groups[(name, grid)].append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    out = [(k[0], k[1], len(v), statistics.mean(v) / 1e3, statistics.median(v) / 1e3, min(v) / 1e3)
+           for k, v in groups.items()]
+    out.sort(key=lambda r: -r[2] * r[3])
+    return out
+
+
+def pmc_summary(path: str) -> dict[tuple, dict[str, float]]:
+    """{(kernel, grid): {counter: mean value per dispatch}}."""
+    acc: dict[tuple, dict[str, list[float]]] = defaultdict(lambda: defaultdict(list))
+    for f in _find(path, "counter_collection.csv"):
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                name = short_name(row["Kernel_Name"])
+                grid = int(row.get("Grid_Size") or row.get("Grid_Size_X") or 0)
+                acc[(name, grid)][row["Counter_Name"]].append(float(row["Counter_Value"]))
+    return {k: {c: statistics.mean(v) for c, v in cs.items()} for k, cs in acc.items()}
+
+
+def copy_scale(summary: dict, counter: str, copy_bytes: int) -> float | None:
+    """True bytes per counter unit, from the copy kernel with the largest counter value."""
+    best = None
+    for (name, _grid), cs in summary.items():
+        if "copy" in name.lower() and counter in cs and cs[counter] > 0:
+            if best is None or cs[counter] > best:
+                best = cs[counter]
+    return None if best is None else copy_bytes / best
+
+
+def _main(argv: list[str]) -> int:
+    if not argv or argv[0] not in ("trace", "pmc", "source-hash"):
+        print(__doc__)
+        return 2
+    if argv[0] == "source-hash":
+        print(source_hash())
+        return 0
+    if argv[0] == "trace":
+        match = argv[2] if len(argv) > 2 else ""
+        print(f"{'kernel':90s} {'grid':>9s} {'n':>6s} {'mean_us':>9s} {'median_us':>9s} {'min_us':>9s}")
+        for name, grid, n, mean, med, mn in trace_summary(argv[1], match):
+            print(f"{name:90s} {grid:9d} {n:6d} {mean:9.3f} {med:9.3f} {mn:9.3f}")
+        return 0
+    copy_bytes = None
+    if "--copy-bytes" in argv:
+        copy_bytes = int(argv[argv.index("--copy-bytes") + 1])
+    summary = pmc_summary(argv[1])
+    counters = sorted({c for cs in summary.values() for c in cs})
+    print(f"{'kernel':90s} {'grid':>9s} " + " ".join(f"{c:>14s}" for c in counters))
+    for (name, grid), cs in sorted(summary.items()):
+        print(f"{name:90s} {grid:9d} " + " ".join(f"{cs.get(c, float('nan')):14.1f}" for c in counters))
+    if copy_bytes:
+        for c in counters:
+            scale = copy_scale(summary, c, copy_bytes)
+            if scale is not None:
+                print(f"scale {c}: {scale:.3f} bytes per unit (copy of {copy_bytes} bytes)")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(_main(sys.argv[1:]))
