@@ -42,9 +42,8 @@ extern "C" {
 #define RIBN_AMD_Q5_K 13u
 #define RIBN_AMD_Q6_K 14u
 
-/* Members one batched launch accepts. The reference caps its weights-read-once
- * kernels at 8 (quantized.rs:12); this library serves decode batches up to 64
- * and prefill through ribn_amd_gemm_prefill. */
+/* Members one batched call accepts. The reference caps its weights-read-once
+ * kernels at 8 (quantized.rs:12); this library serves decode batches up to 64. */
 #define RIBN_AMD_MAX_BATCH_MEMBERS 64u
 
 typedef enum ribn_amd_status {
@@ -86,11 +85,12 @@ int32_t ribn_amd_abi_version(void);
 
 /* ------------------------------------------------------------- lifecycle */
 
-/* CudaContext::new(device) + context.default_stream() (quantized.rs:1487-1492):
- * a context owning a fresh non-blocking stream on `device`. */
+/* CudaQ4KGemv::new (quantized.rs:1575-1580; the same in every family):
+ * CudaContext::new(device) + default_stream(). Here: a context owning a fresh
+ * non-blocking stream on `device`. */
 ribn_amd_status ribn_amd_context_create(int32_t device, ribn_amd_context **out);
-/* from_context(&ctx, stream) (quantized.rs:1500-1516): wraps a caller-owned HIP
- * stream; the caller keeps ownership and must outlive the context. */
+/* CudaQ4KGemv::from_context(&ctx, stream) (quantized.rs:1588-1610): wraps a
+ * caller-owned HIP stream; the caller keeps ownership and must outlive the context. */
 ribn_amd_status ribn_amd_context_wrap_stream(int32_t device, void *hip_stream, ribn_amd_context **out);
 void ribn_amd_context_destroy(ribn_amd_context *ctx);
 /* CudaStream::synchronize. */
@@ -159,7 +159,7 @@ ribn_amd_status ribn_amd_gemv_create(ribn_amd_context *ctx, uint32_t value_type,
 void ribn_amd_gemv_destroy(ribn_amd_gemv *gemv);
 uint32_t ribn_amd_gemv_value_type(const ribn_amd_gemv *gemv);
 
-/* execute (quantized.rs:356-388): y[N] = W x[K]. Exact-order kernel: per row,
+/* execute (quantized.rs:368-388): y[N] = W x[K]. Exact-order kernel: per row,
  * elements in K order, each product and sum rounded separately, so results
  * equal the host decoder + sequential f32 dot bit for bit. Correctness oracle;
  * slow. */
@@ -172,7 +172,7 @@ ribn_amd_status ribn_amd_gemv_execute_warp(ribn_amd_gemv *gemv, const ribn_amd_q
 /* execute_warp_batch (quantized.rs:445-487): `members` batch-major rows,
  * weights read once per launch group. input_len == members*K,
  * output_len == members*N, 1 <= members <= RIBN_AMD_MAX_BATCH_MEMBERS.
- * Per row bit-identical to execute_warp for members <= 4. */
+ * Every row is bit-identical to execute_warp on that member alone. */
 ribn_amd_status ribn_amd_gemv_execute_warp_batch(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
                                                  const float *input, size_t input_len, float *output,
                                                  size_t output_len, size_t members);

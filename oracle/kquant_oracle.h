@@ -12,7 +12,7 @@
  * Compile with -O2 -ffp-contract=off and without -ffast-math: the op order and
  * rounding of every f32 operation below is part of the contract.
  *
- * Pins (tests/test_oracle_*.py): the reference's KATs (crates/gguf/src/lib.rs
+ * Pins (tests/test_oracle.py): the reference's KATs (crates/gguf/src/lib.rs
  * :1369-1514), the reference's fixture encoders with their exact f64 closed
  * forms (crates/nvidia/tests/q{4,5,6}_q8_1.rs fixture()), all 65536 binary16
  * patterns against numpy's IEEE conversion, the GGML scale packing round trip
