@@ -9,12 +9,14 @@ from .kquant import (  # noqa: F401
     Q4_K, Q5_K, Q6_K, BLOCK_BYTES,
     AmdContext, AmdWeightStore, AmdQuantizedWeight,
     AmdQ4KGemv, AmdQ5KGemv, AmdQ6KGemv, QwenGemvKernel, AmdQwenOps,
+    AmdQ4KEmbedding, AmdKQuantEmbedding,
     AmdKernelError, AmdQuantizedKernelError, AmdModelKernelError, AmdWeightError,
     validate_quantized_geometry,
 )
 
 __all__ = [
     "Q4_K", "Q5_K", "Q6_K", "BLOCK_BYTES", "AmdContext", "AmdWeightStore", "AmdQuantizedWeight",
-    "AmdQ4KGemv", "AmdQ5KGemv", "AmdQ6KGemv", "QwenGemvKernel", "AmdQwenOps", "AmdKernelError",
+    "AmdQ4KGemv", "AmdQ5KGemv", "AmdQ6KGemv", "QwenGemvKernel", "AmdQwenOps", "AmdQ4KEmbedding",
+    "AmdKQuantEmbedding", "AmdKernelError",
     "AmdQuantizedKernelError", "AmdModelKernelError", "AmdWeightError", "validate_quantized_geometry",
 ]

@@ -73,6 +73,10 @@ SIGNATURES = {
     "ribn_amd_gemv_execute_group": (_i32, [_vp, _pvp, _sz, _vp, _sz, _vp, _sz, _f32, _pvp,
                                            ctypes.POINTER(_sz), _sz]),
     "ribn_amd_dequantize": (_i32, [_vp, _vp, _vp, _sz]),
+    "ribn_amd_embedding_create": (_i32, [_vp, _u32, _pvp]),
+    "ribn_amd_embedding_destroy": (None, [_vp]),
+    "ribn_amd_embedding_execute": (_i32, [_vp, _vp, _u32, _vp, _sz]),
+    "ribn_amd_embedding_execute_batch": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
     "ribn_amd_rms_norm": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _f32]),
     "ribn_amd_rms_norm_batch": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _f32]),
 }

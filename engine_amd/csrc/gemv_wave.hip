@@ -365,22 +365,29 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
     // offset, which returns zeros), so each stays where it is issued and the
     // wave waits for exactly the unit it reduces next.
     RowData<T> ring[NBUF];
-    int lrow = r_begin, lslice = 0;  // next unit to load
-    auto load_next = [&](RowData<T>& dst) {
-        const bool live_row = lrow < r_end;
+    // Unit order: one slice of K = 4096 carries whole rows (row-major units);
+    // longer K goes in groups of NBUF rows, slice by slice, so ring slot r
+    // always holds row r of the group and the activations of a slice are read
+    // once per group.
+    int lrow = r_begin, lslice = 0;  // next unit to load (group base row when K spans slices)
+    auto load_next = [&](RowData<T>& dst, int r) {
+        const int row = ONE_SLICE ? lrow : lrow + r;
+        const bool live_row = row < r_end;
         int mat, local;
-        locate(live_row ? lrow : r_begin, mat, local);
+        locate(live_row ? row : r_begin, mat, local);
         const __amdgpu_buffer_rsrc_t rs = pick_w(mat);
         const int b = lslice * 16 + bs;
         const bool live = live_row && b < nb;
         load_row<T>(dst, rs, live ? (uint32_t)local * row_bytes + (uint32_t)b * BB : kOutOfRange, p);
-        if (ONE_SLICE || ++lslice == slices) {
-            lslice = 0;
+        if constexpr (ONE_SLICE) {
             ++lrow;
+        } else if (r == NBUF - 1 && ++lslice == slices) {
+            lslice = 0;
+            lrow += NBUF;
         }
     };
 #pragma unroll
-    for (int r = 0; r < NBUF; ++r) load_next(ring[r]);
+    for (int r = 0; r < NBUF; ++r) load_next(ring[r], r);
 
     // ---- staging: x (times gamma) into per-group fixed point, in lane order.
     float ssq[MT];
@@ -493,47 +500,57 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
     // ---- ring: reduce a unit, store its row when the unit completes it
     // (other stores go to an out-of-range offset and are dropped), refill the
     // slot with the unit NBUF ahead.
-    int crow = r_begin, cslice = 0;  // unit being reduced
-    float acc[MT];
+    int crow = r_begin, cslice = 0;  // unit being reduced (group base row when K spans slices)
+    float acc[NBUF][MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = 0.f;
-    auto consume = [&](const RowData<T>& d) {
-        if constexpr (!ONE_SLICE) read_act(cslice);
+    for (int r = 0; r < NBUF; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
+    auto consume = [&](const RowData<T>& d, int r) {
+        if constexpr (!ONE_SLICE) {
+            if (r == 0) read_act(cslice);
+        }
         float part[MT];
         row_dot<T, MT>(d, p, xa, part);
+        const int row = ONE_SLICE ? crow : crow + r;
         const bool last = ONE_SLICE || cslice == slices - 1;
         int mat, local;
-        locate(crow, mat, local);
+        locate(row < r_end ? row : r_begin, mat, local);
         int rows_mat;
         const __amdgpu_buffer_rsrc_t yr = pick_y(mat, rows_mat);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            acc[m] = (ONE_SLICE || cslice == 0) ? part[m] : acc[m] + part[m];
-            const float total = wave_sum_uniform(acc[m]) * inv[m];
-            const uint32_t off =
-                (last && lane == 0 && m < members) ? (uint32_t)(m * rows_mat + local) * 4u : kOutOfRange;
+            acc[r][m] = (ONE_SLICE || cslice == 0) ? part[m] : acc[r][m] + part[m];
+            const float total = wave_sum_uniform(acc[r][m]) * inv[m];
+            const uint32_t off = (last && row < r_end && lane == 0 && m < members)
+                                     ? (uint32_t)(m * rows_mat + local) * 4u
+                                     : kOutOfRange;
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, total), yr, (int)off, 0, 0);
         }
-        if (ONE_SLICE || ++cslice == slices) {
-            cslice = 0;
+        if constexpr (ONE_SLICE) {
             ++crow;
+        } else if (r == NBUF - 1 && ++cslice == slices) {
+            cslice = 0;
+            crow += NBUF;
         }
     };
 
-    const int units = (r_end - r_begin) * slices;
-    const int passes = (units + NBUF - 1) / NBUF;
+    const int rows_w = r_end - r_begin;
+    // Passes of NBUF units; a partial last group (K spanning slices) runs on
+    // zero-filled loads and stores nothing.
+    const int passes = ONE_SLICE ? (rows_w + NBUF - 1) / NBUF : (rows_w + NBUF - 1) / NBUF * slices;
     for (int pass = 0; pass + 1 < passes; ++pass) {
 #pragma unroll
         for (int r = 0; r < NBUF; ++r) {
-            consume(ring[r]);
-            load_next(ring[r]);
+            consume(ring[r], r);
+            load_next(ring[r], r);
         }
     }
     if (passes > 0) {
-        const int left = units - (passes - 1) * NBUF;
+        const int left = ONE_SLICE ? rows_w - (passes - 1) * NBUF : NBUF;
 #pragma unroll
         for (int r = 0; r < NBUF; ++r) {
-            if (r < left) consume(ring[r]);
+            if (r < left) consume(ring[r], r);
         }
     }
 }

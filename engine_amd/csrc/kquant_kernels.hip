@@ -126,6 +126,32 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
 }
 
 // ---------------------------------------------------------------------------
+// Embedding gather (q4_k.cu:1-67 q4_k_embedding / _batch): row `token` of a
+// [hidden, vocab] k-quant table, dequantised bit-exactly. One workgroup per
+// (member, super-block); tokens come from a device array (batch) or a value.
+// Batch ids outside the vocabulary leave their output row unwritten, as the
+// reference kernel does (the single-token call validates on the host).
+// ---------------------------------------------------------------------------
+template <int T>
+__global__ __launch_bounds__(256) void embedding_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
+                                                        const uint32_t* __restrict__ tokens, uint32_t token,
+                                                        float* __restrict__ out, uint32_t blocks_per_token,
+                                                        uint32_t vocab) {
+    constexpr int BB = BlockTraits<T>::bytes;
+    __shared__ uint8_t blk[256];
+    const uint32_t member = blockIdx.y;
+    const uint32_t tok = tokens ? tokens[member] : token;
+    if (tok >= vocab) return;  // uniform across the workgroup
+    const uint32_t block = (uint32_t)tok * blocks_per_token + blockIdx.x;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(w, wbytes);
+    if (threadIdx.x < BB) {
+        blk[threadIdx.x] = (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)(block * BB + threadIdx.x), 0, 0);
+    }
+    __syncthreads();
+    out[((size_t)member * blocks_per_token + blockIdx.x) * 256 + threadIdx.x] = dequant_element<T>(blk, threadIdx.x);
+}
+
+// ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
 template <int T>
@@ -160,6 +186,26 @@ hipError_t launch_gemv_exact(int value_type, const uint8_t* w, uint32_t wbytes, 
     case kQ4K: return launch_exact_t<kQ4K>(w, wbytes, x, y, K, N, members, stream);
     case kQ5K: return launch_exact_t<kQ5K>(w, wbytes, x, y, K, N, members, stream);
     case kQ6K: return launch_exact_t<kQ6K>(w, wbytes, x, y, K, N, members, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int T>
+static hipError_t launch_embedding_t(const uint8_t* w, uint32_t wbytes, const uint32_t* tokens, uint32_t token,
+                                     float* out, uint32_t blocks_per_token, uint32_t vocab, uint32_t members,
+                                     hipStream_t stream) {
+    hipLaunchKernelGGL(embedding_kernel<T>, dim3(blocks_per_token, members), dim3(256), 0, stream, w, wbytes, tokens,
+                       token, out, blocks_per_token, vocab);
+    return hipGetLastError();
+}
+
+hipError_t launch_embedding(int value_type, const uint8_t* w, uint32_t wbytes, const uint32_t* tokens,
+                            uint32_t token, float* out, uint32_t blocks_per_token, uint32_t vocab, uint32_t members,
+                            hipStream_t stream) {
+    switch (value_type) {
+    case kQ4K: return launch_embedding_t<kQ4K>(w, wbytes, tokens, token, out, blocks_per_token, vocab, members, stream);
+    case kQ5K: return launch_embedding_t<kQ5K>(w, wbytes, tokens, token, out, blocks_per_token, vocab, members, stream);
+    case kQ6K: return launch_embedding_t<kQ6K>(w, wbytes, tokens, token, out, blocks_per_token, vocab, members, stream);
     default: return hipErrorInvalidValue;
     }
 }

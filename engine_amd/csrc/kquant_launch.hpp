@@ -42,6 +42,12 @@ hipError_t launch_gemv_exact(int value_type, const uint8_t* w, uint32_t wbytes, 
 // args.gamma == nullptr: plain GEMV; otherwise RMSNorm(x; gamma, eps) is fused into the activation load.
 hipError_t launch_gemv_wave(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
 
+// Gathers and dequantises rows of a [hidden, vocab] table: tokens[m] (device
+// array) or `token` when tokens is null; out is [members][hidden].
+hipError_t launch_embedding(int value_type, const uint8_t* w, uint32_t wbytes, const uint32_t* tokens,
+                            uint32_t token, float* out, uint32_t blocks_per_token, uint32_t vocab, uint32_t members,
+                            hipStream_t stream);
+
 hipError_t launch_rms_norm(const float* x, const float* w, float* y, int length, int members, float eps,
                            hipStream_t stream);
 

@@ -38,6 +38,11 @@ struct ribn_amd_gemv {
     uint32_t value_type;
 };
 
+struct ribn_amd_embedding {
+    ribn_amd_context* ctx;
+    uint32_t value_type;
+};
+
 namespace {
 
 thread_local ribn_amd_error g_last_error = {RIBN_AMD_OK, 0, 0, {0}};
@@ -102,11 +107,12 @@ struct DeviceGuard {
 
 // The ContextMismatch check of quantized.rs:260-266 for raw device pointers:
 // the buffer must be device (or managed) memory of the context's device.
-ribn_amd_status check_device_ptr(const ribn_amd_context* ctx, const void* ptr, const char* what) {
+ribn_amd_status check_device_ptr(const ribn_amd_context* ctx, const void* ptr, const char* what,
+                                 uintptr_t align = 16) {
     if (ptr == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "%s is null", what);
-    if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) {
-        return fail(RIBN_AMD_INVALID_ARGUMENT, 16, reinterpret_cast<uintptr_t>(ptr) & 15u,
-                    "%s must be 16-byte aligned", what);
+    if ((reinterpret_cast<uintptr_t>(ptr) & (align - 1)) != 0) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, align, reinterpret_cast<uintptr_t>(ptr) & (align - 1),
+                    "%s must be %u-byte aligned", what, (unsigned)align);
     }
     hipPointerAttribute_t attr;
     hipError_t e = hipPointerGetAttributes(&attr, ptr);
@@ -667,6 +673,113 @@ ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv* g, const ribn_amd_quantized_w
     hipError_t e = ribn_amd::launch_dequant((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, output,
                                             (uint32_t)(k / 256 * n), g->ctx->stream);
     if (e != hipSuccess) return driver(e, "launch dequantize");
+    return ok();
+}
+
+// ------------------------------------------------------------ embedding
+
+ribn_amd_status ribn_amd_embedding_create(ribn_amd_context* ctx, uint32_t value_type, ribn_amd_embedding** out) {
+    if (!ctx || !out) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (!supported(value_type)) {
+        return fail(RIBN_AMD_UNSUPPORTED_VALUE_TYPE, RIBN_AMD_Q4_K, value_type,
+                    "GGML value type %u has no MI355X embedding kernel", value_type);
+    }
+    auto* e = new (std::nothrow) ribn_amd_embedding{ctx, value_type};
+    if (!e) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    *out = e;
+    return ok();
+}
+
+void ribn_amd_embedding_destroy(ribn_amd_embedding* e) { delete e; }
+
+namespace {
+
+// quantized.rs:961-1057 (execute) and 1058-1160 (execute_batch), in order:
+// contexts, value type, shape, encoded length.
+ribn_amd_status validate_embedding(const ribn_amd_embedding* e, const ribn_amd_quantized_weight* w,
+                                   const float* output, uint64_t* hidden, uint64_t* vocab) {
+    if (!e || !w) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null embedding or weight handle");
+    if (w->ctx->device != e->ctx->device) {
+        return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)e->ctx->device, (uint64_t)w->ctx->device,
+                    "weight and embedding kernel belong to different devices");
+    }
+    ribn_amd_status st = check_device_ptr(e->ctx, output, "output");
+    if (st != RIBN_AMD_OK) return st;
+    if (w->value_type != e->value_type) {
+        return fail(RIBN_AMD_UNSUPPORTED_VALUE_TYPE, e->value_type, w->value_type,
+                    "%s embedding got a weight of GGML value type %u", type_label(e->value_type), w->value_type);
+    }
+    *hidden = w->input_size;
+    *vocab = w->output_size;
+    if (*hidden == 0 || *vocab == 0 || *hidden % 256 != 0) {
+        return fail(RIBN_AMD_INVALID_WEIGHT, 0, 0,
+                    "%s embedding shape is %llux%llu; hidden size must be a positive multiple of 256",
+                    type_label(e->value_type), (unsigned long long)*hidden, (unsigned long long)*vocab);
+    }
+    const uint64_t per_token = *hidden / 256;
+    if (*vocab > std::numeric_limits<uint64_t>::max() / per_token) return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "shape overflows");
+    const uint64_t blocks = per_token * *vocab;
+    const uint64_t bb = block_bytes(e->value_type);
+    if (blocks > std::numeric_limits<uint64_t>::max() / bb) return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "shape overflows");
+    if (w->encoded_bytes != blocks * bb) {
+        return fail(RIBN_AMD_INVALID_WEIGHT, blocks * bb, w->encoded_bytes, "encoded length is %llu, expected %llu",
+                    (unsigned long long)w->encoded_bytes, (unsigned long long)(blocks * bb));
+    }
+    return RIBN_AMD_OK;
+}
+
+}  // namespace
+
+ribn_amd_status ribn_amd_embedding_execute(ribn_amd_embedding* e, const ribn_amd_quantized_weight* w, uint32_t token,
+                                           float* output, size_t output_len) {
+    uint64_t hidden, vocab;
+    ribn_amd_status st = validate_embedding(e, w, output, &hidden, &vocab);
+    if (st != RIBN_AMD_OK) return st;
+    if (token >= vocab) {
+        return fail(RIBN_AMD_INVALID_WEIGHT, vocab, token, "token index %u is outside vocabulary size %llu", token,
+                    (unsigned long long)vocab);
+    }
+    if (hidden > (uint64_t)std::numeric_limits<int>::max() || vocab > (uint64_t)std::numeric_limits<int>::max() ||
+        w->encoded_bytes > 0xffffffffull) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "embedding table exceeds the kernel's index range");
+    }
+    if (output_len != hidden) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, hidden, output_len, "embedding output has %zu values, expected %llu",
+                    output_len, (unsigned long long)hidden);
+    }
+    DeviceGuard guard(e->ctx->device);
+    hipError_t he = ribn_amd::launch_embedding((int)e->value_type, w->data, (uint32_t)w->encoded_bytes, nullptr, token,
+                                               output, (uint32_t)(hidden / 256), (uint32_t)vocab, 1, e->ctx->stream);
+    if (he != hipSuccess) return driver(he, "launch embedding");
+    return ok();
+}
+
+ribn_amd_status ribn_amd_embedding_execute_batch(ribn_amd_embedding* e, const ribn_amd_quantized_weight* w,
+                                                 const uint32_t* tokens, size_t members, float* output,
+                                                 size_t output_len) {
+    uint64_t hidden, vocab;
+    ribn_amd_status st = validate_embedding(e, w, output, &hidden, &vocab);
+    if (st != RIBN_AMD_OK) return st;
+    if (members != 0) {
+        st = check_device_ptr(e->ctx, tokens, "token indices", 4);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    if (hidden > (uint64_t)std::numeric_limits<int>::max() || vocab > (uint64_t)std::numeric_limits<int>::max() ||
+        w->encoded_bytes > 0xffffffffull) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "embedding table exceeds the kernel's index range");
+    }
+    if (members == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "embedding batch needs at least one token");
+    if (members > 65535) return fail(RIBN_AMD_SHAPE_OVERFLOW, 65535, members, "embedding batch exceeds 65535 tokens");
+    if (output_len / members != hidden || output_len % members != 0) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, members * hidden, output_len,
+                    "embedding output has %zu values, expected %llu", output_len,
+                    (unsigned long long)(members * hidden));
+    }
+    DeviceGuard guard(e->ctx->device);
+    hipError_t he = ribn_amd::launch_embedding((int)e->value_type, w->data, (uint32_t)w->encoded_bytes, tokens, 0,
+                                               output, (uint32_t)(hidden / 256), (uint32_t)vocab, (uint32_t)members,
+                                               e->ctx->stream);
+    if (he != hipSuccess) return driver(he, "launch embedding batch");
     return ok();
 }
 

@@ -281,6 +281,60 @@ class AmdQ6KGemv(_AmdQuantizedGemv):
     VALUE_TYPE = Q6_K
 
 
+class _AmdEmbedding:
+    """Gather of dequantised table rows (CudaQ4KEmbedding, quantized.rs:913-1160)."""
+
+    VALUE_TYPE = Q4_K
+
+    def __init__(self, ctx: AmdContext, value_type: int):
+        self.ctx = ctx
+        self._lib = ctx._lib
+        self.handle = ctypes.c_void_p()
+        _check(self._lib.ribn_amd_embedding_create(ctx.handle, value_type, ctypes.byref(self.handle)))
+
+    @classmethod
+    def from_context(cls, ctx: AmdContext):
+        return cls(ctx, cls.VALUE_TYPE)
+
+    @classmethod
+    def new(cls, device: int = 0):
+        return cls(AmdContext(device), cls.VALUE_TYPE)
+
+    def execute(self, weight, token_index: int, output):
+        _check(self._lib.ribn_amd_embedding_execute(self.handle, weight.handle, int(token_index), _ptr(output),
+                                                    output.numel()))
+
+    def execute_batch(self, weight, token_indices, output):
+        """token_indices: device tensor of 32-bit token ids, one per member."""
+        members = token_indices.numel()
+        tok = _ptr(token_indices) if members else None
+        _check(self._lib.ribn_amd_embedding_execute_batch(self.handle, weight.handle, tok, members, _ptr(output),
+                                                          output.numel()))
+
+    def close(self):
+        if self.handle and _live():
+            self._lib.ribn_amd_embedding_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class AmdQ4KEmbedding(_AmdEmbedding):
+    VALUE_TYPE = Q4_K
+
+
+class AmdKQuantEmbedding(_AmdEmbedding):
+    """Embedding gather for any served k-quant type (Q4_K / Q5_K / Q6_K tables)."""
+
+    @classmethod
+    def from_value_type(cls, ctx: AmdContext, value_type: int):
+        return cls(ctx, value_type)
+
+
 class QwenGemvKernel:
     """Per-GGML-type kernel selection (staging.rs:90-217)."""
 

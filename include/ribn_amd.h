@@ -74,6 +74,7 @@ typedef struct ribn_amd_error {
 typedef struct ribn_amd_context ribn_amd_context;
 typedef struct ribn_amd_quantized_weight ribn_amd_quantized_weight;
 typedef struct ribn_amd_gemv ribn_amd_gemv;
+typedef struct ribn_amd_embedding ribn_amd_embedding;
 
 /* ---------------------------------------------------------------- errors */
 
@@ -198,6 +199,24 @@ ribn_amd_status ribn_amd_gemv_execute_group(ribn_amd_gemv *gemv, const ribn_amd_
  * the reference's device equivalent is the q4_k_embedding gather, q4_k.cu:1-67). */
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight, float *output,
                                     size_t output_len);
+
+/* ------------------------------------------------------------- embedding */
+
+/* CudaQ4KEmbedding::from_context (quantized.rs:913-960): gather kernel for a
+ * [hidden, vocab] k-quant table (token_embd). The reference serves Q4_K; Q5_K
+ * and Q6_K tables use the same kernel. */
+ribn_amd_status ribn_amd_embedding_create(ribn_amd_context *ctx, uint32_t value_type, ribn_amd_embedding **out);
+void ribn_amd_embedding_destroy(ribn_amd_embedding *embedding);
+/* CudaQ4KEmbedding::execute (quantized.rs:961-1057): output[hidden] = the
+ * bit-exact dequantised row `token`. token >= vocab is InvalidWeight. */
+ribn_amd_status ribn_amd_embedding_execute(ribn_amd_embedding *embedding, const ribn_amd_quantized_weight *weight,
+                                           uint32_t token, float *output, size_t output_len);
+/* CudaQ4KEmbedding::execute_batch (quantized.rs:1058-1160): `members` token ids
+ * in device memory, output [members][hidden]. Ids outside the vocabulary leave
+ * their output row unwritten, as the reference kernel does (q4_k.cu:30-67). */
+ribn_amd_status ribn_amd_embedding_execute_batch(ribn_amd_embedding *embedding,
+                                                 const ribn_amd_quantized_weight *weight, const uint32_t *tokens,
+                                                 size_t members, float *output, size_t output_len);
 
 /* ------------------------------------------------------------- model ops */
 
