@@ -18,7 +18,7 @@ STATUS_NAMES = {
     0: "Ok", 1: "Driver", 2: "Module", 3: "InvalidWeight", 4: "UnsupportedValueType",
     5: "ShapeOverflow", 6: "InputLength", 7: "OutputLength", 8: "ContextMismatch",
     9: "EmptyInput", 10: "WeightLength", 11: "InvalidEpsilon", 12: "InvalidArgument",
-    13: "EmptyEncoding", 14: "SourceIncomplete",
+    13: "EmptyEncoding", 14: "SourceIncomplete", 15: "WorkspaceTooSmall",
 }
 
 
@@ -73,6 +73,9 @@ SIGNATURES = {
     "ribn_amd_gemv_execute_group": (_i32, [_vp, _pvp, _sz, _vp, _sz, _vp, _sz, _f32, _pvp,
                                            ctypes.POINTER(_sz), _sz]),
     "ribn_amd_dequantize": (_i32, [_vp, _vp, _vp, _sz]),
+    "ribn_amd_gemm_workspace_bytes": (_sz, [_sz, _sz]),
+    "ribn_amd_context_reserve_prefill": (_i32, [_vp, _sz, _sz]),
+    "ribn_amd_gemm_prefill": (_i32, [_vp, _vp, _vp, _u32, _sz, _sz, _vp, _sz, _f32, _vp, _sz]),
     "ribn_amd_embedding_create": (_i32, [_vp, _u32, _pvp]),
     "ribn_amd_embedding_destroy": (None, [_vp]),
     "ribn_amd_embedding_execute": (_i32, [_vp, _vp, _u32, _vp, _sz]),

@@ -1,0 +1,393 @@
+// Prefill / large-batch matmul for Q4_K / Q5_K / Q6_K on gfx950: y[M][N] =
+// x[M][K] . W^T with the weights dequantised in registers straight into MFMA
+// operand layout and multiplied on the matrix cores (v_mfma_f32_32x32x16_f16),
+// accumulating in f32.
+//
+// Two kernels:
+//  - act_f16_kernel: one workgroup per token. Optional RMSNorm
+//    (x * 1/sqrt(sum(x^2)/K + eps) * gamma, qwen_reference.rs:550-556), then
+//    conversion to f16 after a power-of-two scale that maps the token's
+//    largest |x| just below 2^15. bf16 inputs convert exactly (8-bit into
+//    11-bit significands) down to 2^-24 of the token maximum; f32 inputs round
+//    once (RNE, 2^-11 relative). The per-token unscale goes to a side array.
+//  - qgemm_kernel: a workgroup of WAVES waves owns 32*WAVES weight rows and
+//    32*CB tokens; wave w owns rows [32w, 32w+32) of the tile. K advances in
+//    half super-blocks (128 elements): the x tile [32*CB][128] f16 is staged
+//    in LDS (padded rows, double-buffered, prefetched through registers one
+//    step ahead), weights are loaded per lane straight from HBM (two steps
+//    ahead) and dequantised in f32, (d*sc)*q - dmin*m, then rounded once to
+//    f16 (RNE) in the A-operand layout. Each A fragment feeds CB MFMAs.
+//
+// MFMA 32x32x16 operand layout (measured on gfx950): lane l holds
+// A[l%32][8*(l/32)+j], B[8*(l/32)+j][l%32] (j = 0..7) and
+// C[8*(i/4)+4*(l/32)+(i%4)][l%32] (i = 0..15). Here A = W rows, B = x^T, so
+// C[n][m]. A dot product does not depend on the order of its k terms, so
+// each 16-wide MFMA k-chunk is a set of 16 block elements chosen to make the
+// lane's 8 elements come from 8 consecutive payload bytes; the B fragment
+// reads the same 8 activations, consecutive in k.
+#include "kquant_device.hpp"
+#include "kquant_launch.hpp"
+
+#include <algorithm>
+
+namespace ribn_amd {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_v __attribute__((ext_vector_type(2)));
+typedef float float2_v __attribute__((ext_vector_type(2)));
+typedef float float16_v __attribute__((ext_vector_type(16)));
+
+constexpr int kActThreads = 256;
+constexpr int kActMaxPerThread = kGemmMaxK / kActThreads;  // 64
+constexpr int kStepK = 128;                                // K per pipeline step (half a super-block)
+constexpr int kXRow = kStepK + 8;                          // padded LDS row (halfs): 272 B, bank-conflict free
+constexpr uint32_t kGemmOutOfRange = 0xffffff00u;
+
+// ------------------------------------------------------------ activations
+
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return t;
+}
+
+__device__ __forceinline__ float block_max_256(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return t;
+}
+
+template <bool BF16_IN, bool NORM>
+__global__ __launch_bounds__(kActThreads) void act_f16_kernel(const void* __restrict__ xin,
+                                                               const float* __restrict__ gamma, float eps, int K,
+                                                               _Float16* __restrict__ xh, float* __restrict__ unscale) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    float v[kActMaxPerThread];
+#pragma unroll
+    for (int i = 0; i < kActMaxPerThread; ++i) {
+        const int k = threadIdx.x + i * kActThreads;
+        float x = 0.f;
+        if (k < K) {
+            if constexpr (BF16_IN) {
+                const uint16_t b = static_cast<const uint16_t*>(xin)[(size_t)m * K + k];
+                x = __builtin_bit_cast(float, (uint32_t)b << 16);
+            } else {
+                x = static_cast<const float*>(xin)[(size_t)m * K + k];
+            }
+        }
+        v[i] = x;
+    }
+    if constexpr (NORM) {
+        float ssq = 0.f;
+#pragma unroll
+        for (int i = 0; i < kActMaxPerThread; ++i) ssq += v[i] * v[i];
+        const float inv = 1.0f / sqrtf(block_sum_256(ssq, red) / (float)K + eps);
+#pragma unroll
+        for (int i = 0; i < kActMaxPerThread; ++i) {
+            const int k = threadIdx.x + i * kActThreads;
+            v[i] = k < K ? v[i] * inv * gamma[k] : 0.f;
+        }
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < kActMaxPerThread; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = block_max_256(amax, red);
+    int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;  // amax < 2^e
+    e = e < -100 ? -100 : e;
+#pragma unroll
+    for (int i = 0; i < kActMaxPerThread; ++i) {
+        const int k = threadIdx.x + i * kActThreads;
+        if (k < K) xh[(size_t)m * K + k] = (_Float16)__builtin_amdgcn_ldexpf(v[i], 15 - e);
+    }
+    if (threadIdx.x == 0) unscale[m] = __builtin_amdgcn_ldexpf(1.0f, e - 15);
+}
+
+// ------------------------------------------------------------ weight fragments
+
+// Per-lane weight bytes for one pipeline step (half super-block `half`).
+template <int T> struct StepW;
+template <> struct StepW<kQ4K> { uint4 h, q0, q1; };        // header; qs bytes 32t+16hl.. for t = 2*half, 2*half+1
+template <> struct StepW<kQ5K> { uint4 h, qh, q0, q1; };    // + qh bytes 16hl..16hl+15
+template <> struct StepW<kQ6K> {
+    uint4 l0, l1, qh, sc;             // dword-aligned-down windows of ql (two), qh, scales
+    uint32_t l0t, l1t, qht, sct;      // the dword after each window
+    uint32_t d16, shift;
+};
+
+template <int T>
+__device__ __forceinline__ void load_step(StepW<T>& s, __amdgpu_buffer_rsrc_t r, uint32_t blk, int half, int hl) {
+    if constexpr (T == kQ4K) {
+        s.h = load_b128(r, blk);
+        s.q0 = load_b128(r, blk + 16 + 32 * (2 * half) + 16 * hl);
+        s.q1 = load_b128(r, blk + 16 + 32 * (2 * half + 1) + 16 * hl);
+    } else if constexpr (T == kQ5K) {
+        s.h = load_b128(r, blk);
+        s.qh = load_b128(r, blk + 16 + 16 * hl);
+        s.q0 = load_b128(r, blk + 48 + 32 * (2 * half) + 16 * hl);
+        s.q1 = load_b128(r, blk + 48 + 32 * (2 * half + 1) + 16 * hl);
+    } else {
+        const uint32_t base = blk & ~3u;
+        s.shift = (blk & 3u) * 8u;
+        const uint32_t l0 = base + 64 * half + 16 * hl;
+        const uint32_t l1 = l0 + 32;
+        const uint32_t qh = base + 128 + 32 * half + 16 * hl;
+        s.l0 = load_b128(r, l0);
+        s.l0t = load_b32(r, l0 + 16);
+        s.l1 = load_b128(r, l1);
+        s.l1t = load_b32(r, l1 + 16);
+        s.qh = load_b128(r, qh);
+        s.qht = load_b32(r, qh + 16);
+        s.sc = load_b128(r, base + 192);
+        s.sct = load_b32(r, base + 208);
+        s.d16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)(blk + 208), 0, kStreamPolicy);
+    }
+}
+
+__device__ __forceinline__ uint4 funnel4(uint4 a, uint32_t t, uint32_t sh) {
+    uint4 o;
+    o.x = __builtin_amdgcn_alignbit(a.y, a.x, sh);
+    o.y = __builtin_amdgcn_alignbit(a.z, a.y, sh);
+    o.z = __builtin_amdgcn_alignbit(a.w, a.z, sh);
+    o.w = __builtin_amdgcn_alignbit(t, a.w, sh);
+    return o;
+}
+
+// Eight f16 weights (a*q_j - b), q_j = byte j of (lo, hi) after masking
+// (byte-to-float converts are single v_cvt_f32_ubyteN instructions).
+__device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float a, float b) {
+    float w[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        w[j] = __builtin_fmaf(a, (float)((lo >> (8 * j)) & 0xffu), -b);
+        w[4 + j] = __builtin_fmaf(a, (float)((hi >> (8 * j)) & 0xffu), -b);
+    }
+    half8_t h;
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        const float2_v f = {w[j], w[j + 1]};
+        const half2_v p = __builtin_convertvector(f, half2_v);
+        h[j] = p[0];
+        h[j + 1] = p[1];
+    }
+    return h;
+}
+
+// Chunk c (0..7) of a step: the lane's 8 weights and the k offset (within the
+// 128-element step) of the 8 activations they multiply.
+//   Q4_K/Q5_K: c = (t', p, s): payload bytes 32t+16hl+8s+j, nibble p, group 2t+p;
+//              element 64t + 32p + 16hl + 8s + j (t = 2*half + t').
+//   Q6_K:      c = (v, s): element 128*half + 32v + 16hl + 8s + j, scale 8*half + 2v + hl.
+template <int T>
+__device__ __forceinline__ half8_t chunk_weights(const StepW<T>& s, int half, int hl, int c, int& koff) {
+    if constexpr (T == kQ4K || T == kQ5K) {
+        const int tp = c >> 2, p = (c >> 1) & 1, ss = c & 1;
+        const int t = 2 * half + tp;
+        const int g = 2 * t + p;
+        koff = 64 * tp + 32 * p + 16 * hl + 8 * ss;
+        const uint4 q = tp ? s.q1 : s.q0;
+        uint32_t lo = ss ? q.z : q.x;
+        uint32_t hi = ss ? q.w : q.y;
+        lo = (lo >> (4 * p)) & 0x0f0f0f0fu;
+        hi = (hi >> (4 * p)) & 0x0f0f0f0fu;
+        if constexpr (T == kQ5K) {
+            const uint32_t hlo = ss ? s.qh.z : s.qh.x;
+            const uint32_t hhi = ss ? s.qh.w : s.qh.y;
+            lo |= ((hlo >> g) & 0x01010101u) << 4;
+            hi |= ((hhi >> g) & 0x01010101u) << 4;
+        }
+        uint32_t sc, mn;
+        q4k_scale_min(s.h.y, s.h.z, s.h.w, g, sc, mn);
+        const float d = half_bits_to_float(s.h.x & 0xffffu);
+        const float dmin = half_bits_to_float(s.h.x >> 16);
+        return dequant8(lo, hi, d * (float)sc, dmin * (float)mn);
+    } else {
+        const int v = c >> 1, ss = c & 1;
+        koff = 32 * v + 16 * hl + 8 * ss;
+        const uint4 lw = funnel4((v & 1) ? s.l1 : s.l0, (v & 1) ? s.l1t : s.l0t, s.shift);
+        const uint4 hw = funnel4(s.qh, s.qht, s.shift);
+        const uint4 scw = funnel4(s.sc, s.sct, s.shift);
+        uint32_t lo = ss ? lw.z : lw.x;
+        uint32_t hi = ss ? lw.w : lw.y;
+        const uint32_t hlo = ss ? hw.z : hw.x;
+        const uint32_t hhi = ss ? hw.w : hw.y;
+        lo = ((lo >> (4 * (v >> 1))) & 0x0f0f0f0fu) | (((hlo >> (2 * v)) & 0x03030303u) << 4);
+        hi = ((hi >> (4 * (v >> 1))) & 0x0f0f0f0fu) | (((hhi >> (2 * v)) & 0x03030303u) << 4);
+        const int si = 8 * half + 2 * v + hl;  // scale byte
+        const uint32_t sw = si < 4 ? scw.x : si < 8 ? scw.y : si < 12 ? scw.z : scw.w;
+        const float a = half_bits_to_float(s.d16) * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu);
+        return dequant8(lo, hi, a, 32.f * a);
+    }
+}
+
+// ------------------------------------------------------------------- GEMM
+
+template <int T, int CB, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
+                                                           const _Float16* __restrict__ xh,
+                                                           const float* __restrict__ unscale, float* __restrict__ y,
+                                                           int M, int N, int K) {
+    constexpr int BB = BlockTraits<T>::bytes;
+    constexpr int TOK = 32 * CB;                      // tokens per workgroup
+    constexpr int THREADS = WAVES * 64;
+    constexpr int XCH = TOK * (kStepK / 8) / THREADS;  // 16-byte x chunks per thread per step
+    static_assert(XCH * THREADS == TOK * kStepK / 8, "x tile must split evenly");
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][TOK * kXRow];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int hl = lane >> 5;
+    const int n0 = blockIdx.x * 32 * WAVES + 32 * wave;
+    const int m0 = blockIdx.y * TOK;
+    const int nb = K >> 8;
+    const int steps = 2 * nb;
+    const int row = n0 + (lane & 31);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, wbytes);
+    const uint32_t row_off = row < N ? (uint32_t)row * (uint32_t)(nb * BB) : kGemmOutOfRange;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
+
+    // x tile chunk i of a step: token i / 16, 16-byte piece i % 16.
+    auto load_x = [&](uint4 (&buf)[XCH], int step) {
+#pragma unroll
+        for (int j = 0; j < XCH; ++j) {
+            const int i = threadIdx.x + THREADS * j;
+            const int tok = m0 + (i >> 4);
+            const uint32_t off = (tok < M && step < steps)
+                                     ? ((uint32_t)tok * (uint32_t)K + (uint32_t)step * kStepK + (i & 15) * 8) * 2u
+                                     : kGemmOutOfRange;
+            buf[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+        }
+    };
+    auto store_x = [&](const uint4 (&buf)[XCH], int slot) {
+#pragma unroll
+        for (int j = 0; j < XCH; ++j) {
+            const int i = threadIdx.x + THREADS * j;
+            *reinterpret_cast<uint4*>(&xs[slot][(i >> 4) * kXRow + (i & 15) * 8]) = buf[j];
+        }
+    };
+    auto w_off = [&](int step) {
+        return (row_off == kGemmOutOfRange || step >= steps) ? kGemmOutOfRange
+                                                              : row_off + (uint32_t)(step >> 1) * BB;
+    };
+
+    float16_v acc[CB];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) acc[c] = float16_v{};
+
+    // Prologue: x for step 0 first (waited for below), then the weights of
+    // steps 0 and 1 (a three-slot ring, two steps ahead).
+    uint4 xbuf[XCH];
+    load_x(xbuf, 0);
+    asm volatile("" ::: "memory");
+    StepW<T> wring[3];
+    load_step<T>(wring[0], wr, w_off(0), 0, hl);
+    load_step<T>(wring[1], wr, w_off(1), 1, hl);
+    store_x(xbuf, 0);
+    __syncthreads();
+
+    // Steps run in threes so the ring slot of each is static; the padding
+    // steps past K load out of range (zeros) and skip the MFMAs.
+    const int padded = (steps + 2) / 3 * 3;
+    for (int s0 = 0; s0 < padded; s0 += 3) {
+#pragma unroll
+        for (int r = 0; r < 3; ++r) {
+            const int step = s0 + r;
+            load_x(xbuf, step + 1);
+            load_step<T>(wring[(r + 2) % 3], wr, w_off(step + 2), (step + 2) & 1, hl);
+            if (step < steps) {
+                const int half = step & 1;
+                const _Float16* xt = &xs[step & 1][(lane & 31) * kXRow];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    int koff;
+                    const half8_t a = chunk_weights<T>(wring[r], half, hl, c, koff);
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) {
+                        const half8_t b = *reinterpret_cast<const half8_t*>(xt + cb * 32 * kXRow + koff);
+                        acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[cb], 0, 0, 0);
+                    }
+                }
+            }
+            store_x(xbuf, (step + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // epilogue: C[n][m] -> y[m][n] * unscale[m]
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        const int m = m0 + 32 * cb + (lane & 31);
+        if (m >= M) continue;
+        const float us = unscale[m];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 8 * j + 4 * hl;
+            float4 o;
+            o.x = acc[cb][4 * j + 0] * us;
+            o.y = acc[cb][4 * j + 1] * us;
+            o.z = acc[cb][4 * j + 2] * us;
+            o.w = acc[cb][4 * j + 3] * us;
+            float* dst = y + (size_t)m * N + n;
+            if (n + 3 < N) {
+                *reinterpret_cast<float4*>(dst) = o;
+            } else {
+                if (n < N) dst[0] = o.x;
+                if (n + 1 < N) dst[1] = o.y;
+                if (n + 2 < N) dst[2] = o.z;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- launchers
+
+size_t gemm_workspace_bytes(size_t tokens, size_t K) {
+    // f16 activations + one f32 unscale per token, each region 256-byte aligned
+    const size_t xbytes = (tokens * K * 2 + 255) & ~(size_t)255;
+    return xbytes + ((tokens * 4 + 255) & ~(size_t)255);
+}
+
+hipError_t launch_act_f16(bool bf16_in, const void* x, const float* gamma, float eps, int M, int K, void* workspace,
+                          hipStream_t stream) {
+    _Float16* xh = static_cast<_Float16*>(workspace);
+    float* us = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                         ((((size_t)M * K * 2) + 255) & ~(size_t)255));
+    if (bf16_in) {
+        if (gamma) hipLaunchKernelGGL((act_f16_kernel<true, true>), dim3(M), dim3(kActThreads), 0, stream, x, gamma, eps, K, xh, us);
+        else hipLaunchKernelGGL((act_f16_kernel<true, false>), dim3(M), dim3(kActThreads), 0, stream, x, gamma, eps, K, xh, us);
+    } else {
+        if (gamma) hipLaunchKernelGGL((act_f16_kernel<false, true>), dim3(M), dim3(kActThreads), 0, stream, x, gamma, eps, K, xh, us);
+        else hipLaunchKernelGGL((act_f16_kernel<false, false>), dim3(M), dim3(kActThreads), 0, stream, x, gamma, eps, K, xh, us);
+    }
+    return hipGetLastError();
+}
+
+template <int T, int CB, int WAVES>
+static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, const void* workspace, float* y, int M, int N,
+                                 int K, hipStream_t stream) {
+    const _Float16* xh = static_cast<const _Float16*>(workspace);
+    const float* us = reinterpret_cast<const float*>(static_cast<const uint8_t*>(workspace) +
+                                                     ((((size_t)M * K * 2) + 255) & ~(size_t)255));
+    const dim3 grid((N + 32 * WAVES - 1) / (32 * WAVES), (M + 32 * CB - 1) / (32 * CB));
+    hipLaunchKernelGGL((qgemm_kernel<T, CB, WAVES>), grid, dim3(WAVES * 64), 0, stream, w, wbytes, xh, us, y, M, N, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_qgemm(int value_type, const uint8_t* w, uint32_t wbytes, const void* workspace, float* y, int M,
+                        int N, int K, hipStream_t stream) {
+    switch (value_type) {
+    case kQ4K: return launch_qgemm_t<kQ4K, 4, 4>(w, wbytes, workspace, y, M, N, K, stream);
+    case kQ5K: return launch_qgemm_t<kQ5K, 4, 4>(w, wbytes, workspace, y, M, N, K, stream);
+    case kQ6K: return launch_qgemm_t<kQ6K, 4, 4>(w, wbytes, workspace, y, M, N, K, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace ribn_amd

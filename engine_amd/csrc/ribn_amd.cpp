@@ -20,6 +20,8 @@ struct ribn_amd_context {
     hipStream_t stream;
     bool owns_stream;
     int cu_count;
+    void* workspace;  // prefill activation workspace (ribn_amd_context_reserve_prefill)
+    size_t workspace_bytes;
 };
 
 struct ribn_amd_quantized_weight {
@@ -252,7 +254,7 @@ ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_
     hipDeviceProp_t prop;
     hipError_t e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return driver(e, "hipGetDeviceProperties");
-    auto* ctx = new (std::nothrow) ribn_amd_context{device, stream, owns, prop.multiProcessorCount};
+    auto* ctx = new (std::nothrow) ribn_amd_context{device, stream, owns, prop.multiProcessorCount, nullptr, 0};
     if (!ctx) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
     *out = ctx;
     return ok();
@@ -285,6 +287,7 @@ const char* ribn_amd_status_name(int32_t status) {
     case RIBN_AMD_INVALID_ARGUMENT: return "InvalidArgument";
     case RIBN_AMD_EMPTY_ENCODING: return "EmptyEncoding";
     case RIBN_AMD_SOURCE_INCOMPLETE: return "SourceIncomplete";
+    case RIBN_AMD_WORKSPACE_TOO_SMALL: return "WorkspaceTooSmall";
     default: return "Unknown";
     }
 }
@@ -331,12 +334,44 @@ ribn_amd_status ribn_amd_context_wrap_stream(int32_t device, void* hip_stream, r
 
 void ribn_amd_context_destroy(ribn_amd_context* ctx) {
     if (!ctx) return;
+    DeviceGuard guard(ctx->device);
+    if (ctx->workspace) {
+        hipStreamSynchronize(ctx->stream);
+        hipFree(ctx->workspace);
+    }
     if (ctx->owns_stream) {
-        DeviceGuard guard(ctx->device);
         hipStreamSynchronize(ctx->stream);
         hipStreamDestroy(ctx->stream);
     }
     delete ctx;
+}
+
+size_t ribn_amd_gemm_workspace_bytes(size_t tokens, size_t k) { return ribn_amd::gemm_workspace_bytes(tokens, k); }
+
+ribn_amd_status ribn_amd_context_reserve_prefill(ribn_amd_context* ctx, size_t max_tokens, size_t max_k) {
+    if (!ctx) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null context");
+    if (max_tokens == 0 || max_k == 0 || max_k > (size_t)ribn_amd::kGemmMaxK || max_k % 256 != 0 ||
+        max_tokens > (size_t)std::numeric_limits<int>::max() / max_k) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kGemmMaxK, max_k,
+                    "prefill workspace needs 1 <= tokens, K a multiple of 256 up to %d, tokens*K < 2^31",
+                    ribn_amd::kGemmMaxK);
+    }
+    const size_t need = ribn_amd::gemm_workspace_bytes(max_tokens, max_k);
+    if (need <= ctx->workspace_bytes) return ok();
+    DeviceGuard guard(ctx->device);
+    if (ctx->workspace) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return driver(e, "hipStreamSynchronize");
+        hipFree(ctx->workspace);
+        ctx->workspace = nullptr;
+        ctx->workspace_bytes = 0;
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, need);
+    if (e != hipSuccess) return driver(e, "hipMalloc prefill workspace");
+    ctx->workspace = p;
+    ctx->workspace_bytes = need;
+    return ok();
 }
 
 ribn_amd_status ribn_amd_context_synchronize(ribn_amd_context* ctx) {
@@ -673,6 +708,54 @@ ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv* g, const ribn_amd_quantized_w
     hipError_t e = ribn_amd::launch_dequant((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, output,
                                             (uint32_t)(k / 256 * n), g->ctx->stream);
     if (e != hipSuccess) return driver(e, "launch dequantize");
+    return ok();
+}
+
+// ------------------------------------------------------------ prefill GEMM
+
+ribn_amd_status ribn_amd_gemm_prefill(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const void* input,
+                                      uint32_t input_dtype, size_t input_len, size_t members, const float* gamma,
+                                      size_t gamma_len, float epsilon, float* output, size_t output_len) {
+    if (input_dtype != RIBN_AMD_F32 && input_dtype != RIBN_AMD_BF16) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, RIBN_AMD_BF16, input_dtype, "input dtype %u is neither f32 nor bf16",
+                    input_dtype);
+    }
+    uint64_t k, n;
+    // Pointer checks take f32 alignment for either dtype; rows of bf16 input
+    // are read one element at a time.
+    ribn_amd_status st = validate_launch(g, w, static_cast<const float*>(input), input_len, output, output_len,
+                                         members, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    if (members == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "prefill needs at least one token");
+    if (gamma != nullptr) {
+        st = check_device_ptr(g->ctx, gamma, "gamma");
+        if (st != RIBN_AMD_OK) return st;
+        if (gamma_len != k) {
+            return fail(RIBN_AMD_WEIGHT_LENGTH, k, gamma_len, "RMSNorm weight has %zu values, expected %llu",
+                        gamma_len, (unsigned long long)k);
+        }
+        st = check_epsilon(epsilon);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    if (k > (uint64_t)ribn_amd::kGemmMaxK || members > (size_t)std::numeric_limits<int>::max() / k ||
+        n > (uint64_t)std::numeric_limits<int>::max() || w->encoded_bytes > 0xffffffffull) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kGemmMaxK, k,
+                    "prefill supports K up to %d and tokens*K < 2^31", ribn_amd::kGemmMaxK);
+    }
+    const size_t need = ribn_amd::gemm_workspace_bytes(members, k);
+    if (need > g->ctx->workspace_bytes) {
+        return fail(RIBN_AMD_WORKSPACE_TOO_SMALL, need, g->ctx->workspace_bytes,
+                    "prefill of %zu tokens x K=%llu needs %zu workspace bytes; reserve them with "
+                    "ribn_amd_context_reserve_prefill",
+                    members, (unsigned long long)k, need);
+    }
+    DeviceGuard guard(g->ctx->device);
+    hipError_t e = ribn_amd::launch_act_f16(input_dtype == RIBN_AMD_BF16, input, gamma, epsilon, (int)members, (int)k,
+                                            g->ctx->workspace, g->ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch prefill activation stage");
+    e = ribn_amd::launch_qgemm((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, g->ctx->workspace, output,
+                               (int)members, (int)n, (int)k, g->ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch prefill matmul");
     return ok();
 }
 

@@ -94,6 +94,10 @@ class AmdContext:
     def synchronize(self):
         _check(self._lib.ribn_amd_context_synchronize(self.handle))
 
+    def reserve_prefill(self, max_tokens: int, max_k: int):
+        """Set-up call: device workspace for prefill of up to max_tokens x max_k."""
+        _check(self._lib.ribn_amd_context_reserve_prefill(self.handle, max_tokens, max_k))
+
     def close(self):
         if self.handle and _live():
             self._lib.ribn_amd_context_destroy(self.handle)
@@ -253,6 +257,18 @@ class _AmdQuantizedGemv:
         gl = gamma.numel() if gamma is not None else 0
         _check(self._lib.ribn_amd_gemv_execute_group(self.handle, wh, n, _ptr(input), input.numel(), g, gl,
                                                      epsilon, oh, ol, members))
+
+    def gemm_prefill(self, weight, input, output, members: int, gamma=None, epsilon: float = 1e-6):
+        """y[members][N] = x[members][K] W^T on the matrix cores; x is f32 or bf16.
+        Needs AmdContext.reserve_prefill(members, K) beforehand."""
+        import torch
+        dtype = {torch.float32: 0, torch.bfloat16: 1}.get(input.dtype)
+        if dtype is None:
+            raise TypeError(f"prefill input must be float32 or bfloat16, got {input.dtype}")
+        g = _ptr(gamma) if gamma is not None else None
+        gl = gamma.numel() if gamma is not None else 0
+        _check(self._lib.ribn_amd_gemm_prefill(self.handle, weight.handle, _ptr(input), dtype, input.numel(), members,
+                                               g, gl, epsilon, _ptr(output), output.numel()))
 
     def dequantize(self, weight, output):
         _check(self._lib.ribn_amd_dequantize(self.handle, weight.handle, _ptr(output), output.numel()))

@@ -14,8 +14,8 @@ FETCH_SIZE and WRITE_SIZE are reported by rocprofv3 in KiB; with
 in the run (a device-to-device copy of N bytes reads N and writes N bytes) and
 prints the scale factor that maps the counter onto true bytes.
 
-`source-hash` prints the hash of the kernel sources, recorded in profile
-summaries so a stale measurement is recognisable.
+`source-hash` prints the hash of the decode GEMV's sources, recorded in
+profile summaries so a stale measurement is recognisable.
 """
 from __future__ import annotations
 
@@ -28,8 +28,8 @@ import sys
 from collections import defaultdict
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-KERNEL_SOURCES = ("csrc/gemv_wave.hip", "csrc/kquant_kernels.hip", "csrc/kquant_device.hpp",
-                  "csrc/kquant_launch.hpp")
+# The decode GEMV's sources (the kernel the roofline and traffic figures are about).
+KERNEL_SOURCES = ("csrc/gemv_wave.hip", "csrc/kquant_device.hpp", "csrc/kquant_launch.hpp")
 
 
 def source_hash() -> str:

@@ -46,6 +46,10 @@ extern "C" {
  * kernels at 8 (quantized.rs:12); this library serves decode batches up to 64. */
 #define RIBN_AMD_MAX_BATCH_MEMBERS 64u
 
+/* Activation element types accepted by ribn_amd_gemm_prefill. */
+#define RIBN_AMD_F32 0u
+#define RIBN_AMD_BF16 1u
+
 typedef enum ribn_amd_status {
     RIBN_AMD_OK = 0,
     RIBN_AMD_DRIVER = 1,                 /* Driver(String): a HIP runtime call failed */
@@ -62,6 +66,7 @@ typedef enum ribn_amd_status {
     RIBN_AMD_INVALID_ARGUMENT = 12,      /* null handle / misaligned pointer (no reference twin) */
     RIBN_AMD_EMPTY_ENCODING = 13,        /* CudaWeightError::EmptyEncoding (cuda.rs:335-337) */
     RIBN_AMD_SOURCE_INCOMPLETE = 14,     /* CudaWeightError::SourceIncomplete (cuda.rs:350-356) */
+    RIBN_AMD_WORKSPACE_TOO_SMALL = 15,   /* prefill workspace not reserved (no reference twin) */
 } ribn_amd_status;
 
 typedef struct ribn_amd_error {
@@ -199,6 +204,29 @@ ribn_amd_status ribn_amd_gemv_execute_group(ribn_amd_gemv *gemv, const ribn_amd_
  * the reference's device equivalent is the q4_k_embedding gather, q4_k.cu:1-67). */
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight, float *output,
                                     size_t output_len);
+
+/* ----------------------------------------------------------- prefill GEMM */
+
+/* Bytes of device workspace a prefill of `tokens` x K activations uses. */
+size_t ribn_amd_gemm_workspace_bytes(size_t tokens, size_t k);
+/* Reserves (grows, never shrinks) the context's prefill workspace for up to
+ * `max_tokens` tokens of K <= max_k. This is the only allocating call of the
+ * prefill path, made once at set-up like the reference's decode scratch
+ * (alloc_scratch / BatchScratch, decode.rs:1188-1216,1582-1617); execute calls
+ * that need more return WorkspaceTooSmall { expected: bytes needed, actual:
+ * bytes reserved }. Synchronises the context's stream if it replaces a buffer. */
+ribn_amd_status ribn_amd_context_reserve_prefill(ribn_amd_context *ctx, size_t max_tokens, size_t max_k);
+/* Prefill matmul (north-star prefill path, M >= 128; the reference runs
+ * prefill through gemv_batch, decode.rs:1516-1558): y[members][N] =
+ * x[members][K] W^T for a Q4_K/Q5_K/Q6_K weight, x in f32 or bf16
+ * (input_dtype), RMSNorm fused into the activation stage when gamma is not
+ * NULL. Weights are dequantised in registers and multiplied with f16 MFMA,
+ * accumulating in f32; within 1e-3 normwise relative error of the f32
+ * reference. K <= 16384. */
+ribn_amd_status ribn_amd_gemm_prefill(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
+                                      const void *input, uint32_t input_dtype, size_t input_len, size_t members,
+                                      const float *gamma, size_t gamma_len, float epsilon, float *output,
+                                      size_t output_len);
 
 /* ------------------------------------------------------------- embedding */
 

@@ -1,0 +1,145 @@
+"""GPU tests of the prefill matmul (bf16 MFMA-class path),
+called through the C ABI.
+
+Bar (north star): outputs within max relative error 1e-3 (normwise,
+gpu_helpers.RTOL) of the f32-accumulated oracle on the same inputs. bf16
+inputs are generated as bf16 values and handed to the oracle as the same
+values in f32, so the comparison isolates the kernel's own rounding.
+"""
+import numpy as np
+import pytest
+
+from engine_amd import synth
+from oracle import kquant_oracle as O
+
+from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    import engine_amd as E
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    ctx = E.AmdContext(0)
+    ctx.reserve_prefill(512, 12288)
+    store = E.AmdWeightStore(ctx)
+    kernels = {t: E.QwenGemvKernel.from_value_type(ctx, t) for t in (12, 13, 14)}
+    return {"E": E, "ctx": ctx, "store": store, "k": kernels, "n": [0]}
+
+
+def upload(env, t, k, n, enc):
+    env["n"][0] += 1
+    name = f"p{env['n'][0]}"
+    env["store"].materialize_quantized(name, [k, n], t, enc)
+    return env["store"].quantized_tensor(name)
+
+
+def bf16_values(x):
+    """Round f32 to bf16 (RNE) and return both the device bf16 tensor and the exact f32 values."""
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16)
+    return t.to("cuda:0"), t.to(torch.float32).numpy()
+
+
+def oracle_rows(t, enc, k, n, x, threads=1):
+    return np.stack([O.quant_gemv(t, enc, k, n, x[m], threads=threads) for m in range(x.shape[0])])
+
+
+@pytest.mark.parametrize("t", (12, 13, 14))
+@pytest.mark.parametrize("k,n,m", [(256, 32, 1), (512, 96, 40), (1024, 200, 130), (2304, 128, 257)])
+@pytest.mark.parametrize("dtype", ("f32", "bf16"))
+def test_prefill_against_oracle(env, t, k, n, m, dtype):
+    print("CASE prefill", t, k, n, m, dtype, flush=True)
+    enc = synth.kquant_numpy(t, k, n, seed=k + n + t)
+    w = upload(env, t, k, n, enc)
+    x = synth.activations_numpy(k, m, seed=m + 3)
+    if dtype == "bf16":
+        xd, x = bf16_values(x)
+    else:
+        xd = to_dev(x)
+    y = empty_dev(m * n)
+    env["k"][t].gemm_prefill(w, xd, y, m)
+    got = to_host(y, env["ctx"]).reshape(m, n)
+    ref = oracle_rows(t, enc, k, n, x)
+    assert max_rel_err(got, ref) <= RTOL
+
+
+@pytest.mark.parametrize("t", (12, 14))
+def test_prefill_fused_rms_norm(env, t):
+    k, n, m = 1024, 160, 48
+    print("CASE prefill rmsnorm", t, flush=True)
+    enc = synth.kquant_numpy(t, k, n, seed=77 + t)
+    w = upload(env, t, k, n, enc)
+    x = synth.activations_numpy(k, m, seed=5) * 3.0
+    gamma = synth.gamma_numpy(k, seed=6)
+    y = empty_dev(m * n)
+    env["k"][t].gemm_prefill(w, to_dev(x), y, m, gamma=to_dev(gamma), epsilon=1e-6)
+    got = to_host(y, env["ctx"]).reshape(m, n)
+    normed = np.stack([O.rms_norm_raw(x[i], gamma, 1e-6) for i in range(m)])
+    ref = oracle_rows(t, enc, k, n, normed)
+    assert max_rel_err(got, ref) <= RTOL
+
+
+@pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (14, 12288, 4096)])
+def test_prefill_config3_full_size(env, t, k, n):
+    # M = 512 bf16 tokens; the oracle checks a token sample
+    import torch
+    m = 512
+    print("CASE prefill config3", t, k, n, flush=True)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(31 + t)
+    enc_dev = synth.kquant_torch(t, k, n, gen, torch.device("cuda:0"))
+    w = upload(env, t, k, n, enc_dev)
+    x = synth.activations_numpy(k, m, seed=9)
+    xd, x = bf16_values(x)
+    y = empty_dev(m * n)
+    env["k"][t].gemm_prefill(w, xd, y, m)
+    got = to_host(y, env["ctx"]).reshape(m, n)
+    enc = enc_dev.cpu().numpy()
+    sample = [0, 1, 127, 128, 255, 300, 511]
+    ref = np.stack([O.quant_gemv(t, enc, k, n, x[i], threads=16) for i in sample])
+    assert max_rel_err(got[sample], ref) <= RTOL
+    assert np.all(np.isfinite(got))
+
+
+def test_prefill_matches_wave_gemv_rows(env):
+    # the two paths agree on the same tokens (both within tolerance of f32)
+    k, n, m = 4096, 512, 8
+    print("CASE prefill vs wave", flush=True)
+    enc = synth.kquant_numpy(12, k, n, seed=123)
+    w = upload(env, 12, k, n, enc)
+    x = synth.activations_numpy(k, m, seed=124)
+    y1 = empty_dev(m * n)
+    env["k"][12].gemm_prefill(w, to_dev(x), y1, m)
+    y2 = empty_dev(m * n)
+    env["k"][12].execute_warp_batch(w, to_dev(x), y2, m)
+    a = to_host(y1, env["ctx"])
+    b = to_host(y2, env["ctx"])
+    assert max_rel_err(a, b) <= 2 * RTOL
+
+
+def test_prefill_validation(env):
+    E = env["E"]
+    k, n = 512, 64
+    enc = synth.kquant_numpy(12, k, n, seed=1)
+    w = upload(env, 12, k, n, enc)
+    kern = env["k"][12]
+    x = to_dev(synth.activations_numpy(k, 4, seed=2))
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        kern.gemm_prefill(w, x, empty_dev(4 * n + 1), 4)
+    assert e.value.kind == "OutputLength" and (e.value.expected, e.value.actual) == (4 * n, 4 * n + 1)
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        kern.gemm_prefill(w, x, empty_dev(4 * n), 4, gamma=to_dev(np.ones(k - 256, np.float32)))
+    assert e.value.kind == "WeightLength" and (e.value.expected, e.value.actual) == (k, k - 256)
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        kern.gemm_prefill(w, x, empty_dev(4 * n), 4, gamma=to_dev(np.ones(k, np.float32)), epsilon=0.0)
+    assert e.value.kind == "InvalidEpsilon"
+    # a context without a reserved workspace reports the bytes it needs
+    ctx2 = E.AmdContext(0)
+    kern2 = E.QwenGemvKernel.from_value_type(ctx2, 12)
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        kern2.gemm_prefill(w, x, empty_dev(4 * n), 4)
+    assert e.value.kind == "WorkspaceTooSmall" and e.value.actual == 0
+    assert e.value.expected == E._lib.load().ribn_amd_gemm_workspace_bytes(4, k)
