@@ -275,8 +275,9 @@ __device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneAc
 
 // ------------------------------------------------------------------ kernel
 
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES>
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES, int GROUP>
 __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args) {
+    static_assert(NBUF % GROUP == 0, "the ring holds whole row groups");
     constexpr int kWaves = WAVES;
     constexpr int kThreads = WAVES * 64;
     constexpr int BB = BlockTraits<T>::bytes;
@@ -366,12 +367,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
     // wave waits for exactly the unit it reduces next.
     RowData<T> ring[NBUF];
     // Unit order: one slice of K = 4096 carries whole rows (row-major units);
-    // longer K goes in groups of NBUF rows, slice by slice, so ring slot r
-    // always holds row r of the group and the activations of a slice are read
-    // once per group.
+    // longer K goes in groups of GROUP rows, slice by slice (row-minor), so
+    // ring slot r always holds row r % GROUP of a group and the activations of
+    // a slice are read once per group. The ring spans NBUF / GROUP slices.
     int lrow = r_begin, lslice = 0;  // next unit to load (group base row when K spans slices)
     auto load_next = [&](RowData<T>& dst, int r) {
-        const int row = ONE_SLICE ? lrow : lrow + r;
+        const int row = ONE_SLICE ? lrow : lrow + r % GROUP;
         const bool live_row = row < r_end;
         int mat, local;
         locate(live_row ? row : r_begin, mat, local);
@@ -381,9 +382,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
         load_row<T>(dst, rs, live ? (uint32_t)local * row_bytes + (uint32_t)b * BB : kOutOfRange, p);
         if constexpr (ONE_SLICE) {
             ++lrow;
-        } else if (r == NBUF - 1 && ++lslice == slices) {
+        } else if (r % GROUP == GROUP - 1 && ++lslice == slices) {
             lslice = 0;
-            lrow += NBUF;
+            lrow += GROUP;
         }
     };
 #pragma unroll
@@ -501,18 +502,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
     // (other stores go to an out-of-range offset and are dropped), refill the
     // slot with the unit NBUF ahead.
     int crow = r_begin, cslice = 0;  // unit being reduced (group base row when K spans slices)
-    float acc[NBUF][MT];
+    constexpr int kAcc = ONE_SLICE ? 1 : GROUP;
+    float acc[kAcc][MT];
 #pragma unroll
-    for (int r = 0; r < NBUF; ++r)
+    for (int r = 0; r < kAcc; ++r)
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
     auto consume = [&](const RowData<T>& d, int r) {
         if constexpr (!ONE_SLICE) {
-            if (r == 0) read_act(cslice);
+            if (r % GROUP == 0) read_act(cslice);
         }
         float part[MT];
         row_dot<T, MT>(d, p, xa, part);
-        const int row = ONE_SLICE ? crow : crow + r;
+        const int ai = ONE_SLICE ? 0 : r % GROUP;
+        const int row = ONE_SLICE ? crow : crow + r % GROUP;
         const bool last = ONE_SLICE || cslice == slices - 1;
         int mat, local;
         locate(row < r_end ? row : r_begin, mat, local);
@@ -520,8 +523,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
         const __amdgpu_buffer_rsrc_t yr = pick_y(mat, rows_mat);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            acc[r][m] = (ONE_SLICE || cslice == 0) ? part[m] : acc[r][m] + part[m];
-            const float total = wave_sum_uniform(acc[r][m]) * inv[m];
+            acc[ai][m] = (ONE_SLICE || cslice == 0) ? part[m] : acc[ai][m] + part[m];
+            const float total = wave_sum_uniform(acc[ai][m]) * inv[m];
             const uint32_t off = (last && row < r_end && lane == 0 && m < members)
                                      ? (uint32_t)(m * rows_mat + local) * 4u
                                      : kOutOfRange;
@@ -529,16 +532,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
         }
         if constexpr (ONE_SLICE) {
             ++crow;
-        } else if (r == NBUF - 1 && ++cslice == slices) {
+        } else if (r % GROUP == GROUP - 1 && ++cslice == slices) {
             cslice = 0;
-            crow += NBUF;
+            crow += GROUP;
         }
     };
 
     const int rows_w = r_end - r_begin;
     // Passes of NBUF units; a partial last group (K spanning slices) runs on
     // zero-filled loads and stores nothing.
-    const int passes = ONE_SLICE ? (rows_w + NBUF - 1) / NBUF : (rows_w + NBUF - 1) / NBUF * slices;
+    const int units = ONE_SLICE ? rows_w : (rows_w + GROUP - 1) / GROUP * GROUP * slices;
+    const int passes = (units + NBUF - 1) / NBUF;
     for (int pass = 0; pass + 1 < passes; ++pass) {
 #pragma unroll
         for (int r = 0; r < NBUF; ++r) {
@@ -547,7 +551,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
         }
     }
     if (passes > 0) {
-        const int left = ONE_SLICE ? rows_w - (passes - 1) * NBUF : NBUF;
+        const int left = units - (passes - 1) * NBUF;
 #pragma unroll
         for (int r = 0; r < NBUF; ++r) {
             if (r < left) consume(ring[r], r);
@@ -564,13 +568,13 @@ static size_t act_lds_bytes(int members, int K) {
     return (size_t)members * slices * 64 * ActTraits<T>::stride * sizeof(uint32_t);
 }
 
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES>
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES, int GROUP = 1>
 struct WaveInstance {
     static std::atomic<int> occupancy;  // resident workgroups per CU at the largest LDS size (0: not queried)
     // Launches `per_cu` workgroups on every CU (capped by occupancy; fewer
     // when the problem has fewer than two units per wave).
     static hipError_t launch(const WaveGemvArgs& a, int cu_count, int per_cu, hipStream_t stream) {
-        auto kern = gemv_wave_kernel<T, MT, NORM, ONE_SLICE, NBUF, WAVES>;
+        auto kern = gemv_wave_kernel<T, MT, NORM, ONE_SLICE, NBUF, WAVES, GROUP>;
         const size_t lds = act_lds_bytes<T>(MT, a.K);
         int occ = occupancy.load(std::memory_order_relaxed);
         if (occ == 0) {
@@ -596,8 +600,8 @@ struct WaveInstance {
         return hipGetLastError();
     }
 };
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES>
-std::atomic<int> WaveInstance<T, MT, NORM, ONE_SLICE, NBUF, WAVES>::occupancy{0};
+template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES, int GROUP>
+std::atomic<int> WaveInstance<T, MT, NORM, ONE_SLICE, NBUF, WAVES, GROUP>::occupancy{0};
 
 // Launch shape by units (row x slice) per CU, from sweeps on MI355X over
 // workgroup size {2,4,8,16} waves x ring depth {2,4,8} x workgroups per CU
@@ -613,6 +617,11 @@ static hipError_t launch_ring(const WaveGemvArgs& a, int cu_count, hipStream_t s
             if constexpr (T == kQ6K) return WaveInstance<T, MT, NORM, ONE_SLICE, 8, 4>::launch(a, cu_count, 1, stream);
             return WaveInstance<T, MT, NORM, ONE_SLICE, 4, 8>::launch(a, cu_count, 4, stream);
         }
+    }
+    if constexpr (!ONE_SLICE) {
+        // K spanning slices: pairs of rows, slice by slice (deeper rings
+        // measured slower for the 12288-wide down projection).
+        return WaveInstance<T, MT, NORM, ONE_SLICE, 2, 8, 2>::launch(a, cu_count, 1, stream);
     }
     return WaveInstance<T, MT, NORM, ONE_SLICE, 2, 8>::launch(a, cu_count, per_cu > 48 ? 2 : 1, stream);
 }

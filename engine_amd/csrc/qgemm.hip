@@ -13,10 +13,11 @@
 //  - qgemm_kernel: a workgroup of WAVES waves owns 32*WAVES weight rows and
 //    32*CB tokens; wave w owns rows [32w, 32w+32) of the tile. K advances in
 //    half super-blocks (128 elements): the x tile [32*CB][128] f16 is staged
-//    in LDS (padded rows, double-buffered, prefetched through registers one
-//    step ahead), weights are loaded per lane straight from HBM (two steps
-//    ahead) and dequantised in f32, (d*sc)*q - dmin*m, then rounded once to
-//    f16 (RNE) in the A-operand layout. Each A fragment feeds CB MFMAs.
+//    in LDS (padded rows, double-buffered; a step's tile is loaded into
+//    registers two steps ahead and written to LDS one step ahead), weights are
+//    loaded per lane straight from HBM (three steps ahead) and dequantised in
+//    f32, (d*sc)*q - dmin*m, then rounded once to f16 (RNE) in the A-operand
+//    layout. Each A fragment feeds CB MFMAs.
 //
 // MFMA 32x32x16 operand layout (measured on gfx950): lane l holds
 // A[l%32][8*(l/32)+j], B[8*(l/32)+j][l%32] (j = 0..7) and
@@ -29,6 +30,7 @@
 #include "kquant_launch.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace ribn_amd {
 
@@ -163,6 +165,9 @@ __device__ __forceinline__ uint4 funnel4(uint4 a, uint32_t t, uint32_t sh) {
 // Eight f16 weights (a*q_j - b), q_j = byte j of (lo, hi) after masking
 // (byte-to-float converts are single v_cvt_f32_ubyteN instructions).
 __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float a, float b) {
+    // Opaque to the optimiser, so each byte converts with one v_cvt_f32_ubyteN
+    // instead of a bit-field extract plus a convert.
+    asm volatile("" : "+v"(lo), "+v"(hi));
     float w[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -180,54 +185,79 @@ __device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float a, f
     return h;
 }
 
-// Chunk c (0..7) of a step: the lane's 8 weights and the k offset (within the
-// 128-element step) of the 8 activations they multiply.
-//   Q4_K/Q5_K: c = (t', p, s): payload bytes 32t+16hl+8s+j, nibble p, group 2t+p;
-//              element 64t + 32p + 16hl + 8s + j (t = 2*half + t').
-//   Q6_K:      c = (v, s): element 128*half + 32v + 16hl + 8s + j, scale 8*half + 2v + hl.
-template <int T>
-__device__ __forceinline__ half8_t chunk_weights(const StepW<T>& s, int half, int hl, int c, int& koff) {
+// A step's weights decoded once: scale and offset of each scale group the
+// lane touches, and (Q6_K) the payload windows realigned.
+template <int T> struct StepDec;
+template <> struct StepDec<kQ4K> { float a[4], b[4]; };
+template <> struct StepDec<kQ5K> { float a[4], b[4]; };
+template <> struct StepDec<kQ6K> { float a[4]; uint4 l0, l1, qh; };
+
+template <int T, int HALF>
+__device__ __forceinline__ void decode_step(const StepW<T>& s, int hl, StepDec<T>& o) {
     if constexpr (T == kQ4K || T == kQ5K) {
-        const int tp = c >> 2, p = (c >> 1) & 1, ss = c & 1;
-        const int t = 2 * half + tp;
-        const int g = 2 * t + p;
-        koff = 64 * tp + 32 * p + 16 * hl + 8 * ss;
-        const uint4 q = tp ? s.q1 : s.q0;
-        uint32_t lo = ss ? q.z : q.x;
-        uint32_t hi = ss ? q.w : q.y;
-        lo = (lo >> (4 * p)) & 0x0f0f0f0fu;
-        hi = (hi >> (4 * p)) & 0x0f0f0f0fu;
-        if constexpr (T == kQ5K) {
-            const uint32_t hlo = ss ? s.qh.z : s.qh.x;
-            const uint32_t hhi = ss ? s.qh.w : s.qh.y;
-            lo |= ((hlo >> g) & 0x01010101u) << 4;
-            hi |= ((hhi >> g) & 0x01010101u) << 4;
-        }
-        uint32_t sc, mn;
-        q4k_scale_min(s.h.y, s.h.z, s.h.w, g, sc, mn);
+        // groups 4*HALF + i, i = 2t' + p; six-bit scales/minima (lib.rs:573-587)
         const float d = half_bits_to_float(s.h.x & 0xffffu);
         const float dmin = half_bits_to_float(s.h.x >> 16);
-        return dequant8(lo, hi, d * (float)sc, dmin * (float)mn);
+        const uint32_t scw = HALF ? ((s.h.w & 0x0f0f0f0fu) | ((s.h.y >> 2) & 0x30303030u)) : (s.h.y & 0x3f3f3f3fu);
+        const uint32_t mnw = HALF ? (((s.h.w >> 4) & 0x0f0f0f0fu) | ((s.h.z >> 2) & 0x30303030u))
+                                  : (s.h.z & 0x3f3f3f3fu);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o.a[i] = d * (float)((scw >> (8 * i)) & 0xffu);
+            o.b[i] = dmin * (float)((mnw >> (8 * i)) & 0xffu);
+        }
     } else {
-        const int v = c >> 1, ss = c & 1;
-        koff = 32 * v + 16 * hl + 8 * ss;
-        const uint4 lw = funnel4((v & 1) ? s.l1 : s.l0, (v & 1) ? s.l1t : s.l0t, s.shift);
-        const uint4 hw = funnel4(s.qh, s.qht, s.shift);
+        o.l0 = funnel4(s.l0, s.l0t, s.shift);
+        o.l1 = funnel4(s.l1, s.l1t, s.shift);
+        o.qh = funnel4(s.qh, s.qht, s.shift);
         const uint4 scw = funnel4(s.sc, s.sct, s.shift);
+        const float d = half_bits_to_float(s.d16);
+        // scale 8*HALF + 2v + hl: bytes hl and hl+2 of dwords 2*HALF (v = 0, 1) and 2*HALF+1 (v = 2, 3)
+        const uint32_t w0 = (HALF ? scw.z : scw.x) >> (8 * hl);
+        const uint32_t w1 = (HALF ? scw.w : scw.y) >> (8 * hl);
+        o.a[0] = d * (float)(int8_t)(w0 & 0xffu);
+        o.a[1] = d * (float)(int8_t)((w0 >> 16) & 0xffu);
+        o.a[2] = d * (float)(int8_t)(w1 & 0xffu);
+        o.a[3] = d * (float)(int8_t)((w1 >> 16) & 0xffu);
+    }
+}
+
+// Chunk C (0..7) of a step: the lane's 8 f16 weights and the k offset
+// (within the 128-element step) of the 8 activations they multiply.
+//   Q4_K/Q5_K: C = (t', p, s): payload bytes 32t+16hl+8s+j, nibble p, group 2t+p;
+//              element 64t' + 32p + 16hl + 8s + j of the step (t = 2*HALF + t').
+//   Q6_K:      C = (v, s): element 32v + 16hl + 8s + j of the step, scale 8*HALF + 2v + hl.
+template <int T, int HALF, int C>
+__device__ __forceinline__ half8_t chunk_weights(const StepW<T>& s, const StepDec<T>& dec, int hl, int& koff) {
+    if constexpr (T == kQ4K || T == kQ5K) {
+        constexpr int tp = C >> 2, p = (C >> 1) & 1, ss = C & 1;
+        constexpr int g = 4 * HALF + 2 * tp + p;
+        koff = 64 * tp + 32 * p + 16 * hl + 8 * ss;
+        const uint4 q = tp ? s.q1 : s.q0;
+        uint32_t lo = ((ss ? q.z : q.x) >> (4 * p)) & 0x0f0f0f0fu;
+        uint32_t hi = ((ss ? q.w : q.y) >> (4 * p)) & 0x0f0f0f0fu;
+        if constexpr (T == kQ5K) {
+            lo |= (((ss ? s.qh.z : s.qh.x) >> g) & 0x01010101u) << 4;
+            hi |= (((ss ? s.qh.w : s.qh.y) >> g) & 0x01010101u) << 4;
+        }
+        return dequant8(lo, hi, dec.a[2 * tp + p], dec.b[2 * tp + p]);
+    } else {
+        constexpr int v = C >> 1, ss = C & 1;
+        koff = 32 * v + 16 * hl + 8 * ss;
+        const uint4 lw = (v & 1) ? dec.l1 : dec.l0;
         uint32_t lo = ss ? lw.z : lw.x;
         uint32_t hi = ss ? lw.w : lw.y;
-        const uint32_t hlo = ss ? hw.z : hw.x;
-        const uint32_t hhi = ss ? hw.w : hw.y;
+        const uint32_t hlo = ss ? dec.qh.z : dec.qh.x;
+        const uint32_t hhi = ss ? dec.qh.w : dec.qh.y;
         lo = ((lo >> (4 * (v >> 1))) & 0x0f0f0f0fu) | (((hlo >> (2 * v)) & 0x03030303u) << 4);
         hi = ((hi >> (4 * (v >> 1))) & 0x0f0f0f0fu) | (((hhi >> (2 * v)) & 0x03030303u) << 4);
-        const int si = 8 * half + 2 * v + hl;  // scale byte
-        const uint32_t sw = si < 4 ? scw.x : si < 8 ? scw.y : si < 12 ? scw.z : scw.w;
-        const float a = half_bits_to_float(s.d16) * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xffu);
-        return dequant8(lo, hi, a, 32.f * a);
+        return dequant8(lo, hi, dec.a[v], 32.f * dec.a[v]);
     }
 }
 
 // ------------------------------------------------------------------- GEMM
+
+constexpr int kRing = 4;  // weight steps in flight per lane (the current one + three ahead)
 
 template <int T, int CB, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
@@ -282,42 +312,59 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __rest
     for (int c = 0; c < CB; ++c) acc[c] = float16_v{};
 
     // Prologue: x for step 0 first (waited for below), then the weights of
-    // steps 0 and 1 (a three-slot ring, two steps ahead).
+    // steps 0..2 (a four-slot ring, three steps ahead).
     uint4 xbuf[XCH];
     load_x(xbuf, 0);
     asm volatile("" ::: "memory");
-    StepW<T> wring[3];
-    load_step<T>(wring[0], wr, w_off(0), 0, hl);
-    load_step<T>(wring[1], wr, w_off(1), 1, hl);
+    StepW<T> wring[kRing];
+#pragma unroll
+    for (int r = 0; r < kRing - 1; ++r) load_step<T>(wring[r], wr, w_off(r), r & 1, hl);
     store_x(xbuf, 0);
+    load_x(xbuf, 1);
     __syncthreads();
 
-    // Steps run in threes so the ring slot of each is static; the padding
-    // steps past K load out of range (zeros) and skip the MFMAs.
-    const int padded = (steps + 2) / 3 * 3;
-    for (int s0 = 0; s0 < padded; s0 += 3) {
+    // Steps run in fours so each one's ring slot and block half are static;
+    // padding steps past K load out of range (zeros) and skip the MFMAs.
+    auto run_step = [&](auto r_const, int s0) {
+        constexpr int r = decltype(r_const)::value;
+        constexpr int HALF = r & 1;
+        const int step = s0 + r;
+        // x of step+1 (loaded a step ago) into the other LDS slot, which every
+        // wave finished reading before the last barrier; then x two steps ahead.
+        store_x(xbuf, (r + 1) & 1);
+        load_x(xbuf, step + 2);
+        load_step<T>(wring[(r + kRing - 1) % kRing], wr, w_off(step + kRing - 1), (r + kRing - 1) & 1, hl);
+        if (step < steps) {
+            StepDec<T> dec;
+            decode_step<T, HALF>(wring[r], hl, dec);
+            const _Float16* xt = &xs[r & 1][(lane & 31) * kXRow];
+            auto chunk = [&](auto c_const) {
+                constexpr int C = decltype(c_const)::value;
+                int koff;
+                const half8_t a = chunk_weights<T, HALF, C>(wring[r], dec, hl, koff);
 #pragma unroll
-        for (int r = 0; r < 3; ++r) {
-            const int step = s0 + r;
-            load_x(xbuf, step + 1);
-            load_step<T>(wring[(r + 2) % 3], wr, w_off(step + 2), (step + 2) & 1, hl);
-            if (step < steps) {
-                const int half = step & 1;
-                const _Float16* xt = &xs[step & 1][(lane & 31) * kXRow];
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    int koff;
-                    const half8_t a = chunk_weights<T>(wring[r], half, hl, c, koff);
-#pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
-                        const half8_t b = *reinterpret_cast<const half8_t*>(xt + cb * 32 * kXRow + koff);
-                        acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[cb], 0, 0, 0);
-                    }
+                for (int cb = 0; cb < CB; ++cb) {
+                    const half8_t b = *reinterpret_cast<const half8_t*>(xt + cb * 32 * kXRow + koff);
+                    acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[cb], 0, 0, 0);
                 }
-            }
-            store_x(xbuf, (step + 1) & 1);
-            __syncthreads();
+            };
+            chunk(std::integral_constant<int, 0>{});
+            chunk(std::integral_constant<int, 1>{});
+            chunk(std::integral_constant<int, 2>{});
+            chunk(std::integral_constant<int, 3>{});
+            chunk(std::integral_constant<int, 4>{});
+            chunk(std::integral_constant<int, 5>{});
+            chunk(std::integral_constant<int, 6>{});
+            chunk(std::integral_constant<int, 7>{});
         }
+        __syncthreads();
+    };
+    const int padded = (steps + kRing - 1) / kRing * kRing;
+    for (int s0 = 0; s0 < padded; s0 += kRing) {
+        run_step(std::integral_constant<int, 0>{}, s0);
+        run_step(std::integral_constant<int, 1>{}, s0);
+        run_step(std::integral_constant<int, 2>{}, s0);
+        run_step(std::integral_constant<int, 3>{}, s0);
     }
 
     // epilogue: C[n][m] -> y[m][n] * unscale[m]
@@ -380,12 +427,23 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, const void* 
     return hipGetLastError();
 }
 
+// Tile by token count: few tokens take small tiles (more workgroups for the
+// weight stream); many tokens take 128x128 tiles (each dequantised weight
+// fragment feeds four MFMAs).
+template <int T>
+static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, const void* workspace, float* y, int M, int N,
+                                 int K, hipStream_t stream) {
+    if (M <= 32) return launch_qgemm_t<T, 1, 1>(w, wbytes, workspace, y, M, N, K, stream);
+    if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, y, M, N, K, stream);
+    return launch_qgemm_t<T, 4, 4>(w, wbytes, workspace, y, M, N, K, stream);
+}
+
 hipError_t launch_qgemm(int value_type, const uint8_t* w, uint32_t wbytes, const void* workspace, float* y, int M,
                         int N, int K, hipStream_t stream) {
     switch (value_type) {
-    case kQ4K: return launch_qgemm_t<kQ4K, 4, 4>(w, wbytes, workspace, y, M, N, K, stream);
-    case kQ5K: return launch_qgemm_t<kQ5K, 4, 4>(w, wbytes, workspace, y, M, N, K, stream);
-    case kQ6K: return launch_qgemm_t<kQ6K, 4, 4>(w, wbytes, workspace, y, M, N, K, stream);
+    case kQ4K: return launch_qgemm_m<kQ4K>(w, wbytes, workspace, y, M, N, K, stream);
+    case kQ5K: return launch_qgemm_m<kQ5K>(w, wbytes, workspace, y, M, N, K, stream);
+    case kQ6K: return launch_qgemm_m<kQ6K>(w, wbytes, workspace, y, M, N, K, stream);
     default: return hipErrorInvalidValue;
     }
 }
