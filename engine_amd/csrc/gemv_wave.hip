@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 namespace ribn_amd {
 
@@ -461,40 +462,97 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
         }
     }
 
+    // One member's lane record of one slice, from LDS.
+    auto read_member = [&](LaneAct<T>& dst, int m, int slice) {
+        const uint32_t* src = xs + ((m * slices + slice) * 64 + lane) * STRIDE;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 a = *reinterpret_cast<const uint4*>(src + 4 * i);
+            const uint4 b = *reinterpret_cast<const uint4*>(src + 16 + 4 * i);
+            dst.h[4 * i + 0] = a.x;
+            dst.h[4 * i + 1] = a.y;
+            dst.h[4 * i + 2] = a.z;
+            dst.h[4 * i + 3] = a.w;
+            dst.l[4 * i + 0] = b.x;
+            dst.l[4 * i + 1] = b.y;
+            dst.l[4 * i + 2] = b.z;
+            dst.l[4 * i + 3] = b.w;
+        }
+        uint32_t prm[2 * G];
+#pragma unroll
+        for (int i = 0; i < 2 * G; i += 4) {
+            const uint4 a = *reinterpret_cast<const uint4*>(src + 32 + i);
+            prm[i] = a.x;
+            prm[i + 1] = a.y;
+            prm[i + 2] = a.z;
+            prm[i + 3] = a.w;
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            dst.unscale[g] = __builtin_bit_cast(float, prm[g]);
+            dst.xsum[g] = (float)(int)prm[G + g];
+            dst.xsum32[g] = -32 * (int)prm[G + g];
+        }
+    };
+
+    if constexpr (MT > 2) {
+        // ---- many members (K within one slice): member records stay in LDS.
+        // A pass runs over members (a real loop, one record live at a time):
+        // each member's record is read once and dotted with every unit of the
+        // ring, and its rows are reduced and stored at once; then the ring is
+        // refilled. The per-member arithmetic is the single-member kernel's,
+        // so each row is bit-identical to a one-member launch.
+        static_assert(ONE_SLICE, "the member-serial form covers one slice");
+        __shared__ float inv_s[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (threadIdx.x == m) inv_s[m] = inv[m];
+        }
+        __syncthreads();
+        int crow = r_begin;
+        auto pass = [&](auto refill_const, int left) {
+            constexpr bool REFILL = decltype(refill_const)::value;
+            int mat[NBUF], local[NBUF], rows_mat[NBUF];
+            __amdgpu_buffer_rsrc_t yr[NBUF];
+#pragma unroll
+            for (int r = 0; r < NBUF; ++r) {
+                const int row = crow + r;
+                locate(row < r_end ? row : r_begin, mat[r], local[r]);
+                yr[r] = pick_y(mat[r], rows_mat[r]);
+            }
+#pragma unroll 1
+            for (int m = 0; m < members; ++m) {
+                LaneAct<T> x1[1];
+                read_member(x1[0], m, 0);
+                const float im = inv_s[m];
+#pragma unroll
+                for (int r = 0; r < NBUF; ++r) {
+                    float pr[1];
+                    row_dot<T, 1>(ring[r], p, x1, pr);
+                    const float total = wave_sum_uniform(pr[0]) * im;
+                    const bool live = r < left && crow + r < r_end;
+                    const uint32_t off =
+                        (live && lane == 0) ? (uint32_t)(m * rows_mat[r] + local[r]) * 4u : kOutOfRange;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, total), yr[r], (int)off, 0, 0);
+                }
+            }
+            if constexpr (REFILL) {
+#pragma unroll
+                for (int r = 0; r < NBUF; ++r) load_next(ring[r], r);
+            }
+            crow += NBUF;
+        };
+        const int rows_w = r_end - r_begin;
+        const int passes = (rows_w + NBUF - 1) / NBUF;
+        for (int ps = 0; ps + 1 < passes; ++ps) pass(std::true_type{}, NBUF);
+        if (passes > 0) pass(std::false_type{}, rows_w - (passes - 1) * NBUF);
+        return;
+    }
+
     LaneAct<T> xa[MT];
     auto read_act = [&](int slice) {
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            const uint32_t* src = xs + ((m * slices + slice) * 64 + lane) * STRIDE;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint4 a = *reinterpret_cast<const uint4*>(src + 4 * i);
-                const uint4 b = *reinterpret_cast<const uint4*>(src + 16 + 4 * i);
-                xa[m].h[4 * i + 0] = a.x;
-                xa[m].h[4 * i + 1] = a.y;
-                xa[m].h[4 * i + 2] = a.z;
-                xa[m].h[4 * i + 3] = a.w;
-                xa[m].l[4 * i + 0] = b.x;
-                xa[m].l[4 * i + 1] = b.y;
-                xa[m].l[4 * i + 2] = b.z;
-                xa[m].l[4 * i + 3] = b.w;
-            }
-            uint32_t prm[2 * G];
-#pragma unroll
-            for (int i = 0; i < 2 * G; i += 4) {
-                const uint4 a = *reinterpret_cast<const uint4*>(src + 32 + i);
-                prm[i] = a.x;
-                prm[i + 1] = a.y;
-                prm[i + 2] = a.z;
-                prm[i + 3] = a.w;
-            }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                xa[m].unscale[g] = __builtin_bit_cast(float, prm[g]);
-                xa[m].xsum[g] = (float)(int)prm[G + g];
-                xa[m].xsum32[g] = -32 * (int)prm[G + g];
-            }
-        }
+        for (int m = 0; m < MT; ++m) read_member(xa[m], m, slice);
     };
     if constexpr (ONE_SLICE) read_act(0);
 
@@ -635,15 +693,18 @@ static hipError_t launch_tm(const WaveGemvArgs& a, int cu_count, hipStream_t str
 template <int T, bool NORM>
 static hipError_t launch_t(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
     if (a.members <= 1) return launch_tm<T, 1, NORM>(a, cu_count, stream);
-    return launch_tm<T, 2, NORM>(a, cu_count, stream);
+    if (a.members <= 2 || a.K > kSliceElems) return launch_tm<T, 2, NORM>(a, cu_count, stream);
+    // 3..8 members: member-serial passes over a four-unit ring
+    if (a.members <= 4) return WaveInstance<T, 4, NORM, true, 4, 8>::launch(a, cu_count, 1, stream);
+    return WaveInstance<T, 8, NORM, true, 4, 8>::launch(a, cu_count, 1, stream);
 }
 
 int wave_max_members(int K) {
     if (K > kWaveMaxK) return 0;
     const long long per_member = (long long)act_lds_bytes<kQ6K>(1, K);
     const long long fit = kWaveMaxLdsBytes / per_member;
-    if (fit >= 2) return 2;
-    return fit >= 1 ? 1 : 0;
+    const long long cap = K <= kSliceElems ? kWaveMaxMembers : 2;  // many members: one slice only
+    return (int)std::min<long long>(fit, cap);
 }
 
 hipError_t launch_gemv_wave(int value_type, const WaveGemvArgs& a, int cu_count, hipStream_t stream) {

@@ -6,9 +6,10 @@
 
 namespace ribn_amd {
 
-// Members one wave-GEMV launch accumulates (their activations live in registers);
-// larger batches are split by the host into launch groups.
-constexpr int kWaveMaxMembers = 2;
+// Members one wave-GEMV launch serves (weights read once for all of them);
+// larger batches are split by the host into launch groups. K above one slice
+// (4096) takes two members per launch.
+constexpr int kWaveMaxMembers = 8;
 // Weights one grouped wave-GEMV launch streams (they share one activation vector).
 constexpr int kMaxGroup = 4;
 // LDS the wave GEMV may use for its quantized [members][K] activation

@@ -301,6 +301,9 @@ def test_validation_errors(env):
                                                  (12, 4096, (12288, 12288), 1, True),
                                                  (12, 4096, (512, 96, 33), 3, True),
                                                  (13, 12288, (256, 100), 2, False),
+                                                 (12, 4096, (512, 96), 6, True),
+                                                 (14, 4096, (300, 40), 7, True),
+                                                 (13, 2048, (130,), 8, False),
                                                  (14, 2304, (77, 5, 64, 9), 1, False)])
 def test_grouped_launch_matches_separate(env, t, k, ns, members, norm):
     # one launch over weights sharing the input equals the per-weight launches bit for bit
