@@ -178,6 +178,135 @@ def cpu_baseline(seconds_budget=12.0):
     }
 
 
+PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense f16/bf16
+
+
+def _graph_time_us(torch, stream, fn, reps):
+    """Mean microseconds of fn() replayed as a HIP graph `reps` times on `stream`."""
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    with torch.cuda.stream(stream):
+        g.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            g.replay()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
+
+
+def bench_batched(E, synth, torch, args):
+    """the Qwen3-8B FFN (gate/up Q4_K 4096->12288, down Q5_K 12288->4096)
+    for M tokens. M <= 8 runs the weights-read-once wave GEMV (gate/up as one grouped launch);
+    larger M the matrix-core path. Activations are synthetic f32 ~N(0,1)."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    ctx = E.AmdContext(0, stream=stream)
+    ctx.reserve_prefill(64, FFN, FFN)
+    store = E.AmdWeightStore(ctx)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    layers = []
+    n_layers = 8  # 730 MB of distinct weights, ~3x the 256 MB Infinity Cache
+    for i in range(n_layers):
+        for name, t, k, n in (("gate", 12, HIDDEN, FFN), ("up", 12, HIDDEN, FFN), ("down", 13, FFN, HIDDEN)):
+            store.materialize_quantized(f"{name}{i}", [k, n], t, synth.kquant_torch(t, k, n, gen, dev))
+        layers.append({nm: store.quantized_tensor(f"{nm}{i}") for nm in ("gate", "up", "down")})
+    k4, k5 = E.AmdQ4KGemv.from_context(ctx), E.AmdQ5KGemv.from_context(ctx)
+    wbytes = 2 * (FFN * HIDDEN // 256 * 144) + HIDDEN * FFN // 256 * 176
+    per_m = {}
+    for m in (1, 4, 16, 64):
+        x = torch.randn(m, HIDDEN, device=dev, generator=gen)
+        h = torch.randn(m, FFN, device=dev, generator=gen)
+        g, u, d = (torch.empty(m * n, device=dev) for n in (FFN, FFN, HIDDEN))
+        if m <= 8:
+            path = "wave GEMV (weights read once per launch)"
+
+            def fn():
+                for ly in layers:
+                    k4.execute_group([ly["gate"], ly["up"]], x, [g, u], m)
+                    k5.execute_warp_batch(ly["down"], h, d, m)
+        else:
+            path = "matrix-core matmul (f16 MFMA)"
+
+            def fn():
+                for ly in layers:
+                    k4.gemm_prefill(ly["gate"], x, g, m)
+                    k4.gemm_prefill(ly["up"], x, u, m)
+                    k5.gemm_prefill(ly["down"], h, d, m)
+        us = _graph_time_us(torch, stream, fn, max(2, args.steps // 10)) / n_layers
+        per_m[m] = {"us_per_ffn": round(us, 2), "tokens_per_s": round(m * 1e6 / us, 1),
+                    "weight_GBps": round(wbytes / us / 1e3, 1),
+                    "tflops": round(2.0 * m * 3 * FFN * HIDDEN / us / 1e6, 2), "path": path}
+        log(f"bench batched: M={m} {us:.2f} us per FFN ({path})")
+    top = per_m[64]
+    return {
+        "metric": "batched decode FFN throughput (BASELINE config 2), tokens/s at M=64",
+        "value": top["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(top["us_per_ffn"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "i8dot4-f32 (M<=8), f16-mfma-f32 (M>8)", "data": "synthetic",
+        "config": {"workload": "qwen3-8b-ffn-batched", "ffn_weight_bytes": wbytes, "layers_cycled": n_layers,
+                   "per_m": per_m},
+        "roofline": {"bound": "hbm", "achieved": per_m[1]["weight_GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(per_m[1]["weight_GBps"] / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "M=1 FFN (gate/up group + down)"},
+        "cpu_baseline": None,
+    }
+
+
+def bench_prefill(E, synth, torch, args):
+    """M = 512 bf16 tokens against Q4_K 4096->12288 and Q6_K 12288->4096
+    (weights dequantised in registers, f16 MFMA, f32 accumulation)."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    ctx = E.AmdContext(0, stream=stream)
+    m = 512
+    ctx.reserve_prefill(m, FFN, FFN)
+    store = E.AmdWeightStore(ctx)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    copies = 4
+    shapes = (("q4k_4096x12288", 12, HIDDEN, FFN), ("q6k_12288x4096", 14, FFN, HIDDEN))
+    out = {}
+    total_flop, total_us = 0.0, 0.0
+    for label, t, k, n in shapes:
+        ws = []
+        for c in range(copies):
+            store.materialize_quantized(f"{label}{c}", [k, n], t, synth.kquant_torch(t, k, n, gen, dev))
+            ws.append(store.quantized_tensor(f"{label}{c}"))
+        kern = E.QwenGemvKernel.from_value_type(ctx, t)
+        x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+        y = torch.empty(m * n, device=dev)
+
+        def fn():
+            for w in ws:
+                kern.gemm_prefill(w, x, y, m)
+
+        us = _graph_time_us(torch, stream, fn, max(2, args.steps // 10)) / copies
+        flop = 2.0 * m * n * k
+        out[label] = {"us": round(us, 2), "tflops": round(flop / us / 1e6, 1)}
+        total_flop += flop
+        total_us += us
+        log(f"bench prefill: {label} M={m}: {us:.2f} us, {flop / us / 1e6:.1f} TFLOP/s")
+    achieved = total_flop / total_us / 1e6
+    return {
+        "metric": "prefill matmul TFLOP/s (BASELINE config 3, M=512 bf16)",
+        "value": round(achieved, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(total_us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16-mfma-f32", "data": "synthetic",
+        "config": {"workload": "prefill-m512", "shapes": out},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_MFMA_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None,
+                     "kernel": "qgemm_kernel (activation stage + matmul) over both shapes"},
+        "cpu_baseline": None,
+    }
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_wave_q4k_gate_up_traffic.md")
 
 
@@ -220,6 +349,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="issue launches eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workload", choices=("decode", "batched", "prefill"), default="decode",
+                    help="decode: BASELINE config 1 (the headline line, default); batched: config 2 "
+                         "(FFN at M = 1, 4, 16, 64); prefill: config 3 (M = 512 bf16 matmuls)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed work, copy a MIB-MiB device buffer three times: a kernel of known "
                          "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE onto bytes")
@@ -238,6 +370,10 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.workload != "decode":
+        result = (bench_batched if args.workload == "batched" else bench_prefill)(E, synth, torch, args)
+        print(json.dumps(result), flush=True)
+        return
     log(f"bench: generating {args.layers} layers + lm_head of synthetic weights on the device")
     weights, head, out_gamma, acts = build_model(E, synth, torch, args.layers, args.seed)
     stream = torch.cuda.Stream()

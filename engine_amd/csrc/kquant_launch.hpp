@@ -53,11 +53,13 @@ hipError_t launch_embedding(int value_type, const uint8_t* w, uint32_t wbytes, c
 // f16 workspace of gemm_workspace_bytes(M, K) bytes: launch_act_f16 fills it
 // (optionally RMSNorm-fused), launch_qgemm consumes it.
 constexpr int kGemmMaxK = 16384;
-size_t gemm_workspace_bytes(size_t tokens, size_t K);
+// The workspace layout covers the activations and up to eight split-K partial
+// [tokens][N] tiles; launch_qgemm splits K only as far as the space reserved.
+size_t gemm_workspace_bytes(size_t tokens, size_t K, size_t N);
 hipError_t launch_act_f16(bool bf16_in, const void* x, const float* gamma, float eps, int M, int K, void* workspace,
                           hipStream_t stream);
-hipError_t launch_qgemm(int value_type, const uint8_t* w, uint32_t wbytes, const void* workspace, float* y, int M,
-                        int N, int K, hipStream_t stream);
+hipError_t launch_qgemm(int value_type, const uint8_t* w, uint32_t wbytes, void* workspace, size_t workspace_bytes,
+                        float* y, int M, int N, int K, int cu_count, hipStream_t stream);
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* y, int length, int members, float eps,
                            hipStream_t stream);

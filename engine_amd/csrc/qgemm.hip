@@ -259,11 +259,15 @@ __device__ __forceinline__ half8_t chunk_weights(const StepW<T>& s, const StepDe
 
 constexpr int kRing = 4;  // weight steps in flight per lane (the current one + three ahead)
 
+// Split K: workgroup z covers steps [z*split_steps, (z+1)*split_steps) (a
+// multiple of the four-step unroll); with partial != null it writes its raw
+// tile to partial[z][M][N] and qgemm_reduce_kernel adds the splits in order.
 template <int T, int CB, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __restrict__ w, uint32_t wbytes,
                                                            const _Float16* __restrict__ xh,
                                                            const float* __restrict__ unscale, float* __restrict__ y,
-                                                           int M, int N, int K) {
+                                                           float* __restrict__ partial, int M, int N, int K,
+                                                           int split_steps) {
     constexpr int BB = BlockTraits<T>::bytes;
     constexpr int TOK = 32 * CB;                      // tokens per workgroup
     constexpr int THREADS = WAVES * 64;
@@ -277,7 +281,8 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __rest
     const int n0 = blockIdx.x * 32 * WAVES + 32 * wave;
     const int m0 = blockIdx.y * TOK;
     const int nb = K >> 8;
-    const int steps = 2 * nb;
+    const int s_begin = blockIdx.z * split_steps;
+    const int steps = min(2 * nb, s_begin + split_steps);  // end of this workgroup's steps
     const int row = n0 + (lane & 31);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, wbytes);
     const uint32_t row_off = row < N ? (uint32_t)row * (uint32_t)(nb * BB) : kGemmOutOfRange;
@@ -314,13 +319,13 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __rest
     // Prologue: x for step 0 first (waited for below), then the weights of
     // steps 0..2 (a four-slot ring, three steps ahead).
     uint4 xbuf[XCH];
-    load_x(xbuf, 0);
+    load_x(xbuf, s_begin);
     asm volatile("" ::: "memory");
     StepW<T> wring[kRing];
 #pragma unroll
-    for (int r = 0; r < kRing - 1; ++r) load_step<T>(wring[r], wr, w_off(r), r & 1, hl);
+    for (int r = 0; r < kRing - 1; ++r) load_step<T>(wring[r], wr, w_off(s_begin + r), r & 1, hl);
     store_x(xbuf, 0);
-    load_x(xbuf, 1);
+    load_x(xbuf, s_begin + 1);
     __syncthreads();
 
     // Steps run in fours so each one's ring slot and block half are static;
@@ -359,20 +364,21 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __rest
         }
         __syncthreads();
     };
-    const int padded = (steps + kRing - 1) / kRing * kRing;
-    for (int s0 = 0; s0 < padded; s0 += kRing) {
+    const int padded = s_begin + (steps - s_begin + kRing - 1) / kRing * kRing;
+    for (int s0 = s_begin; s0 < padded; s0 += kRing) {
         run_step(std::integral_constant<int, 0>{}, s0);
         run_step(std::integral_constant<int, 1>{}, s0);
         run_step(std::integral_constant<int, 2>{}, s0);
         run_step(std::integral_constant<int, 3>{}, s0);
     }
 
-    // epilogue: C[n][m] -> y[m][n] * unscale[m]
+    // epilogue: C[n][m] -> y[m][n] * unscale[m], or the raw split tile
+    float* out = partial ? partial + (size_t)blockIdx.z * M * N : y;
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
         const int m = m0 + 32 * cb + (lane & 31);
         if (m >= M) continue;
-        const float us = unscale[m];
+        const float us = partial ? 1.0f : unscale[m];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int n = n0 + 8 * j + 4 * hl;
@@ -381,7 +387,7 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __rest
             o.y = acc[cb][4 * j + 1] * us;
             o.z = acc[cb][4 * j + 2] * us;
             o.w = acc[cb][4 * j + 3] * us;
-            float* dst = y + (size_t)m * N + n;
+            float* dst = out + (size_t)m * N + n;
             if (n + 3 < N) {
                 *reinterpret_cast<float4*>(dst) = o;
             } else {
@@ -393,19 +399,34 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __rest
     }
 }
 
+// y[m][n] = unscale[m] * sum over splits z (in order) of partial[z][m][n]
+__global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restrict__ partial,
+                                                           const float* __restrict__ unscale, float* __restrict__ y,
+                                                           int M, int N, int splits) {
+    const size_t total = (size_t)M * N;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        float acc = partial[i];
+        for (int z = 1; z < splits; ++z) acc += partial[(size_t)z * total + i];
+        y[i] = acc * unscale[i / N];
+    }
+}
+
 // ---------------------------------------------------------------- launchers
 
-size_t gemm_workspace_bytes(size_t tokens, size_t K) {
-    // f16 activations + one f32 unscale per token, each region 256-byte aligned
-    const size_t xbytes = (tokens * K * 2 + 255) & ~(size_t)255;
-    return xbytes + ((tokens * 4 + 255) & ~(size_t)255);
+constexpr int kMaxSplits = 8;
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t gemm_workspace_bytes(size_t tokens, size_t K, size_t N) {
+    // f16 activations, one f32 unscale per token, and room for kMaxSplits
+    // partial [tokens][N] tiles (split K)
+    return align256(tokens * K * 2) + align256(tokens * 4) + align256((size_t)kMaxSplits * tokens * N * 4);
 }
 
 hipError_t launch_act_f16(bool bf16_in, const void* x, const float* gamma, float eps, int M, int K, void* workspace,
                           hipStream_t stream) {
     _Float16* xh = static_cast<_Float16*>(workspace);
-    float* us = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
-                                         ((((size_t)M * K * 2) + 255) & ~(size_t)255));
+    float* us = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + align256((size_t)M * K * 2));
     if (bf16_in) {
         if (gamma) hipLaunchKernelGGL((act_f16_kernel<true, true>), dim3(M), dim3(kActThreads), 0, stream, x, gamma, eps, K, xh, us);
         else hipLaunchKernelGGL((act_f16_kernel<true, false>), dim3(M), dim3(kActThreads), 0, stream, x, gamma, eps, K, xh, us);
@@ -417,13 +438,39 @@ hipError_t launch_act_f16(bool bf16_in, const void* x, const float* gamma, float
 }
 
 template <int T, int CB, int WAVES>
-static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, const void* workspace, float* y, int M, int N,
-                                 int K, hipStream_t stream) {
-    const _Float16* xh = static_cast<const _Float16*>(workspace);
-    const float* us = reinterpret_cast<const float*>(static_cast<const uint8_t*>(workspace) +
-                                                     ((((size_t)M * K * 2) + 255) & ~(size_t)255));
-    const dim3 grid((N + 32 * WAVES - 1) / (32 * WAVES), (M + 32 * CB - 1) / (32 * CB));
-    hipLaunchKernelGGL((qgemm_kernel<T, CB, WAVES>), grid, dim3(WAVES * 64), 0, stream, w, wbytes, xh, us, y, M, N, K);
+static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, void* workspace, size_t workspace_bytes,
+                                 float* y, int M, int N, int K, int cu_count, hipStream_t stream) {
+    uint8_t* base = static_cast<uint8_t*>(workspace);
+    const _Float16* xh = reinterpret_cast<const _Float16*>(base);
+    const size_t us_off = align256((size_t)M * K * 2);
+    const float* us = reinterpret_cast<const float*>(base + us_off);
+    const size_t part_off = us_off + align256((size_t)M * 4);
+    float* part = reinterpret_cast<float*>(base + part_off);
+    const int gx = (N + 32 * WAVES - 1) / (32 * WAVES), gy = (M + 32 * CB - 1) / (32 * CB);
+    // A grid with fewer waves than SIMDs splits K toward two waves per SIMD
+    // (whole four-step rounds, as far as the reserved partial space allows);
+    // fuller grids do not, since the partial tiles then cost more traffic
+    // than they save.
+    const int steps = 2 * (K >> 8);
+    const int rounds = (steps + kRing - 1) / kRing;
+    const long long waves = (long long)gx * gy * WAVES;
+    int splits = 1;
+    if (waves < 4LL * cu_count) splits = (int)((8LL * cu_count + waves - 1) / waves);
+    splits = std::min({splits, kMaxSplits, rounds});
+    const size_t tile_bytes = (size_t)M * N * 4;
+    const size_t room = workspace_bytes > part_off ? workspace_bytes - part_off : 0;
+    if ((size_t)splits * tile_bytes > room) splits = (int)std::max<size_t>(1, room / tile_bytes);
+    if (splits < 1) splits = 1;
+    const int split_steps = (rounds + splits - 1) / splits * kRing;
+    splits = (steps + split_steps - 1) / split_steps;
+    const dim3 grid(gx, gy, splits);
+    hipLaunchKernelGGL((qgemm_kernel<T, CB, WAVES>), grid, dim3(WAVES * 64), 0, stream, w, wbytes, xh, us, y,
+                       splits > 1 ? part : nullptr, M, N, K, split_steps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
+    const size_t total = (size_t)M * N;
+    const int rgrid = (int)std::min<size_t>((total + 255) / 256, (size_t)cu_count * 8);
+    hipLaunchKernelGGL(qgemm_reduce_kernel, dim3(rgrid), dim3(256), 0, stream, part, us, y, M, N, splits);
     return hipGetLastError();
 }
 
@@ -431,19 +478,19 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, const void* 
 // weight stream); many tokens take 128x128 tiles (each dequantised weight
 // fragment feeds four MFMAs).
 template <int T>
-static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, const void* workspace, float* y, int M, int N,
-                                 int K, hipStream_t stream) {
-    if (M <= 32) return launch_qgemm_t<T, 1, 1>(w, wbytes, workspace, y, M, N, K, stream);
-    if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, y, M, N, K, stream);
-    return launch_qgemm_t<T, 4, 4>(w, wbytes, workspace, y, M, N, K, stream);
+static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, void* workspace, size_t workspace_bytes, float* y,
+                                 int M, int N, int K, int cu_count, hipStream_t stream) {
+    if (M <= 32) return launch_qgemm_t<T, 1, 1>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
+    if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
+    return launch_qgemm_t<T, 4, 4>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
 }
 
-hipError_t launch_qgemm(int value_type, const uint8_t* w, uint32_t wbytes, const void* workspace, float* y, int M,
-                        int N, int K, hipStream_t stream) {
+hipError_t launch_qgemm(int value_type, const uint8_t* w, uint32_t wbytes, void* workspace, size_t workspace_bytes,
+                        float* y, int M, int N, int K, int cu_count, hipStream_t stream) {
     switch (value_type) {
-    case kQ4K: return launch_qgemm_m<kQ4K>(w, wbytes, workspace, y, M, N, K, stream);
-    case kQ5K: return launch_qgemm_m<kQ5K>(w, wbytes, workspace, y, M, N, K, stream);
-    case kQ6K: return launch_qgemm_m<kQ6K>(w, wbytes, workspace, y, M, N, K, stream);
+    case kQ4K: return launch_qgemm_m<kQ4K>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
+    case kQ5K: return launch_qgemm_m<kQ5K>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
+    case kQ6K: return launch_qgemm_m<kQ6K>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
     default: return hipErrorInvalidValue;
     }
 }

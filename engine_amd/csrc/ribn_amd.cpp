@@ -346,17 +346,23 @@ void ribn_amd_context_destroy(ribn_amd_context* ctx) {
     delete ctx;
 }
 
-size_t ribn_amd_gemm_workspace_bytes(size_t tokens, size_t k) { return ribn_amd::gemm_workspace_bytes(tokens, k); }
+size_t ribn_amd_gemm_workspace_bytes(size_t tokens, size_t k, size_t n) {
+    return ribn_amd::gemm_workspace_bytes(tokens, k, n);
+}
 
-ribn_amd_status ribn_amd_context_reserve_prefill(ribn_amd_context* ctx, size_t max_tokens, size_t max_k) {
+ribn_amd_status ribn_amd_context_reserve_prefill(ribn_amd_context* ctx, size_t max_tokens, size_t max_k,
+                                                 size_t max_n) {
     if (!ctx) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null context");
+    if (max_n > (size_t)std::numeric_limits<int>::max()) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)std::numeric_limits<int>::max(), max_n, "max_n overflows");
+    }
     if (max_tokens == 0 || max_k == 0 || max_k > (size_t)ribn_amd::kGemmMaxK || max_k % 256 != 0 ||
         max_tokens > (size_t)std::numeric_limits<int>::max() / max_k) {
         return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kGemmMaxK, max_k,
                     "prefill workspace needs 1 <= tokens, K a multiple of 256 up to %d, tokens*K < 2^31",
                     ribn_amd::kGemmMaxK);
     }
-    const size_t need = ribn_amd::gemm_workspace_bytes(max_tokens, max_k);
+    const size_t need = ribn_amd::gemm_workspace_bytes(max_tokens, max_k, max_n);
     if (need <= ctx->workspace_bytes) return ok();
     DeviceGuard guard(ctx->device);
     if (ctx->workspace) {
@@ -742,7 +748,8 @@ ribn_amd_status ribn_amd_gemm_prefill(ribn_amd_gemv* g, const ribn_amd_quantized
         return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kGemmMaxK, k,
                     "prefill supports K up to %d and tokens*K < 2^31", ribn_amd::kGemmMaxK);
     }
-    const size_t need = ribn_amd::gemm_workspace_bytes(members, k);
+    // the activation stage's part is required; split-K room is used as far as reserved
+    const size_t need = ribn_amd::gemm_workspace_bytes(members, k, 0);
     if (need > g->ctx->workspace_bytes) {
         return fail(RIBN_AMD_WORKSPACE_TOO_SMALL, need, g->ctx->workspace_bytes,
                     "prefill of %zu tokens x K=%llu needs %zu workspace bytes; reserve them with "
@@ -753,8 +760,9 @@ ribn_amd_status ribn_amd_gemm_prefill(ribn_amd_gemv* g, const ribn_amd_quantized
     hipError_t e = ribn_amd::launch_act_f16(input_dtype == RIBN_AMD_BF16, input, gamma, epsilon, (int)members, (int)k,
                                             g->ctx->workspace, g->ctx->stream);
     if (e != hipSuccess) return driver(e, "launch prefill activation stage");
-    e = ribn_amd::launch_qgemm((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, g->ctx->workspace, output,
-                               (int)members, (int)n, (int)k, g->ctx->stream);
+    e = ribn_amd::launch_qgemm((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, g->ctx->workspace,
+                               g->ctx->workspace_bytes, output, (int)members, (int)n, (int)k, g->ctx->cu_count,
+                               g->ctx->stream);
     if (e != hipSuccess) return driver(e, "launch prefill matmul");
     return ok();
 }

@@ -94,9 +94,10 @@ class AmdContext:
     def synchronize(self):
         _check(self._lib.ribn_amd_context_synchronize(self.handle))
 
-    def reserve_prefill(self, max_tokens: int, max_k: int):
-        """Set-up call: device workspace for prefill of up to max_tokens x max_k."""
-        _check(self._lib.ribn_amd_context_reserve_prefill(self.handle, max_tokens, max_k))
+    def reserve_prefill(self, max_tokens: int, max_k: int, max_n: int = 0):
+        """Set-up call: device workspace for prefill of up to max_tokens x max_k
+        activations and split-K room for [max_tokens][max_n] outputs."""
+        _check(self._lib.ribn_amd_context_reserve_prefill(self.handle, max_tokens, max_k, max_n))
 
     def close(self):
         if self.handle and _live():

@@ -207,15 +207,18 @@ ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv *gemv, const ribn_amd_quantize
 
 /* ----------------------------------------------------------- prefill GEMM */
 
-/* Bytes of device workspace a prefill of `tokens` x K activations uses. */
-size_t ribn_amd_gemm_workspace_bytes(size_t tokens, size_t k);
+/* Bytes of device workspace for `tokens` x K activations plus split-K room for
+ * [tokens][n] outputs (n = 0: the minimum, no split-K room). */
+size_t ribn_amd_gemm_workspace_bytes(size_t tokens, size_t k, size_t n);
 /* Reserves (grows, never shrinks) the context's prefill workspace for up to
- * `max_tokens` tokens of K <= max_k. This is the only allocating call of the
- * prefill path, made once at set-up like the reference's decode scratch
- * (alloc_scratch / BatchScratch, decode.rs:1188-1216,1582-1617); execute calls
- * that need more return WorkspaceTooSmall { expected: bytes needed, actual:
- * bytes reserved }. Synchronises the context's stream if it replaces a buffer. */
-ribn_amd_status ribn_amd_context_reserve_prefill(ribn_amd_context *ctx, size_t max_tokens, size_t max_k);
+ * `max_tokens` tokens of K <= max_k and N <= max_n. This is the only allocating
+ * call of the prefill path, made once at set-up like the reference's decode
+ * scratch (alloc_scratch / BatchScratch, decode.rs:1188-1216,1582-1617).
+ * Execute calls whose activations do not fit return WorkspaceTooSmall
+ * { expected: bytes needed, actual: bytes reserved }; split-K uses the rest of
+ * the reservation. Synchronises the context's stream if it replaces a buffer. */
+ribn_amd_status ribn_amd_context_reserve_prefill(ribn_amd_context *ctx, size_t max_tokens, size_t max_k,
+                                                 size_t max_n);
 /* Prefill matmul (north-star prefill path, M >= 128; the reference runs
  * prefill through gemv_batch, decode.rs:1516-1558): y[members][N] =
  * x[members][K] W^T for a Q4_K/Q5_K/Q6_K weight, x in f32 or bf16

@@ -23,7 +23,7 @@ def env():
     import engine_amd as E
     assert torch.cuda.is_available(), "GPU tests need a ROCm device"
     ctx = E.AmdContext(0)
-    ctx.reserve_prefill(512, 12288)
+    ctx.reserve_prefill(512, 12288, 12288)
     store = E.AmdWeightStore(ctx)
     kernels = {t: E.QwenGemvKernel.from_value_type(ctx, t) for t in (12, 13, 14)}
     return {"E": E, "ctx": ctx, "store": store, "k": kernels, "n": [0]}
@@ -142,4 +142,4 @@ def test_prefill_validation(env):
     with pytest.raises(E.AmdQuantizedKernelError) as e:
         kern2.gemm_prefill(w, x, empty_dev(4 * n), 4)
     assert e.value.kind == "WorkspaceTooSmall" and e.value.actual == 0
-    assert e.value.expected == E._lib.load().ribn_amd_gemm_workspace_bytes(4, k)
+    assert e.value.expected == E._lib.load().ribn_amd_gemm_workspace_bytes(4, k, 0)
