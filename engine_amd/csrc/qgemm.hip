@@ -40,7 +40,6 @@ typedef float float2_v __attribute__((ext_vector_type(2)));
 typedef float float16_v __attribute__((ext_vector_type(16)));
 
 constexpr int kActThreads = 256;
-constexpr int kActMaxPerThread = kGemmMaxK / kActThreads;  // 64
 constexpr int kStepK = 128;                                // K per pipeline step (half a super-block)
 constexpr int kXRow = kStepK + 8;                          // padded LDS row (halfs): 272 B, bank-conflict free
 constexpr uint32_t kGemmOutOfRange = 0xffffff00u;
@@ -70,46 +69,79 @@ template <bool BF16_IN, bool NORM>
 __global__ __launch_bounds__(kActThreads) void act_f16_kernel(const void* __restrict__ xin,
                                                                const float* __restrict__ gamma, float eps, int K,
                                                                _Float16* __restrict__ xh, float* __restrict__ unscale) {
+    // Thread t owns chunks of 8 consecutive elements, 8*(t + 256c): one
+    // 16-byte load (bf16) or two (f32) in, one 16-byte f16 store out.
+    constexpr int kChunks = kGemmMaxK / 8 / kActThreads;  // 8
     __shared__ float red[4];
     const int m = blockIdx.x;
-    float v[kActMaxPerThread];
+    float v[kChunks][8];
 #pragma unroll
-    for (int i = 0; i < kActMaxPerThread; ++i) {
-        const int k = threadIdx.x + i * kActThreads;
-        float x = 0.f;
-        if (k < K) {
+    for (int c = 0; c < kChunks; ++c) {
+        const int e = 8 * ((int)threadIdx.x + kActThreads * c);
+        if (e < K) {
             if constexpr (BF16_IN) {
-                const uint16_t b = static_cast<const uint16_t*>(xin)[(size_t)m * K + k];
-                x = __builtin_bit_cast(float, (uint32_t)b << 16);
+                const uint4 raw = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xin) + (size_t)m * K + e);
+                const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    v[c][2 * j] = __builtin_bit_cast(float, wv[j] << 16);
+                    v[c][2 * j + 1] = __builtin_bit_cast(float, wv[j] & 0xffff0000u);
+                }
             } else {
-                x = static_cast<const float*>(xin)[(size_t)m * K + k];
+                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(xin) + (size_t)m * K + e);
+                const float4 a = src[0], b = src[1];
+                v[c][0] = a.x; v[c][1] = a.y; v[c][2] = a.z; v[c][3] = a.w;
+                v[c][4] = b.x; v[c][5] = b.y; v[c][6] = b.z; v[c][7] = b.w;
             }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[c][j] = 0.f;
         }
-        v[i] = x;
     }
     if constexpr (NORM) {
         float ssq = 0.f;
 #pragma unroll
-        for (int i = 0; i < kActMaxPerThread; ++i) ssq += v[i] * v[i];
+        for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ssq += v[c][j] * v[c][j];
         const float inv = 1.0f / sqrtf(block_sum_256(ssq, red) / (float)K + eps);
 #pragma unroll
-        for (int i = 0; i < kActMaxPerThread; ++i) {
-            const int k = threadIdx.x + i * kActThreads;
-            v[i] = k < K ? v[i] * inv * gamma[k] : 0.f;
+        for (int c = 0; c < kChunks; ++c) {
+            const int e = 8 * ((int)threadIdx.x + kActThreads * c);
+            if (e < K) {
+                const float4 g0 = *reinterpret_cast<const float4*>(gamma + e);
+                const float4 g1 = *reinterpret_cast<const float4*>(gamma + e + 4);
+                const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[c][j] = v[c][j] * inv * g[j];
+            }
         }
     }
     float amax = 0.f;
 #pragma unroll
-    for (int i = 0; i < kActMaxPerThread; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = block_max_256(amax, red);
-    int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;  // amax < 2^e
-    e = e < -100 ? -100 : e;
+    for (int c = 0; c < kChunks; ++c)
 #pragma unroll
-    for (int i = 0; i < kActMaxPerThread; ++i) {
-        const int k = threadIdx.x + i * kActThreads;
-        if (k < K) xh[(size_t)m * K + k] = (_Float16)__builtin_amdgcn_ldexpf(v[i], 15 - e);
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
+    amax = block_max_256(amax, red);
+    int ex = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;  // amax < 2^ex
+    ex = ex < -100 ? -100 : ex;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        const int e = 8 * ((int)threadIdx.x + kActThreads * c);
+        if (e < K) {
+            half8_t h;
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const float2_v f = {__builtin_amdgcn_ldexpf(v[c][j], 15 - ex),
+                                    __builtin_amdgcn_ldexpf(v[c][j + 1], 15 - ex)};
+                const half2_v p = __builtin_convertvector(f, half2_v);
+                h[j] = p[0];
+                h[j + 1] = p[1];
+            }
+            *reinterpret_cast<half8_t*>(xh + (size_t)m * K + e) = h;
+        }
     }
-    if (threadIdx.x == 0) unscale[m] = __builtin_amdgcn_ldexpf(1.0f, e - 15);
+    if (threadIdx.x == 0) unscale[m] = __builtin_amdgcn_ldexpf(1.0f, ex - 15);
 }
 
 // ------------------------------------------------------------ weight fragments

@@ -23,6 +23,7 @@ import csv
 import glob
 import hashlib
 import os
+import re
 import statistics
 import sys
 from collections import defaultdict
@@ -46,7 +47,26 @@ def _find(path: str, suffix: str) -> list[str]:
     return sorted(glob.glob(os.path.join(path, "**", f"*{suffix}"), recursive=True))
 
 
+def _demangle(name: str) -> str:
+    """`_ZN<len>ns<len>name I <literal args> E ...` -> `ns::name<args>` (the kernels' own
+    mangling: a namespace, a function and integer/bool template arguments); other
+    names come back unchanged."""
+    m = re.match(r"_ZN((?:\d+[A-Za-z_][A-Za-z0-9_]*)+)I((?:L[a-z]\d+E)+)E", name)
+    if not m:
+        return name
+    parts, rest = [], m.group(1)
+    while rest:
+        n = re.match(r"\d+", rest).group(0)
+        parts.append(rest[len(n):len(n) + int(n)])
+        rest = rest[len(n) + int(n):]
+    args = []
+    for kind, val in re.findall(r"L([a-z])(\d+)E", m.group(2)):
+        args.append(("true" if val == "1" else "false") if kind == "b" else val)
+    return "::".join(parts) + "<" + ", ".join(args) + ">"
+
+
 def short_name(name: str) -> str:
+    name = _demangle(name)
     name = name.replace("void ", "", 1).replace("ribn_amd::", "")
     depth, out = 0, []
     for ch in name:  # drop the argument list, keep template arguments
