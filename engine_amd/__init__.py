@@ -13,10 +13,12 @@ from .kquant import (  # noqa: F401
     AmdKernelError, AmdQuantizedKernelError, AmdModelKernelError, AmdWeightError,
     validate_quantized_geometry,
 )
+from .qwen3 import AmdKvCache, AmdQwen3Config, AmdQwen3Decode, QWEN3_8B, attention_decode  # noqa: F401
 
 __all__ = [
     "Q4_K", "Q5_K", "Q6_K", "BLOCK_BYTES", "AmdContext", "AmdWeightStore", "AmdQuantizedWeight",
     "AmdQ4KGemv", "AmdQ5KGemv", "AmdQ6KGemv", "QwenGemvKernel", "AmdQwenOps", "AmdQ4KEmbedding",
     "AmdKQuantEmbedding", "AmdKernelError",
     "AmdQuantizedKernelError", "AmdModelKernelError", "AmdWeightError", "validate_quantized_geometry",
+    "AmdKvCache", "AmdQwen3Config", "AmdQwen3Decode", "QWEN3_8B", "attention_decode",
 ]

@@ -18,13 +18,30 @@ STATUS_NAMES = {
     0: "Ok", 1: "Driver", 2: "Module", 3: "InvalidWeight", 4: "UnsupportedValueType",
     5: "ShapeOverflow", 6: "InputLength", 7: "OutputLength", 8: "ContextMismatch",
     9: "EmptyInput", 10: "WeightLength", 11: "InvalidEpsilon", 12: "InvalidArgument",
-    13: "EmptyEncoding", 14: "SourceIncomplete", 15: "WorkspaceTooSmall",
+    13: "EmptyEncoding", 14: "SourceIncomplete", 15: "WorkspaceTooSmall", 16: "InvalidPlan",
+    17: "PositionOverflow", 18: "MissingTensor",
 }
 
 
 class RibnAmdError(ctypes.Structure):
     _fields_ = [("status", ctypes.c_int32), ("expected", ctypes.c_uint64),
                 ("actual", ctypes.c_uint64), ("message", ctypes.c_char * 512)]
+
+
+class Qwen3Config(ctypes.Structure):
+    """ribn_amd_qwen3_config."""
+    _fields_ = [("layers", ctypes.c_uint32), ("hidden", ctypes.c_uint32), ("q_heads", ctypes.c_uint32),
+                ("kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32), ("ffn", ctypes.c_uint32),
+                ("vocab", ctypes.c_uint32), ("rope_base", ctypes.c_float), ("epsilon", ctypes.c_float)]
+
+
+QWEN3_LAYER_FIELDS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down",
+                      "attn_norm", "attn_q_norm", "attn_k_norm", "ffn_norm")
+
+
+class Qwen3Layer(ctypes.Structure):
+    """ribn_amd_qwen3_layer: seven weight handles, then four device norm vectors."""
+    _fields_ = [(name, ctypes.c_void_p) for name in QWEN3_LAYER_FIELDS]
 
 
 READ_FN = ctypes.CFUNCTYPE(ctypes.c_int64, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint8), ctypes.c_size_t)
@@ -82,6 +99,26 @@ SIGNATURES = {
     "ribn_amd_embedding_execute_batch": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
     "ribn_amd_rms_norm": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _f32]),
     "ribn_amd_rms_norm_batch": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _f32]),
+    "ribn_amd_gemv_execute_fused": (_i32, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _f32, _vp, _sz, _sz, _u32]),
+    "ribn_amd_kv_cache_create": (_i32, [_vp, ctypes.POINTER(Qwen3Config), _u32, _pvp]),
+    "ribn_amd_kv_cache_destroy": (None, [_vp]),
+    "ribn_amd_kv_cache_capacity": (_u32, [_vp]),
+    "ribn_amd_kv_cache_layer": (_i32, [_vp, _u32, _pvp, _pvp]),
+    "ribn_amd_attention_decode": (_i32, [_vp, ctypes.POINTER(Qwen3Config), _pvp, _sz, _u32, _vp, _vp, _vp, _vp,
+                                         _vp, _vp, _vp, _sz]),
+    "ribn_amd_argmax": (_i32, [_vp, _vp, _sz, _sz, _vp]),
+    "ribn_amd_qwen3_decode_create": (_i32, [_vp, ctypes.POINTER(Qwen3Config), _vp, _vp, _vp,
+                                            ctypes.POINTER(Qwen3Layer), _u32, _pvp]),
+    "ribn_amd_qwen3_decode_destroy": (None, [_vp]),
+    "ribn_amd_qwen3_decode_set_graphs": (_i32, [_vp, _i32]),
+    "ribn_amd_qwen3_prefill_step": (_i32, [_vp, _vp, _u32, _u32]),
+    "ribn_amd_qwen3_decode_step": (_i32, [_vp, _vp, _u32, _u32, ctypes.POINTER(_u32)]),
+    "ribn_amd_qwen3_decode_step_batch": (_i32, [_vp, _pvp, ctypes.POINTER(_u32), ctypes.POINTER(_u32), _sz,
+                                                ctypes.POINTER(_u32)]),
+    "ribn_amd_qwen3_generate": (_i32, [_vp, _pvp, ctypes.POINTER(_u32), ctypes.POINTER(_u32), _sz, _u32,
+                                       ctypes.POINTER(_u32)]),
+    "ribn_amd_qwen3_copy_hidden": (_i32, [_vp, _sz, _vp, _sz]),
+    "ribn_amd_qwen3_copy_logits": (_i32, [_vp, _sz, _vp, _sz]),
 }
 
 _lib = None

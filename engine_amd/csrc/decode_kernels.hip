@@ -1,0 +1,398 @@
+// Decode-step kernels for gfx950 (CDNA4, wave64) around the k-quant GEMVs.
+//
+// attn_decode_kernel: one layer's attention for a batch of decode members.
+// It fuses what the reference runs as five launches per layer
+// (crates/nvidia/src/decode.rs:929-1034):
+//   per-head q/k RMSNorm       strided_rms_norm / q_gate_norm (model_ops.rs:660-685,1009-1041)
+//   NEOX rope of q and k       rope_neox (model_ops.rs:393-425)
+//   f16 append of the new K/V  kv_append_f16 (model_ops.rs:1256-1275)
+//   GQA attention              attn_score_gqa (model_ops.rs:430-566)
+// Qwen3 has no q gate, so the attention output is not gated.
+//
+// Work split (split-T "flash decoding"): the grid is (chunk, KV head,
+// member). A workgroup takes one contiguous chunk of the member's tokens for
+// one KV head and all q_per_kv query heads that share it, so each K/V byte is
+// read once. Within the workgroup a 16-lane row of a wave owns one token per
+// step (lane j of the row holds dims 8j..8j+7: one 16-byte load of K and one
+// of V), and keeps an online-softmax state (running max, denominator and
+// output sums) per query head. The 16 states of a workgroup are merged across
+// rows with lane shuffles and across waves in LDS into one partial per
+// (chunk, head); the last workgroup of a (member, KV
+// head) to finish (an atomic ticket) merges the kAttnChunks partials into the
+// output. The new token's K/V are computed by the workgroup whose chunk holds
+// the position: written to the cache, and used from LDS by that workgroup.
+//
+// argmax_kernel: greedy selection (argmax, model_ops.rs:201-258) with the
+// same ordering key, tie rule and NaN rule.
+#include "decode_launch.hpp"
+#include "kquant_device.hpp"
+
+#include <float.h>
+
+namespace ribn_amd {
+
+namespace {
+
+constexpr uint32_t kOOR = 0xffffff00u;  // buffer offset past any cache: loads return 0
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRing = 4;                  // steps of K/V loads in flight per wave
+constexpr int kStepTokens = kWaves * 4;   // tokens a workgroup covers per step
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives it.
+__device__ __forceinline__ float row16_sum(float v) {
+    v = dpp_step<0xb1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_step<0x4e>(v);   // quad_perm [2,3,0,1]
+    v = dpp_step<0x141>(v);  // row_half_mirror
+    v = dpp_step<0x140>(v);  // row_mirror
+    return v;
+}
+
+__device__ __forceinline__ void unpack_f16x8(uint4 w, float (&f)[8]) {
+    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = half_bits_to_float(a[i] & 0xffffu);
+        f[2 * i + 1] = half_bits_to_float(a[i] >> 16);
+    }
+}
+
+// One 128-wide head held by a wave as lane l: x0 = dim l, x1 = dim l + 64.
+// RMSNorm with the shared per-head weight (x * inv * w, model_ops.rs:660-685),
+// then the NEOX rotation of the pair (l, l + 64) by pos * base^(-2l/128)
+// (model_ops.rs:393-425).
+__device__ __forceinline__ void norm_rope(float& x0, float& x1, float w0, float w1, float eps, float pos,
+                                          float base, int lane) {
+    const float ssq = wave_sum(x0 * x0 + x1 * x1);
+    const float inv = 1.0f / sqrtf(ssq / (float)kHeadDim + eps);
+    const float y0 = x0 * inv * w0;
+    const float y1 = x1 * inv * w1;
+    const float theta = pos * powf(base, -(2.0f * (float)lane) / (float)kHeadDim);
+    float s, c;
+    sincosf(theta, &s, &c);
+    x0 = y0 * c - y1 * s;
+    x1 = y0 * s + y1 * c;
+}
+
+template <int QPK>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
+    constexpr int kHeadsPerWave = (QPK + kWaves - 1) / kWaves;
+    __shared__ float qs[QPK][kHeadDim];
+    __shared__ float kv_new[2][kHeadDim];
+    __shared__ float st_m[kWaves][QPK];
+    __shared__ float st_l[kWaves][QPK];
+    __shared__ float st_o[kWaves][QPK][kHeadDim];
+    __shared__ float cm[kAttnChunks][QPK];
+    __shared__ float cl[kAttnChunks][QPK];
+    __shared__ int last_s;
+
+    const int chunk = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int m = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = lane >> 4;  // token slot of this lane's row
+    const int j = lane & 15;    // dims 8j..8j+7
+    const AttnMember mb = a.mem[m];
+
+    const int pos = a.positions[m];
+    const int tokens = pos + 1;
+    int len = (tokens + kAttnChunks - 1) / kAttnChunks;
+    len = (len + kStepTokens - 1) / kStepTokens * kStepTokens;
+    const int t0 = chunk * len;
+    const int t1 = min(t0 + len, tokens);
+    const int steps = t1 > t0 ? (t1 - t0 + kStepTokens - 1) / kStepTokens : 0;
+    const bool has_new = t0 <= pos && pos < t1;
+
+    // ---- cached K/V of this chunk: the first kRing steps are issued before
+    // anything else. The new token's slot is not read (it is written below).
+    const size_t head_elems = (size_t)mb.capacity * kHeadDim;
+    const uint32_t head_bytes = (uint32_t)(head_elems * 2u);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(mb.keys + (size_t)kvh * head_elems, head_bytes);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(mb.values + (size_t)kvh * head_elems, head_bytes);
+    uint4 kring[kRing], vring[kRing];
+    auto issue = [&](int r, int s) {
+        const int t = t0 + s * kStepTokens + 4 * wave + grp;
+        const bool live = s < steps && t < t1 && t != pos;
+        const uint32_t off = live ? ((uint32_t)t * kHeadDim + 8u * (uint32_t)j) * 2u : kOOR;
+        kring[r] = load_b128(kr, off);
+        vring[r] = load_b128(vr, off);
+    };
+#pragma unroll
+    for (int r = 0; r < kRing; ++r) issue(r, r);
+
+    // ---- query heads (and the new K/V): norm + rope into LDS
+    const float* qm = a.q + ((size_t)m * a.q_heads + (size_t)kvh * QPK) * kHeadDim;
+    float qx[kHeadsPerWave][2];
+#pragma unroll
+    for (int i = 0; i < kHeadsPerWave; ++i) {
+        const int h = wave + kWaves * i;
+        qx[i][0] = qx[i][1] = 0.f;
+        if (h < QPK) {
+            qx[i][0] = qm[h * kHeadDim + lane];
+            qx[i][1] = qm[h * kHeadDim + 64 + lane];
+        }
+    }
+    const bool new_wave = has_new && wave < 2;  // wave 0: K, wave 1: V
+    float nx0 = 0.f, nx1 = 0.f;
+    if (new_wave) {
+        const float* src = (wave == 0 ? a.k : a.v) + ((size_t)m * a.kv_heads + kvh) * kHeadDim;
+        nx0 = src[lane];
+        nx1 = src[lane + 64];
+    }
+    const float qw0 = a.q_norm[lane];
+    const float qw1 = a.q_norm[lane + 64];
+    const float fpos = (float)pos;
+#pragma unroll
+    for (int i = 0; i < kHeadsPerWave; ++i) {
+        const int h = wave + kWaves * i;
+        if (h < QPK) {
+            norm_rope(qx[i][0], qx[i][1], qw0, qw1, a.eps, fpos, a.rope_base, lane);
+            qs[h][lane] = qx[i][0];
+            qs[h][lane + 64] = qx[i][1];
+        }
+    }
+    if (new_wave) {
+        if (wave == 0) norm_rope(nx0, nx1, a.k_norm[lane], a.k_norm[lane + 64], a.eps, fpos, a.rope_base, lane);
+        // f16 round to nearest even, as kv_append_f16 stores it
+        const _Float16 h0 = (_Float16)nx0;
+        const _Float16 h1 = (_Float16)nx1;
+        if (pos < mb.capacity) {
+            uint16_t* dst = (wave == 0 ? mb.keys : mb.values) + (size_t)kvh * head_elems + (size_t)pos * kHeadDim;
+            dst[lane] = __builtin_bit_cast(uint16_t, h0);
+            dst[lane + 64] = __builtin_bit_cast(uint16_t, h1);
+        }
+        kv_new[wave][lane] = (float)h0;
+        kv_new[wave][lane + 64] = (float)h1;
+    }
+    __syncthreads();
+
+    float qr[QPK][8];
+#pragma unroll
+    for (int h = 0; h < QPK; ++h)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qr[h][i] = qs[h][8 * j + i];
+
+    // ---- online softmax over the chunk (the reference's running max and
+    // rescaled total, model_ops.rs:508-523, extended to the output sums)
+    float mrun[QPK], lrun[QPK], o[QPK][8];
+#pragma unroll
+    for (int h = 0; h < QPK; ++h) {
+        mrun[h] = -FLT_MAX;
+        lrun[h] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[h][i] = 0.f;
+    }
+    auto consume = [&](uint4 kw, uint4 vw, int s) {
+        const int t = t0 + s * kStepTokens + 4 * wave + grp;
+        const bool live = t < t1;
+        float kf[8], vf[8];
+        unpack_f16x8(kw, kf);
+        unpack_f16x8(vw, vf);
+        if (t == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                kf[i] = kv_new[0][8 * j + i];
+                vf[i] = kv_new[1][8 * j + i];
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < QPK; ++h) {
+            float d = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d = __builtin_fmaf(qr[h][i], kf[i], d);
+            d = row16_sum(d);
+            const float sc = live ? d * a.scale : -INFINITY;
+            const float mn = fmaxf(mrun[h], sc);
+            const float c = expf(mrun[h] - mn);
+            const float p = expf(sc - mn);
+            lrun[h] = lrun[h] * c + p;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[h][i] = __builtin_fmaf(p, vf[i], o[h][i] * c);
+            mrun[h] = mn;
+        }
+    };
+    for (int s = 0; s < steps; s += kRing) {
+#pragma unroll
+        for (int r = 0; r < kRing; ++r) {
+            if (s + r < steps) {
+                consume(kring[r], vring[r], s + r);
+                issue(r, s + r + kRing);
+            }
+        }
+    }
+
+    // ---- merge the four row states of each wave (lane xor 16, xor 32), then
+    // the waves' states through LDS into this chunk's partial
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+        for (int h = 0; h < QPK; ++h) {
+            const float m2 = __shfl_xor(mrun[h], off, 64);
+            const float l2 = __shfl_xor(lrun[h], off, 64);
+            const float mx = fmaxf(mrun[h], m2);
+            const float f1 = expf(mrun[h] - mx);
+            const float f2 = expf(m2 - mx);
+            lrun[h] = lrun[h] * f1 + l2 * f2;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float o2 = __shfl_xor(o[h][i], off, 64);
+                o[h][i] = o[h][i] * f1 + o2 * f2;
+            }
+            mrun[h] = mx;
+        }
+    }
+    if (grp == 0) {
+#pragma unroll
+        for (int h = 0; h < QPK; ++h) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) st_o[wave][h][8 * j + i] = o[h][i];
+            if (j == 0) {
+                st_m[wave][h] = mrun[h];
+                st_l[wave][h] = lrun[h];
+            }
+        }
+    }
+    __syncthreads();
+    float* part = mb.partials + ((size_t)kvh * kAttnChunks + chunk) * QPK * kPartStride;
+    for (int idx = tid; idx < QPK * kHeadDim; idx += kThreads) {
+        const int h = idx / kHeadDim;
+        const int d = idx - h * kHeadDim;
+        float mx = -FLT_MAX;
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q) mx = fmaxf(mx, st_m[q][h]);
+        float l = 0.f, acc = 0.f;
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q) {
+            const float f = expf(st_m[q][h] - mx);
+            l = __builtin_fmaf(st_l[q][h], f, l);
+            acc = __builtin_fmaf(st_o[q][h][d], f, acc);
+        }
+        part[h * kPartStride + d] = acc;
+        if (d == 0) {
+            part[h * kPartStride + kHeadDim] = mx;
+            part[h * kPartStride + kHeadDim + 1] = l;
+        }
+    }
+
+    // ---- the last chunk of this (member, KV head) to finish merges all chunks
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last_s = atomicAdd(&mb.counters[kvh], 1u) == (uint32_t)(kAttnChunks - 1);
+    __syncthreads();
+    if (!last_s) return;
+    __threadfence();
+    const float* pbase = mb.partials + (size_t)kvh * kAttnChunks * QPK * kPartStride;
+    for (int i = tid; i < kAttnChunks * QPK; i += kThreads) {
+        const int c = i / QPK;
+        const int h = i - c * QPK;
+        cm[c][h] = pbase[(c * QPK + h) * kPartStride + kHeadDim];
+        cl[c][h] = pbase[(c * QPK + h) * kPartStride + kHeadDim + 1];
+    }
+    __syncthreads();
+    float* outm = a.out + ((size_t)m * a.q_heads + (size_t)kvh * QPK) * kHeadDim;
+    for (int idx = tid; idx < QPK * kHeadDim; idx += kThreads) {
+        const int h = idx / kHeadDim;
+        const int d = idx - h * kHeadDim;
+        float mx = -FLT_MAX;
+        for (int c = 0; c < kAttnChunks; ++c) mx = fmaxf(mx, cm[c][h]);
+        float l = 0.f, acc = 0.f;
+        for (int c = 0; c < kAttnChunks; ++c) {
+            const float f = expf(cm[c][h] - mx);
+            l = __builtin_fmaf(cl[c][h], f, l);
+            acc = __builtin_fmaf(pbase[(c * QPK + h) * kPartStride + d], f, acc);
+        }
+        outm[h * kHeadDim + d] = acc / l;
+    }
+    if (tid == 0) atomicExch(&mb.counters[kvh], 0u);
+}
+
+// Order-preserving key of a float (model_ops.rs:151-155).
+__device__ __forceinline__ uint32_t logit_key(float v) {
+    const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+    return (bits >> 31) ? ~bits : (bits ^ 0x80000000u);
+}
+
+__device__ __forceinline__ void take_better(uint32_t& key, uint32_t& idx, uint32_t ok, uint32_t oi) {
+    if (ok > key || (ok == key && oi < idx)) {
+        key = ok;
+        idx = oi;
+    }
+}
+
+constexpr int kArgmaxThreads = 1024;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* logits, int vocab, uint32_t* selected,
+                                                               uint32_t* tokens, int32_t* positions, int32_t* steps,
+                                                               uint32_t* history, int history_stride) {
+    __shared__ uint32_t wkey[kArgmaxThreads / 64];
+    __shared__ uint32_t widx[kArgmaxThreads / 64];
+    const int m = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float* row = logits + (size_t)m * vocab;
+    uint32_t key = 0u, idx = 0u;
+    for (int p = tid; p < vocab; p += kArgmaxThreads) {
+        const float v = row[p];
+        const uint32_t k = logit_key(v);
+        // v == v rejects NaN like the scalar reference's strict comparisons
+        if (v == v && k > key) {
+            key = k;
+            idx = (uint32_t)p;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t ok = (uint32_t)__shfl_xor((int)key, off, 64);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)idx, off, 64);
+        take_better(key, idx, ok, oi);
+    }
+    if ((tid & 63) == 0) {
+        wkey[tid >> 6] = key;
+        widx[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        key = wkey[0];
+        idx = widx[0];
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) take_better(key, idx, wkey[w], widx[w]);
+        selected[m] = idx;
+        if (tokens != nullptr) tokens[m] = idx;
+        if (positions != nullptr) {
+            const int s = steps[m];
+            history[(size_t)m * history_stride + s] = idx;
+            steps[m] = s + 1;
+            positions[m] = positions[m] + 1;
+        }
+    }
+}
+
+}  // namespace
+
+size_t attn_partials_floats(int q_heads) { return (size_t)q_heads * kAttnChunks * kPartStride; }
+
+hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t stream) {
+    if (members < 1 || members > kAttnMaxMembers || args.kv_heads < 1 || args.q_heads % args.kv_heads != 0) {
+        return hipErrorInvalidValue;
+    }
+    const dim3 grid(kAttnChunks, (unsigned)args.kv_heads, (unsigned)members);
+    switch (args.q_heads / args.kv_heads) {
+    case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(kThreads), 0, stream, args); break;
+    case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(kThreads), 0, stream, args); break;
+    case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(kThreads), 0, stream, args); break;
+    case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(kThreads), 0, stream, args); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, int vocab, int members, uint32_t* selected, uint32_t* tokens,
+                         int32_t* positions, int32_t* steps, uint32_t* history, int history_stride,
+                         hipStream_t stream) {
+    if (members < 1 || vocab < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)members), dim3(kArgmaxThreads), 0, stream, logits, vocab,
+                       selected, tokens, positions, steps, history, history_stride);
+    return hipGetLastError();
+}
+
+}  // namespace ribn_amd

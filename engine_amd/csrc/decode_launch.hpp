@@ -1,0 +1,62 @@
+// Internal launcher API of the decode-step kernels (decode_kernels.hip):
+// attention over the f16 KV cache and the greedy token selection.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ribn_amd {
+
+// Head geometry the attention kernel is built for (Qwen3: 128-wide heads).
+constexpr int kHeadDim = 128;
+// Token chunks per (member, KV head): the work of one workgroup. The count is
+// fixed, so a member's arithmetic does not depend on the batch it runs in and
+// a captured step serves every position.
+constexpr int kAttnChunks = 32;
+// Members one attention launch serves (the host splits larger batches).
+constexpr int kAttnMaxMembers = 8;
+// Floats per (chunk, query head) partial: 128 output sums, the running
+// maximum, the running denominator, two pad words (16-byte rows).
+constexpr int kPartStride = kHeadDim + 4;
+
+// One member's cache views for one layer.
+struct AttnMember {
+    uint16_t* keys;      // f16 [kv_heads][capacity][128]
+    uint16_t* values;    // f16 [kv_heads][capacity][128]
+    float* partials;     // [kv_heads][kAttnChunks][q_per_kv][kPartStride]
+    uint32_t* counters;  // [kv_heads], zero between launches
+    int capacity;        // cache tokens per (layer, KV head)
+};
+
+struct AttnArgs {
+    AttnMember mem[kAttnMaxMembers];
+    const float* q;            // [members][q_heads * 128], raw projection
+    const float* k;            // [members][kv_heads * 128], raw projection
+    const float* v;            // [members][kv_heads * 128]
+    const float* q_norm;       // [128] per-head RMSNorm weight
+    const float* k_norm;       // [128]
+    const int32_t* positions;  // [members] device positions of the new token
+    float* out;                // [members][q_heads * 128]
+    int q_heads;
+    int kv_heads;
+    float eps;
+    float rope_base;
+    float scale;               // 1/sqrt(head_dim)
+};
+
+// Floats of one sequence's attention partials ([q_heads][kAttnChunks][kPartStride]).
+size_t attn_partials_floats(int q_heads);
+
+// members <= kAttnMaxMembers; q_heads / kv_heads in {1, 2, 4, 8}.
+hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t stream);
+
+// Greedy selection per member over logits [members][vocab] (ties to the lowest
+// index, NaN never selected). Writes selected[m]; when `tokens` is not null
+// also tokens[m] (the next step's input). When `positions` is not null the
+// member's generation advances on the device: history[m * history_stride +
+// steps[m]] = selected, then steps[m] and positions[m] grow by one.
+hipError_t launch_argmax(const float* logits, int vocab, int members, uint32_t* selected, uint32_t* tokens,
+                         int32_t* positions, int32_t* steps, uint32_t* history, int history_stride,
+                         hipStream_t stream);
+
+}  // namespace ribn_amd

@@ -276,9 +276,11 @@ __device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneAc
 
 // ------------------------------------------------------------------ kernel
 
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES, int GROUP>
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP>
 __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args) {
     static_assert(NBUF % GROUP == 0, "the ring holds whole row groups");
+    constexpr bool NORM = PRO == kProNorm;
+    constexpr bool SWIGLU = PRO == kProSwiglu;
     constexpr int kWaves = WAVES;
     constexpr int kThreads = WAVES * 64;
     constexpr int BB = BlockTraits<T>::bytes;
@@ -348,15 +350,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
     // staging below waits for these and not for the weight loads after them.
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(args.x, (uint32_t)members * (uint32_t)K * 4u);
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(args.gamma, NORM ? (uint32_t)K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t ur = make_rsrc(args.x2, SWIGLU ? (uint32_t)members * (uint32_t)K * 4u : 0u);
     float4 xv[MT][CH];
     float4 gv[CH];
+    float4 uv[SWIGLU ? MT : 1][CH];
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int e = 4 * ((int)threadIdx.x + kThreads * c);
         const bool in = e < K;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            xv[m][c] = load_f4(xr, (in && m < members) ? (uint32_t)(m * K + e) * 4u : kOutOfRange);
+            const uint32_t off = (in && m < members) ? (uint32_t)(m * K + e) * 4u : kOutOfRange;
+            xv[m][c] = load_f4(xr, off);
+            if constexpr (SWIGLU) uv[m][c] = load_f4(ur, off);
         }
         if constexpr (NORM) gv[c] = load_f4(gr, in ? (uint32_t)e * 4u : kOutOfRange);
     }
@@ -404,6 +410,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             float4 v = xv[m][c];
+            if constexpr (SWIGLU) {
+                // silu(gate) * up, in the reference's operation order (model_ops.rs:316-328)
+                v.x = (v.x / (1.0f + expf(-v.x))) * uv[m][c].x;
+                v.y = (v.y / (1.0f + expf(-v.y))) * uv[m][c].y;
+                v.z = (v.z / (1.0f + expf(-v.z))) * uv[m][c].z;
+                v.w = (v.w / (1.0f + expf(-v.w))) * uv[m][c].w;
+            }
             if constexpr (NORM) {
                 ssq[m] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
                 v.x *= gv[c].x;
@@ -461,6 +474,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
             inv[m] = 1.0f / sqrtf(total / (float)K + args.eps);
         }
     }
+
+    // Output of one row: a store, or (args.accumulate) an add into y, which
+    // fuses the residual connection (each row is added exactly once, so the
+    // result is the same as a store followed by an elementwise add).
+    const bool accumulate = args.accumulate != 0;
+    auto put = [&](float value, __amdgpu_buffer_rsrc_t yr, uint32_t off) {
+        if (accumulate) {
+            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(value, yr, (int)off, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), yr, (int)off, 0, 0);
+        }
+    };
 
     // One member's lane record of one slice, from LDS.
     auto read_member = [&](LaneAct<T>& dst, int m, int slice) {
@@ -533,7 +558,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
                     const bool live = r < left && crow + r < r_end;
                     const uint32_t off =
                         (live && lane == 0) ? (uint32_t)(m * rows_mat[r] + local[r]) * 4u : kOutOfRange;
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, total), yr[r], (int)off, 0, 0);
+                    put(total, yr[r], off);
                 }
             }
             if constexpr (REFILL) {
@@ -586,7 +611,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
             const uint32_t off = (last && row < r_end && lane == 0 && m < members)
                                      ? (uint32_t)(m * rows_mat + local) * 4u
                                      : kOutOfRange;
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, total), yr, (int)off, 0, 0);
+            put(total, yr, off);
         }
         if constexpr (ONE_SLICE) {
             ++crow;
@@ -626,18 +651,18 @@ static size_t act_lds_bytes(int members, int K) {
     return (size_t)members * slices * 64 * ActTraits<T>::stride * sizeof(uint32_t);
 }
 
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES, int GROUP = 1>
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP = 1>
 struct WaveInstance {
     static std::atomic<int> occupancy;  // resident workgroups per CU at the largest LDS size (0: not queried)
     // Launches `per_cu` workgroups on every CU (capped by occupancy; fewer
     // when the problem has fewer than two units per wave).
     static hipError_t launch(const WaveGemvArgs& a, int cu_count, int per_cu, hipStream_t stream) {
-        auto kern = gemv_wave_kernel<T, MT, NORM, ONE_SLICE, NBUF, WAVES, GROUP>;
+        auto kern = gemv_wave_kernel<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP>;
         const size_t lds = act_lds_bytes<T>(MT, a.K);
         int occ = occupancy.load(std::memory_order_relaxed);
         if (occ == 0) {
             const int max_lds = (int)act_lds_bytes<T>(MT, ONE_SLICE ? kSliceElems : kWaveMaxK);
-            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+            (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)kern, WAVES * 64, max_lds) !=
                     hipSuccess ||
                 occ < 1) {
@@ -658,45 +683,50 @@ struct WaveInstance {
         return hipGetLastError();
     }
 };
-template <int T, int MT, bool NORM, bool ONE_SLICE, int NBUF, int WAVES, int GROUP>
-std::atomic<int> WaveInstance<T, MT, NORM, ONE_SLICE, NBUF, WAVES, GROUP>::occupancy{0};
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP>
+std::atomic<int> WaveInstance<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP>::occupancy{0};
 
 // Launch shape by units (row x slice) per CU, from sweeps on MI355X over
 // workgroup size {2,4,8,16} waves x ring depth {2,4,8} x workgroups per CU
 // {1,2,4}: short launches want every wave started at once with a shallow
 // ring; long streams want fewer, deeper streams per CU.
-template <int T, int MT, bool NORM, bool ONE_SLICE>
+template <int T, int MT, int PRO, bool ONE_SLICE>
 static hipError_t launch_ring(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
     const int slices = ONE_SLICE ? 1 : ((a.K >> 8) + 15) >> 4;
     const long long units = (long long)a.total_rows * slices;
     const long long per_cu = (units + cu_count - 1) / cu_count;
     if constexpr (MT == 1 && ONE_SLICE) {
         if (per_cu >= 128) {
-            if constexpr (T == kQ6K) return WaveInstance<T, MT, NORM, ONE_SLICE, 8, 4>::launch(a, cu_count, 1, stream);
-            return WaveInstance<T, MT, NORM, ONE_SLICE, 4, 8>::launch(a, cu_count, 4, stream);
+            if constexpr (T == kQ6K) return WaveInstance<T, MT, PRO, ONE_SLICE, 8, 4>::launch(a, cu_count, 1, stream);
+            return WaveInstance<T, MT, PRO, ONE_SLICE, 4, 8>::launch(a, cu_count, 4, stream);
         }
     }
     if constexpr (!ONE_SLICE) {
         // K spanning slices: pairs of rows, slice by slice (deeper rings
         // measured slower for the 12288-wide down projection).
-        return WaveInstance<T, MT, NORM, ONE_SLICE, 2, 8, 2>::launch(a, cu_count, 1, stream);
+        return WaveInstance<T, MT, PRO, ONE_SLICE, 2, 8, 2>::launch(a, cu_count, 1, stream);
+    } else {
+        return WaveInstance<T, MT, PRO, ONE_SLICE, 2, 8>::launch(a, cu_count, per_cu > 48 ? 2 : 1, stream);
     }
-    return WaveInstance<T, MT, NORM, ONE_SLICE, 2, 8>::launch(a, cu_count, per_cu > 48 ? 2 : 1, stream);
 }
 
-template <int T, int MT, bool NORM>
+template <int T, int MT, int PRO>
 static hipError_t launch_tm(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
-    if (a.K <= kSliceElems) return launch_ring<T, MT, NORM, true>(a, cu_count, stream);
-    return launch_ring<T, MT, NORM, false>(a, cu_count, stream);
+    if (a.K <= kSliceElems) return launch_ring<T, MT, PRO, true>(a, cu_count, stream);
+    return launch_ring<T, MT, PRO, false>(a, cu_count, stream);
 }
 
-template <int T, bool NORM>
+template <int T, int PRO>
 static hipError_t launch_t(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
-    if (a.members <= 1) return launch_tm<T, 1, NORM>(a, cu_count, stream);
-    if (a.members <= 2 || a.K > kSliceElems) return launch_tm<T, 2, NORM>(a, cu_count, stream);
-    // 3..8 members: member-serial passes over a four-unit ring
-    if (a.members <= 4) return WaveInstance<T, 4, NORM, true, 4, 8>::launch(a, cu_count, 1, stream);
-    return WaveInstance<T, 8, NORM, true, 4, 8>::launch(a, cu_count, 1, stream);
+    if (a.members <= 1) return launch_tm<T, 1, PRO>(a, cu_count, stream);
+    if (a.members <= 2 || a.K > kSliceElems) return launch_tm<T, 2, PRO>(a, cu_count, stream);
+    if constexpr (PRO == kProSwiglu) {
+        return hipErrorInvalidValue;  // the host splits SwiGLU launches into pairs of members
+    } else {
+        // 3..8 members: member-serial passes over a four-unit ring
+        if (a.members <= 4) return WaveInstance<T, 4, PRO, true, 4, 8>::launch(a, cu_count, 1, stream);
+        return WaveInstance<T, 8, PRO, true, 4, 8>::launch(a, cu_count, 1, stream);
+    }
 }
 
 int wave_max_members(int K) {
@@ -707,12 +737,21 @@ int wave_max_members(int K) {
     return (int)std::min<long long>(fit, cap);
 }
 
+template <int T>
+static hipError_t launch_type(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
+    if (a.x2 != nullptr) {
+        if (a.gamma != nullptr || a.members > kSwigluMaxMembers) return hipErrorInvalidValue;
+        return launch_t<T, kProSwiglu>(a, cu_count, stream);
+    }
+    if (a.gamma != nullptr) return launch_t<T, kProNorm>(a, cu_count, stream);
+    return launch_t<T, kProPlain>(a, cu_count, stream);
+}
+
 hipError_t launch_gemv_wave(int value_type, const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
-    const bool norm = a.gamma != nullptr;
     switch (value_type) {
-    case kQ4K: return norm ? launch_t<kQ4K, true>(a, cu_count, stream) : launch_t<kQ4K, false>(a, cu_count, stream);
-    case kQ5K: return norm ? launch_t<kQ5K, true>(a, cu_count, stream) : launch_t<kQ5K, false>(a, cu_count, stream);
-    case kQ6K: return norm ? launch_t<kQ6K, true>(a, cu_count, stream) : launch_t<kQ6K, false>(a, cu_count, stream);
+    case kQ4K: return launch_type<kQ4K>(a, cu_count, stream);
+    case kQ5K: return launch_type<kQ5K>(a, cu_count, stream);
+    case kQ6K: return launch_type<kQ6K>(a, cu_count, stream);
     default: return hipErrorInvalidValue;
     }
 }

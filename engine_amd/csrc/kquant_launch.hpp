@@ -17,6 +17,14 @@ constexpr int kMaxGroup = 4;
 constexpr long long kWaveMaxLdsBytes = 128 * 1024;
 constexpr int kWaveMaxK = 16384;
 
+// Activation prologue of the wave GEMV: plain x, RMSNorm(x; gamma), or
+// SwiGLU silu(x) * x2.
+constexpr int kProPlain = 0;
+constexpr int kProNorm = 1;
+constexpr int kProSwiglu = 2;
+// Members one SwiGLU-prologue launch serves (the host splits larger batches).
+constexpr int kSwigluMaxMembers = 2;
+
 struct WaveGemvArgs {
     const uint8_t* w[kMaxGroup];
     uint32_t wbytes[kMaxGroup];
@@ -26,9 +34,11 @@ struct WaveGemvArgs {
     int total_rows;
     const float* x;           // [members][K]
     const float* gamma;       // RMSNorm weight [K], or null for a plain GEMV
+    const float* x2;          // SwiGLU: the up projection [members][K] (x is the gate), or null
     float eps;
     int K;
     int members;
+    int accumulate;           // nonzero: y += W x' (fused residual add) instead of y = W x'
 };
 
 // Largest member count one wave launch can stage for this K (0 if none).
@@ -40,7 +50,9 @@ hipError_t launch_dequant(int value_type, const uint8_t* w, uint32_t wbytes, flo
 hipError_t launch_gemv_exact(int value_type, const uint8_t* w, uint32_t wbytes, const float* x, float* y,
                              int K, int N, int members, hipStream_t stream);
 
-// args.gamma == nullptr: plain GEMV; otherwise RMSNorm(x; gamma, eps) is fused into the activation load.
+// args.gamma != nullptr: RMSNorm(x; gamma, eps) is fused into the activation
+// load; args.x2 != nullptr: the activation is silu(x) * x2 (members <= 2, no
+// gamma); args.accumulate: outputs are added into y.
 hipError_t launch_gemv_wave(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
 
 // Gathers and dequantises rows of a [hidden, vocab] table: tokens[m] (device

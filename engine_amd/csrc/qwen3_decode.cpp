@@ -1,0 +1,738 @@
+// Host runtime of the Qwen3 decode step behind the C ABI (include/ribn_amd.h):
+// per-sequence KV caches, the step's device buffers, the launch sequence and
+// its capture as HIP graphs.
+//
+// One step for `members` sequences, in the reference's order
+// (crates/nvidia/src/decode.rs:544-631 run_step, 929-1034 full_attention_layer),
+// with the elementwise launches fused into their neighbours:
+//   embedding of tokens[m]                          (q4_k_embedding; device token ids)
+//   per layer:
+//     q/k/v GEMV, RMSNorm(attn_norm) in the prologue   (rms_norm + 3 gemv)
+//     attention: q/k norm, rope, KV append, GQA        (5 launches in the reference)
+//     o GEMV added into the residual stream            (gemv + residual_add)
+//     gate/up GEMV, RMSNorm(ffn_norm) in the prologue  (rms_norm + 2 gemv)
+//     down GEMV of silu(gate)*up, added into the stream (silu_mul + gemv + residual_add)
+//   output head: RMSNorm(output_norm) + lm_head GEMV, argmax (run_output_head, 655-677)
+// Five launches per layer instead of the reference's 14. Positions and token
+// ids live in device memory, so one captured graph serves every position and
+// a generation loop needs no host round trip between steps.
+#include "ribn_amd.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <new>
+#include <vector>
+
+#include "abi_internal.hpp"
+#include "decode_launch.hpp"
+#include "kquant_launch.hpp"
+
+using namespace ribn_amd_abi;
+
+struct ribn_amd_kv_cache {
+    ribn_amd_context* ctx;
+    int device;
+    uint64_t id;  // distinguishes caches in captured-graph keys
+    ribn_amd_qwen3_config cfg;
+    uint32_t capacity;
+    size_t layer_elems;  // kv_heads * capacity * head_dim
+    void* block;         // one allocation: keys, values, partials, counters
+    uint16_t* keys;      // [layers][kv_heads][capacity][head_dim]
+    uint16_t* values;
+    float* partials;     // attention partials ([q_heads][kAttnChunks][kPartStride])
+    uint32_t* counters;  // [kv_heads] attention tickets, zero between launches
+};
+
+namespace {
+
+std::atomic<uint64_t> g_cache_ids{1};
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct GraphEntry {
+    std::vector<uint64_t> caches;  // cache ids, in member order
+    bool head;
+    bool advance;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+constexpr size_t kMaxGraphs = 32;
+
+ribn_amd_status check_config(const ribn_amd_qwen3_config* c) {
+    if (c == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null config");
+    if (c->layers == 0) return fail(RIBN_AMD_INVALID_PLAN, 1, 0, "the plan has no layers");
+    if (c->head_dim != (uint32_t)ribn_amd::kHeadDim) {
+        return fail(RIBN_AMD_INVALID_PLAN, ribn_amd::kHeadDim, c->head_dim, "head_dim %u is not %d", c->head_dim,
+                    ribn_amd::kHeadDim);
+    }
+    if (c->kv_heads == 0 || c->q_heads == 0 || c->q_heads % c->kv_heads != 0) {
+        return fail(RIBN_AMD_INVALID_PLAN, c->kv_heads, c->q_heads, "%u query heads do not group over %u KV heads",
+                    c->q_heads, c->kv_heads);
+    }
+    const uint32_t group = c->q_heads / c->kv_heads;
+    if (group != 1 && group != 2 && group != 4 && group != 8) {
+        return fail(RIBN_AMD_INVALID_PLAN, 8, group, "query heads per KV head must be 1, 2, 4 or 8 (got %u)", group);
+    }
+    const uint64_t qdim = (uint64_t)c->q_heads * c->head_dim;
+    const uint64_t dims[3] = {c->hidden, c->ffn, qdim};
+    for (uint64_t d : dims) {
+        if (d == 0 || d % 256 != 0 || d > (uint64_t)ribn_amd::kWaveMaxK) {
+            return fail(RIBN_AMD_INVALID_PLAN, (uint64_t)ribn_amd::kWaveMaxK, d,
+                        "hidden, ffn and q_heads*head_dim must be multiples of 256 up to %d (got %llu)",
+                        ribn_amd::kWaveMaxK, (unsigned long long)d);
+        }
+    }
+    if (c->vocab == 0 || c->vocab > (uint32_t)std::numeric_limits<int>::max()) {
+        return fail(RIBN_AMD_INVALID_PLAN, 1, c->vocab, "vocabulary size %u is out of range", c->vocab);
+    }
+    if (!(c->rope_base > 0.f) || !std::isfinite(c->rope_base)) {
+        return fail(RIBN_AMD_INVALID_PLAN, 0, 0, "rope base must be finite and positive");
+    }
+    return check_epsilon(c->epsilon);
+}
+
+bool same_geometry(const ribn_amd_qwen3_config& a, const ribn_amd_qwen3_config& b) {
+    return a.layers == b.layers && a.q_heads == b.q_heads && a.kv_heads == b.kv_heads && a.head_dim == b.head_dim;
+}
+
+}  // namespace
+
+struct ribn_amd_qwen3_decode {
+    ribn_amd_context* ctx;
+    ribn_amd_qwen3_config cfg;
+    uint32_t max_members;
+    const ribn_amd_quantized_weight* token_embd;
+    const ribn_amd_quantized_weight* output;
+    const float* output_norm;
+    std::vector<ribn_amd_qwen3_layer> layers;
+    void* block;  // step buffers, one allocation
+    float* hidden;    // [members][hidden] residual stream
+    float* q;         // [members][q_heads*128]
+    float* k;         // [members][kv_heads*128]
+    float* v;
+    float* attn;      // [members][q_heads*128]
+    float* gate;      // [members][ffn]
+    float* up;
+    float* logits;    // [members][vocab]
+    uint32_t* tokens;     // [members] input token of the next step
+    uint32_t* selected;   // [members] greedy selection of the last step
+    int32_t* positions;   // [members]
+    int32_t* steps;       // [members] generated-token counters
+    uint32_t* history;    // [members][history_steps]
+    uint32_t history_steps;
+    hipStream_t capture;  // private stream for graph capture
+    bool graphs;
+    std::vector<GraphEntry> graph_cache;
+};
+
+namespace {
+
+// Wave GEMV over `count` weights of one value type sharing the activation x,
+// in launch groups of as many members as one launch stages.
+hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight* const* ws, int count,
+                const float* x, const float* x2, const float* gamma, float* const* ys, int members, bool accumulate,
+                hipStream_t stream) {
+    const int K = (int)ws[0]->input_size;
+    int per = std::min(ribn_amd::wave_max_members(K), ribn_amd::kWaveMaxMembers);
+    if (x2 != nullptr) per = std::min(per, ribn_amd::kSwigluMaxMembers);
+    if (per <= 0) return hipErrorInvalidValue;
+    for (int m0 = 0; m0 < members; m0 += per) {
+        const int mc = std::min(per, members - m0);
+        ribn_amd::WaveGemvArgs a{};
+        int rows = 0;
+        for (int i = 0; i < count; ++i) {
+            const int n = (int)ws[i]->output_size;
+            a.w[i] = ws[i]->data;
+            a.wbytes[i] = (uint32_t)ws[i]->encoded_bytes;
+            a.y[i] = ys[i] + (size_t)m0 * n;
+            rows += n;
+            a.rows_end[i] = rows;
+        }
+        a.count = count;
+        a.total_rows = rows;
+        a.x = x + (size_t)m0 * K;
+        a.x2 = x2 != nullptr ? x2 + (size_t)m0 * K : nullptr;
+        a.gamma = gamma;
+        a.eps = d->cfg.epsilon;
+        a.K = K;
+        a.members = mc;
+        a.accumulate = accumulate ? 1 : 0;
+        hipError_t e = ribn_amd::launch_gemv_wave((int)ws[0]->value_type, a, d->ctx->cu_count, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// RMSNorm-fused GEMVs of weights sharing one input: one launch per run of
+// equal value types (q/k/v or gate/up of Q4_K_M files may mix types).
+hipError_t wave_shared(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight* const* ws, float* const* ys,
+                       int count, const float* x, const float* gamma, int members, hipStream_t stream) {
+    int i = 0;
+    while (i < count) {
+        int j = i + 1;
+        while (j < count && ws[j]->value_type == ws[i]->value_type) ++j;
+        hipError_t e = wave(d, ws + i, j - i, x, nullptr, gamma, ys + i, members, false, stream);
+        if (e != hipSuccess) return e;
+        i = j;
+    }
+    return hipSuccess;
+}
+
+hipError_t attention(const ribn_amd_qwen3_config& cfg, ribn_amd_kv_cache* const* caches, int members, uint32_t layer,
+                     const float* q, const float* k, const float* v, const float* q_norm, const float* k_norm,
+                     const int32_t* positions, float* out, hipStream_t stream) {
+    const size_t qdim = (size_t)cfg.q_heads * cfg.head_dim;
+    const size_t kvdim = (size_t)cfg.kv_heads * cfg.head_dim;
+    for (int m0 = 0; m0 < members; m0 += ribn_amd::kAttnMaxMembers) {
+        const int mc = std::min(ribn_amd::kAttnMaxMembers, members - m0);
+        ribn_amd::AttnArgs a{};
+        for (int i = 0; i < mc; ++i) {
+            ribn_amd_kv_cache* c = caches[m0 + i];
+            a.mem[i].keys = c->keys + (size_t)layer * c->layer_elems;
+            a.mem[i].values = c->values + (size_t)layer * c->layer_elems;
+            a.mem[i].partials = c->partials;
+            a.mem[i].counters = c->counters;
+            a.mem[i].capacity = (int)c->capacity;
+        }
+        a.q = q + m0 * qdim;
+        a.k = k + m0 * kvdim;
+        a.v = v + m0 * kvdim;
+        a.q_norm = q_norm;
+        a.k_norm = k_norm;
+        a.positions = positions + m0;
+        a.out = out + m0 * qdim;
+        a.q_heads = (int)cfg.q_heads;
+        a.kv_heads = (int)cfg.kv_heads;
+        a.eps = cfg.epsilon;
+        a.rope_base = cfg.rope_base;
+        a.scale = 1.0f / sqrtf((float)cfg.head_dim);
+        hipError_t e = ribn_amd::launch_attention(a, mc, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// The launches of one step (see the file comment).
+hipError_t enqueue_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches, int members, bool head,
+                        bool advance, hipStream_t stream) {
+    const ribn_amd_qwen3_config& c = d->cfg;
+    hipError_t e = ribn_amd::launch_embedding((int)d->token_embd->value_type, d->token_embd->data,
+                                              (uint32_t)d->token_embd->encoded_bytes, d->tokens, 0, d->hidden,
+                                              c.hidden / 256, c.vocab, (uint32_t)members, stream);
+    if (e != hipSuccess) return e;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const ribn_amd_qwen3_layer& L = d->layers[l];
+        const ribn_amd_quantized_weight* qkv[3] = {L.attn_q, L.attn_k, L.attn_v};
+        float* qkv_out[3] = {d->q, d->k, d->v};
+        e = wave_shared(d, qkv, qkv_out, 3, d->hidden, L.attn_norm, members, stream);
+        if (e != hipSuccess) return e;
+        e = attention(c, caches, members, l, d->q, d->k, d->v, L.attn_q_norm, L.attn_k_norm, d->positions, d->attn,
+                      stream);
+        if (e != hipSuccess) return e;
+        e = wave(d, &L.attn_output, 1, d->attn, nullptr, nullptr, &d->hidden, members, true, stream);
+        if (e != hipSuccess) return e;
+        const ribn_amd_quantized_weight* gu[2] = {L.ffn_gate, L.ffn_up};
+        float* gu_out[2] = {d->gate, d->up};
+        e = wave_shared(d, gu, gu_out, 2, d->hidden, L.ffn_norm, members, stream);
+        if (e != hipSuccess) return e;
+        e = wave(d, &L.ffn_down, 1, d->gate, d->up, nullptr, &d->hidden, members, true, stream);
+        if (e != hipSuccess) return e;
+    }
+    if (!head) return hipSuccess;
+    e = wave(d, &d->output, 1, d->hidden, nullptr, d->output_norm, &d->logits, members, false, stream);
+    if (e != hipSuccess) return e;
+    return ribn_amd::launch_argmax(d->logits, (int)c.vocab, members, d->selected, d->tokens,
+                                   advance ? d->positions : nullptr, d->steps, d->history, (int)d->history_steps,
+                                   stream);
+}
+
+void destroy_graphs(ribn_amd_qwen3_decode* d) {
+    for (GraphEntry& g : d->graph_cache) {
+        hipGraphExecDestroy(g.exec);
+        hipGraphDestroy(g.graph);
+    }
+    d->graph_cache.clear();
+}
+
+// Runs one step on the context stream: replays (capturing on first use) the
+// step's graph, or launches directly when graphs are off.
+ribn_amd_status run_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches, int members, bool head,
+                         bool advance) {
+    hipStream_t stream = d->ctx->stream;
+    if (!d->graphs) {
+        hipError_t e = enqueue_step(d, caches, members, head, advance, stream);
+        return e == hipSuccess ? ok() : driver(e, "launch decode step");
+    }
+    std::vector<uint64_t> ids(members);
+    for (int m = 0; m < members; ++m) ids[m] = caches[m]->id;
+    GraphEntry* hit = nullptr;
+    for (GraphEntry& g : d->graph_cache) {
+        if (g.head == head && g.advance == advance && g.caches == ids) {
+            hit = &g;
+            break;
+        }
+    }
+    if (hit == nullptr) {
+        if (d->graph_cache.size() >= kMaxGraphs) {
+            hipError_t e = hipStreamSynchronize(stream);
+            if (e != hipSuccess) return driver(e, "hipStreamSynchronize");
+            hipGraphExecDestroy(d->graph_cache.front().exec);
+            hipGraphDestroy(d->graph_cache.front().graph);
+            d->graph_cache.erase(d->graph_cache.begin());
+        }
+        hipError_t e = hipStreamBeginCapture(d->capture, hipStreamCaptureModeRelaxed);
+        if (e != hipSuccess) return driver(e, "hipStreamBeginCapture");
+        const hipError_t le = enqueue_step(d, caches, members, head, advance, d->capture);
+        hipGraph_t graph = nullptr;
+        e = hipStreamEndCapture(d->capture, &graph);
+        if (le != hipSuccess || e != hipSuccess) {
+            if (graph) hipGraphDestroy(graph);
+            return driver(le != hipSuccess ? le : e, "capture decode step");
+        }
+        hipGraphExec_t exec = nullptr;
+        e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            hipGraphDestroy(graph);
+            return driver(e, "hipGraphInstantiate");
+        }
+        d->graph_cache.push_back(GraphEntry{std::move(ids), head, advance, graph, exec});
+        hit = &d->graph_cache.back();
+    }
+    hipError_t e = hipGraphLaunch(hit->exec, stream);
+    return e == hipSuccess ? ok() : driver(e, "hipGraphLaunch");
+}
+
+ribn_amd_status check_weight(const ribn_amd_context* ctx, const ribn_amd_quantized_weight* w, uint64_t K, uint64_t N,
+                             uint32_t layer, const char* name) {
+    if (w == nullptr) return fail(RIBN_AMD_MISSING_TENSOR, 0, 0, "layer %u lacks %s", layer, name);
+    if (w->device != ctx->device) {
+        return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)ctx->device, (uint64_t)w->device,
+                    "%s of layer %u lives on device %d", name, layer, w->device);
+    }
+    const uint64_t dims[2] = {w->input_size, w->output_size};
+    uint64_t k = 0, n = 0;
+    ribn_amd_status st =
+        ribn_amd_validate_quantized_geometry(w->value_type, w->value_type, dims, 2, w->encoded_bytes, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    if (k != K || n != N) {
+        return fail(RIBN_AMD_INVALID_PLAN, K, k, "%s of layer %u is [%llu, %llu], expected [%llu, %llu]", name, layer,
+                    (unsigned long long)k, (unsigned long long)n, (unsigned long long)K, (unsigned long long)N);
+    }
+    if (w->encoded_bytes > 0xffffffffull) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0xffffffffull, w->encoded_bytes, "%s of layer %u exceeds 4 GiB", name,
+                    layer);
+    }
+    return RIBN_AMD_OK;
+}
+
+// Validates one step's members: caches of this decoder's geometry on its
+// device, distinct; tokens in the vocabulary; positions (plus `extra` further
+// steps) within each cache.
+ribn_amd_status check_members(const ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches,
+                              const uint32_t* tokens, const uint32_t* positions, size_t members, uint32_t extra) {
+    if (members == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "a step needs at least one member");
+    if (members > d->max_members) {
+        return fail(RIBN_AMD_INVALID_PLAN, d->max_members, members, "the decoder was built for %u members",
+                    d->max_members);
+    }
+    for (size_t m = 0; m < members; ++m) {
+        const ribn_amd_kv_cache* c = caches[m];
+        if (c == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "member %zu has no KV cache", m);
+        if (c->device != d->ctx->device) {
+            return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)d->ctx->device, (uint64_t)c->device,
+                        "member %zu's cache lives on device %d", m, c->device);
+        }
+        if (!same_geometry(c->cfg, d->cfg)) {
+            return fail(RIBN_AMD_INVALID_PLAN, 0, 0, "member %zu's cache has another layer or head geometry", m);
+        }
+        for (size_t o = 0; o < m; ++o) {
+            if (caches[o] == c) return fail(RIBN_AMD_INVALID_PLAN, o, m, "members %zu and %zu share a cache", o, m);
+        }
+        if (tokens[m] >= d->cfg.vocab) {
+            return fail(RIBN_AMD_INVALID_PLAN, d->cfg.vocab, tokens[m], "token %u is outside vocabulary %u",
+                        tokens[m], d->cfg.vocab);
+        }
+        if ((uint64_t)positions[m] + extra >= c->capacity) {
+            return fail(RIBN_AMD_POSITION_OVERFLOW, c->capacity, (uint64_t)positions[m] + extra,
+                        "token position %llu exceeds KV capacity %u", (unsigned long long)positions[m] + extra,
+                        c->capacity);
+        }
+    }
+    return RIBN_AMD_OK;
+}
+
+// Stream-ordered upload of the members' tokens and positions.
+ribn_amd_status upload_step(ribn_amd_qwen3_decode* d, const uint32_t* tokens, const uint32_t* positions,
+                            size_t members) {
+    std::vector<int32_t> pos(members);
+    for (size_t m = 0; m < members; ++m) pos[m] = (int32_t)positions[m];
+    hipError_t e = hipMemcpyAsync(d->tokens, tokens, members * sizeof(uint32_t), hipMemcpyHostToDevice, d->ctx->stream);
+    if (e == hipSuccess) {
+        e = hipMemcpyAsync(d->positions, pos.data(), members * sizeof(int32_t), hipMemcpyHostToDevice, d->ctx->stream);
+    }
+    // pageable sources: the copies are complete before the vectors go away
+    if (e == hipSuccess) e = hipStreamSynchronize(d->ctx->stream);
+    return e == hipSuccess ? ok() : driver(e, "upload step inputs");
+}
+
+}  // namespace
+
+extern "C" {
+
+ribn_amd_status ribn_amd_kv_cache_create(ribn_amd_context* ctx, const ribn_amd_qwen3_config* config,
+                                         uint32_t capacity, ribn_amd_kv_cache** out) {
+    if (!ctx || !out) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    ribn_amd_status st = check_config(config);
+    if (st != RIBN_AMD_OK) return st;
+    if (capacity == 0 || capacity > (1u << 20)) {
+        return fail(RIBN_AMD_INVALID_PLAN, 1u << 20, capacity, "KV capacity must be 1..%u tokens", 1u << 20);
+    }
+    const size_t layer_elems = (size_t)config->kv_heads * capacity * config->head_dim;
+    const size_t cache_bytes = align_up(layer_elems * config->layers * sizeof(uint16_t));
+    const size_t part_bytes = align_up(ribn_amd::attn_partials_floats((int)config->q_heads) * sizeof(float));
+    const size_t counter_bytes = align_up(config->kv_heads * sizeof(uint32_t));
+    DeviceGuard guard(ctx->device);
+    void* block = nullptr;
+    hipError_t e = hipMalloc(&block, 2 * cache_bytes + part_bytes + counter_bytes);
+    if (e != hipSuccess) return driver(e, "hipMalloc KV cache");
+    char* p = static_cast<char*>(block);
+    auto* c = new (std::nothrow) ribn_amd_kv_cache{};
+    if (!c) {
+        hipFree(block);
+        return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    }
+    c->ctx = ctx;
+    c->device = ctx->device;
+    c->id = g_cache_ids.fetch_add(1);
+    c->cfg = *config;
+    c->capacity = capacity;
+    c->layer_elems = layer_elems;
+    c->block = block;
+    c->keys = reinterpret_cast<uint16_t*>(p);
+    c->values = reinterpret_cast<uint16_t*>(p + cache_bytes);
+    c->partials = reinterpret_cast<float*>(p + 2 * cache_bytes);
+    c->counters = reinterpret_cast<uint32_t*>(p + 2 * cache_bytes + part_bytes);
+    // the attention tickets start at zero; the cache needs no clearing (a
+    // position is always written before it is read)
+    e = hipMemsetAsync(c->counters, 0, counter_bytes, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        hipFree(block);
+        delete c;
+        return driver(e, "clear KV cache tickets");
+    }
+    *out = c;
+    return ok();
+}
+
+void ribn_amd_kv_cache_destroy(ribn_amd_kv_cache* cache) {
+    if (!cache) return;
+    DeviceGuard guard(cache->device);
+    hipFree(cache->block);  // waits for outstanding work on the device
+    delete cache;
+}
+
+uint32_t ribn_amd_kv_cache_capacity(const ribn_amd_kv_cache* cache) { return cache ? cache->capacity : 0; }
+
+ribn_amd_status ribn_amd_kv_cache_layer(ribn_amd_kv_cache* cache, uint32_t layer, uint16_t** keys, uint16_t** values) {
+    if (!cache || !keys || !values) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (layer >= cache->cfg.layers) {
+        return fail(RIBN_AMD_INVALID_PLAN, cache->cfg.layers, layer, "layer %u of a %u-layer cache", layer,
+                    cache->cfg.layers);
+    }
+    *keys = cache->keys + (size_t)layer * cache->layer_elems;
+    *values = cache->values + (size_t)layer * cache->layer_elems;
+    return ok();
+}
+
+ribn_amd_status ribn_amd_attention_decode(ribn_amd_context* ctx, const ribn_amd_qwen3_config* config,
+                                          ribn_amd_kv_cache* const* caches, size_t members, uint32_t layer,
+                                          const float* q, const float* k, const float* v, const float* q_norm,
+                                          const float* k_norm, const int32_t* positions, float* output,
+                                          size_t output_len) {
+    if (!ctx || !caches) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    ribn_amd_status st = check_config(config);
+    if (st != RIBN_AMD_OK) return st;
+    if (members == 0 || members > RIBN_AMD_MAX_BATCH_MEMBERS) {
+        return fail(RIBN_AMD_INPUT_LENGTH, RIBN_AMD_MAX_BATCH_MEMBERS, members, "attention takes 1..%u members",
+                    RIBN_AMD_MAX_BATCH_MEMBERS);
+    }
+    const void* ptrs[7] = {q, k, v, q_norm, k_norm, positions, output};
+    const char* names[7] = {"q", "k", "v", "q_norm", "k_norm", "positions", "output"};
+    for (int i = 0; i < 7; ++i) {
+        st = check_device_ptr(ctx, ptrs[i], names[i], i == 5 ? 4 : 16);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    for (size_t m = 0; m < members; ++m) {
+        const ribn_amd_kv_cache* c = caches[m];
+        if (c == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "member %zu has no KV cache", m);
+        if (c->device != ctx->device) {
+            return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)ctx->device, (uint64_t)c->device,
+                        "member %zu's cache lives on device %d", m, c->device);
+        }
+        if (!same_geometry(c->cfg, *config) || layer >= c->cfg.layers) {
+            return fail(RIBN_AMD_INVALID_PLAN, c->cfg.layers, layer, "member %zu's cache does not hold layer %u", m,
+                        layer);
+        }
+        for (size_t o = 0; o < m; ++o) {
+            if (caches[o] == c) return fail(RIBN_AMD_INVALID_PLAN, o, m, "members %zu and %zu share a cache", o, m);
+        }
+    }
+    const size_t want = members * config->q_heads * config->head_dim;
+    if (output_len != want) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, want, output_len, "attention output has %zu values, expected %zu",
+                    output_len, want);
+    }
+    DeviceGuard guard(ctx->device);
+    // Positions are device values: the kernel checks them against each cache
+    // and drops an append past its capacity.
+    hipError_t e = attention(*config, caches, (int)members, layer, q, k, v, q_norm, k_norm, positions, output,
+                             ctx->stream);
+    return e == hipSuccess ? ok() : driver(e, "launch attention");
+}
+
+ribn_amd_status ribn_amd_argmax(ribn_amd_context* ctx, const float* logits, size_t logits_len, size_t length,
+                                uint32_t* selected) {
+    if (!ctx) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null context");
+    ribn_amd_status st = check_device_ptr(ctx, logits, "logits", 4);
+    if (st == RIBN_AMD_OK) st = check_device_ptr(ctx, selected, "selected", 4);
+    if (st != RIBN_AMD_OK) return st;
+    // model_ops.rs:1583-1674: empty logits, then rows of `length`
+    if (logits_len == 0 || length == 0) return fail(RIBN_AMD_EMPTY_INPUT, 1, 0, "argmax input is empty");
+    if (logits_len % length != 0) {
+        return fail(RIBN_AMD_INPUT_LENGTH, logits_len, length, "logits of %zu values are not rows of %zu", logits_len,
+                    length);
+    }
+    const size_t members = logits_len / length;
+    if (length > (size_t)std::numeric_limits<int>::max() || members > 65535) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "argmax shape exceeds launch limits");
+    }
+    DeviceGuard guard(ctx->device);
+    hipError_t e = ribn_amd::launch_argmax(logits, (int)length, (int)members, selected, nullptr, nullptr, nullptr,
+                                           nullptr, 0, ctx->stream);
+    return e == hipSuccess ? ok() : driver(e, "launch argmax");
+}
+
+ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context* ctx, const ribn_amd_qwen3_config* config,
+                                             const ribn_amd_quantized_weight* token_embd,
+                                             const ribn_amd_quantized_weight* output, const float* output_norm,
+                                             const ribn_amd_qwen3_layer* layers, uint32_t max_members,
+                                             ribn_amd_qwen3_decode** out) {
+    if (!ctx || !out || !layers) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    ribn_amd_status st = check_config(config);
+    if (st != RIBN_AMD_OK) return st;
+    const ribn_amd_qwen3_config& c = *config;
+    if (max_members == 0 || max_members > RIBN_AMD_MAX_BATCH_MEMBERS) {
+        return fail(RIBN_AMD_INVALID_PLAN, RIBN_AMD_MAX_BATCH_MEMBERS, max_members, "max_members must be 1..%u",
+                    RIBN_AMD_MAX_BATCH_MEMBERS);
+    }
+    const uint64_t qdim = (uint64_t)c.q_heads * c.head_dim;
+    const uint64_t kvdim = (uint64_t)c.kv_heads * c.head_dim;
+    // token_embd.weight / output.weight / output_norm.weight (decode.rs:572-576, 662-675)
+    st = check_weight(ctx, token_embd, c.hidden, c.vocab, 0, "token_embd");
+    if (st == RIBN_AMD_OK) st = check_weight(ctx, output, c.hidden, c.vocab, 0, "output");
+    if (st != RIBN_AMD_OK) return st;
+    if (output_norm == nullptr) return fail(RIBN_AMD_MISSING_TENSOR, 0, 0, "the plan lacks output_norm");
+    st = check_device_ptr(ctx, output_norm, "output_norm");
+    if (st != RIBN_AMD_OK) return st;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const ribn_amd_qwen3_layer& L = layers[l];
+        struct {
+            const ribn_amd_quantized_weight* w;
+            uint64_t K, N;
+            const char* name;
+        } ws[7] = {{L.attn_q, c.hidden, qdim, "attn_q"},        {L.attn_k, c.hidden, kvdim, "attn_k"},
+                   {L.attn_v, c.hidden, kvdim, "attn_v"},       {L.attn_output, qdim, c.hidden, "attn_output"},
+                   {L.ffn_gate, c.hidden, c.ffn, "ffn_gate"},   {L.ffn_up, c.hidden, c.ffn, "ffn_up"},
+                   {L.ffn_down, c.ffn, c.hidden, "ffn_down"}};
+        for (auto& w : ws) {
+            st = check_weight(ctx, w.w, w.K, w.N, l, w.name);
+            if (st != RIBN_AMD_OK) return st;
+        }
+        const float* norms[4] = {L.attn_norm, L.attn_q_norm, L.attn_k_norm, L.ffn_norm};
+        const char* norm_names[4] = {"attn_norm", "attn_q_norm", "attn_k_norm", "ffn_norm"};
+        for (int i = 0; i < 4; ++i) {
+            if (norms[i] == nullptr) return fail(RIBN_AMD_MISSING_TENSOR, 0, 0, "layer %u lacks %s", l, norm_names[i]);
+            st = check_device_ptr(ctx, norms[i], norm_names[i]);
+            if (st != RIBN_AMD_OK) return st;
+        }
+    }
+
+    const size_t M = max_members;
+    const size_t f32_counts[8] = {M * c.hidden, M * qdim, M * kvdim, M * kvdim, M * qdim, M * c.ffn, M * c.ffn,
+                                  M * c.vocab};
+    size_t bytes = 0;
+    size_t offsets[12];
+    for (int i = 0; i < 8; ++i) {
+        offsets[i] = bytes;
+        bytes += align_up(f32_counts[i] * sizeof(float));
+    }
+    for (int i = 8; i < 12; ++i) {  // tokens, selected, positions, steps
+        offsets[i] = bytes;
+        bytes += align_up(M * sizeof(uint32_t));
+    }
+    DeviceGuard guard(ctx->device);
+    auto* d = new (std::nothrow) ribn_amd_qwen3_decode{};
+    if (!d) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    d->ctx = ctx;
+    d->cfg = c;
+    d->max_members = max_members;
+    d->token_embd = token_embd;
+    d->output = output;
+    d->output_norm = output_norm;
+    d->layers.assign(layers, layers + c.layers);
+    d->graphs = true;
+    hipError_t e = hipMalloc(&d->block, bytes);
+    if (e != hipSuccess) {
+        delete d;
+        return driver(e, "hipMalloc decode buffers");
+    }
+    char* p = static_cast<char*>(d->block);
+    float** f32s[8] = {&d->hidden, &d->q, &d->k, &d->v, &d->attn, &d->gate, &d->up, &d->logits};
+    for (int i = 0; i < 8; ++i) *f32s[i] = reinterpret_cast<float*>(p + offsets[i]);
+    d->tokens = reinterpret_cast<uint32_t*>(p + offsets[8]);
+    d->selected = reinterpret_cast<uint32_t*>(p + offsets[9]);
+    d->positions = reinterpret_cast<int32_t*>(p + offsets[10]);
+    d->steps = reinterpret_cast<int32_t*>(p + offsets[11]);
+    d->history_steps = 256;
+    e = hipMalloc(&d->history, M * d->history_steps * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemsetAsync(d->block, 0, bytes, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&d->capture, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        if (d->history) hipFree(d->history);
+        hipFree(d->block);
+        delete d;
+        return driver(e, "set up decode buffers");
+    }
+    *out = d;
+    return ok();
+}
+
+void ribn_amd_qwen3_decode_destroy(ribn_amd_qwen3_decode* d) {
+    if (!d) return;
+    DeviceGuard guard(d->ctx->device);
+    hipStreamSynchronize(d->ctx->stream);
+    destroy_graphs(d);
+    hipStreamDestroy(d->capture);
+    hipFree(d->history);
+    hipFree(d->block);
+    delete d;
+}
+
+ribn_amd_status ribn_amd_qwen3_decode_set_graphs(ribn_amd_qwen3_decode* d, int32_t enabled) {
+    if (!d) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null decoder");
+    d->graphs = enabled != 0;
+    return ok();
+}
+
+ribn_amd_status ribn_amd_qwen3_decode_step_batch(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches,
+                                                 const uint32_t* tokens, const uint32_t* positions, size_t members,
+                                                 uint32_t* selected) {
+    if (!d || !caches || !tokens || !positions || !selected) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    }
+    ribn_amd_status st = check_members(d, caches, tokens, positions, members, 0);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(d->ctx->device);
+    st = upload_step(d, tokens, positions, members);
+    if (st != RIBN_AMD_OK) return st;
+    st = run_step(d, caches, (int)members, true, false);
+    if (st != RIBN_AMD_OK) return st;
+    // the reference's blocking token readback (decode.rs:634-645)
+    hipError_t e = hipMemcpyAsync(selected, d->selected, members * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                  d->ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->ctx->stream);
+    return e == hipSuccess ? ok() : driver(e, "read selected tokens");
+}
+
+ribn_amd_status ribn_amd_qwen3_decode_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* cache, uint32_t token,
+                                           uint32_t position, uint32_t* selected) {
+    ribn_amd_kv_cache* caches[1] = {cache};
+    return ribn_amd_qwen3_decode_step_batch(d, caches, &token, &position, 1, selected);
+}
+
+ribn_amd_status ribn_amd_qwen3_prefill_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* cache, uint32_t token,
+                                            uint32_t position) {
+    if (!d || !cache) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    ribn_amd_kv_cache* caches[1] = {cache};
+    ribn_amd_status st = check_members(d, caches, &token, &position, 1, 0);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(d->ctx->device);
+    st = upload_step(d, &token, &position, 1);
+    if (st != RIBN_AMD_OK) return st;
+    return run_step(d, caches, 1, false, false);
+}
+
+ribn_amd_status ribn_amd_qwen3_generate(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches,
+                                        const uint32_t* tokens, const uint32_t* positions, size_t members,
+                                        uint32_t steps, uint32_t* out_tokens) {
+    if (!d || !caches || !tokens || !positions || !out_tokens) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    }
+    if (steps == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "generation needs at least one step");
+    ribn_amd_status st = check_members(d, caches, tokens, positions, members, steps - 1);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(d->ctx->device);
+    hipStream_t stream = d->ctx->stream;
+    if (steps > d->history_steps) {
+        // the history buffer is part of the captured graphs: replace both
+        hipError_t e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return driver(e, "hipStreamSynchronize");
+        destroy_graphs(d);
+        hipFree(d->history);
+        d->history = nullptr;
+        d->history_steps = 0;
+        e = hipMalloc(&d->history, (size_t)d->max_members * steps * sizeof(uint32_t));
+        if (e != hipSuccess) return driver(e, "hipMalloc generation history");
+        d->history_steps = steps;
+    }
+    st = upload_step(d, tokens, positions, members);
+    if (st != RIBN_AMD_OK) return st;
+    std::vector<int32_t> zeros(members, 0);
+    hipError_t e = hipMemcpyAsync(d->steps, zeros.data(), members * sizeof(int32_t), hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return driver(e, "reset generation counters");
+    for (uint32_t s = 0; s < steps; ++s) {
+        st = run_step(d, caches, (int)members, true, true);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    for (size_t m = 0; m < members; ++m) {
+        e = hipMemcpyAsync(out_tokens + m * steps, d->history + m * d->history_steps, steps * sizeof(uint32_t),
+                           hipMemcpyDeviceToHost, stream);
+        if (e != hipSuccess) return driver(e, "read generated tokens");
+    }
+    e = hipStreamSynchronize(stream);
+    return e == hipSuccess ? ok() : driver(e, "hipStreamSynchronize");
+}
+
+static ribn_amd_status copy_member(ribn_amd_qwen3_decode* d, const float* base, size_t width, size_t member,
+                                   float* host, size_t len) {
+    if (!d || !host) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (member >= d->max_members) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, d->max_members, member, "member %zu of %u", member, d->max_members);
+    }
+    if (len != width) return fail(RIBN_AMD_OUTPUT_LENGTH, width, len, "host buffer holds %zu values, need %zu", len, width);
+    DeviceGuard guard(d->ctx->device);
+    hipError_t e = hipMemcpyAsync(host, base + member * width, width * sizeof(float), hipMemcpyDeviceToHost,
+                                  d->ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->ctx->stream);
+    return e == hipSuccess ? ok() : driver(e, "copy to host");
+}
+
+ribn_amd_status ribn_amd_qwen3_copy_hidden(ribn_amd_qwen3_decode* d, size_t member, float* host, size_t len) {
+    return copy_member(d, d ? d->hidden : nullptr, d ? d->cfg.hidden : 0, member, host, len);
+}
+
+ribn_amd_status ribn_amd_qwen3_copy_logits(ribn_amd_qwen3_decode* d, size_t member, float* host, size_t len) {
+    return copy_member(d, d ? d->logits : nullptr, d ? d->cfg.vocab : 0, member, host, len);
+}
+
+}  // extern "C"

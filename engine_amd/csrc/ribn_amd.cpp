@@ -13,39 +13,10 @@
 #include <new>
 #include <vector>
 
+#include "abi_internal.hpp"
 #include "kquant_launch.hpp"
 
-struct ribn_amd_context {
-    int device;
-    hipStream_t stream;
-    bool owns_stream;
-    int cu_count;
-    void* workspace;  // prefill activation workspace (ribn_amd_context_reserve_prefill)
-    size_t workspace_bytes;
-};
-
-struct ribn_amd_quantized_weight {
-    ribn_amd_context* ctx;
-    int device;  // kept so destruction never touches the (possibly destroyed) context
-    uint32_t value_type;
-    uint64_t input_size;
-    uint64_t output_size;
-    uint64_t encoded_bytes;
-    uint8_t* data;
-    bool owns_data;
-};
-
-struct ribn_amd_gemv {
-    ribn_amd_context* ctx;
-    uint32_t value_type;
-};
-
-struct ribn_amd_embedding {
-    ribn_amd_context* ctx;
-    uint32_t value_type;
-};
-
-namespace {
+namespace ribn_amd_abi {
 
 thread_local ribn_amd_error g_last_error = {RIBN_AMD_OK, 0, 0, {0}};
 
@@ -96,21 +67,9 @@ uint64_t block_bytes(uint32_t t) {
 
 bool supported(uint32_t t) { return block_bytes(t) != 0; }
 
-struct DeviceGuard {
-    int previous = -1;
-    explicit DeviceGuard(int device) {
-        if (hipGetDevice(&previous) != hipSuccess) previous = -1;
-        if (previous != device) hipSetDevice(device);
-    }
-    ~DeviceGuard() {
-        if (previous >= 0) hipSetDevice(previous);
-    }
-};
-
 // The ContextMismatch check of quantized.rs:260-266 for raw device pointers:
 // the buffer must be device (or managed) memory of the context's device.
-ribn_amd_status check_device_ptr(const ribn_amd_context* ctx, const void* ptr, const char* what,
-                                 uintptr_t align = 16) {
+ribn_amd_status check_device_ptr(const ribn_amd_context* ctx, const void* ptr, const char* what, uintptr_t align) {
     if (ptr == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "%s is null", what);
     if ((reinterpret_cast<uintptr_t>(ptr) & (align - 1)) != 0) {
         return fail(RIBN_AMD_INVALID_ARGUMENT, align, reinterpret_cast<uintptr_t>(ptr) & (align - 1),
@@ -193,13 +152,14 @@ ribn_amd_status validate_members(const ribn_amd_gemv* g, size_t members) {
 // vector. Members are split into launch groups that fit the LDS staging of K.
 ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_weight* const* ws, size_t count,
                                   const float* in, const float* gamma, float eps, float* const* outs, uint64_t k,
-                                  size_t members) {
+                                  size_t members, const float* up = nullptr, bool accumulate = false) {
     DeviceGuard guard(g->ctx->device);
-    const int per_launch = std::min(ribn_amd::wave_max_members((int)k), ribn_amd::kWaveMaxMembers);
+    int per_launch = std::min(ribn_amd::wave_max_members((int)k), ribn_amd::kWaveMaxMembers);
+    if (up != nullptr) per_launch = std::min(per_launch, ribn_amd::kSwigluMaxMembers);
     if (per_launch <= 0) {
         // K too large to stage in LDS: the exact-order kernel still serves it.
-        if (gamma != nullptr) {
-            return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kWaveMaxK, k, "fused RMSNorm supports K up to %d",
+        if (gamma != nullptr || up != nullptr || accumulate) {
+            return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kWaveMaxK, k, "fused GEMV forms support K up to %d",
                         ribn_amd::kWaveMaxK);
         }
         for (size_t i = 0; i < count; ++i) {
@@ -225,6 +185,8 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
         a.count = (int)count;
         a.total_rows = rows;
         a.x = in + m0 * k;
+        a.x2 = up != nullptr ? up + m0 * k : nullptr;
+        a.accumulate = accumulate ? 1 : 0;
         a.gamma = gamma;
         a.eps = eps;
         a.K = (int)k;
@@ -260,7 +222,9 @@ ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_
     return ok();
 }
 
-}  // namespace
+}  // namespace ribn_amd_abi
+
+using namespace ribn_amd_abi;
 
 extern "C" {
 
@@ -288,6 +252,9 @@ const char* ribn_amd_status_name(int32_t status) {
     case RIBN_AMD_EMPTY_ENCODING: return "EmptyEncoding";
     case RIBN_AMD_SOURCE_INCOMPLETE: return "SourceIncomplete";
     case RIBN_AMD_WORKSPACE_TOO_SMALL: return "WorkspaceTooSmall";
+    case RIBN_AMD_INVALID_PLAN: return "InvalidPlan";
+    case RIBN_AMD_POSITION_OVERFLOW: return "PositionOverflow";
+    case RIBN_AMD_MISSING_TENSOR: return "MissingTensor";
     default: return "Unknown";
     }
 }
@@ -696,6 +663,42 @@ ribn_amd_status ribn_amd_gemv_execute_group(ribn_amd_gemv* g, const ribn_amd_qua
         if (st != RIBN_AMD_OK) return st;
     }
     return launch_wave_group(g, weights, count, input, gamma, epsilon, outputs, k0, members);
+}
+
+ribn_amd_status ribn_amd_gemv_execute_fused(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w,
+                                           const float* input, const float* up, size_t input_len, const float* gamma,
+                                           size_t gamma_len, float epsilon, float* output, size_t output_len,
+                                           size_t members, uint32_t flags) {
+    ribn_amd_status st = validate_members(g, members);
+    if (st != RIBN_AMD_OK) return st;
+    if ((flags & ~(RIBN_AMD_FUSE_SWIGLU | RIBN_AMD_FUSE_ACCUMULATE)) != 0) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, 0, flags, "unknown fusion flags 0x%x", flags);
+    }
+    const bool swiglu = (flags & RIBN_AMD_FUSE_SWIGLU) != 0;
+    if (swiglu && gamma != nullptr) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "the SwiGLU and RMSNorm prologues do not combine");
+    }
+    uint64_t k, n;
+    st = validate_launch(g, w, input, input_len, output, output_len, members, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    if (swiglu) {
+        st = check_device_ptr(g->ctx, up, "up");
+        if (st != RIBN_AMD_OK) return st;
+    }
+    if (gamma != nullptr) {
+        st = check_device_ptr(g->ctx, gamma, "gamma");
+        if (st != RIBN_AMD_OK) return st;
+        if (gamma_len != k) {
+            return fail(RIBN_AMD_WEIGHT_LENGTH, k, gamma_len, "RMSNorm weight has %zu values, expected %llu", gamma_len,
+                        (unsigned long long)k);
+        }
+        st = check_epsilon(epsilon);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    const ribn_amd_quantized_weight* ws[1] = {w};
+    float* outs[1] = {output};
+    return launch_wave_group(g, ws, 1, input, gamma, epsilon, outs, k, members, swiglu ? up : nullptr,
+                             (flags & RIBN_AMD_FUSE_ACCUMULATE) != 0);
 }
 
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, float* output,

@@ -259,6 +259,18 @@ class _AmdQuantizedGemv:
         _check(self._lib.ribn_amd_gemv_execute_group(self.handle, wh, n, _ptr(input), input.numel(), g, gl,
                                                      epsilon, oh, ol, members))
 
+    def execute_fused(self, weight, input, output, members: int = 1, up=None, gamma=None, epsilon: float = 1e-6,
+                      accumulate: bool = False):
+        """execute_warp_batch with the decode step's neighbours fused: `up` given,
+        the activation is silu(input) * up; `accumulate`, output += W x; `gamma`
+        given, the RMSNorm prologue."""
+        flags = (1 if up is not None else 0) | (2 if accumulate else 0)
+        g = _ptr(gamma) if gamma is not None else None
+        gl = gamma.numel() if gamma is not None else 0
+        u = _ptr(up) if up is not None else None
+        _check(self._lib.ribn_amd_gemv_execute_fused(self.handle, weight.handle, _ptr(input), u, input.numel(), g,
+                                                     gl, epsilon, _ptr(output), output.numel(), members, flags))
+
     def gemm_prefill(self, weight, input, output, members: int, gamma=None, epsilon: float = 1e-6):
         """y[members][N] = x[members][K] W^T on the matrix cores; x is f32 or bf16.
         Needs AmdContext.reserve_prefill(members, K) beforehand."""
@@ -386,6 +398,16 @@ class AmdQwenOps:
         _check(self._lib.ribn_amd_rms_norm_batch(self.ctx.handle, _ptr(input), input.numel(), _ptr(weight),
                                                  weight.numel(), _ptr(output), output.numel(), length,
                                                  epsilon), AmdModelKernelError)
+
+    def argmax_into(self, logits, selected):
+        """argmax_into (model_ops.rs:1583-1620): selected[0] = greedy index of logits."""
+        _check(self._lib.ribn_amd_argmax(self.ctx.handle, _ptr(logits), logits.numel(), logits.numel(),
+                                         _ptr(selected)), AmdModelKernelError)
+
+    def argmax_into_batch(self, logits, length: int, selected):
+        """argmax_into_batch (model_ops.rs:1634-1674): one selection per row of `length`."""
+        _check(self._lib.ribn_amd_argmax(self.ctx.handle, _ptr(logits), logits.numel(), length, _ptr(selected)),
+               AmdModelKernelError)
 
 
 def validate_quantized_geometry(kernel_value_type: int, weight_value_type: int, dims, encoded_bytes: int):

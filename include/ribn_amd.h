@@ -67,6 +67,9 @@ typedef enum ribn_amd_status {
     RIBN_AMD_EMPTY_ENCODING = 13,        /* CudaWeightError::EmptyEncoding (cuda.rs:335-337) */
     RIBN_AMD_SOURCE_INCOMPLETE = 14,     /* CudaWeightError::SourceIncomplete (cuda.rs:350-356) */
     RIBN_AMD_WORKSPACE_TOO_SMALL = 15,   /* prefill workspace not reserved (no reference twin) */
+    RIBN_AMD_INVALID_PLAN = 16,          /* CudaDecodeError::InvalidPlan (decode.rs:91-93) */
+    RIBN_AMD_POSITION_OVERFLOW = 17,     /* CudaDecodeError::PositionOverflow { position, capacity } */
+    RIBN_AMD_MISSING_TENSOR = 18,        /* CudaDecodeError::MissingTensor (decode.rs:86-87) */
 } ribn_amd_status;
 
 typedef struct ribn_amd_error {
@@ -200,6 +203,24 @@ ribn_amd_status ribn_amd_gemv_execute_group(ribn_amd_gemv *gemv, const ribn_amd_
                                             size_t count, const float *input, size_t input_len,
                                             const float *gamma, size_t gamma_len, float epsilon,
                                             float *const *outputs, const size_t *output_lens, size_t members);
+/* Fusion flags of ribn_amd_gemv_execute_fused. */
+#define RIBN_AMD_FUSE_SWIGLU 1u     /* activation = silu(input) * up */
+#define RIBN_AMD_FUSE_ACCUMULATE 2u /* output += W activation (residual add) */
+/* execute_warp_batch with the decode step's elementwise neighbours fused in;
+ * no single reference counterpart. The reference runs them as separate
+ * launches around gemv (decode.rs:596-631,1021-1031):
+ *   RIBN_AMD_FUSE_SWIGLU: the activation is silu(input) * up, the
+ *     reference's silu_mul (model_ops.rs:316-328, 1888-1929); `up` holds
+ *     input_len values (members <= RIBN_AMD_MAX_BATCH_MEMBERS, launched in
+ *     pairs).
+ *   RIBN_AMD_FUSE_ACCUMULATE: output += W x (residual_add, model_ops.rs:600-611,
+ *     2314-2350); each output element is added exactly once.
+ *   gamma != NULL: the RMSNorm prologue of execute_rms_norm (not with SWIGLU).
+ * Every row is computed as execute_warp_batch computes it. */
+ribn_amd_status ribn_amd_gemv_execute_fused(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
+                                            const float *input, const float *up, size_t input_len,
+                                            const float *gamma, size_t gamma_len, float epsilon, float *output,
+                                            size_t output_len, size_t members, uint32_t flags);
 /* Bit-exact device dequantisation to f32 [N][K] (twin of lib.rs:596-661;
  * the reference's device equivalent is the q4_k_embedding gather, q4_k.cu:1-67). */
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight, float *output,
@@ -259,6 +280,121 @@ ribn_amd_status ribn_amd_rms_norm(ribn_amd_context *ctx, const float *input, siz
 ribn_amd_status ribn_amd_rms_norm_batch(ribn_amd_context *ctx, const float *input, size_t input_len,
                                         const float *weight, size_t weight_len, float *output,
                                         size_t output_len, size_t length, float epsilon);
+
+/* ------------------------------------------------------ Qwen3 decode step */
+
+typedef struct ribn_amd_kv_cache ribn_amd_kv_cache;
+typedef struct ribn_amd_qwen3_decode ribn_amd_qwen3_decode;
+
+/* Decoder geometry. Qwen3-8B: 36 layers, hidden 4096, 32 query / 8 KV heads
+ * of 128, FFN 12288, vocab 151936, rope base 1e6, RMSNorm eps 1e-6. */
+typedef struct ribn_amd_qwen3_config {
+    uint32_t layers;
+    uint32_t hidden;
+    uint32_t q_heads;
+    uint32_t kv_heads;
+    uint32_t head_dim; /* 128 */
+    uint32_t ffn;
+    uint32_t vocab;
+    float rope_base;
+    float epsilon;
+} ribn_amd_qwen3_config;
+
+/* One layer's tensors: the reference's full-attention layer
+ * (FULL_ATTENTION_LAYER_TENSORS, decode.rs:62-74) without a q gate, as Qwen3
+ * has none. Weights are GGML [K, N] k-quant tensors; norm weights are device
+ * f32 vectors, used as stored (GGUF keeps them already +1'd,
+ * qwen_reference.rs:383). */
+typedef struct ribn_amd_qwen3_layer {
+    const ribn_amd_quantized_weight *attn_q;      /* [hidden, q_heads*head_dim] */
+    const ribn_amd_quantized_weight *attn_k;      /* [hidden, kv_heads*head_dim] */
+    const ribn_amd_quantized_weight *attn_v;      /* [hidden, kv_heads*head_dim] */
+    const ribn_amd_quantized_weight *attn_output; /* [q_heads*head_dim, hidden] */
+    const ribn_amd_quantized_weight *ffn_gate;    /* [hidden, ffn] */
+    const ribn_amd_quantized_weight *ffn_up;      /* [hidden, ffn] */
+    const ribn_amd_quantized_weight *ffn_down;    /* [ffn, hidden] */
+    const float *attn_norm;                       /* [hidden] */
+    const float *attn_q_norm;                     /* [head_dim] */
+    const float *attn_k_norm;                     /* [head_dim] */
+    const float *ffn_norm;                        /* [hidden] (post_attention_norm) */
+} ribn_amd_qwen3_layer;
+
+/* The KV part of the reference's per-sequence state (CudaKvState,
+ * state.rs:99-254, inside CudaHybridState 529-660; F16 caches as
+ * decode.rs:1000-1011 requires): f16 keys and
+ * values of every layer for `capacity` tokens, laid out
+ * [layer][kv_head][token][head_dim] so a KV head's tokens are contiguous, plus
+ * the sequence's attention scratch. The one allocating call of a sequence. */
+ribn_amd_status ribn_amd_kv_cache_create(ribn_amd_context *ctx, const ribn_amd_qwen3_config *config,
+                                         uint32_t capacity, ribn_amd_kv_cache **out);
+void ribn_amd_kv_cache_destroy(ribn_amd_kv_cache *cache);
+uint32_t ribn_amd_kv_cache_capacity(const ribn_amd_kv_cache *cache);
+/* Device views of one layer's f16 caches, [kv_heads][capacity][head_dim]
+ * each (for staging a context or inspecting the cache). */
+ribn_amd_status ribn_amd_kv_cache_layer(ribn_amd_kv_cache *cache, uint32_t layer, uint16_t **keys,
+                                        uint16_t **values);
+
+/* One layer's decode attention for `members` sequences, fusing the
+ * reference's per-layer sequence (decode.rs:944-1020): per-head q/k RMSNorm
+ * (q_gate_norm / strided_rms_norm, model_ops.rs:3784-3839, 2475-2529), NEOX
+ * rope of q and k (rope_neox, 2012-2070), the f16 append of the new K/V at
+ * `positions[m]` (kv_append_f16, 3854-3922) and GQA attention over tokens
+ * 0..positions[m] (attn_score_gqa, 2135-2220). q is [members][q_heads*128],
+ * k and v [members][kv_heads*128] (raw projections), positions a device
+ * int32 array, output [members][q_heads*128]. */
+ribn_amd_status ribn_amd_attention_decode(ribn_amd_context *ctx, const ribn_amd_qwen3_config *config,
+                                          ribn_amd_kv_cache *const *caches, size_t members, uint32_t layer,
+                                          const float *q, const float *k, const float *v, const float *q_norm,
+                                          const float *k_norm, const int32_t *positions, float *output,
+                                          size_t output_len);
+
+/* CudaQwen35Ops::argmax_into / argmax_into_batch (model_ops.rs:1583-1674):
+ * selected[m] = the first index of the largest non-NaN value of
+ * logits[m*length .. (m+1)*length) (device u32 array). */
+ribn_amd_status ribn_amd_argmax(ribn_amd_context *ctx, const float *logits, size_t logits_len, size_t length,
+                                uint32_t *selected);
+
+/* CudaQwen35Decode::new (decode.rs:412-475) and CudaQwen35BatchDecode::new
+ * (1660-1690) in one: validates the plan (geometry of every tensor, non-null
+ * norms) and allocates the step's device buffers for up to `max_members`
+ * sequences (<= 64). Weights stay owned by the caller. `layers` is a host
+ * array of config->layers entries, copied. */
+ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context *ctx, const ribn_amd_qwen3_config *config,
+                                             const ribn_amd_quantized_weight *token_embd,
+                                             const ribn_amd_quantized_weight *output, const float *output_norm,
+                                             const ribn_amd_qwen3_layer *layers, uint32_t max_members,
+                                             ribn_amd_qwen3_decode **out);
+void ribn_amd_qwen3_decode_destroy(ribn_amd_qwen3_decode *decode);
+/* Steps are captured once per shape (members, caches, head or not) as HIP
+ * graphs and replayed (default); disabled, every step launches its kernels
+ * directly. Both run the same kernels with the same arguments. */
+ribn_amd_status ribn_amd_qwen3_decode_set_graphs(ribn_amd_qwen3_decode *decode, int32_t enabled);
+/* CudaQwen35Decode::prefill_step (decode.rs:489-499): advances `cache` by
+ * `token` at `position` without the output head. */
+ribn_amd_status ribn_amd_qwen3_prefill_step(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
+                                            uint32_t token, uint32_t position);
+/* CudaQwen35Decode::decode_step (decode.rs:508-516): one forward pass and the
+ * greedy token (blocking, as the reference). */
+ribn_amd_status ribn_amd_qwen3_decode_step(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
+                                           uint32_t token, uint32_t position, uint32_t *selected);
+/* CudaQwen35BatchDecode::decode_step_batch (decode.rs:1859-1872): one step for
+ * `members` sequences (distinct caches); selected[m] per member. Every
+ * member's result equals its single-sequence decode_step bit for bit. */
+ribn_amd_status ribn_amd_qwen3_decode_step_batch(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *const *caches,
+                                                 const uint32_t *tokens, const uint32_t *positions, size_t members,
+                                                 uint32_t *selected);
+/* Greedy generation of `steps` tokens per member with no host round trip
+ * between steps (no reference counterpart: the reference's driver calls
+ * decode_step per token). Member m starts from tokens[m] at positions[m];
+ * out_tokens is a host [members][steps] array. Equal to `steps` calls of
+ * decode_step_batch feeding each selection back. */
+ribn_amd_status ribn_amd_qwen3_generate(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *const *caches,
+                                        const uint32_t *tokens, const uint32_t *positions, size_t members,
+                                        uint32_t steps, uint32_t *out_tokens);
+/* copy_hidden / copy_logits (decode.rs:764-784, 1924-1930): a member's
+ * residual stream [hidden] or logits [vocab] after the last step, to host. */
+ribn_amd_status ribn_amd_qwen3_copy_hidden(ribn_amd_qwen3_decode *decode, size_t member, float *host, size_t len);
+ribn_amd_status ribn_amd_qwen3_copy_logits(ribn_amd_qwen3_decode *decode, size_t member, float *host, size_t len);
 
 #ifdef __cplusplus
 }

@@ -372,6 +372,171 @@ void oracle_swiglu(const float *gate, const float *up, size_t len, float *out)
     }
 }
 
+/*
+ * f32 -> IEEE binary16 bits, round to nearest even: the conversion the
+ * reference's device KV append applies (crates/nvidia/src/model_ops.rs
+ * :1211-1250 f32_to_f16_bits). Restated from the IEEE 754 definition; NaN
+ * keeps its sign and becomes the quiet NaN 0x7e00 as in the reference.
+ */
+uint16_t oracle_f32_to_f16_bits(float value)
+{
+    uint32_t bits;
+    memcpy(&bits, &value, sizeof bits);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const uint32_t biased = (bits >> 23) & 0xffu;
+    const uint32_t frac = bits & 0x7fffffu;
+    if (biased == 0xffu) return (uint16_t)(sign | 0x7c00u | (frac ? 0x0200u : 0u));
+    const int e = (int)biased - 127; /* unbiased exponent of a normal f32 */
+    if (e > 15) return (uint16_t)(sign | 0x7c00u);
+    /* the value's magnitude is m * 2^(e-23) with m the 24-bit significand */
+    const uint32_t m = biased ? (frac | 0x800000u) : frac;
+    /* target unit: 2^-24 for subnormal halves (e < -14), else 2^(e-10) */
+    const int unit_exp = e < -14 ? -24 : e - 10;
+    const int shift = (biased ? e - 23 : -149) - unit_exp; /* m * 2^shift units */
+    uint32_t q;
+    if (shift >= 0) {
+        q = m << shift;
+    } else if (shift < -25) {
+        q = 0;
+    } else {
+        const int r = -shift;
+        q = m >> r;
+        const uint32_t rem = m & ((1u << r) - 1u);
+        const uint32_t half = 1u << (r - 1);
+        if (rem > half || (rem == half && (q & 1u))) q += 1u;
+    }
+    if (e < -14) {
+        /* subnormal half: q counts 2^-24; q == 1024 rounds up into the normals */
+        return (uint16_t)(sign | q);
+    }
+    /* normal half: q in [1024, 2048]; 2048 carries into the exponent */
+    int he = e + 15;
+    if (q >= 2048u) {
+        q >>= 1;
+        he += 1;
+    }
+    if (he >= 31) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | ((uint32_t)he << 10) | (q & 0x3ffu));
+}
+
+/*
+ * NEOX rope over `heads` heads of head_dim values: pair (p, p + rot_dims/2)
+ * of the first rot_dims dims rotates by theta_p = pos * base^(-2p/rot_dims)
+ * (crates/nvidia/src/qwen_reference.rs:403-419 apply_rope, with the pair stride
+ * rot_dims/2 that rope_neox uses for any rot_dims, model_ops.rs:393-425).
+ */
+void oracle_rope_neox(float *values, size_t heads, size_t head_dim, size_t rot_dims, size_t pos,
+                      float base)
+{
+    const size_t half = rot_dims / 2;
+    for (size_t head = 0; head < heads; ++head) {
+        const size_t b = head * head_dim;
+        for (size_t pair = 0; pair < half; ++pair) {
+            const float theta = (float)pos * powf(base, -(2.0f * (float)pair) / (float)rot_dims);
+            const float sn = sinf(theta), cs = cosf(theta);
+            const float x0 = values[b + pair];
+            const float x1 = values[b + half + pair];
+            values[b + pair] = x0 * cs - x1 * sn;
+            values[b + half + pair] = x0 * sn + x1 * cs;
+        }
+    }
+}
+
+/*
+ * One decode step's attention for a Qwen3 layer:
+ * crates/nvidia/src/qwen_reference.rs:368-455 host_full_attn_ar_step_traced with
+ * Qwen3's geometry (no q gate: q_raw is [q_heads][head_dim]; full-width rope)
+ * and the device decode's F16 cache (decode.rs:997-1033: kv_append_f16 then
+ * attention over the F16 cache).
+ *   per-head RMSNorm of q and k (rms_norm_raw with the shared head weight),
+ *   rope of q and k at `pos`,
+ *   kv_keys/kv_values[pos] = f16(k), f16(v)    ([capacity][kv_heads][head_dim]),
+ *   out[h] = softmax(q_h . K_t * scale) . V_t over t = 0..pos, KV head h / (q_heads / kv_heads).
+ * q_scratch and k_scratch hold q_heads*head_dim and kv_heads*head_dim floats.
+ */
+int oracle_qwen3_attention(const float *q_raw, const float *k_raw, const float *v_raw,
+                           const float *q_norm, const float *k_norm, float eps, float rope_base,
+                           size_t q_heads, size_t kv_heads, size_t head_dim, size_t pos,
+                           uint16_t *kv_keys, uint16_t *kv_values, size_t capacity,
+                           float *out)
+{
+    if (q_heads == 0 || kv_heads == 0 || q_heads % kv_heads || head_dim == 0 || head_dim > 65535 ||
+        pos >= capacity) {
+        return ORACLE_BAD_ARGUMENT;
+    }
+    float *q = malloc(q_heads * head_dim * sizeof *q);
+    float *k = malloc(kv_heads * head_dim * sizeof *k);
+    float *scores = malloc((pos + 1) * sizeof *scores);
+    float *exps = malloc((pos + 1) * sizeof *exps);
+    if (!q || !k || !scores || !exps) {
+        free(q); free(k); free(scores); free(exps);
+        return ORACLE_BAD_ARGUMENT;
+    }
+    for (size_t h = 0; h < q_heads; ++h) {
+        oracle_rms_norm_raw(q_raw + h * head_dim, q_norm, head_dim, eps, q + h * head_dim);
+    }
+    for (size_t h = 0; h < kv_heads; ++h) {
+        oracle_rms_norm_raw(k_raw + h * head_dim, k_norm, head_dim, eps, k + h * head_dim);
+    }
+    oracle_rope_neox(q, q_heads, head_dim, head_dim, pos, rope_base);
+    oracle_rope_neox(k, kv_heads, head_dim, head_dim, pos, rope_base);
+    const size_t row = kv_heads * head_dim;
+    for (size_t i = 0; i < row; ++i) {
+        kv_keys[pos * row + i] = oracle_f32_to_f16_bits(k[i]);
+        kv_values[pos * row + i] = oracle_f32_to_f16_bits(v_raw[i]);
+    }
+    const size_t tokens = pos + 1;
+    const size_t q_per_kv = q_heads / kv_heads;
+    /* 1.0 / f32::sqrt(f32::from(head_dim)) */
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    for (size_t qh = 0; qh < q_heads; ++qh) {
+        const size_t kvh = qh / q_per_kv;
+        const float *qv = q + qh * head_dim;
+        for (size_t t = 0; t < tokens; ++t) {
+            const uint16_t *key = kv_keys + (t * kv_heads + kvh) * head_dim;
+            float dot = -0.0f;
+            for (size_t d = 0; d < head_dim; ++d) dot += qv[d] * oracle_f16_to_f32(key[d]);
+            scores[t] = dot * scale;
+        }
+        float mx = -INFINITY;
+        for (size_t t = 0; t < tokens; ++t) mx = fmaxf(mx, scores[t]);
+        float total = -0.0f;
+        for (size_t t = 0; t < tokens; ++t) {
+            exps[t] = expf(scores[t] - mx);
+            total += exps[t];
+        }
+        float *o = out + qh * head_dim;
+        for (size_t d = 0; d < head_dim; ++d) o[d] = 0.0f;
+        for (size_t t = 0; t < tokens; ++t) {
+            const uint16_t *value = kv_values + (t * kv_heads + kvh) * head_dim;
+            const float weight = exps[t] / total;
+            for (size_t d = 0; d < head_dim; ++d) o[d] += weight * oracle_f16_to_f32(value[d]);
+        }
+    }
+    free(q); free(k); free(scores); free(exps);
+    return ORACLE_OK;
+}
+
+/* decode.rs:655-677 argmax_into: first index of the largest non-NaN value
+ * (model_ops.rs:201-258 key order: -0.0 ranks below +0.0). */
+size_t oracle_argmax(const float *logits, size_t len)
+{
+    uint32_t best_key = 0;
+    size_t best = 0;
+    for (size_t i = 0; i < len; ++i) {
+        const float v = logits[i];
+        if (v != v) continue;
+        uint32_t bits;
+        memcpy(&bits, &v, sizeof bits);
+        const uint32_t key = (bits >> 31) ? ~bits : (bits ^ 0x80000000u);
+        if (key > best_key) {
+            best_key = key;
+            best = i;
+        }
+    }
+    return best;
+}
+
 static double now_seconds(void)
 {
     struct timespec ts;

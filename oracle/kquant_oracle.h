@@ -100,6 +100,28 @@ int oracle_rms_norm_raw(const float *input, const float *weight, size_t len, flo
 /* qwen_reference.rs:529-539 SwiGLU composition g/(1+exp(-g))*u. */
 void oracle_swiglu(const float *gate, const float *up, size_t len, float *out);
 
+/* model_ops.rs:1211-1250 f32_to_f16_bits: IEEE binary16, round to nearest even. */
+uint16_t oracle_f32_to_f16_bits(float value);
+
+/* qwen_reference.rs:403-419 NEOX rope (pair stride rot_dims/2, theta_p = pos*base^(-2p/rot_dims)). */
+void oracle_rope_neox(float *values, size_t heads, size_t head_dim, size_t rot_dims, size_t pos,
+                      float base);
+
+/*
+ * qwen_reference.rs:368-455 one attention step, Qwen3 geometry (no q gate), F16
+ * cache as the device decode keeps it (decode.rs:997-1033). Caches are
+ * [capacity][kv_heads][head_dim] binary16 bits; the step writes slot `pos` and
+ * attends over 0..pos. out is [q_heads][head_dim].
+ */
+int oracle_qwen3_attention(const float *q_raw, const float *k_raw, const float *v_raw,
+                           const float *q_norm, const float *k_norm, float eps, float rope_base,
+                           size_t q_heads, size_t kv_heads, size_t head_dim, size_t pos,
+                           uint16_t *kv_keys, uint16_t *kv_values, size_t capacity,
+                           float *out);
+
+/* model_ops.rs:201-258 argmax: first index of the largest non-NaN value. */
+size_t oracle_argmax(const float *logits, size_t len);
+
 /*
  * Times the CPU baseline (dequantize_block + sequential f32 dot per row) with
  * steady-clock timing: `warmup` untimed runs, then `iters` timed runs. Writes

@@ -58,6 +58,17 @@ def lib():
         l.oracle_rms_norm_raw.argtypes = [f32p, f32p, ctypes.c_size_t, ctypes.c_float, f32p]
         l.oracle_swiglu.argtypes = [f32p, f32p, ctypes.c_size_t, f32p]
         l.oracle_swiglu.restype = None
+        u16p = ctypes.POINTER(ctypes.c_uint16)
+        l.oracle_f32_to_f16_bits.restype = ctypes.c_uint16
+        l.oracle_f32_to_f16_bits.argtypes = [ctypes.c_float]
+        l.oracle_rope_neox.restype = None
+        l.oracle_rope_neox.argtypes = [f32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                       ctypes.c_size_t, ctypes.c_float]
+        l.oracle_qwen3_attention.argtypes = [f32p, f32p, f32p, f32p, f32p, ctypes.c_float, ctypes.c_float,
+                                             ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                             ctypes.c_size_t, u16p, u16p, ctypes.c_size_t, f32p]
+        l.oracle_argmax.restype = ctypes.c_size_t
+        l.oracle_argmax.argtypes = [f32p, ctypes.c_size_t]
         l.oracle_time_quant_gemv.argtypes = [ctypes.c_uint32, u8p, ctypes.c_size_t,
                                              ctypes.c_size_t, ctypes.c_size_t, f32p, f32p,
                                              ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -193,3 +204,36 @@ def time_quant_gemv(value_type, encoded, k, n, x, threads=1, warmup=3, iters=20)
     if st != OK:
         raise OracleError(st)
     return med.value, mn.value, y
+
+
+def f32_to_f16_bits(value: float) -> int:
+    return int(lib().oracle_f32_to_f16_bits(value))
+
+
+def rope_neox(values: np.ndarray, heads: int, head_dim: int, rot_dims: int, pos: int,
+              base: float) -> np.ndarray:
+    out = np.ascontiguousarray(values, dtype=np.float32).copy()
+    lib().oracle_rope_neox(_f32(out), heads, head_dim, rot_dims, pos, base)
+    return out
+
+
+def qwen3_attention(q, k, v, q_norm, k_norm, eps, rope_base, q_heads, kv_heads, head_dim, pos,
+                    kv_keys: np.ndarray, kv_values: np.ndarray) -> np.ndarray:
+    """One attention step; kv_keys / kv_values ([capacity][kv_heads][head_dim]
+    uint16 binary16 bits) are updated in place at `pos`."""
+    arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, q_norm, k_norm)]
+    assert kv_keys.dtype == np.uint16 and kv_keys.flags.c_contiguous
+    assert kv_values.dtype == np.uint16 and kv_values.flags.c_contiguous
+    out = np.zeros(q_heads * head_dim, np.float32)
+    u16 = ctypes.POINTER(ctypes.c_uint16)
+    st = lib().oracle_qwen3_attention(*[_f32(a) for a in arrs], eps, rope_base, q_heads, kv_heads,
+                                      head_dim, pos, kv_keys.ctypes.data_as(u16),
+                                      kv_values.ctypes.data_as(u16), kv_keys.shape[0], _f32(out))
+    if st != OK:
+        raise OracleError(st)
+    return out
+
+
+def argmax(logits: np.ndarray) -> int:
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    return int(lib().oracle_argmax(_f32(x), x.size))
