@@ -179,6 +179,72 @@ def cpu_baseline(seconds_budget=12.0):
 
 
 PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense f16/bf16
+KV_BYTES_PER_TOKEN = 36 * 8 * 128 * 2 * 2  # f16 K and V of every layer: 147,456 B
+
+
+def build_decoder(E, synth, torch, ctx, step, out_gamma, layers, seed, members):
+    """The full Qwen3-8B-shaped decoder over the step's weights:
+    adds a Q4_K token_embd table and per-head q/k norms; random-init, seeded."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed + 1)
+    if step.store.quantized_tensor("token_embd") is None:
+        step.store.materialize_quantized("token_embd", [HIDDEN, VOCAB], 12,
+                                         synth.kquant_torch(12, HIDDEN, VOCAB, gen, dev))
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
+             "up": "ffn_up", "down": "ffn_down"}
+    plan = []
+    for entry in step.layers[:layers]:
+        lw = {names[n]: entry[n][0] for n in names}
+        lw["attn_norm"] = entry["attn_gamma"]
+        lw["ffn_norm"] = entry["ffn_gamma"]
+        lw["attn_q_norm"] = 1.0 + 0.02 * torch.randn(128, device=dev, generator=gen)
+        lw["attn_k_norm"] = 1.0 + 0.02 * torch.randn(128, device=dev, generator=gen)
+        plan.append(lw)
+    cfg = E.AmdQwen3Config(layers=layers)
+    return E.AmdQwen3Decode(ctx, cfg, step.store.quantized_tensor("token_embd"), step.head, out_gamma, plan,
+                            members), cfg
+
+
+def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed):
+    """Prefills `context` prompt tokens per member, then times `gen_tokens`
+    greedy steps of the graph-replayed generation loop (wall clock, which
+    includes the step's host work)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    prompts = rng.integers(0, VOCAB, size=(members, context))
+    caches = [E.AmdKvCache(ctx, cfg, context + gen_tokens) for _ in range(members)]
+    t0 = time.perf_counter()
+    for p in range(context - 1):
+        if members == 1:
+            dec.prefill_step(caches[0], int(prompts[0, p]), p)
+        else:
+            dec.decode_step_batch(caches, prompts[:, p], [p] * members)
+    ctx.synchronize()
+    prefill_s = time.perf_counter() - t0
+    last = prompts[:, context - 1]
+    start = [context - 1] * members
+    dec.generate(caches, last, start, 1)  # captures the loop's graph; rewrites slot context-1 identically
+    t0 = time.perf_counter()
+    out = dec.generate(caches, last, start, gen_tokens)
+    dt = time.perf_counter() - t0
+    kv_read = sum((context + s) * KV_BYTES_PER_TOKEN * cfg.layers // 36 for s in range(gen_tokens)) / gen_tokens
+    return {"members": members, "context": context, "generated": gen_tokens,
+            "tok_s": round(members * gen_tokens / dt, 1), "ms_per_step": round(dt * 1e3 / gen_tokens, 4),
+            "prefill_s": round(prefill_s, 2), "kv_bytes_per_step": int(kv_read * members),
+            "distinct_tokens": int(len(set(out.reshape(-1).tolist())))}
+
+
+def model_decode_results(E, synth, torch, ctx, step, out_gamma, args):
+    dec, cfg = build_decoder(E, synth, torch, ctx, step, out_gamma, args.layers, args.seed, 8)
+    res = {}
+    for members in (1, 8):
+        r = time_model_decode(E, dec, cfg, ctx, members, args.context, args.gen_tokens, args.seed + members)
+        log(f"bench model: batch {members}: {r['tok_s']} tok/s ({r['ms_per_step']} ms/step, "
+            f"prefill {r['prefill_s']} s)")
+        res[members] = r
+    dec.close()
+    return res
 
 
 def _graph_time_us(torch, stream, fn, reps):
@@ -307,6 +373,27 @@ def bench_prefill(E, synth, torch, args):
     }
 
 
+def bench_model(E, synth, torch, ctx, step, out_gamma, args):
+    """BASELINE config 4 alone: the full Qwen3-8B-shaped decoder at batch 1 and 8."""
+    res = model_decode_results(E, synth, torch, ctx, step, out_gamma, args)
+    b1 = res[1]
+    weight_bytes = step.bytes_per_step + HIDDEN // 256 * 144  # + one embedding row
+    bytes_tok = weight_bytes + b1["kv_bytes_per_step"]
+    achieved = bytes_tok * b1["tok_s"] / 1e9
+    return {
+        "metric": "Qwen3-8B-shaped Q4_K batch-1 decode tok/s (BASELINE config 4)",
+        "value": b1["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.gen_tokens, "warmup": 1,
+        "ms_per_step": b1["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "i8dot4-f32 GEMV, f16 KV, f32 attention", "data": "synthetic",
+        "config": {"workload": "qwen3-8b-decode-model", "layers": args.layers, "context": args.context,
+                   "generated": args.gen_tokens, "batches": res},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "whole decode step (weights + KV cache per token)", "bytes_per_token": bytes_tok},
+        "cpu_baseline": None,
+    }
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_wave_q4k_gate_up_traffic.md")
 
 
@@ -349,9 +436,13 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="issue launches eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "batched", "prefill"), default="decode",
-                    help="decode: BASELINE config 1 (the headline line, default); batched: config 2 "
-                         "(FFN at M = 1, 4, 16, 64); prefill: config 3 (M = 512 bf16 matmuls)")
+    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model"), default="decode",
+                    help="decode: BASELINE config 1 (the headline line, default, which also carries the "
+                         "config-4 tok/s); batched: config 2 (FFN at M = 1, 4, 16, 64); prefill: config 3 "
+                         "(M = 512 bf16 matmuls); model: config 4 alone (full decoder, batch 1 and 8)")
+    ap.add_argument("--context", type=int, default=2048, help="config 4: prompt tokens before generation")
+    ap.add_argument("--gen-tokens", type=int, default=128, help="config 4: greedy tokens timed")
+    ap.add_argument("--no-model", action="store_true", help="skip the config-4 full-decoder measurement")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed work, copy a MIB-MiB device buffer three times: a kernel of known "
                          "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE onto bytes")
@@ -370,7 +461,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    if args.workload != "decode":
+    if args.workload in ("batched", "prefill"):
         result = (bench_batched if args.workload == "batched" else bench_prefill)(E, synth, torch, args)
         print(json.dumps(result), flush=True)
         return
@@ -381,6 +472,10 @@ def main():
     ctx = E.AmdContext(0, stream=stream)
     step = DecodeGemvStep(E, torch, ctx, weights, head, out_gamma, acts)
     log(f"bench: {step.bytes_per_step / 1e9:.3f} GB of algorithmic traffic per step")
+
+    if args.workload == "model":
+        print(json.dumps(bench_model(E, synth, torch, ctx, step, out_gamma, args)), flush=True)
+        return
 
     with torch.cuda.stream(stream):
         step.run()  # eager warm-up (and validation of every launch)
@@ -445,6 +540,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
 
+    model = None
+    if not args.no_model:
+        model = model_decode_results(E, synth, torch, ctx, step, out_gamma, args)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: timing the CPU baseline")
@@ -465,7 +564,12 @@ def main():
         "dtype": "i8dot4-f32",
         "data": "synthetic",
         "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
-        "decode_tok_s": round(1000.0 / ms_step, 2),
+        # the full decoder (embedding, 36 layers with attention
+        # over a 2048-token f16 KV cache, lm_head, argmax), greedy, graph-replayed
+        "decode_tok_s": model[1]["tok_s"] if model else None,
+        "decode_tok_s_b8": model[8]["tok_s"] if model else None,
+        "decode_model": model,
+        "gemv_chain_tok_s": round(1000.0 / ms_step, 2),
         "config": {
             "workload": "qwen3-8b-decode-gemv-b1",
             "layers": args.layers,

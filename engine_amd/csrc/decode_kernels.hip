@@ -17,10 +17,10 @@
 // of V), and keeps an online-softmax state (running max, denominator and
 // output sums) per query head. The 16 states of a workgroup are merged across
 // rows with lane shuffles and across waves in LDS into one partial per
-// (chunk, head); the last workgroup of a (member, KV
-// head) to finish (an atomic ticket) merges the kAttnChunks partials into the
-// output. The new token's K/V are computed by the workgroup whose chunk holds
-// the position: written to the cache, and used from LDS by that workgroup.
+// (chunk, head); attn_combine_kernel then merges the kAttnChunks partials of
+// each (member, head) into the output. The new token's K/V are computed by the
+// workgroup whose chunk holds the position: written to the cache, and used
+// from LDS by that workgroup.
 //
 // argmax_kernel: greedy selection (argmax, model_ops.rs:201-258) with the
 // same ordering key, tie rule and NaN rule.
@@ -82,9 +82,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     __shared__ float st_m[kWaves][QPK];
     __shared__ float st_l[kWaves][QPK];
     __shared__ float st_o[kWaves][QPK][kHeadDim];
-    __shared__ float cm[kAttnChunks][QPK];
-    __shared__ float cl[kAttnChunks][QPK];
-    __shared__ int last_s;
 
     const int chunk = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -255,10 +252,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
-    float* part = mb.partials + ((size_t)kvh * kAttnChunks + chunk) * QPK * kPartStride;
     for (int idx = tid; idx < QPK * kHeadDim; idx += kThreads) {
         const int h = idx / kHeadDim;
         const int d = idx - h * kHeadDim;
+        float* part = mb.partials + ((size_t)(kvh * QPK + h) * kAttnChunks + chunk) * kPartStride;
         float mx = -FLT_MAX;
 #pragma unroll
         for (int q = 0; q < kWaves; ++q) mx = fmaxf(mx, st_m[q][h]);
@@ -269,43 +266,46 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
             l = __builtin_fmaf(st_l[q][h], f, l);
             acc = __builtin_fmaf(st_o[q][h][d], f, acc);
         }
-        part[h * kPartStride + d] = acc;
+        part[d] = acc;
         if (d == 0) {
-            part[h * kPartStride + kHeadDim] = mx;
-            part[h * kPartStride + kHeadDim + 1] = l;
+            part[kHeadDim] = mx;
+            part[kHeadDim + 1] = l;
         }
     }
 
-    // ---- the last chunk of this (member, KV head) to finish merges all chunks
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last_s = atomicAdd(&mb.counters[kvh], 1u) == (uint32_t)(kAttnChunks - 1);
-    __syncthreads();
-    if (!last_s) return;
-    __threadfence();
-    const float* pbase = mb.partials + (size_t)kvh * kAttnChunks * QPK * kPartStride;
-    for (int i = tid; i < kAttnChunks * QPK; i += kThreads) {
-        const int c = i / QPK;
-        const int h = i - c * QPK;
-        cm[c][h] = pbase[(c * QPK + h) * kPartStride + kHeadDim];
-        cl[c][h] = pbase[(c * QPK + h) * kPartStride + kHeadDim + 1];
+}
+
+// Merges the kAttnChunks partials of one (member, query head) into the
+// attention output: o = sum_c O_c e^(m_c - M) / sum_c L_c e^(m_c - M).
+// A separate launch: the kernel boundary orders the partials' writes before
+// these reads, where an in-kernel hand-off would need a device-scope release
+// (an L2 write-back) in every attention workgroup.
+static_assert(kAttnChunks <= kHeadDim, "one combine thread per chunk loads its maximum");
+__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(AttnArgs a) {
+    const int qh = blockIdx.x;
+    const int m = blockIdx.y;
+    const int d = threadIdx.x;
+    __shared__ float mc[kAttnChunks], lc[kAttnChunks];
+    const float* part = a.mem[m].partials + (size_t)qh * kAttnChunks * kPartStride;
+    float o[kAttnChunks];
+#pragma unroll
+    for (int c = 0; c < kAttnChunks; ++c) o[c] = part[c * kPartStride + d];
+    if (d < kAttnChunks) {
+        mc[d] = part[d * kPartStride + kHeadDim];
+        lc[d] = part[d * kPartStride + kHeadDim + 1];
     }
     __syncthreads();
-    float* outm = a.out + ((size_t)m * a.q_heads + (size_t)kvh * QPK) * kHeadDim;
-    for (int idx = tid; idx < QPK * kHeadDim; idx += kThreads) {
-        const int h = idx / kHeadDim;
-        const int d = idx - h * kHeadDim;
-        float mx = -FLT_MAX;
-        for (int c = 0; c < kAttnChunks; ++c) mx = fmaxf(mx, cm[c][h]);
-        float l = 0.f, acc = 0.f;
-        for (int c = 0; c < kAttnChunks; ++c) {
-            const float f = expf(cm[c][h] - mx);
-            l = __builtin_fmaf(cl[c][h], f, l);
-            acc = __builtin_fmaf(pbase[(c * QPK + h) * kPartStride + d], f, acc);
-        }
-        outm[h * kHeadDim + d] = acc / l;
+    float mx = -FLT_MAX;
+#pragma unroll
+    for (int c = 0; c < kAttnChunks; ++c) mx = fmaxf(mx, mc[c]);
+    float l = 0.f, acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < kAttnChunks; ++c) {
+        const float f = expf(mc[c] - mx);
+        l = __builtin_fmaf(lc[c], f, l);
+        acc = __builtin_fmaf(o[c], f, acc);
     }
-    if (tid == 0) atomicExch(&mb.counters[kvh], 0u);
+    a.out[((size_t)m * a.q_heads + qh) * kHeadDim + d] = acc / l;
 }
 
 // Order-preserving key of a float (model_ops.rs:151-155).
@@ -332,15 +332,37 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* log
     const int tid = threadIdx.x;
     const float* row = logits + (size_t)m * vocab;
     uint32_t key = 0u, idx = 0u;
-    for (int p = tid; p < vocab; p += kArgmaxThreads) {
-        const float v = row[p];
+    // v == v rejects NaN like the scalar reference's strict comparisons; each
+    // thread visits its indices in increasing order, so `>` keeps the first
+    auto consider = [&](float v, int p) {
         const uint32_t k = logit_key(v);
-        // v == v rejects NaN like the scalar reference's strict comparisons
         if (v == v && k > key) {
             key = k;
             idx = (uint32_t)p;
         }
+    };
+    // 16-byte loads, eight in flight per thread
+    constexpr int U = 8;
+    const bool wide = (vocab & 3) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
+    const int vec = wide ? vocab / 4 : 0;
+    const float4* row4 = reinterpret_cast<const float4*>(row);
+    for (int base = 0; base < vec; base += kArgmaxThreads * U) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = base + u * kArgmaxThreads + tid;
+            v[u] = i < vec ? row4[i] : make_float4(NAN, NAN, NAN, NAN);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int p = 4 * (base + u * kArgmaxThreads + tid);
+            consider(v[u].x, p);
+            consider(v[u].y, p + 1);
+            consider(v[u].z, p + 2);
+            consider(v[u].w, p + 3);
+        }
     }
+    for (int p = 4 * vec + tid; p < vocab; p += kArgmaxThreads) consider(row[p], p);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const uint32_t ok = (uint32_t)__shfl_xor((int)key, off, 64);
@@ -383,6 +405,10 @@ hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t strea
     case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(kThreads), 0, stream, args); break;
     default: return hipErrorInvalidValue;
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)args.q_heads, (unsigned)members), dim3(kHeadDim), 0, stream,
+                       args);
     return hipGetLastError();
 }
 

@@ -23,8 +23,7 @@ constexpr int kPartStride = kHeadDim + 4;
 struct AttnMember {
     uint16_t* keys;      // f16 [kv_heads][capacity][128]
     uint16_t* values;    // f16 [kv_heads][capacity][128]
-    float* partials;     // [kv_heads][kAttnChunks][q_per_kv][kPartStride]
-    uint32_t* counters;  // [kv_heads], zero between launches
+    float* partials;     // [q_heads][kAttnChunks][kPartStride]
     int capacity;        // cache tokens per (layer, KV head)
 };
 
@@ -47,7 +46,8 @@ struct AttnArgs {
 // Floats of one sequence's attention partials ([q_heads][kAttnChunks][kPartStride]).
 size_t attn_partials_floats(int q_heads);
 
-// members <= kAttnMaxMembers; q_heads / kv_heads in {1, 2, 4, 8}.
+// Two launches: the chunked attention writing partials, then their merge into
+// `out`. members <= kAttnMaxMembers; q_heads / kv_heads in {1, 2, 4, 8}.
 hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t stream);
 
 // Greedy selection per member over logits [members][vocab] (ties to the lowest

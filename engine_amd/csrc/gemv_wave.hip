@@ -42,7 +42,7 @@
 namespace ribn_amd {
 
 constexpr uint32_t kOutOfRange = 0xffffff00u;  // buffer offset past any tensor: loads return 0, stores drop
-constexpr int kSliceElems = 16 * kQK;          // elements a wave covers per unit
+constexpr int kSliceElems = kSliceK;           // elements a wave covers per unit (16 super-blocks)
 
 template <int T> struct ActTraits {
     static constexpr int group = (T == kQ6K) ? 16 : 32;  // elements per scale group
@@ -276,9 +276,10 @@ __device__ __forceinline__ void row_dot(const RowData<T>& d, int p, const LaneAc
 
 // ------------------------------------------------------------------ kernel
 
-template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP>
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP, bool PAIR>
 __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args) {
     static_assert(NBUF % GROUP == 0, "the ring holds whole row groups");
+    static_assert(!PAIR || (ONE_SLICE && NBUF % 2 == 0), "pairs are whole ring slots of one-slice rows");
     constexpr bool NORM = PRO == kProNorm;
     constexpr bool SWIGLU = PRO == kProSwiglu;
     constexpr int kWaves = WAVES;
@@ -300,14 +301,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
     const int bs = lane >> 2;
     const int nwaves = gridDim.x * kWaves;
     const int wg = blockIdx.x * kWaves + wave;
-    const int r_begin = (int)((long long)args.total_rows * wg / nwaves);
-    const int r_end = (int)((long long)args.total_rows * (wg + 1) / nwaves);
+    // PAIR: units alternate (gate row n, up row n); a wave takes whole pairs
+    const int split = PAIR ? args.total_rows >> 1 : args.total_rows;
+    const int r_begin = (PAIR ? 2 : 1) * (int)((long long)split * wg / nwaves);
+    const int r_end = (PAIR ? 2 : 1) * (int)((long long)split * (wg + 1) / nwaves);
     const uint32_t row_bytes = (uint32_t)nb * BB;
 
     // Row -> (matrix, local row); the row index is wave-uniform. Fields of
     // the argument arrays are picked by selects, not by a dynamic index
     // (which would reload them from the argument segment every unit).
     auto locate = [&](int row, int& mat, int& local) {
+        if constexpr (PAIR) {
+            mat = row & 1;
+            local = row >> 1;
+            return;
+        }
         mat = 0;
         int start = 0;
 #pragma unroll
@@ -487,6 +495,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
         }
     };
 
+    // silu(gate) * up of one output row, in the reference's operation order
+    // (model_ops.rs:316-328)
+    auto swiglu = [](float g, float u) { return (g / (1.0f + expf(-g))) * u; };
+
     // One member's lane record of one slice, from LDS.
     auto read_member = [&](LaneAct<T>& dst, int m, int slice) {
         const uint32_t* src = xs + ((m * slices + slice) * 64 + lane) * STRIDE;
@@ -543,13 +555,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
             for (int r = 0; r < NBUF; ++r) {
                 const int row = crow + r;
                 locate(row < r_end ? row : r_begin, mat[r], local[r]);
-                yr[r] = pick_y(mat[r], rows_mat[r]);
+                yr[r] = pick_y(PAIR ? 0 : mat[r], rows_mat[r]);
             }
 #pragma unroll 1
             for (int m = 0; m < members; ++m) {
                 LaneAct<T> x1[1];
                 read_member(x1[0], m, 0);
                 const float im = inv_s[m];
+                float gk = 0.f;
 #pragma unroll
                 for (int r = 0; r < NBUF; ++r) {
                     float pr[1];
@@ -558,7 +571,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
                     const bool live = r < left && crow + r < r_end;
                     const uint32_t off =
                         (live && lane == 0) ? (uint32_t)(m * rows_mat[r] + local[r]) * 4u : kOutOfRange;
-                    put(total, yr[r], off);
+                    if constexpr (PAIR) {
+                        if (r % 2 == 0) {
+                            gk = total;
+                        } else {
+                            put(swiglu(gk, total), yr[r], off);
+                        }
+                    } else {
+                        put(total, yr[r], off);
+                    }
                 }
             }
             if constexpr (REFILL) {
@@ -587,6 +608,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
     int crow = r_begin, cslice = 0;  // unit being reduced (group base row when K spans slices)
     constexpr int kAcc = ONE_SLICE ? 1 : GROUP;
     float acc[kAcc][MT];
+    float gk[MT];  // PAIR: the gate row's output, waiting for its up row
 #pragma unroll
     for (int r = 0; r < kAcc; ++r)
 #pragma unroll
@@ -603,7 +625,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
         int mat, local;
         locate(row < r_end ? row : r_begin, mat, local);
         int rows_mat;
-        const __amdgpu_buffer_rsrc_t yr = pick_y(mat, rows_mat);
+        const __amdgpu_buffer_rsrc_t yr = pick_y(PAIR ? 0 : mat, rows_mat);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             acc[ai][m] = (ONE_SLICE || cslice == 0) ? part[m] : acc[ai][m] + part[m];
@@ -611,7 +633,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wave_kernel(WaveGemvArgs args
             const uint32_t off = (last && row < r_end && lane == 0 && m < members)
                                      ? (uint32_t)(m * rows_mat + local) * 4u
                                      : kOutOfRange;
-            put(total, yr, off);
+            if constexpr (PAIR) {
+                // ring slots alternate gate / up rows (r_begin and NBUF are even)
+                if (r % 2 == 0) {
+                    gk[m] = total;
+                } else {
+                    put(swiglu(gk[m], total), yr, off);
+                }
+            } else {
+                put(total, yr, off);
+            }
         }
         if constexpr (ONE_SLICE) {
             ++crow;
@@ -651,13 +682,13 @@ static size_t act_lds_bytes(int members, int K) {
     return (size_t)members * slices * 64 * ActTraits<T>::stride * sizeof(uint32_t);
 }
 
-template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP = 1>
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP = 1, bool PAIR = false>
 struct WaveInstance {
     static std::atomic<int> occupancy;  // resident workgroups per CU at the largest LDS size (0: not queried)
     // Launches `per_cu` workgroups on every CU (capped by occupancy; fewer
     // when the problem has fewer than two units per wave).
     static hipError_t launch(const WaveGemvArgs& a, int cu_count, int per_cu, hipStream_t stream) {
-        auto kern = gemv_wave_kernel<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP>;
+        auto kern = gemv_wave_kernel<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP, PAIR>;
         const size_t lds = act_lds_bytes<T>(MT, a.K);
         int occ = occupancy.load(std::memory_order_relaxed);
         if (occ == 0) {
@@ -683,22 +714,24 @@ struct WaveInstance {
         return hipGetLastError();
     }
 };
-template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP>
-std::atomic<int> WaveInstance<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP>::occupancy{0};
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP, bool PAIR>
+std::atomic<int> WaveInstance<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP, PAIR>::occupancy{0};
 
 // Launch shape by units (row x slice) per CU, from sweeps on MI355X over
 // workgroup size {2,4,8,16} waves x ring depth {2,4,8} x workgroups per CU
 // {1,2,4}: short launches want every wave started at once with a shallow
 // ring; long streams want fewer, deeper streams per CU.
-template <int T, int MT, int PRO, bool ONE_SLICE>
+template <int T, int MT, int PRO, bool ONE_SLICE, bool PAIR = false>
 static hipError_t launch_ring(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
     const int slices = ONE_SLICE ? 1 : ((a.K >> 8) + 15) >> 4;
     const long long units = (long long)a.total_rows * slices;
     const long long per_cu = (units + cu_count - 1) / cu_count;
     if constexpr (MT == 1 && ONE_SLICE) {
         if (per_cu >= 128) {
-            if constexpr (T == kQ6K) return WaveInstance<T, MT, PRO, ONE_SLICE, 8, 4>::launch(a, cu_count, 1, stream);
-            return WaveInstance<T, MT, PRO, ONE_SLICE, 4, 8>::launch(a, cu_count, 4, stream);
+            if constexpr (T == kQ6K) {
+                return WaveInstance<T, MT, PRO, ONE_SLICE, 8, 4, 1, PAIR>::launch(a, cu_count, 1, stream);
+            }
+            return WaveInstance<T, MT, PRO, ONE_SLICE, 4, 8, 1, PAIR>::launch(a, cu_count, 4, stream);
         }
     }
     if constexpr (!ONE_SLICE) {
@@ -706,7 +739,7 @@ static hipError_t launch_ring(const WaveGemvArgs& a, int cu_count, hipStream_t s
         // measured slower for the 12288-wide down projection).
         return WaveInstance<T, MT, PRO, ONE_SLICE, 2, 8, 2>::launch(a, cu_count, 1, stream);
     } else {
-        return WaveInstance<T, MT, PRO, ONE_SLICE, 2, 8>::launch(a, cu_count, per_cu > 48 ? 2 : 1, stream);
+        return WaveInstance<T, MT, PRO, ONE_SLICE, 2, 8, 1, PAIR>::launch(a, cu_count, per_cu > 48 ? 2 : 1, stream);
     }
 }
 
@@ -737,8 +770,24 @@ int wave_max_members(int K) {
     return (int)std::min<long long>(fit, cap);
 }
 
+// Gate/up pairs with the SwiGLU epilogue (one-slice K; members as launch_t).
+template <int T, int PRO>
+static hipError_t launch_pair(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
+    if (a.members <= 1) return launch_ring<T, 1, PRO, true, true>(a, cu_count, stream);
+    if (a.members <= 2) return launch_ring<T, 2, PRO, true, true>(a, cu_count, stream);
+    if (a.members <= 4) return WaveInstance<T, 4, PRO, true, 4, 8, 1, true>::launch(a, cu_count, 1, stream);
+    return WaveInstance<T, 8, PRO, true, 4, 8, 1, true>::launch(a, cu_count, 1, stream);
+}
+
 template <int T>
 static hipError_t launch_type(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
+    if (a.pair_swiglu) {
+        if (a.x2 != nullptr || a.count != 2 || a.rows_end[1] != 2 * a.rows_end[0] || a.K > kSliceElems) {
+            return hipErrorInvalidValue;
+        }
+        return a.gamma != nullptr ? launch_pair<T, kProNorm>(a, cu_count, stream)
+                                  : launch_pair<T, kProPlain>(a, cu_count, stream);
+    }
     if (a.x2 != nullptr) {
         if (a.gamma != nullptr || a.members > kSwigluMaxMembers) return hipErrorInvalidValue;
         return launch_t<T, kProSwiglu>(a, cu_count, stream);

@@ -16,6 +16,9 @@ constexpr int kMaxGroup = 4;
 // records, and the largest K its staging covers.
 constexpr long long kWaveMaxLdsBytes = 128 * 1024;
 constexpr int kWaveMaxK = 16384;
+// K one wave covers per unit (16 super-blocks); the many-member and gate/up
+// pair forms need K within it.
+constexpr int kSliceK = 4096;
 
 // Activation prologue of the wave GEMV: plain x, RMSNorm(x; gamma), or
 // SwiGLU silu(x) * x2.
@@ -39,6 +42,9 @@ struct WaveGemvArgs {
     int K;
     int members;
     int accumulate;           // nonzero: y += W x' (fused residual add) instead of y = W x'
+    // nonzero: w[0] / w[1] are gate / up of equal shape, and y[0] [members][N]
+    // receives silu(gate . x') * (up . x') (K <= 4096; y[1] unused)
+    int pair_swiglu;
 };
 
 // Largest member count one wave launch can stage for this K (0 if none).
@@ -52,7 +58,8 @@ hipError_t launch_gemv_exact(int value_type, const uint8_t* w, uint32_t wbytes, 
 
 // args.gamma != nullptr: RMSNorm(x; gamma, eps) is fused into the activation
 // load; args.x2 != nullptr: the activation is silu(x) * x2 (members <= 2, no
-// gamma); args.accumulate: outputs are added into y.
+// gamma); args.accumulate: outputs are added into y; args.pair_swiglu: the
+// gate/up pair epilogue (see WaveGemvArgs).
 hipError_t launch_gemv_wave(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
 
 // Gathers and dequantises rows of a [hidden, vocab] table: tokens[m] (device

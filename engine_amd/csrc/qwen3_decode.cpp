@@ -8,12 +8,14 @@
 //   embedding of tokens[m]                          (q4_k_embedding; device token ids)
 //   per layer:
 //     q/k/v GEMV, RMSNorm(attn_norm) in the prologue   (rms_norm + 3 gemv)
-//     attention: q/k norm, rope, KV append, GQA        (5 launches in the reference)
+//     attention: q/k norm, rope, KV append, GQA, then  (5 launches in the reference)
+//       the merge of its chunks
 //     o GEMV added into the residual stream            (gemv + residual_add)
-//     gate/up GEMV, RMSNorm(ffn_norm) in the prologue  (rms_norm + 2 gemv)
-//     down GEMV of silu(gate)*up, added into the stream (silu_mul + gemv + residual_add)
+//     gate/up GEMV pairs, RMSNorm(ffn_norm) in the prologue, silu(gate)*up in
+//       the epilogue                                    (rms_norm + 2 gemv + silu_mul)
+//     down GEMV added into the stream                  (gemv + residual_add)
 //   output head: RMSNorm(output_norm) + lm_head GEMV, argmax (run_output_head, 655-677)
-// Five launches per layer instead of the reference's 14. Positions and token
+// Six launches per layer (attention is two) instead of the reference's 14. Positions and token
 // ids live in device memory, so one captured graph serves every position and
 // a generation loop needs no host round trip between steps.
 #include "ribn_amd.h"
@@ -41,11 +43,10 @@ struct ribn_amd_kv_cache {
     ribn_amd_qwen3_config cfg;
     uint32_t capacity;
     size_t layer_elems;  // kv_heads * capacity * head_dim
-    void* block;         // one allocation: keys, values, partials, counters
+    void* block;         // one allocation: keys, values, partials
     uint16_t* keys;      // [layers][kv_heads][capacity][head_dim]
     uint16_t* values;
     float* partials;     // attention partials ([q_heads][kAttnChunks][kPartStride])
-    uint32_t* counters;  // [kv_heads] attention tickets, zero between launches
 };
 
 namespace {
@@ -138,7 +139,7 @@ namespace {
 // in launch groups of as many members as one launch stages.
 hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight* const* ws, int count,
                 const float* x, const float* x2, const float* gamma, float* const* ys, int members, bool accumulate,
-                hipStream_t stream) {
+                hipStream_t stream, bool pair = false) {
     const int K = (int)ws[0]->input_size;
     int per = std::min(ribn_amd::wave_max_members(K), ribn_amd::kWaveMaxMembers);
     if (x2 != nullptr) per = std::min(per, ribn_amd::kSwigluMaxMembers);
@@ -164,6 +165,7 @@ hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight*
         a.K = K;
         a.members = mc;
         a.accumulate = accumulate ? 1 : 0;
+        a.pair_swiglu = pair ? 1 : 0;
         hipError_t e = ribn_amd::launch_gemv_wave((int)ws[0]->value_type, a, d->ctx->cu_count, stream);
         if (e != hipSuccess) return e;
     }
@@ -198,7 +200,6 @@ hipError_t attention(const ribn_amd_qwen3_config& cfg, ribn_amd_kv_cache* const*
             a.mem[i].keys = c->keys + (size_t)layer * c->layer_elems;
             a.mem[i].values = c->values + (size_t)layer * c->layer_elems;
             a.mem[i].partials = c->partials;
-            a.mem[i].counters = c->counters;
             a.mem[i].capacity = (int)c->capacity;
         }
         a.q = q + m0 * qdim;
@@ -239,10 +240,18 @@ hipError_t enqueue_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* cach
         e = wave(d, &L.attn_output, 1, d->attn, nullptr, nullptr, &d->hidden, members, true, stream);
         if (e != hipSuccess) return e;
         const ribn_amd_quantized_weight* gu[2] = {L.ffn_gate, L.ffn_up};
-        float* gu_out[2] = {d->gate, d->up};
-        e = wave_shared(d, gu, gu_out, 2, d->hidden, L.ffn_norm, members, stream);
-        if (e != hipSuccess) return e;
-        e = wave(d, &L.ffn_down, 1, d->gate, d->up, nullptr, &d->hidden, members, true, stream);
+        if (L.ffn_gate->value_type == L.ffn_up->value_type && c.hidden <= (uint32_t)ribn_amd::kSliceK) {
+            // gate/up pairs store silu(gate) * up; down reads it as a plain input
+            float* act[2] = {d->gate, d->gate};
+            e = wave(d, gu, 2, d->hidden, nullptr, L.ffn_norm, act, members, false, stream, true);
+            if (e != hipSuccess) return e;
+            e = wave(d, &L.ffn_down, 1, d->gate, nullptr, nullptr, &d->hidden, members, true, stream);
+        } else {
+            float* gu_out[2] = {d->gate, d->up};
+            e = wave_shared(d, gu, gu_out, 2, d->hidden, L.ffn_norm, members, stream);
+            if (e != hipSuccess) return e;
+            e = wave(d, &L.ffn_down, 1, d->gate, d->up, nullptr, &d->hidden, members, true, stream);
+        }
         if (e != hipSuccess) return e;
     }
     if (!head) return hipSuccess;
@@ -397,10 +406,9 @@ ribn_amd_status ribn_amd_kv_cache_create(ribn_amd_context* ctx, const ribn_amd_q
     const size_t layer_elems = (size_t)config->kv_heads * capacity * config->head_dim;
     const size_t cache_bytes = align_up(layer_elems * config->layers * sizeof(uint16_t));
     const size_t part_bytes = align_up(ribn_amd::attn_partials_floats((int)config->q_heads) * sizeof(float));
-    const size_t counter_bytes = align_up(config->kv_heads * sizeof(uint32_t));
     DeviceGuard guard(ctx->device);
     void* block = nullptr;
-    hipError_t e = hipMalloc(&block, 2 * cache_bytes + part_bytes + counter_bytes);
+    hipError_t e = hipMalloc(&block, 2 * cache_bytes + part_bytes);
     if (e != hipSuccess) return driver(e, "hipMalloc KV cache");
     char* p = static_cast<char*>(block);
     auto* c = new (std::nothrow) ribn_amd_kv_cache{};
@@ -418,16 +426,8 @@ ribn_amd_status ribn_amd_kv_cache_create(ribn_amd_context* ctx, const ribn_amd_q
     c->keys = reinterpret_cast<uint16_t*>(p);
     c->values = reinterpret_cast<uint16_t*>(p + cache_bytes);
     c->partials = reinterpret_cast<float*>(p + 2 * cache_bytes);
-    c->counters = reinterpret_cast<uint32_t*>(p + 2 * cache_bytes + part_bytes);
-    // the attention tickets start at zero; the cache needs no clearing (a
-    // position is always written before it is read)
-    e = hipMemsetAsync(c->counters, 0, counter_bytes, ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) {
-        hipFree(block);
-        delete c;
-        return driver(e, "clear KV cache tickets");
-    }
+    // nothing is cleared: a position is written before it is read, and every
+    // partial is written before the merge reads it
     *out = c;
     return ok();
 }

@@ -701,6 +701,60 @@ ribn_amd_status ribn_amd_gemv_execute_fused(ribn_amd_gemv* g, const ribn_amd_qua
                              (flags & RIBN_AMD_FUSE_ACCUMULATE) != 0);
 }
 
+ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv* g, const ribn_amd_quantized_weight* gate,
+                                                     const ribn_amd_quantized_weight* up, const float* input,
+                                                     size_t input_len, const float* gamma, size_t gamma_len,
+                                                     float epsilon, float* output, size_t output_len,
+                                                     size_t members) {
+    ribn_amd_status st = validate_members(g, members);
+    if (st != RIBN_AMD_OK) return st;
+    uint64_t k, n, k2, n2;
+    st = validate_launch(g, gate, input, input_len, output, output_len, members, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    st = validate_launch(g, up, input, input_len, output, output_len, members, &k2, &n2);
+    if (st != RIBN_AMD_OK) return st;
+    if (k > (uint64_t)ribn_amd::kSliceK) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, ribn_amd::kSliceK, k, "the gate/up pair epilogue supports K up to %d",
+                    ribn_amd::kSliceK);
+    }
+    if (2 * n > (uint64_t)std::numeric_limits<int32_t>::max()) return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "rows exceed i32");
+    if (gamma != nullptr) {
+        st = check_device_ptr(g->ctx, gamma, "gamma");
+        if (st != RIBN_AMD_OK) return st;
+        if (gamma_len != k) {
+            return fail(RIBN_AMD_WEIGHT_LENGTH, k, gamma_len, "RMSNorm weight has %zu values, expected %llu", gamma_len,
+                        (unsigned long long)k);
+        }
+        st = check_epsilon(epsilon);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    DeviceGuard guard(g->ctx->device);
+    const int per_launch = std::min(ribn_amd::wave_max_members((int)k), ribn_amd::kWaveMaxMembers);
+    for (size_t m0 = 0; m0 < members; m0 += (size_t)per_launch) {
+        const size_t mc = std::min<size_t>((size_t)per_launch, members - m0);
+        ribn_amd::WaveGemvArgs a{};
+        a.w[0] = gate->data;
+        a.wbytes[0] = (uint32_t)gate->encoded_bytes;
+        a.w[1] = up->data;
+        a.wbytes[1] = (uint32_t)up->encoded_bytes;
+        a.y[0] = output + m0 * n;
+        a.y[1] = output + m0 * n;
+        a.rows_end[0] = (int)n;
+        a.rows_end[1] = (int)(2 * n);
+        a.count = 2;
+        a.total_rows = (int)(2 * n);
+        a.x = input + m0 * k;
+        a.gamma = gamma;
+        a.eps = epsilon;
+        a.K = (int)k;
+        a.members = (int)mc;
+        a.pair_swiglu = 1;
+        hipError_t e = ribn_amd::launch_gemv_wave((int)g->value_type, a, g->ctx->cu_count, g->ctx->stream);
+        if (e != hipSuccess) return driver(e, "launch gate/up GEMV");
+    }
+    return ok();
+}
+
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, float* output,
                                     size_t output_len) {
     if (!g || !w) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null kernel or weight handle");

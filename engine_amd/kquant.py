@@ -271,6 +271,14 @@ class _AmdQuantizedGemv:
         _check(self._lib.ribn_amd_gemv_execute_fused(self.handle, weight.handle, _ptr(input), u, input.numel(), g,
                                                      gl, epsilon, _ptr(output), output.numel(), members, flags))
 
+    def execute_gate_up_swiglu(self, gate, up, input, output, members: int = 1, gamma=None, epsilon: float = 1e-6):
+        """output = silu(gate x') * (up x') in one launch (x' = RMSNorm(input) when gamma is given)."""
+        g = _ptr(gamma) if gamma is not None else None
+        gl = gamma.numel() if gamma is not None else 0
+        _check(self._lib.ribn_amd_gemv_execute_gate_up_swiglu(self.handle, gate.handle, up.handle, _ptr(input),
+                                                              input.numel(), g, gl, epsilon, _ptr(output),
+                                                              output.numel(), members))
+
     def gemm_prefill(self, weight, input, output, members: int, gamma=None, epsilon: float = 1e-6):
         """y[members][N] = x[members][K] W^T on the matrix cores; x is f32 or bf16.
         Needs AmdContext.reserve_prefill(members, K) beforehand."""

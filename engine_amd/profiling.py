@@ -78,6 +78,13 @@ def short_name(name: str) -> str:
     return "".join(out)[:90]
 
 
+def _grid(row) -> int:
+    """Work-items of a dispatch (X * Y * Z of the grid)."""
+    if row.get("Grid_Size_X"):
+        return int(row["Grid_Size_X"]) * int(row.get("Grid_Size_Y") or 1) * int(row.get("Grid_Size_Z") or 1)
+    return int(row.get("Grid_Size") or 0)
+
+
 def trace_summary(path: str, match: str = "") -> list[tuple]:
     """[(kernel, grid, count, mean_us, median_us, min_us)] sorted by total time."""
     groups: dict[tuple, list[int]] = defaultdict(list)
@@ -87,7 +94,7 @@ def trace_summary(path: str, match: str = "") -> list[tuple]:
                 name = short_name(row["Kernel_Name"])
                 if match and match not in name:
                     continue
-                grid = int(row.get("Grid_Size_X") or row.get("Grid_Size") or 0)
+                grid = _grid(row)
                 groups[(name, grid)].append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
     out = [(k[0], k[1], len(v), statistics.mean(v) / 1e3, statistics.median(v) / 1e3, min(v) / 1e3)
            for k, v in groups.items()]

@@ -221,6 +221,18 @@ ribn_amd_status ribn_amd_gemv_execute_fused(ribn_amd_gemv *gemv, const ribn_amd_
                                             const float *input, const float *up, size_t input_len,
                                             const float *gamma, size_t gamma_len, float epsilon, float *output,
                                             size_t output_len, size_t members, uint32_t flags);
+/* Gate/up projection pair with the SwiGLU activation fused into the epilogue:
+ * output_m = silu(gate . x'_m) * (up . x'_m), x' = input or its RMSNorm
+ * (gamma != NULL). It replaces the reference's gemv(ffn_gate) + gemv(ffn_up) +
+ * silu_mul (decode.rs:608-631, model_ops.rs:316-328): one wave reduces row n
+ * of both weights back to back and stores only the product, so the gate and
+ * up vectors never reach memory. gate and up are this kernel's type, equal
+ * [K, N] shapes, K <= 4096; output holds members*N values. */
+ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *gate,
+                                                     const ribn_amd_quantized_weight *up, const float *input,
+                                                     size_t input_len, const float *gamma, size_t gamma_len,
+                                                     float epsilon, float *output, size_t output_len,
+                                                     size_t members);
 /* Bit-exact device dequantisation to f32 [N][K] (twin of lib.rs:596-661;
  * the reference's device equivalent is the q4_k_embedding gather, q4_k.cu:1-67). */
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight, float *output,

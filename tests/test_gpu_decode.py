@@ -122,6 +122,28 @@ def test_accumulate_equals_store_plus_add(env, t, k, n, members):
         assert np.array_equal(to_host(a2, env["ctx"]).view(np.uint32), (base + to_host(s)).view(np.uint32))
 
 
+@pytest.mark.parametrize("t,n,members", [(12, 3072, 1), (12, 3072, 3), (12, 3072, 8), (13, 2048, 2), (14, 2048, 5),
+                                         (12, 16384, 1), (14, 16384, 1)])
+def test_gate_up_swiglu_pairs_match_oracle(env, t, n, members):
+    print_case(test="gate_up_pairs", t=t, n=n, members=members)
+    k = 4096
+    ge, ue = synth.kquant_numpy(t, k, n, 300 + n), synth.kquant_numpy(t, k, n, 301 + n)
+    gw, uw = upload(env, t, k, n, ge), upload(env, t, k, n, ue)
+    x = synth.activations_numpy(k, members, seed=n + members)
+    gamma = synth.gamma_numpy(k, seed=5)
+    out = to_dev(np.full(members * n, np.nan, np.float32))
+    env["k"][t].execute_gate_up_swiglu(gw, uw, to_dev(x), out, members, gamma=to_dev(gamma))
+    got = to_host(out, env["ctx"]).reshape(members, n)
+    for m in range(members):
+        normed = O.rms_norm_raw(x[m], gamma, 1e-6)
+        ref = O.swiglu(O.quant_gemv(t, ge, k, n, normed), O.quant_gemv(t, ue, k, n, normed))
+        assert max_rel_err(got[m], ref) <= RTOL, m
+    if members > 1:
+        one = to_dev(np.full(n, np.nan, np.float32))
+        env["k"][t].execute_gate_up_swiglu(gw, uw, to_dev(x[members - 1]), one, 1, gamma=to_dev(gamma))
+        assert np.array_equal(to_host(one, env["ctx"]).view(np.uint32), got[members - 1].view(np.uint32))
+
+
 def test_fused_rejects_swiglu_with_norm(env):
     E = env["E"]
     enc = synth.kquant_numpy(12, 256, 4, 1)
@@ -200,7 +222,7 @@ def test_attention_matches_oracle(env, qh, kvh):
                 to_dev(kn), posd)
         E.attention_decode(env["ctx"], config(env, cfg), caches, 0, *args, out)
         got = to_host(out, env["ctx"]).reshape(members, -1)
-        # a second launch at the same positions: the tickets were reset
+        # a second launch at the same positions repeats the result bit for bit
         out2 = to_dev(np.full(members * qh * 128, np.nan, np.float32))
         E.attention_decode(env["ctx"], config(env, cfg), caches, 0, *args, out2)
         assert np.array_equal(to_host(out2, env["ctx"]).reshape(members, -1).view(np.uint32), got.view(np.uint32))
