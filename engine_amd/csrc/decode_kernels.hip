@@ -10,15 +10,19 @@
 // Qwen3 has no q gate, so the attention output is not gated.
 //
 // Work split (split-T "flash decoding"): the grid is (chunk, KV head,
-// member). A workgroup takes one contiguous chunk of the member's tokens for
-// one KV head and all q_per_kv query heads that share it, so each K/V byte is
-// read once. Within the workgroup a 16-lane row of a wave owns one token per
-// step (lane j of the row holds dims 8j..8j+7: one 16-byte load of K and one
-// of V), and keeps an online-softmax state (running max, denominator and
-// output sums) per query head. The 16 states of a workgroup are merged across
+// member). A workgroup takes one contiguous chunk (at least kMinChunkTokens,
+// at most kAttnChunks chunks per context) of the member's tokens for one KV
+// head and all q_per_kv query heads that share it, so each K/V byte is read
+// once; workgroups past the context exit. Within the workgroup a 16-lane row
+// of a wave owns one token per step (lane j of the row holds dims 8j..8j+7:
+// one 16-byte load of K and one of V, kRing steps in flight), and keeps an
+// online-softmax state (running max, denominator and output sums) per query
+// head, rescaled once per kRing-step block, with scores in log2 units so each
+// weight is one exp2. The 16 states of a workgroup are merged across
 // rows with lane shuffles and across waves in LDS into one partial per
-// (chunk, head); attn_combine_kernel then merges the kAttnChunks partials of
-// each (member, head) into the output. The new token's K/V are computed by the
+// (chunk, head); attn_combine_kernel then merges the chunks' partials of each
+// (member, head) into the output (a context within one chunk is written
+// directly). The new token's K/V are computed by the
 // workgroup whose chunk holds the position: written to the cache, and used
 // from LDS by that workgroup.
 //
@@ -29,6 +33,8 @@
 
 #include <float.h>
 
+#include <algorithm>
+
 namespace ribn_amd {
 
 namespace {
@@ -38,6 +44,19 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kRing = 4;                  // steps of K/V loads in flight per wave
 constexpr int kStepTokens = kWaves * 4;   // tokens a workgroup covers per step
+// A chunk spans at least this many tokens (sweep on MI355X over workgroups of
+// 256/512 threads and 16-256-token minimum chunks: batch 1 at 2048 tokens is
+// fastest here, and short contexts need fewer chunks and merges).
+constexpr int kMinChunkTokens = 64;
+static_assert(kMinChunkTokens % kStepTokens == 0, "chunks are whole steps");
+
+// Tokens per chunk for a context of `tokens`: kMinChunkTokens, or more when
+// the context needs more than kAttnChunks chunks of that size.
+__device__ __forceinline__ int chunk_tokens(int tokens) {
+    int len = (tokens + kAttnChunks - 1) / kAttnChunks;
+    len = len < kMinChunkTokens ? kMinChunkTokens : len;
+    return (len + kStepTokens - 1) / kStepTokens * kStepTokens;
+}
 
 // Sum over the 16 lanes of a DPP row; every lane of the row receives it.
 __device__ __forceinline__ float row16_sum(float v) {
@@ -93,14 +112,43 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     const int j = lane & 15;    // dims 8j..8j+7
     const AttnMember mb = a.mem[m];
 
+    // ---- loads that do not need the position go first: this workgroup's
+    // query heads and norm weight, and the new token's raw K (wave 0) and V
+    // (wave 1) with the K norm weight
+    const float* qm = a.q + ((size_t)m * a.q_heads + (size_t)kvh * QPK) * kHeadDim;
+    float qx[kHeadsPerWave][2];
+#pragma unroll
+    for (int i = 0; i < kHeadsPerWave; ++i) {
+        const int h = wave + kWaves * i;
+        qx[i][0] = qx[i][1] = 0.f;
+        if (h < QPK) {
+            qx[i][0] = qm[h * kHeadDim + lane];
+            qx[i][1] = qm[h * kHeadDim + 64 + lane];
+        }
+    }
+    const float qw0 = a.q_norm[lane];
+    const float qw1 = a.q_norm[lane + 64];
+    float nx0 = 0.f, nx1 = 0.f, kw0 = 0.f, kw1 = 0.f;
+    if (wave < 2) {
+        const float* src = (wave == 0 ? a.k : a.v) + ((size_t)m * a.kv_heads + kvh) * kHeadDim;
+        nx0 = src[lane];
+        nx1 = src[lane + 64];
+        if (wave == 0) {
+            kw0 = a.k_norm[lane];
+            kw1 = a.k_norm[lane + 64];
+        }
+    }
+
     const int pos = a.positions[m];
     const int tokens = pos + 1;
-    int len = (tokens + kAttnChunks - 1) / kAttnChunks;
-    len = (len + kStepTokens - 1) / kStepTokens * kStepTokens;
+    const int len = chunk_tokens(tokens);
     const int t0 = chunk * len;
+    if (t0 >= tokens) return;  // no tokens in this chunk (uniform over the workgroup)
     const int t1 = min(t0 + len, tokens);
-    const int steps = t1 > t0 ? (t1 - t0 + kStepTokens - 1) / kStepTokens : 0;
-    const bool has_new = t0 <= pos && pos < t1;
+    const int steps = (t1 - t0 + kStepTokens - 1) / kStepTokens;
+    const bool has_new = pos < t1;
+    // a context within one chunk is finished here; the merge launch skips it
+    const bool single = tokens <= len;
 
     // ---- cached K/V of this chunk: the first kRing steps are issued before
     // anything else. The new token's slot is not read (it is written below).
@@ -120,26 +168,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     for (int r = 0; r < kRing; ++r) issue(r, r);
 
     // ---- query heads (and the new K/V): norm + rope into LDS
-    const float* qm = a.q + ((size_t)m * a.q_heads + (size_t)kvh * QPK) * kHeadDim;
-    float qx[kHeadsPerWave][2];
-#pragma unroll
-    for (int i = 0; i < kHeadsPerWave; ++i) {
-        const int h = wave + kWaves * i;
-        qx[i][0] = qx[i][1] = 0.f;
-        if (h < QPK) {
-            qx[i][0] = qm[h * kHeadDim + lane];
-            qx[i][1] = qm[h * kHeadDim + 64 + lane];
-        }
-    }
     const bool new_wave = has_new && wave < 2;  // wave 0: K, wave 1: V
-    float nx0 = 0.f, nx1 = 0.f;
-    if (new_wave) {
-        const float* src = (wave == 0 ? a.k : a.v) + ((size_t)m * a.kv_heads + kvh) * kHeadDim;
-        nx0 = src[lane];
-        nx1 = src[lane + 64];
-    }
-    const float qw0 = a.q_norm[lane];
-    const float qw1 = a.q_norm[lane + 64];
     const float fpos = (float)pos;
 #pragma unroll
     for (int i = 0; i < kHeadsPerWave; ++i) {
@@ -151,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         }
     }
     if (new_wave) {
-        if (wave == 0) norm_rope(nx0, nx1, a.k_norm[lane], a.k_norm[lane + 64], a.eps, fpos, a.rope_base, lane);
+        if (wave == 0) norm_rope(nx0, nx1, kw0, kw1, a.eps, fpos, a.rope_base, lane);
         // f16 round to nearest even, as kv_append_f16 stores it
         const _Float16 h0 = (_Float16)nx0;
         const _Float16 h1 = (_Float16)nx1;
@@ -172,7 +201,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         for (int i = 0; i < 8; ++i) qr[h][i] = qs[h][8 * j + i];
 
     // ---- online softmax over the chunk (the reference's running max and
-    // rescaled total, model_ops.rs:508-523, extended to the output sums)
+    // rescaled total, model_ops.rs:508-523, extended to the output sums), one
+    // block of kRing steps at a time: the block's scores first, then one
+    // maximum and one rescale per block. Scores are kept in log2 units
+    // (a.scale carries log2 e), so each weight is one v_exp_f32.
     float mrun[QPK], lrun[QPK], o[QPK][8];
 #pragma unroll
     for (int h = 0; h < QPK; ++h) {
@@ -181,43 +213,67 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[h][i] = 0.f;
     }
-    auto consume = [&](uint4 kw, uint4 vw, int s) {
-        const int t = t0 + s * kStepTokens + 4 * wave + grp;
-        const bool live = t < t1;
-        float kf[8], vf[8];
-        unpack_f16x8(kw, kf);
-        unpack_f16x8(vw, vf);
-        if (t == pos) {
+    for (int s0 = 0; s0 < steps; s0 += kRing) {
+        // Steps past the chunk are skipped (uniform guards). One of them can
+        // cover the new token's position, whose K/V live in kv_new only in the
+        // workgroup whose chunk holds it; anywhere else that LDS is
+        // uninitialised, and even a zero weight times a NaN left there is NaN.
+        const int nr = steps - s0 < kRing ? steps - s0 : kRing;
+        float sc[kRing][QPK];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                kf[i] = kv_new[0][8 * j + i];
-                vf[i] = kv_new[1][8 * j + i];
+        for (int r = 0; r < kRing; ++r) {
+#pragma unroll
+            for (int h = 0; h < QPK; ++h) sc[r][h] = -INFINITY;
+            if (r >= nr) continue;
+            const int t = t0 + (s0 + r) * kStepTokens + 4 * wave + grp;
+            const bool live = t < t1;
+            float kf[8];
+            unpack_f16x8(kring[r], kf);
+            if (has_new && t == pos) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kf[i] = kv_new[0][8 * j + i];
+            }
+#pragma unroll
+            for (int h = 0; h < QPK; ++h) {
+                float d = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) d = __builtin_fmaf(qr[h][i], kf[i], d);
+                d = row16_sum(d);
+                sc[r][h] = live ? d * a.scale : -INFINITY;
             }
         }
 #pragma unroll
         for (int h = 0; h < QPK; ++h) {
-            float d = 0.f;
+            float mb = sc[0][h];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) d = __builtin_fmaf(qr[h][i], kf[i], d);
-            d = row16_sum(d);
-            const float sc = live ? d * a.scale : -INFINITY;
-            const float mn = fmaxf(mrun[h], sc);
-            const float c = expf(mrun[h] - mn);
-            const float p = expf(sc - mn);
-            lrun[h] = lrun[h] * c + p;
+            for (int r = 1; r < kRing; ++r) mb = fmaxf(mb, sc[r][h]);
+            const float mn = fmaxf(mrun[h], mb);
+            const float c = __builtin_amdgcn_exp2f(mrun[h] - mn);
+            lrun[h] *= c;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[h][i] = __builtin_fmaf(p, vf[i], o[h][i] * c);
+            for (int i = 0; i < 8; ++i) o[h][i] *= c;
             mrun[h] = mn;
         }
-    };
-    for (int s = 0; s < steps; s += kRing) {
 #pragma unroll
         for (int r = 0; r < kRing; ++r) {
-            if (s + r < steps) {
-                consume(kring[r], vring[r], s + r);
-                issue(r, s + r + kRing);
+            if (r >= nr) continue;
+            const int t = t0 + (s0 + r) * kStepTokens + 4 * wave + grp;
+            float vf[8];
+            unpack_f16x8(vring[r], vf);
+            if (has_new && t == pos) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) vf[i] = kv_new[1][8 * j + i];
+            }
+#pragma unroll
+            for (int h = 0; h < QPK; ++h) {
+                const float p = __builtin_amdgcn_exp2f(sc[r][h] - mrun[h]);
+                lrun[h] += p;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[h][i] = __builtin_fmaf(p, vf[i], o[h][i]);
             }
         }
+#pragma unroll
+        for (int r = 0; r < kRing; ++r) issue(r, s0 + r + kRing);
     }
 
     // ---- merge the four row states of each wave (lane xor 16, xor 32), then
@@ -229,8 +285,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
             const float m2 = __shfl_xor(mrun[h], off, 64);
             const float l2 = __shfl_xor(lrun[h], off, 64);
             const float mx = fmaxf(mrun[h], m2);
-            const float f1 = expf(mrun[h] - mx);
-            const float f2 = expf(m2 - mx);
+            const float f1 = __builtin_amdgcn_exp2f(mrun[h] - mx);
+            const float f2 = __builtin_amdgcn_exp2f(m2 - mx);
             lrun[h] = lrun[h] * f1 + l2 * f2;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -252,6 +308,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
+    float* outm = a.out + ((size_t)m * a.q_heads + (size_t)kvh * QPK) * kHeadDim;
     for (int idx = tid; idx < QPK * kHeadDim; idx += kThreads) {
         const int h = idx / kHeadDim;
         const int d = idx - h * kHeadDim;
@@ -262,17 +319,20 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         float l = 0.f, acc = 0.f;
 #pragma unroll
         for (int q = 0; q < kWaves; ++q) {
-            const float f = expf(st_m[q][h] - mx);
+            const float f = __builtin_amdgcn_exp2f(st_m[q][h] - mx);
             l = __builtin_fmaf(st_l[q][h], f, l);
             acc = __builtin_fmaf(st_o[q][h][d], f, acc);
         }
-        part[d] = acc;
-        if (d == 0) {
-            part[kHeadDim] = mx;
-            part[kHeadDim + 1] = l;
+        if (single) {
+            outm[h * kHeadDim + d] = acc / l;
+        } else {
+            part[d] = acc;
+            if (d == 0) {
+                part[kHeadDim] = mx;
+                part[kHeadDim + 1] = l;
+            }
         }
     }
-
 }
 
 // Merges the kAttnChunks partials of one (member, query head) into the
@@ -286,14 +346,26 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(AttnArgs a) {
     const int m = blockIdx.y;
     const int d = threadIdx.x;
     __shared__ float mc[kAttnChunks], lc[kAttnChunks];
+    // every chunk slot is requested together with the position. Slots past
+    // the context's chunks hold stale memory (possibly NaN bit patterns): they
+    // are replaced by a neutral state (sum 0, maximum -FLT_MAX, denominator 0)
+    // before any arithmetic, so no guard on later operations is needed.
     const float* part = a.mem[m].partials + (size_t)qh * kAttnChunks * kPartStride;
     float o[kAttnChunks];
 #pragma unroll
     for (int c = 0; c < kAttnChunks; ++c) o[c] = part[c * kPartStride + d];
+    const float mcv = d < kAttnChunks ? part[d * kPartStride + kHeadDim] : 0.f;
+    const float lcv = d < kAttnChunks ? part[d * kPartStride + kHeadDim + 1] : 0.f;
+    const int tokens = a.positions[m] + 1;
+    const int len = chunk_tokens(tokens);
+    const int chunks = (tokens + len - 1) / len;
+    if (chunks <= 1) return;  // the attention launch wrote the output
     if (d < kAttnChunks) {
-        mc[d] = part[d * kPartStride + kHeadDim];
-        lc[d] = part[d * kPartStride + kHeadDim + 1];
+        mc[d] = d < chunks ? mcv : -FLT_MAX;
+        lc[d] = d < chunks ? lcv : 0.f;
     }
+#pragma unroll
+    for (int c = 0; c < kAttnChunks; ++c) o[c] = c < chunks ? o[c] : 0.f;
     __syncthreads();
     float mx = -FLT_MAX;
 #pragma unroll
@@ -301,7 +373,7 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(AttnArgs a) {
     float l = 0.f, acc = 0.f;
 #pragma unroll
     for (int c = 0; c < kAttnChunks; ++c) {
-        const float f = expf(mc[c] - mx);
+        const float f = __builtin_amdgcn_exp2f(mc[c] - mx);
         l = __builtin_fmaf(lc[c], f, l);
         acc = __builtin_fmaf(o[c], f, acc);
     }
@@ -397,7 +469,11 @@ hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t strea
     if (members < 1 || members > kAttnMaxMembers || args.kv_heads < 1 || args.q_heads % args.kv_heads != 0) {
         return hipErrorInvalidValue;
     }
-    const dim3 grid(kAttnChunks, (unsigned)args.kv_heads, (unsigned)members);
+    // chunks a context can need: capacity / kMinChunkTokens, up to kAttnChunks
+    int max_capacity = 1;
+    for (int m = 0; m < members; ++m) max_capacity = std::max(max_capacity, args.mem[m].capacity);
+    const int chunks = std::min(kAttnChunks, (max_capacity + kMinChunkTokens - 1) / kMinChunkTokens);
+    const dim3 grid((unsigned)chunks, (unsigned)args.kv_heads, (unsigned)members);
     switch (args.q_heads / args.kv_heads) {
     case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(kThreads), 0, stream, args); break;
     case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(kThreads), 0, stream, args); break;

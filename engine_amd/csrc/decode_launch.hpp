@@ -40,7 +40,7 @@ struct AttnArgs {
     int kv_heads;
     float eps;
     float rope_base;
-    float scale;               // 1/sqrt(head_dim)
+    float scale;               // log2(e) / sqrt(head_dim): scores are kept in log2 units
 };
 
 // Floats of one sequence's attention partials ([q_heads][kAttnChunks][kPartStride]).

@@ -213,7 +213,8 @@ hipError_t attention(const ribn_amd_qwen3_config& cfg, ribn_amd_kv_cache* const*
         a.kv_heads = (int)cfg.kv_heads;
         a.eps = cfg.epsilon;
         a.rope_base = cfg.rope_base;
-        a.scale = 1.0f / sqrtf((float)cfg.head_dim);
+        // softmax weights are exp2 of scores in log2 units: e^x = 2^(x log2 e)
+        a.scale = 1.4426950408889634f / sqrtf((float)cfg.head_dim);
         hipError_t e = ribn_amd::launch_attention(a, mc, stream);
         if (e != hipSuccess) return e;
     }
