@@ -3,6 +3,7 @@
     python -m engine_amd.profiling trace <dir-or-kernel_trace.csv>
     python -m engine_amd.profiling pmc <dir-or-counter_collection.csv> [--copy-bytes N]
     python -m engine_amd.profiling source-hash
+    python -m engine_amd.profiling decode-steps <dir-or-kernel_trace.csv> [--steps N]
 
 `trace` groups dispatches by (kernel, grid size), since one kernel instance can
 serve launches of different shapes (the q/k/v and gate/up groups share one),
@@ -13,6 +14,12 @@ FETCH_SIZE and WRITE_SIZE are reported by rocprofv3 in KiB; with
 `--copy-bytes N` the summary also reads the counter on the largest copy kernel
 in the run (a device-to-device copy of N bytes reads N and writes N bytes) and
 prints the scale factor that maps the counter onto true bytes.
+
+`decode-steps` summarises the last N generation steps of each batch size in
+a trace of the decoder: a step ends with its argmax dispatch, and the argmax
+grid (one workgroup per member) tells the batch sizes apart. Per kernel and
+grid it prints launches per step, mean duration and time per step, and per
+batch size the span and busy time of the window.
 
 `source-hash` prints the hash of the decode GEMV's sources, recorded in
 profile summaries so a stale measurement is recognisable.
@@ -67,7 +74,7 @@ def _demangle(name: str) -> str:
 
 def short_name(name: str) -> str:
     name = _demangle(name)
-    name = name.replace("void ", "", 1).replace("ribn_amd::", "")
+    name = name.replace("void ", "", 1).replace("ribn_amd::", "").replace("(anonymous namespace)::", "")
     depth, out = 0, []
     for ch in name:  # drop the argument list, keep template arguments
         if ch == "(" and depth == 0:
@@ -102,6 +109,43 @@ def trace_summary(path: str, match: str = "") -> list[tuple]:
     return out
 
 
+def _dispatches(path: str) -> list[tuple[str, int, int, int]]:
+    """[(kernel, grid, start_ns, end_ns)] of a kernel trace in start order."""
+    rows = []
+    for f in _find(path, "kernel_trace.csv"):
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                rows.append((short_name(row["Kernel_Name"]), _grid(row), int(row["Start_Timestamp"]),
+                             int(row["End_Timestamp"])))
+    rows.sort(key=lambda r: r[2])
+    return rows
+
+
+def decode_steps_summary(path: str, steps: int = 32) -> list[dict]:
+    """Per batch size (argmax grid): the last `steps` steps' kernels, see the module doc."""
+    rows = _dispatches(path)
+    ends: dict[int, list[int]] = defaultdict(list)
+    for i, (name, grid, _, _) in enumerate(rows):
+        if name.startswith("argmax_kernel"):
+            ends[grid].append(i)
+    out = []
+    for grid in sorted(ends):
+        idx = ends[grid]
+        if len(idx) < steps + 1:
+            continue
+        window = rows[idx[-steps - 1] + 1:idx[-1] + 1]
+        groups: dict[tuple, list[int]] = defaultdict(list)
+        for name, g, t0, t1 in window:
+            groups[(name, g)].append(t1 - t0)
+        kernels = sorted(((k[0], k[1], len(v) / steps, statistics.mean(v) / 1e3, sum(v) / steps / 1e3)
+                          for k, v in groups.items()), key=lambda r: -r[4])
+        span = (window[-1][3] - window[0][2]) / 1e3
+        busy = sum(t1 - t0 for _, _, t0, t1 in window) / 1e3
+        out.append({"argmax_grid": grid, "steps": steps, "dispatches": len(window), "span_us": span,
+                    "busy_us": busy, "kernels": kernels})
+    return out
+
+
 def pmc_summary(path: str) -> dict[tuple, dict[str, float]]:
     """{(kernel, grid): {counter: mean value per dispatch}}."""
     acc: dict[tuple, dict[str, list[float]]] = defaultdict(lambda: defaultdict(list))
@@ -125,11 +169,20 @@ def copy_scale(summary: dict, counter: str, copy_bytes: int) -> float | None:
 
 
 def _main(argv: list[str]) -> int:
-    if not argv or argv[0] not in ("trace", "pmc", "source-hash"):
+    if not argv or argv[0] not in ("trace", "pmc", "source-hash", "decode-steps"):
         print(__doc__)
         return 2
     if argv[0] == "source-hash":
         print(source_hash())
+        return 0
+    if argv[0] == "decode-steps":
+        steps = int(argv[argv.index("--steps") + 1]) if "--steps" in argv else 32
+        for w in decode_steps_summary(argv[1], steps):
+            print(f"== argmax grid {w['argmax_grid']}: {w['steps']} steps, {w['dispatches']} dispatches, "
+                  f"span {w['span_us'] / w['steps']:.1f} us/step, busy {w['busy_us'] / w['steps']:.1f} us/step")
+            print(f"{'kernel':60s} {'grid':>9s} {'per_step':>8s} {'mean_us':>9s} {'us/step':>9s}")
+            for name, grid, n, mean, per in w["kernels"]:
+                print(f"{name:60s} {grid:9d} {n:8.1f} {mean:9.3f} {per:9.1f}")
         return 0
     if argv[0] == "trace":
         match = argv[2] if len(argv) > 2 else ""

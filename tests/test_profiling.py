@@ -1,0 +1,58 @@
+"""CPU tests of the rocprofv3 summary helpers (engine_amd/profiling.py) on
+small synthetic trace and counter files in rocprofv3's CSV layout."""
+import csv
+
+from engine_amd import profiling as P
+
+TRACE_FIELDS = ["Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp", "End_Timestamp"]
+
+
+def _write_trace(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=TRACE_FIELDS)
+        w.writeheader()
+        for name, grid, t0, t1 in rows:
+            w.writerow({"Kernel_Name": name, "Grid_Size_X": grid[0], "Grid_Size_Y": grid[1],
+                        "Grid_Size_Z": grid[2], "Start_Timestamp": t0, "End_Timestamp": t1})
+
+
+def test_short_name_demangles_and_drops_namespaces():
+    assert P.short_name("_ZN8ribn_amd16gemv_wave_kernelILi12ELi1ELi1ELb1ELi2ELi8ELi1ELb0EEEvNS_11WaveGemvArgsE") == \
+        "gemv_wave_kernel<12, 1, 1, true, 2, 8, 1, false>"
+    assert P.short_name("void ribn_amd::(anonymous namespace)::attn_decode_kernel<4>(ribn_amd::AttnArgs)") == \
+        "attn_decode_kernel<4>"
+
+
+def test_trace_summary_groups_by_kernel_and_grid(tmp_path):
+    f = tmp_path / "run_kernel_trace.csv"
+    _write_trace(f, [("void ribn_amd::k<1>(int)", (64, 1, 1), 0, 2000),
+                     ("void ribn_amd::k<1>(int)", (64, 1, 1), 3000, 7000),
+                     ("void ribn_amd::k<1>(int)", (128, 1, 1), 8000, 9000)])
+    rows = {(r[0], r[1]): r for r in P.trace_summary(str(tmp_path))}
+    assert rows[("k<1>", 64)][2:] == (2, 3.0, 3.0, 2.0)
+    assert rows[("k<1>", 128)][2] == 1
+
+
+def test_decode_steps_windows_by_argmax_grid(tmp_path):
+    # batch 1 (argmax grid 1024): three steps of gemv (2 us) + argmax (1 us);
+    # batch 8 (grid 8192) afterwards: two steps of gemv (5 us) + argmax (1 us),
+    # with 4x2x1 grids to check X*Y*Z.
+    rows, t = [], 0
+    for _ in range(3):
+        rows.append(("void ribn_amd::gemv<1>(int)", (4096, 1, 1), t, t + 2000))
+        rows.append(("void ribn_amd::(anonymous namespace)::argmax_kernel(int)", (1024, 1, 1), t + 2000, t + 3000))
+        t += 3000
+    for _ in range(2):
+        rows.append(("void ribn_amd::gemv<8>(int)", (4, 2, 1), t, t + 5000))
+        rows.append(("void ribn_amd::(anonymous namespace)::argmax_kernel(int)", (1024, 8, 1), t + 5000, t + 6000))
+        t += 6000
+    _write_trace(tmp_path / "x_kernel_trace.csv", rows)
+    w = {r["argmax_grid"]: r for r in P.decode_steps_summary(str(tmp_path), steps=1)}
+    assert sorted(w) == [1024, 8192]
+    b1 = w[1024]
+    assert b1["dispatches"] == 2 and b1["span_us"] == 3.0 and b1["busy_us"] == 3.0
+    assert b1["kernels"][0] == ("gemv<1>", 4096, 1.0, 2.0, 2.0)
+    b8 = w[8192]
+    assert b8["kernels"][0] == ("gemv<8>", 8, 1.0, 5.0, 5.0)
+    # more steps than the trace holds: that batch size is left out
+    assert [r["argmax_grid"] for r in P.decode_steps_summary(str(tmp_path), steps=2)] == [1024]
