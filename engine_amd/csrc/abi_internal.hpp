@@ -15,6 +15,7 @@ struct ribn_amd_context {
     int cu_count;
     void* workspace;  // prefill activation workspace (ribn_amd_context_reserve_prefill)
     size_t workspace_bytes;
+    void* act_scratch;  // packed activations of the matrix-core batched GEMV, reserved at creation
 };
 
 struct ribn_amd_quantized_weight {

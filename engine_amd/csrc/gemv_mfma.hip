@@ -1,0 +1,544 @@
+// Batched k-quant GEMV on the int8 matrix cores (gfx950 / CDNA4, wave64),
+// for up to 16 members: the weights-read-once batch product of the decode path
+// (quantized.rs batch GEMV, decode.rs:1480-1558) where the wave GEMV's
+// per-member integer dot products become VALU-bound.
+//
+// Activations (pack_act16_kernel, one launch per product)
+//  - Each member's x (times the RMSNorm weight gamma when given) is cut into
+//    256-element super-blocks. A block with max|x| < 2^e is stored as 15-bit
+//    fixed point v = rint(x * 2^(14-e)), |v| <= 2^14, split into two signed
+//    digits v = 256 h + l with l in [-128, 127] and h in [-64, 64], so both
+//    planes are int8 MFMA operands and every product stays exact.
+//  - Per (member tile of 16, block): 8 groups x 64 lanes x 16 bytes of
+//    fragments in the MFMA A-operand order (lane = member + 16 * chunk, eight
+//    h bytes then eight l bytes of elements 32g + 8 chunk .. + 7), the block
+//    unscale 2^(e-14) of each member, and u * X_g (X_g = sum of v over group g)
+//    for the minimum term. A workgroup also writes its partial sum of x^2, so
+//    the product applies RMSNorm's 1/rms per member at its output (the wave
+//    GEMV's factorisation: y = (W (x * gamma)) / rms).
+//
+// Product (mfma_gemv_kernel)
+//  - A wave owns R tiles of 16 weight rows over a contiguous range of
+//    super-blocks; the KS waves of a workgroup split K and add their results
+//    in LDS in wave order (deterministic).
+//  - Per 32-element k-quant group g, two v_mfma_i32_16x16x32_i8 (h and l
+//    planes; A = activations [member][k], B = quants [k][row]) give the exact
+//    S_g = sum(q v) for 16 members x 16 rows. With the group's scale a_g =
+//    d * sc_g (crates/gguf/src/lib.rs:573-612) the block contributes
+//    u_b * sum_g a_g S_g; the minimum term sum_g (dmin * m_g) (u_b X_g) is a
+//    [member][group] x [group][row] product on v_mfma_f32_16x16x4_f32.
+//  - Lane l holds output rows l % 16 for members 4 (l / 16) .. + 3, so each
+//    lane decodes the scales of one weight row per block.
+// Each member's result depends only on its own activations: a member's output
+// bits do not change with the other members of the batch.
+#include "kquant_device.hpp"
+#include "kquant_launch.hpp"
+
+#include <algorithm>
+
+namespace ribn_amd {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kOOR = 0xffffff00u;   // buffer offset past any tensor: loads return 0, stores drop
+constexpr int kPackBlocks = 8;           // super-blocks one pack workgroup covers
+constexpr int kFragBlockBytes = 8 * 64 * 16;
+constexpr int kMinBlockBytes = 64 * 8;
+constexpr int kUBlockBytes = 16 * 4;
+constexpr int kMaxWaves = 8;             // K-split waves per workgroup (256 VGPRs each)
+
+__device__ __forceinline__ uint2 load_b64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) {
+    return (long)(((unsigned long)hi << 32) | lo);
+}
+
+// ------------------------------------------------------------ activation pack
+
+struct PackArgs {
+    const float* x;      // [members][K]
+    const float* gamma;  // [K] or null
+    uint8_t* act;
+    Act16Layout L;
+    int K;
+};
+
+__global__ __launch_bounds__(256) void pack_act16_kernel(PackArgs a) {
+    __shared__ float wsum[4];
+    const int m = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x * kPackBlocks + (tid >> 5);
+    const int c = tid & 31;
+    const int g = c >> 2, kq = c & 3;
+    const int nb = a.L.nb;
+    const bool live = b < nb;
+    float v[8];
+    float ssq = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = 0.f;
+    if (live) {
+        const size_t e0 = (size_t)m * a.K + (size_t)b * 256 + 32 * g + 8 * kq;
+        const float4 x0 = *reinterpret_cast<const float4*>(a.x + e0);
+        const float4 x1 = *reinterpret_cast<const float4*>(a.x + e0 + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ssq += v[j] * v[j];
+        if (a.gamma != nullptr) {
+            const size_t k0 = (size_t)b * 256 + 32 * g + 8 * kq;
+            const float4 g0 = *reinterpret_cast<const float4*>(a.gamma + k0);
+            const float4 g1 = *reinterpret_cast<const float4*>(a.gamma + k0 + 4);
+            v[0] *= g0.x; v[1] *= g0.y; v[2] *= g0.z; v[3] *= g0.w;
+            v[4] *= g1.x; v[5] *= g1.y; v[6] *= g1.z; v[7] *= g1.w;
+        }
+    }
+    // block maximum over the 32 lanes of this block (a half wave)
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    // mx < 2^ex; blocks below 2^-100 quantize to zero
+    int ex = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) : 0;
+    ex = ex < -100 ? -100 : ex;
+    const int sh = 14 - ex;
+    uint32_t hw[2] = {0u, 0u}, lw[2] = {0u, 0u};
+    int xs = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(v[j], sh));  // |q| <= 2^14
+        xs += q;
+        const int lo = ((q + 128) & 255) - 128;
+        const int hi = (q - lo) >> 8;
+        hw[j >> 2] |= ((uint32_t)hi & 0xffu) << (8 * (j & 3));
+        lw[j >> 2] |= ((uint32_t)lo & 0xffu) << (8 * (j & 3));
+    }
+    xs += __shfl_xor(xs, 1, 64);
+    xs += __shfl_xor(xs, 2, 64);  // X_g over the four chunks of group g
+    if (live) {
+        const int mt = m >> 4, mi = m & 15;
+        const size_t blk = (size_t)mt * nb + b;
+        uint4 f;
+        f.x = hw[0]; f.y = hw[1]; f.z = lw[0]; f.w = lw[1];
+        *reinterpret_cast<uint4*>(a.act + a.L.frag + ((blk * 8 + g) * 64 + mi + 16 * kq) * 16) = f;
+        if (kq == 0) {
+            float* mina = reinterpret_cast<float*>(a.act + a.L.mina);
+            mina[(blk * 64 + mi + 16 * (g & 3)) * 2 + (g >> 2)] = __builtin_amdgcn_ldexpf((float)xs, ex - 14);
+        }
+        if (c == 0) {
+            reinterpret_cast<float*>(a.act + a.L.ublk)[blk * 16 + mi] = __builtin_amdgcn_ldexpf(1.0f, ex - 14);
+        }
+    }
+    // this workgroup's share of sum(x^2), for RMSNorm (summed in part order by the product)
+    const float ws = wave_sum(ssq);
+    if ((tid & 63) == 0) wsum[tid >> 6] = ws;
+    __syncthreads();
+    if (tid == 0) {
+        reinterpret_cast<float*>(a.act + a.L.ssq)[m * a.L.parts + blockIdx.x] =
+            (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    }
+}
+
+// ------------------------------------------------------------------ product
+
+template <int T> struct WRaw;
+template <> struct WRaw<kQ4K> { uint4 h; uint2 q[4]; };
+template <> struct WRaw<kQ5K> { uint4 h; uint2 qh; uint2 q[4]; };
+
+// One lane's bytes of a 16-row tile's super-block: the 16-byte header (d,
+// dmin, packed scales) and, for each group pair p, the 8 quant bytes of
+// elements 8 kq .. 8 kq + 7 (low nibbles: group 2p, high: 2p + 1).
+template <int T>
+__device__ __forceinline__ void load_w(WRaw<T>& d, __amdgpu_buffer_rsrc_t r, bool live, uint32_t base, int kq) {
+    d.h = load_b128(r, live ? base : kOOR);
+    if constexpr (T == kQ5K) {
+        d.qh = load_b64(r, live ? base + 16u + 8u * kq : kOOR);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) d.q[p] = load_b64(r, live ? base + 48u + 32u * p + 8u * kq : kOOR);
+    } else {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) d.q[p] = load_b64(r, live ? base + 16u + 32u * p + 8u * kq : kOOR);
+    }
+}
+
+struct ActBlk {
+    uint4 f[8];   // fragments of the 8 groups
+    float2 mina;  // u X for groups kq and 4 + kq of member lane % 16
+    float4 u;     // block unscale of members 4 kq .. 4 kq + 3
+};
+
+// Lanes of absent members (lane % 16 >= members) load nothing: their A rows
+// only reach output rows that are never stored.
+__device__ __forceinline__ void load_act(ActBlk& x, __amdgpu_buffer_rsrc_t r, const MfmaGemvArgs& A, bool live,
+                                         int b, int lane) {
+    const bool own = live && (lane & 15) < A.members;
+    const uint32_t fb = A.L.frag + ((uint32_t)b * 8u * 64u + (uint32_t)lane) * 16u;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) x.f[g] = load_b128(r, own ? fb + 1024u * g : kOOR);
+    const uint2 mn = load_b64(r, own ? A.L.mina + ((uint32_t)b * 64u + (uint32_t)lane) * 8u : kOOR);
+    x.mina = __builtin_bit_cast(float2, mn);
+    const bool any = live && 4 * (lane >> 4) < A.members;
+    const uint4 uu = load_b128(r, any ? A.L.ublk + ((uint32_t)b * 16u + 4u * (uint32_t)(lane >> 4)) * 4u : kOOR);
+    x.u = __builtin_bit_cast(float4, uu);
+}
+
+template <int T>
+__device__ __forceinline__ void block_mma(const WRaw<T>& d, const ActBlk& x, int kq, v4f& acc, v4f& macc) {
+    const uint4 h = d.h;
+    const float dd = half_bits_to_float(h.x & 0xffffu);
+    const float dmin = half_bits_to_float(h.x >> 16);
+    // six-bit scales / minima of the 8 groups, four per word (lib.rs:573-587)
+    const uint32_t lo_sc = h.y & 0x3f3f3f3fu;
+    const uint32_t lo_mn = h.z & 0x3f3f3f3fu;
+    const uint32_t hi_sc = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t hi_mn = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+    const v4i zero = {0, 0, 0, 0};
+    float accb[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        const int p = g >> 1, sh = 4 * (g & 1);
+        uint32_t q0 = (d.q[p].x >> sh) & 0x0f0f0f0fu;
+        uint32_t q1 = (d.q[p].y >> sh) & 0x0f0f0f0fu;
+        if constexpr (T == kQ5K) {
+            // fifth bit of element i of group g: bit g of qh[i]
+            q0 |= ((d.qh.x >> g) & 0x01010101u) << 4;
+            q1 |= ((d.qh.y >> g) & 0x01010101u) << 4;
+        }
+        const long bq = as_long(q0, q1);
+        const v4i ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(x.f[g].x, x.f[g].y), bq, zero, 0, 0, 0);
+        const v4i cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(x.f[g].z, x.f[g].w), bq, zero, 0, 0, 0);
+        const uint32_t scw = g < 4 ? lo_sc : hi_sc;
+        const float a_g = dd * (float)((scw >> (8 * (g & 3))) & 0xffu);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) accb[t] = __builtin_fmaf(a_g, (float)(ch[t] * 256 + cl[t]), accb[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = __builtin_fmaf(x.u[t], accb[t], acc[t]);
+    // minimum term of groups kq and 4 + kq (the lane's row): A = u X [member][group], B = dmin m [group][row]
+    const float b0 = dmin * (float)((lo_mn >> (8 * kq)) & 0xffu);
+    const float b1 = dmin * (float)((hi_mn >> (8 * kq)) & 0xffu);
+    macc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.mina.x, b0, macc, 0, 0, 0);
+    macc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.mina.y, b1, macc, 0, 0, 0);
+}
+
+// One workgroup of KS waves takes R tiles of 16 weight rows; wave w covers
+// the super-blocks [nb w / KS, nb (w + 1) / KS) of K with a two-slot ring of
+// (R tiles x one super-block) units, and the waves' partial sums meet in LDS
+// in wave order.
+template <int T, int R, bool PAIR>
+__global__ __launch_bounds__(512) void mfma_gemv_kernel(MfmaGemvArgs A) {
+    constexpr int BB = BlockTraits<T>::bytes;
+    constexpr int NBUF = 2;
+    static_assert(!PAIR || R % 2 == 0, "pairs split the tiles into gate and up halves");
+    extern __shared__ float red[];  // [KS - 1][R][4][64]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ks = (int)(blockDim.x >> 6);
+    const int kq = lane >> 4, rl = lane & 15;
+    const int nb = A.K >> 8;
+    const uint32_t row_bytes = (uint32_t)nb * BB;
+    const int kb0 = nb * wave / ks, kb1 = nb * (wave + 1) / ks;
+
+    // tiles: (matrix, first local row); tiles never straddle matrices
+    __amdgpu_buffer_rsrc_t wr[R];
+    int mat[R], local0[R], rows_mat[R];
+    bool live_row[R];
+    uint32_t rowoff[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        if constexpr (PAIR) {
+            mat[i] = i / (R / 2);
+            local0[i] = ((int)blockIdx.x * (R / 2) + i % (R / 2)) * 16;
+            rows_mat[i] = A.rows_end[0];
+        } else {
+            const int row0 = ((int)blockIdx.x * R + i) * 16;
+            int mm = 0, start = 0;
+#pragma unroll
+            for (int j = 0; j < kMaxGroup - 1; ++j) {
+                if (j + 1 < A.count && row0 >= A.rows_end[j]) {
+                    mm = j + 1;
+                    start = A.rows_end[j];
+                }
+            }
+            mat[i] = mm;
+            local0[i] = row0 < A.total_rows ? row0 - start : 1 << 30;
+            rows_mat[i] = A.rows_end[mm] - start;
+        }
+        const int mm = mat[i];
+        const uint8_t* w = A.w[0];
+        uint32_t wb = A.wbytes[0];
+#pragma unroll
+        for (int j = 1; j < kMaxGroup; ++j) {
+            if (mm == j) {
+                w = A.w[j];
+                wb = A.wbytes[j];
+            }
+        }
+        wr[i] = make_rsrc(w, wb);
+        const int lrow = local0[i] + rl;
+        live_row[i] = lrow < rows_mat[i];
+        rowoff[i] = live_row[i] ? (uint32_t)lrow * row_bytes : 0u;
+    }
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A.act, A.act_bytes);
+
+    v4f acc[R], macc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+        macc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+    }
+    WRaw<T> ring[NBUF][R];
+    ActBlk act[NBUF];
+    auto fill = [&](int s, int b) {
+        const bool lb = b < kb1;
+#pragma unroll
+        for (int i = 0; i < R; ++i) load_w<T>(ring[s][i], wr[i], lb && live_row[i], rowoff[i] + (uint32_t)b * BB, kq);
+        load_act(act[s], ar, A, lb, b, lane);
+    };
+#pragma unroll
+    for (int s = 0; s < NBUF; ++s) fill(s, kb0 + s);
+    for (int b = kb0; b < kb1; b += NBUF) {
+#pragma unroll
+        for (int s = 0; s < NBUF; ++s) {
+            if (b + s < kb1) {
+#pragma unroll
+                for (int i = 0; i < R; ++i) block_mma<T>(ring[s][i], act[s], kq, acc[i], macc[i]);
+                fill(s, b + s + NBUF);
+            }
+        }
+    }
+
+    // ---- K-split reduction in wave order, then the epilogue on wave 0
+    float v[R][4];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[i][t] = acc[i][t] - macc[i][t];
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) red[((wave - 1) * R + i) * 256 + t * 64 + lane] = v[i][t];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 1; w < ks; ++w) {
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[i][t] += red[((w - 1) * R + i) * 256 + t * 64 + lane];
+    }
+    float inv[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        inv[t] = 1.f;
+        const int mem = 4 * kq + t;
+        if (A.has_norm && mem < A.members) {
+            const float* ssq = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(A.act) + A.L.ssq);
+            float total = 0.f;
+            for (int p = 0; p < A.L.parts; ++p) total += ssq[mem * A.L.parts + p];
+            // RMSNorm (qwen_reference.rs:550-556): 1/sqrt(sum(x^2)/K + eps)
+            inv[t] = 1.0f / sqrtf(total / (float)A.K + A.eps);
+        }
+    }
+    const bool accumulate = A.accumulate != 0;
+    auto put = [&](float value, __amdgpu_buffer_rsrc_t yr, uint32_t off) {
+        if (accumulate) {
+            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(value, yr, (int)off, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), yr, (int)off, 0, 0);
+        }
+    };
+    if constexpr (PAIR) {
+        const int ffn = A.rows_end[0];
+        const __amdgpu_buffer_rsrc_t yr = make_rsrc(A.y[0], (uint32_t)A.members * (uint32_t)ffn * 4u);
+#pragma unroll
+        for (int i = 0; i < R / 2; ++i) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int mem = 4 * kq + t;
+                const float gt = v[i][t] * inv[t];
+                const float up = v[i + R / 2][t] * inv[t];
+                // silu(gate) * up, in the reference's operation order (model_ops.rs:316-328)
+                const float out = (gt / (1.0f + expf(-gt))) * up;
+                const bool ok = live_row[i] && mem < A.members;
+                put(out, yr, ok ? (uint32_t)(mem * ffn + local0[i] + rl) * 4u : kOOR);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int mm = mat[i];
+            float* y = A.y[0];
+#pragma unroll
+            for (int j = 1; j < kMaxGroup; ++j) {
+                if (mm == j) y = A.y[j];
+            }
+            const __amdgpu_buffer_rsrc_t yr = make_rsrc(y, (uint32_t)A.members * (uint32_t)rows_mat[i] * 4u);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int mem = 4 * kq + t;
+                const bool ok = live_row[i] && mem < A.members;
+                put(v[i][t] * inv[t], yr, ok ? (uint32_t)(mem * rows_mat[i] + local0[i] + rl) * 4u : kOOR);
+            }
+        }
+    }
+}
+
+template <int T, int R, bool PAIR>
+hipError_t launch_shape(const MfmaGemvArgs& a, int groups, int ks, hipStream_t stream) {
+    const size_t lds = (size_t)(ks - 1) * R * 256 * sizeof(float);
+    hipLaunchKernelGGL((mfma_gemv_kernel<T, R, PAIR>), dim3((unsigned)groups), dim3((unsigned)(64 * ks)), lds,
+                       stream, a);
+    return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_t(const MfmaGemvArgs& a, hipStream_t stream) {
+    const int nb = a.K >> 8;
+    const bool pair = a.pair_swiglu != 0;
+    const int tiles = pair ? (a.rows_end[0] + 15) / 16 : (a.total_rows + 15) / 16;
+    const int r = pair ? 4 : (tiles >= 2048 && T == kQ4K ? 4 : 2);  // Q5_K x 4 tiles would spill
+    const int per_group = pair ? r / 2 : r;
+    const int groups = (tiles + per_group - 1) / per_group;
+    // The K split depends on K alone, so a row's summation order (and bits)
+    // is the same in every launch shape: grouped or not, any member count.
+    const int ks = std::min(kMaxWaves, std::max(1, nb / 2));
+    if (pair) return launch_shape<T, 4, true>(a, groups, ks, stream);
+    if constexpr (T == kQ4K) {
+        if (r == 4) return launch_shape<T, 4, false>(a, groups, ks, stream);
+    }
+    return launch_shape<T, 2, false>(a, groups, ks, stream);
+}
+
+bool rows_tile_aligned(const WaveGemvArgs& a) {
+    if (a.pair_swiglu) return a.count == 2 && a.rows_end[1] == 2 * a.rows_end[0];
+    for (int i = 0; i + 1 < a.count; ++i) {
+        if (a.rows_end[i] % 16 != 0) return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+Act16Layout act16_layout(int members, int K) {
+    Act16Layout L{};
+    const int nb = K / 256;
+    const int tiles = (members + 15) / 16;
+    L.nb = nb;
+    L.parts = (nb + kPackBlocks - 1) / kPackBlocks;
+    const uint32_t blocks = (uint32_t)tiles * (uint32_t)nb;
+    L.frag = 0;
+    L.mina = L.frag + blocks * kFragBlockBytes;
+    L.ublk = L.mina + blocks * kMinBlockBytes;
+    L.ssq = L.ublk + blocks * kUBlockBytes;
+    L.total = L.ssq + (uint32_t)members * (uint32_t)L.parts * 4u;
+    return L;
+}
+
+bool gemv_mfma_supported(int value_type) { return value_type == kQ4K || value_type == kQ5K; }
+
+hipError_t launch_pack_act16(const float* x, const float* gamma, int members, int K, void* act,
+                             hipStream_t stream) {
+    if (members < 1 || members > kMfmaMaxMembers || K < 256 || K % 256 != 0 || K > kWaveMaxK) {
+        return hipErrorInvalidValue;
+    }
+    PackArgs a{};
+    a.x = x;
+    a.gamma = gamma;
+    a.act = static_cast<uint8_t*>(act);
+    a.L = act16_layout(members, K);
+    a.K = K;
+    hipLaunchKernelGGL(pack_act16_kernel, dim3((unsigned)a.L.parts, (unsigned)members), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& a, int /*cu_count*/, hipStream_t stream) {
+    if (a.members < 1 || a.members > kMfmaMaxMembers || a.K < 256 || a.K % 256 != 0 || a.K > kWaveMaxK ||
+        a.count < 1 || a.count > kMaxGroup) {
+        return hipErrorInvalidValue;
+    }
+    if (a.pair_swiglu) {
+        if (a.count != 2 || a.rows_end[1] != 2 * a.rows_end[0]) return hipErrorInvalidValue;
+    } else {
+        for (int i = 0; i + 1 < a.count; ++i) {
+            if (a.rows_end[i] % 16 != 0) return hipErrorInvalidValue;  // tiles never straddle matrices
+        }
+    }
+    switch (value_type) {
+    case kQ4K: return launch_t<kQ4K>(a, stream);
+    case kQ5K: return launch_t<kQ5K>(a, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ------------------------------------------------------------ dispatcher
+
+size_t gemv_act_scratch_bytes() { return act16_layout(kMfmaMaxMembers, kWaveMaxK).total; }
+
+int gemv_launch_members(int value_type, int K, bool swiglu_prologue) {
+    if (!swiglu_prologue && gemv_mfma_supported(value_type) && K % 256 == 0 && K <= kWaveMaxK) {
+        return kMfmaMaxMembers;
+    }
+    int per = std::min(wave_max_members(K), kWaveMaxMembers);
+    if (swiglu_prologue) per = std::min(per, kSwigluMaxMembers);
+    return per;
+}
+
+hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch, int cu_count, hipStream_t stream) {
+    // Measured on MI355X: the matrix cores win where the wave GEMV would need
+    // several launches (more than kWaveMaxMembers members; K beyond one slice,
+    // where it takes two members per launch, from kMfmaMinMembers members);
+    // up to 8 members of K <= 4096 stay on the wave GEMV, which matches or
+    // beats them there.
+    const bool wanted = a.members > kWaveMaxMembers || (a.K > kSliceK && a.members >= kMfmaMinMembers);
+    const bool mfma = wanted && a.members <= kMfmaMaxMembers && a.x2 == nullptr && act_scratch != nullptr &&
+                      gemv_mfma_supported(value_type) && a.K % 256 == 0 && a.K <= kWaveMaxK && rows_tile_aligned(a);
+    if (!mfma) {
+        // the wave GEMV, in launch groups of as many members as it stages
+        int per = std::min(wave_max_members(a.K), kWaveMaxMembers);
+        if (a.x2 != nullptr) per = std::min(per, kSwigluMaxMembers);
+        if (per <= 0) return hipErrorInvalidValue;
+        for (int m0 = 0; m0 < a.members; m0 += per) {
+            WaveGemvArgs c = a;
+            c.members = std::min(per, a.members - m0);
+            c.x = a.x + (size_t)m0 * a.K;
+            c.x2 = a.x2 != nullptr ? a.x2 + (size_t)m0 * a.K : nullptr;
+            for (int i = 0; i < a.count; ++i) {
+                const int n = a.rows_end[i] - (i > 0 ? a.rows_end[i - 1] : 0);
+                c.y[i] = a.y[i] + (size_t)m0 * (a.pair_swiglu ? a.rows_end[0] : n);
+            }
+            hipError_t e = launch_gemv_wave(value_type, c, cu_count, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    hipError_t e = launch_pack_act16(a.x, a.gamma, a.members, a.K, act_scratch, stream);
+    if (e != hipSuccess) return e;
+    MfmaGemvArgs m{};
+    for (int i = 0; i < kMaxGroup; ++i) {
+        m.w[i] = a.w[i];
+        m.wbytes[i] = a.wbytes[i];
+        m.y[i] = a.y[i];
+        m.rows_end[i] = a.rows_end[i];
+    }
+    m.count = a.count;
+    m.total_rows = a.total_rows;
+    m.act = act_scratch;
+    m.L = act16_layout(a.members, a.K);
+    m.act_bytes = m.L.total;
+    m.K = a.K;
+    m.members = a.members;
+    m.has_norm = a.gamma != nullptr ? 1 : 0;
+    m.eps = a.eps;
+    m.accumulate = a.accumulate;
+    m.pair_swiglu = a.pair_swiglu;
+    return launch_gemv_mfma(value_type, m, cu_count, stream);
+}
+
+}  // namespace ribn_amd

@@ -50,6 +50,61 @@ struct WaveGemvArgs {
 // Largest member count one wave launch can stage for this K (0 if none).
 int wave_max_members(int K);
 
+// ---- batched GEMV on the int8 matrix cores (gemv_mfma.hip), up to 16 members
+
+constexpr int kMfmaMaxMembers = 16;
+// Below this many members a K spanning several slices stays on the wave GEMV
+// (two members per launch), which is faster there.
+constexpr int kMfmaMinMembers = 6;
+
+// Byte offsets of the packed activations of `members` x K (K a multiple of
+// 256): MFMA fragments, per-group minimum-term inputs, per-block unscales and
+// per-workgroup partial sums of squares.
+struct Act16Layout {
+    uint32_t frag, mina, ublk, ssq, total;
+    int nb;     // super-blocks of K
+    int parts;  // pack workgroups per member (partial sums of squares)
+};
+Act16Layout act16_layout(int members, int K);
+
+struct MfmaGemvArgs {
+    const uint8_t* w[kMaxGroup];
+    uint32_t wbytes[kMaxGroup];
+    float* y[kMaxGroup];      // y[i] is [members][N_i]
+    int rows_end[kMaxGroup];  // prefix sums of N_i; all but the last a multiple of 16
+    int count;
+    int total_rows;
+    const void* act;          // launch_pack_act16 output for these members and K
+    uint32_t act_bytes;
+    Act16Layout L;
+    int K;
+    int members;
+    int has_norm;             // the activations were packed with gamma: outputs are divided by rms(x)
+    float eps;
+    int accumulate;           // nonzero: y += W x'
+    int pair_swiglu;          // w[0] / w[1] gate / up of equal shape; y[0] receives silu(g) * u
+};
+
+bool gemv_mfma_supported(int value_type);
+// Packs x [members][K] (times gamma when given) for launch_gemv_mfma.
+hipError_t launch_pack_act16(const float* x, const float* gamma, int members, int K, void* act,
+                             hipStream_t stream);
+hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& args, int cu_count, hipStream_t stream);
+
+// ---- GEMV dispatch used by the C ABI and the decoder
+
+// Device scratch (bytes) a context reserves for launch_gemv's packed activations.
+size_t gemv_act_scratch_bytes();
+// Members one launch_gemv call may carry for this shape.
+int gemv_launch_members(int value_type, int K, bool swiglu_prologue);
+// Q4_K / Q5_K without the SwiGLU prologue (and with tiles not straddling
+// grouped weights) run packed activations through the matrix-core GEMV (two
+// launches) for 9..16 members, or 6..16 members when K spans more than one
+// slice; every other call runs the wave GEMV, split into the launch groups it
+// stages.
+hipError_t launch_gemv(int value_type, const WaveGemvArgs& args, void* act_scratch, int cu_count,
+                       hipStream_t stream);
+
 hipError_t launch_dequant(int value_type, const uint8_t* w, uint32_t wbytes, float* out, uint32_t nblocks,
                           hipStream_t stream);
 

@@ -135,14 +135,14 @@ struct ribn_amd_qwen3_decode {
 
 namespace {
 
-// Wave GEMV over `count` weights of one value type sharing the activation x,
-// in launch groups of as many members as one launch stages.
+// GEMV over `count` weights of one value type sharing the activation x, in
+// launch groups of as many members as one launch serves (the wave GEMV, or the
+// matrix-core GEMV for 3..16 members of Q4_K / Q5_K).
 hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight* const* ws, int count,
                 const float* x, const float* x2, const float* gamma, float* const* ys, int members, bool accumulate,
                 hipStream_t stream, bool pair = false) {
     const int K = (int)ws[0]->input_size;
-    int per = std::min(ribn_amd::wave_max_members(K), ribn_amd::kWaveMaxMembers);
-    if (x2 != nullptr) per = std::min(per, ribn_amd::kSwigluMaxMembers);
+    const int per = ribn_amd::gemv_launch_members((int)ws[0]->value_type, K, x2 != nullptr);
     if (per <= 0) return hipErrorInvalidValue;
     for (int m0 = 0; m0 < members; m0 += per) {
         const int mc = std::min(per, members - m0);
@@ -166,7 +166,8 @@ hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight*
         a.members = mc;
         a.accumulate = accumulate ? 1 : 0;
         a.pair_swiglu = pair ? 1 : 0;
-        hipError_t e = ribn_amd::launch_gemv_wave((int)ws[0]->value_type, a, d->ctx->cu_count, stream);
+        hipError_t e = ribn_amd::launch_gemv((int)ws[0]->value_type, a, d->ctx->act_scratch, d->ctx->cu_count,
+                                             stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

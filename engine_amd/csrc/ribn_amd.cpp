@@ -170,6 +170,7 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
         }
         return ok();
     }
+    per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, up != nullptr);
     for (size_t m0 = 0; m0 < members; m0 += (size_t)per_launch) {
         const size_t mc = std::min<size_t>((size_t)per_launch, members - m0);
         ribn_amd::WaveGemvArgs a{};
@@ -191,8 +192,9 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
         a.eps = eps;
         a.K = (int)k;
         a.members = (int)mc;
-        hipError_t e = ribn_amd::launch_gemv_wave((int)g->value_type, a, g->ctx->cu_count, g->ctx->stream);
-        if (e != hipSuccess) return driver(e, "launch wave GEMV");
+        hipError_t e = ribn_amd::launch_gemv((int)g->value_type, a, g->ctx->act_scratch, g->ctx->cu_count,
+                                             g->ctx->stream);
+        if (e != hipSuccess) return driver(e, "launch GEMV");
     }
     return ok();
 }
@@ -216,8 +218,19 @@ ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_
     hipDeviceProp_t prop;
     hipError_t e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return driver(e, "hipGetDeviceProperties");
-    auto* ctx = new (std::nothrow) ribn_amd_context{device, stream, owns, prop.multiProcessorCount, nullptr, 0};
-    if (!ctx) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    void* scratch = nullptr;
+    {
+        DeviceGuard guard(device);
+        e = hipMalloc(&scratch, ribn_amd::gemv_act_scratch_bytes());
+        if (e != hipSuccess) return driver(e, "hipMalloc batched-GEMV activation scratch");
+    }
+    auto* ctx =
+        new (std::nothrow) ribn_amd_context{device, stream, owns, prop.multiProcessorCount, nullptr, 0, scratch};
+    if (!ctx) {
+        DeviceGuard guard(device);
+        hipFree(scratch);
+        return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    }
     *out = ctx;
     return ok();
 }
@@ -302,10 +315,9 @@ ribn_amd_status ribn_amd_context_wrap_stream(int32_t device, void* hip_stream, r
 void ribn_amd_context_destroy(ribn_amd_context* ctx) {
     if (!ctx) return;
     DeviceGuard guard(ctx->device);
-    if (ctx->workspace) {
-        hipStreamSynchronize(ctx->stream);
-        hipFree(ctx->workspace);
-    }
+    if (ctx->workspace || ctx->act_scratch) hipStreamSynchronize(ctx->stream);
+    if (ctx->workspace) hipFree(ctx->workspace);
+    if (ctx->act_scratch) hipFree(ctx->act_scratch);
     if (ctx->owns_stream) {
         hipStreamSynchronize(ctx->stream);
         hipStreamDestroy(ctx->stream);
@@ -729,7 +741,7 @@ ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv* g, const rib
         if (st != RIBN_AMD_OK) return st;
     }
     DeviceGuard guard(g->ctx->device);
-    const int per_launch = std::min(ribn_amd::wave_max_members((int)k), ribn_amd::kWaveMaxMembers);
+    const int per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, false);
     for (size_t m0 = 0; m0 < members; m0 += (size_t)per_launch) {
         const size_t mc = std::min<size_t>((size_t)per_launch, members - m0);
         ribn_amd::WaveGemvArgs a{};
@@ -749,7 +761,8 @@ ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv* g, const rib
         a.K = (int)k;
         a.members = (int)mc;
         a.pair_swiglu = 1;
-        hipError_t e = ribn_amd::launch_gemv_wave((int)g->value_type, a, g->ctx->cu_count, g->ctx->stream);
+        hipError_t e = ribn_amd::launch_gemv((int)g->value_type, a, g->ctx->act_scratch, g->ctx->cu_count,
+                                             g->ctx->stream);
         if (e != hipSuccess) return driver(e, "launch gate/up GEMV");
     }
     return ok();

@@ -10,8 +10,9 @@ Bars (the oracle is oracle/kquant_oracle.c + oracle/qwen3_oracle.py):
     prompt and greedy steps (the k-quant GEMV, the f16 cache and the online
     softmax each round differently from the sequential f32 oracle), greedy
     tokens equal wherever the oracle's top-2 margin exceeds the error;
-  * graph replays bit-identical to direct launches, batch members
-    bit-identical to single-sequence steps, generate() equal to stepping.
+  * graph replays bit-identical to direct launches, batch members equal to
+    single-sequence steps (bit for bit on the wave GEMV, within the GEMV bar
+    where 3+ members take the matrix cores), generate() equal to stepping.
 """
 import ctypes
 
@@ -23,7 +24,7 @@ from oracle import kquant_oracle as O
 from oracle.qwen3_oracle import OracleQwen3
 
 from .decode_helpers import small_weights
-from .gpu_helpers import RTOL, max_rel_err, to_dev, to_host
+from .gpu_helpers import RTOL, max_rel_err, mfma_path, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -138,7 +139,8 @@ def test_gate_up_swiglu_pairs_match_oracle(env, t, n, members):
         normed = O.rms_norm_raw(x[m], gamma, 1e-6)
         ref = O.swiglu(O.quant_gemv(t, ge, k, n, normed), O.quant_gemv(t, ue, k, n, normed))
         assert max_rel_err(got[m], ref) <= RTOL, m
-    if members > 1:
+    if members > 1 and not mfma_path(t, k, members):
+        # wave-GEMV batches: rows bit-identical to the single-member launch
         one = to_dev(np.full(n, np.nan, np.float32))
         env["k"][t].execute_gate_up_swiglu(gw, uw, to_dev(x[members - 1]), one, 1, gamma=to_dev(gamma))
         assert np.array_equal(to_host(one, env["ctx"]).view(np.uint32), got[members - 1].view(np.uint32))
@@ -355,9 +357,16 @@ def test_batch_members_equal_single_sequences(env):
         logits_b = [dec.copy_logits(m) for m in range(members)]
         for m in range(members):
             sel = dec.decode_step(single_caches[m], nxt_s[m], pos[m])
-            assert sel == sel_b[m]
-            assert np.array_equal(dec.copy_logits(0).view(np.uint32), logits_b[m].view(np.uint32)), m
-            nxt_s[m] = sel
+            single = dec.copy_logits(0)
+            # batches whose shapes take the matrix cores (gemv_mfma.hip) equal
+            # the single sequence within the GEMV bar (bit for bit on the wave
+            # GEMV); the same token wherever the top two logits are apart by
+            # more than that
+            assert max_rel_err(single, logits_b[m]) <= 2e-3, m
+            top = np.sort(logits_b[m])[-2:]
+            if top[1] - top[0] > 4e-3 * np.abs(logits_b[m]).max():
+                assert sel == sel_b[m]
+            nxt_s[m] = sel_b[m]
         nxt_b = sel_b
         pos = [p + 1 for p in pos]
 

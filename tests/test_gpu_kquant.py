@@ -17,7 +17,7 @@ import pytest
 from engine_amd import synth
 from oracle import kquant_oracle as O
 
-from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host
+from .gpu_helpers import RTOL, empty_dev, max_rel_err, mfma_path, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -174,11 +174,20 @@ def test_batch_matches_oracle_and_single_bitwise(env, t, members):
     got = to_host(y, env["ctx"]).reshape(members, n)
     ref = O.quant_gemv(t, enc, k, n, x.reshape(-1), members=members).reshape(members, n)
     assert max_rel_err(got, ref) <= RTOL
-    # weights-read-once batching keeps every row bit-identical to the single path
-    for m in range(members):
-        ys = empty_dev(n)
-        env["k"][t].execute_warp(w, to_dev(x[m]), ys)
-        assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
+    if not mfma_path(t, k, members):
+        # the wave GEMV's weights-read-once batching keeps every row
+        # bit-identical to the single path
+        for m in range(members):
+            ys = empty_dev(n)
+            env["k"][t].execute_warp(w, to_dev(x[m]), ys)
+            assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
+    else:
+        # matrix-core batches: a member's bits do not depend on the batch
+        # (here: the batch in reverse order)
+        yr = empty_dev(members * n)
+        env["k"][t].execute_warp_batch(w, to_dev(x[::-1].reshape(-1)), yr, members)
+        rev = to_host(yr, env["ctx"]).reshape(members, n)[::-1]
+        assert np.array_equal(rev.view(np.uint32), got.view(np.uint32))
 
 
 @pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096), (14, 4096, 4096)])
