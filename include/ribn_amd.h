@@ -96,7 +96,10 @@ int32_t ribn_amd_abi_version(void);
 
 /* CudaQ4KGemv::new (quantized.rs:1575-1580; the same in every family):
  * CudaContext::new(device) + default_stream(). Here: a context owning a fresh
- * non-blocking stream on `device`. */
+ * non-blocking stream on `device`. Every context (created or wrapping a stream)
+ * reserves about 0.56 MB of device scratch for the packed activations of
+ * batched GEMV launches (calls on one context share it in stream order), so
+ * execute calls allocate nothing. */
 ribn_amd_status ribn_amd_context_create(int32_t device, ribn_amd_context **out);
 /* CudaQ4KGemv::from_context(&ctx, stream) (quantized.rs:1588-1610): wraps a
  * caller-owned HIP stream; the caller keeps ownership and must outlive the context. */
