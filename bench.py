@@ -325,6 +325,65 @@ def bench_batched(E, synth, torch, args):
     }
 
 
+def bench_q8_1(E, synth, torch, args):
+    """The Q8_1 integer-dot path (the reference's GemvMode::IntegerDot, decode.rs:1341-1478):
+    per projection, pack the activations into Q8_1 blocks, then the integer-dot
+    GEMV, over the seven Qwen3-8B layer projections (Q4_K q/k/v/o/gate/up, Q5_K
+    down) of 8 distinct layers, graph-replayed, at batch 1 and 8. Lossy by
+    design (8-bit activations); reported beside the default f32-activation path."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    ctx = E.AmdContext(0, stream=stream)
+    store = E.AmdWeightStore(ctx)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    n_layers = 8
+    layers = []
+    for i in range(n_layers):
+        ly = {}
+        for name, t, k, n, _ in LAYER:
+            store.materialize_quantized(f"{name}{i}", [k, n], t, synth.kquant_torch(t, k, n, gen, dev))
+            ly[name] = (store.quantized_tensor(f"{name}{i}"), t, k, n)
+        layers.append(ly)
+    quant = E.AmdQ8_1Quantizer(ctx)
+    gemv = {12: E.AmdQ4KQ8_1Gemv(ctx), 13: E.AmdQ5KQ8_1Gemv(ctx)}
+    wbytes = sum(launch_bytes(t, k, n) - 4 * k - 4 * n for _, t, k, n, _ in LAYER)
+    per_m = {}
+    for m in (1, 8):
+        xs = {k: torch.randn(m * k, device=dev, generator=gen) for k in (HIDDEN, FFN)}
+        packed = {k: torch.empty(m * k // 32 * 9, dtype=torch.int32, device=dev) for k in (HIDDEN, FFN)}
+        outs = {n: torch.empty(m * n, device=dev) for n in (Q_OUT, KV_OUT, FFN, HIDDEN)}
+
+        def fn():
+            for ly in layers:
+                for name, _, k, n, _ in LAYER:
+                    w, t, k, n = ly[name]
+                    quant.execute(xs[k], packed[k])
+                    if m == 1:
+                        gemv[t].execute(w, packed[k], outs[n])
+                    else:
+                        gemv[t].execute_batch(w, packed[k], outs[n], m)
+
+        us = _graph_time_us(torch, stream, fn, max(2, args.steps // 10)) / n_layers
+        per_m[m] = {"us_per_layer": round(us, 2), "weight_GBps": round(wbytes / us / 1e3, 1),
+                    "tokens_per_s_36_layers": round(m * 1e6 / (36 * us), 1)}
+        log(f"bench q8_1: M={m} {us:.2f} us per layer (7 packs + 7 integer-dot GEMVs), "
+            f"{wbytes / us / 1e3:.0f} GB/s of weights")
+    top = per_m[1]
+    return {
+        "metric": "Q8_1 integer-dot decode projections, weight GB/s at batch 1",
+        "value": top["weight_GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(top["us_per_layer"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "i8dot4 (q8_1 activations)", "data": "synthetic",
+        "config": {"workload": "qwen3-8b-layer-q8_1", "layer_weight_bytes": wbytes, "layers_cycled": n_layers,
+                   "per_m": per_m},
+        "roofline": {"bound": "hbm", "achieved": top["weight_GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(top["weight_GBps"] / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "q8_1_gemv_kernel + quantize_q8_1_kernel over one layer"},
+        "cpu_baseline": None,
+    }
+
+
 def bench_prefill(E, synth, torch, args):
     """M = 512 bf16 tokens against Q4_K 4096->12288 and Q6_K 12288->4096
     (weights dequantised in registers, f16 MFMA, f32 accumulation)."""
@@ -436,10 +495,11 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="issue launches eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1"), default="decode",
                     help="decode: BASELINE config 1 (the headline line, default, which also carries the "
                          "config-4 tok/s); batched: config 2 (FFN at M = 1, 4, 16, 64); prefill: config 3 "
-                         "(M = 512 bf16 matmuls); model: config 4 alone (full decoder, batch 1 and 8)")
+                         "(M = 512 bf16 matmuls); model: config 4 alone (full decoder, batch 1 and 8); q8_1: "
+                         "the Q8_1 integer-dot projections (pack + GEMV) at batch 1 and 8")
     ap.add_argument("--context", type=int, default=2048, help="config 4: prompt tokens before generation")
     ap.add_argument("--gen-tokens", type=int, default=128, help="config 4: greedy tokens timed")
     ap.add_argument("--no-model", action="store_true", help="skip the config-4 full-decoder measurement")
@@ -461,8 +521,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    if args.workload in ("batched", "prefill"):
-        result = (bench_batched if args.workload == "batched" else bench_prefill)(E, synth, torch, args)
+    if args.workload in ("batched", "prefill", "q8_1"):
+        result = {"batched": bench_batched, "prefill": bench_prefill, "q8_1": bench_q8_1}[args.workload](
+            E, synth, torch, args)
         print(json.dumps(result), flush=True)
         return
     log(f"bench: generating {args.layers} layers + lm_head of synthetic weights on the device")

@@ -6,6 +6,7 @@ host-side mirror of the reference's operator API (kquant.py).
 """
 from . import _lib  # noqa: F401
 from .kquant import (  # noqa: F401
+    AmdQ4KQ8_1Gemv, AmdQ5KQ8_1Gemv, AmdQ6KQ8_1Gemv, AmdQ8_1Quantizer,
     Q4_K, Q5_K, Q6_K, BLOCK_BYTES,
     AmdContext, AmdWeightStore, AmdQuantizedWeight,
     AmdQ4KGemv, AmdQ5KGemv, AmdQ6KGemv, QwenGemvKernel, AmdQwenOps,

@@ -101,6 +101,9 @@ SIGNATURES = {
     "ribn_amd_rms_norm_batch": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _f32]),
     "ribn_amd_gemv_execute_fused": (_i32, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _f32, _vp, _sz, _sz, _u32]),
     "ribn_amd_gemv_execute_gate_up_swiglu": (_i32, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _f32, _vp, _sz, _sz]),
+    "ribn_amd_q8_1_quantize": (_i32, [_vp, _vp, _sz, _vp, _sz]),
+    "ribn_amd_gemv_execute_q8_1": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
+    "ribn_amd_gemv_execute_q8_1_batch": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz, _sz]),
     "ribn_amd_kv_cache_create": (_i32, [_vp, ctypes.POINTER(Qwen3Config), _u32, _pvp]),
     "ribn_amd_kv_cache_destroy": (None, [_vp]),
     "ribn_amd_kv_cache_capacity": (_u32, [_vp]),

@@ -91,6 +91,15 @@ hipError_t launch_pack_act16(const float* x, const float* gamma, int members, in
                              hipStream_t stream);
 hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& args, int cu_count, hipStream_t stream);
 
+// ---- Q8_1 activations and the integer-dot GEMV (q8_1.hip)
+
+constexpr int kQ8MaxMembers = 8;
+// Packs `blocks` 32-value blocks of x into nine words each.
+hipError_t launch_quantize_q8_1(const float* x, uint32_t* out, uint32_t blocks, hipStream_t stream);
+// y [members][N] from Q8_1-packed x [members][K / 32][9] (members <= kQ8MaxMembers).
+hipError_t launch_gemv_q8_1(int value_type, const uint8_t* w, uint32_t wbytes, const uint32_t* x, float* y, int K,
+                            int N, int members, hipStream_t stream);
+
 // ---- GEMV dispatch used by the C ABI and the decoder
 
 // Device scratch (bytes) a context reserves for launch_gemv's packed activations.

@@ -768,6 +768,86 @@ ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv* g, const rib
     return ok();
 }
 
+ribn_amd_status ribn_amd_q8_1_quantize(ribn_amd_context* ctx, const float* input, size_t input_len, uint32_t* output,
+                                       size_t output_len) {
+    if (!ctx) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null context");
+    // activation.rs:52-73: whole, non-empty blocks; nine words per block
+    // (lengths first: an empty input is an InputLength error whatever its pointer)
+    if (input_len == 0 || input_len % 32 != 0) {
+        const size_t want = (std::max<size_t>(input_len, 1) + 31) / 32 * 32;
+        return fail(RIBN_AMD_INPUT_LENGTH, want, input_len, "Q8_1 packing needs whole 32-value blocks, got %zu values",
+                    input_len);
+    }
+    const size_t blocks = input_len / 32;
+    if (output_len != blocks * 9) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, blocks * 9, output_len, "Q8_1 output has %zu words, expected %zu",
+                    output_len, blocks * 9);
+    }
+    ribn_amd_status st = check_device_ptr(ctx, input, "input", 4);
+    if (st != RIBN_AMD_OK) return st;
+    st = check_device_ptr(ctx, output, "output", 4);
+    if (st != RIBN_AMD_OK) return st;
+    if (input_len > std::numeric_limits<uint32_t>::max()) return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "input exceeds u32");
+    DeviceGuard guard(ctx->device);
+    hipError_t e = ribn_amd::launch_quantize_q8_1(input, output, (uint32_t)blocks, ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch Q8_1 packing");
+    return ok();
+}
+
+static ribn_amd_status q8_1_gemv(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const uint32_t* input,
+                                 size_t input_len, float* output, size_t output_len, size_t members) {
+    if (g == nullptr || w == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null kernel or weight handle");
+    if (w->ctx->device != g->ctx->device) {
+        return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)g->ctx->device, (uint64_t)w->ctx->device,
+                    "weight and kernel belong to different devices");
+    }
+    ribn_amd_status st = check_device_ptr(g->ctx, input, "input", 4);
+    if (st != RIBN_AMD_OK) return st;
+    st = check_device_ptr(g->ctx, output, "output", 4);
+    if (st != RIBN_AMD_OK) return st;
+    uint64_t k, n;
+    st = validate_geometry(g->value_type, w, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    // q4_q8_1.rs:95-112 / 176-200: K / 32 * 9 words and N outputs per member
+    const uint64_t expected_in = k / 32 * 9 * members;
+    const uint64_t expected_out = n * members;
+    if (input_len != expected_in) {
+        return fail(RIBN_AMD_INPUT_LENGTH, expected_in, input_len, "Q8_1 input has %zu words, expected %llu",
+                    input_len, (unsigned long long)expected_in);
+    }
+    if (output_len != expected_out) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, expected_out, output_len, "output has %zu values, expected %llu",
+                    output_len, (unsigned long long)expected_out);
+    }
+    if (expected_in * 4 > std::numeric_limits<uint32_t>::max() || expected_out * 4 > std::numeric_limits<uint32_t>::max()) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "geometry exceeds u32");
+    }
+    DeviceGuard guard(g->ctx->device);
+    hipError_t e = ribn_amd::launch_gemv_q8_1((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, input, output,
+                                              (int)k, (int)n, (int)members, g->ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch Q8_1 GEMV");
+    return ok();
+}
+
+ribn_amd_status ribn_amd_gemv_execute_q8_1(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const uint32_t* input,
+                                           size_t input_len, float* output, size_t output_len) {
+    return q8_1_gemv(g, w, input, input_len, output, output_len, 1);
+}
+
+ribn_amd_status ribn_amd_gemv_execute_q8_1_batch(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w,
+                                                 const uint32_t* input, size_t input_len, float* output,
+                                                 size_t output_len, size_t members) {
+    // q4_q8_1.rs:149-159: zero members is an input-length error, more than
+    // eight an invalid-weight error naming the family
+    if (members == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "batched GEMV needs at least one member");
+    if (members > (size_t)ribn_amd::kQ8MaxMembers) {
+        return fail(RIBN_AMD_INVALID_WEIGHT, (uint64_t)ribn_amd::kQ8MaxMembers, members,
+                    "%s integer-dot batch variant supports at most %d members", g ? type_label(g->value_type) : "?",
+                    ribn_amd::kQ8MaxMembers);
+    }
+    return q8_1_gemv(g, w, input, input_len, output, output_len, members);
+}
+
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, float* output,
                                     size_t output_len) {
     if (!g || !w) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null kernel or weight handle");

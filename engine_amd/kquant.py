@@ -5,6 +5,8 @@ Same names, argument meaning and error behaviour as crates/nvidia:
   AmdModelKernelError       <- CudaModelKernelError (model_ops.rs:12-22)
   AmdWeightStore            <- CudaWeightStore (cuda.rs:192-459)
   AmdQ4KGemv/AmdQ5KGemv/AmdQ6KGemv <- CudaQ4KGemv/... (quantized.rs:1465-1753)
+  AmdQ8_1Quantizer          <- CudaQ8_1Quantizer (activation.rs:8-88)
+  AmdQ4KQ8_1Gemv/...        <- CudaQ4KQ8_1Gemv/... (q4_q8_1.rs, q5_q8_1.rs, q6_q8_1.rs)
   QwenGemvKernel            <- QwenGemvKernel (staging.rs:90-217)
   AmdQwenOps                <- CudaQwen35Ops::{rms_norm, rms_norm_batch} (model_ops.rs:1714-1824)
 
@@ -304,6 +306,59 @@ class _AmdQuantizedGemv:
             self.close()
         except Exception:
             pass
+
+
+class AmdQ8_1Quantizer:
+    """CudaQ8_1Quantizer (crates/nvidia/src/activation.rs:8-88): packs f32
+    activations into Q8_1 blocks (nine uint32 words per 32 values) on the
+    context stream, into caller-owned storage."""
+
+    def __init__(self, ctx: AmdContext):
+        self.ctx = ctx
+        self._lib = ctx._lib
+
+    @classmethod
+    def new(cls, ctx: AmdContext):
+        return cls(ctx)
+
+    def execute(self, input, output):
+        _check(self._lib.ribn_amd_q8_1_quantize(self.ctx.handle, _ptr(input), input.numel(), _ptr(output),
+                                                output.numel()))
+
+
+class _AmdQ8_1Gemv:
+    """CudaQ4KQ8_1Gemv / CudaQ5KQ8_1Gemv / CudaQ6KQ8_1Gemv (q{4,5,6}_q8_1.rs):
+    the integer-dot GEMV over Q8_1-packed activations (uint32 tensors)."""
+    VALUE_TYPE = 0
+
+    def __init__(self, ctx: AmdContext):
+        self._gemv = _AmdQuantizedGemv(ctx, self.VALUE_TYPE)
+        self.ctx = ctx
+        self._lib = ctx._lib
+
+    @classmethod
+    def new(cls, ctx: AmdContext):
+        return cls(ctx)
+
+    def execute(self, weight, input, output):
+        _check(self._lib.ribn_amd_gemv_execute_q8_1(self._gemv.handle, weight.handle, _ptr(input), input.numel(),
+                                                    _ptr(output), output.numel()))
+
+    def execute_batch(self, weight, input, output, members: int):
+        _check(self._lib.ribn_amd_gemv_execute_q8_1_batch(self._gemv.handle, weight.handle, _ptr(input),
+                                                          input.numel(), _ptr(output), output.numel(), members))
+
+
+class AmdQ4KQ8_1Gemv(_AmdQ8_1Gemv):
+    VALUE_TYPE = Q4_K
+
+
+class AmdQ5KQ8_1Gemv(_AmdQ8_1Gemv):
+    VALUE_TYPE = Q5_K
+
+
+class AmdQ6KQ8_1Gemv(_AmdQ8_1Gemv):
+    VALUE_TYPE = Q6_K
 
 
 class AmdQ4KGemv(_AmdQuantizedGemv):

@@ -236,6 +236,30 @@ ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv *gemv, const 
                                                      size_t input_len, const float *gamma, size_t gamma_len,
                                                      float epsilon, float *output, size_t output_len,
                                                      size_t members);
+/* ------------------------------------------------- Q8_1 integer-dot path */
+
+/* CudaQ8_1Quantizer::execute (crates/nvidia/src/activation.rs:52-88,
+ * kernel activation.cu:1-28): packs `input_len` (a non-zero multiple of 32)
+ * values into input_len / 32 blocks of nine words, half(d) | half(sum) << 16
+ * then 32 int8 q = round(x / d), d = max|x| / 127. Bit-identical to the
+ * reference's packer. Errors: InputLength (empty or partial block),
+ * OutputLength (output_len != blocks * 9), ShapeOverflow. Lossy; the default
+ * decode path does not use it. */
+ribn_amd_status ribn_amd_q8_1_quantize(ribn_amd_context *ctx, const float *input, size_t input_len, uint32_t *output,
+                                       size_t output_len);
+/* CudaQ4KQ8_1Gemv / CudaQ5KQ8_1Gemv / CudaQ6KQ8_1Gemv::execute
+ * (q4_q8_1.rs:74-133, q5_q8_1.rs, q6_q8_1.rs): y[N] from packed input of
+ * K / 32 * 9 words, for the gemv handle's value type (Q4_K, Q5_K, Q6_K).
+ * Errors as ribn_amd_gemv_execute, with InputLength counted in words. */
+ribn_amd_status ribn_amd_gemv_execute_q8_1(ribn_amd_gemv *g, const ribn_amd_quantized_weight *w, const uint32_t *input,
+                                           size_t input_len, float *output, size_t output_len);
+/* ...::execute_batch (q4_q8_1.rs:135-219): `members` (1..8) batch-major packed
+ * rows, weights read once, output [members][N]. members == 0: InputLength;
+ * members > 8: InvalidWeight. */
+ribn_amd_status ribn_amd_gemv_execute_q8_1_batch(ribn_amd_gemv *g, const ribn_amd_quantized_weight *w,
+                                                 const uint32_t *input, size_t input_len, float *output,
+                                                 size_t output_len, size_t members);
+
 /* Bit-exact device dequantisation to f32 [N][K] (twin of lib.rs:596-661;
  * the reference's device equivalent is the q4_k_embedding gather, q4_k.cu:1-67). */
 ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight, float *output,
