@@ -384,6 +384,80 @@ def bench_q8_1(E, synth, torch, args):
     }
 
 
+def bench_gguf(E, synth, torch, args):
+    """GGUF staging (the format step before the path): writes a Qwen3-8B-shaped
+    GGUF (Q4_K token_embd and projections, Q5_K down, Q6_K output, f32 norms)
+    with `--layers` layers to a temporary directory, then times opening it and
+    staging every tensor into HBM through pinned double buffers, and the whole
+    load into a decoder. The file is resident in the page cache (just written),
+    so the figure is host-memory-to-HBM staging, not disk."""
+    import tempfile
+
+    import numpy as np
+
+    from engine_amd import gguf_writer as W
+    from engine_amd.gguf import GgufFile, load_qwen3_decode, qwen3_tensor_names, stage
+
+    layers = args.layers
+    md = [("general.architecture", W.STRING, "qwen3"), ("qwen3.block_count", W.U32, layers),
+          ("qwen3.embedding_length", W.U32, HIDDEN), ("qwen3.feed_forward_length", W.U32, FFN),
+          ("qwen3.attention.head_count", W.U32, 32), ("qwen3.attention.head_count_kv", W.U32, 8),
+          ("qwen3.attention.key_length", W.U32, 128), ("qwen3.rope.freq_base", W.F32, 1.0e6),
+          ("qwen3.attention.layer_norm_rms_epsilon", W.F32, 1.0e-6)]
+    tensors = [("token_embd.weight", [HIDDEN, VOCAB], 12, synth.kquant_numpy(12, HIDDEN, VOCAB, seed=1)),
+               ("output.weight", [HIDDEN, VOCAB], 14, synth.kquant_numpy(14, HIDDEN, VOCAB, seed=2)),
+               ("output_norm.weight", [HIDDEN], 0, synth.gamma_numpy(HIDDEN, seed=3))]
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
+             "up": "ffn_up", "down": "ffn_down"}
+    shared = {name: synth.kquant_numpy(t, k, n, seed=10 + i) for i, (name, t, k, n, _) in enumerate(LAYER)}
+    for li in range(layers):
+        for name, t, k, n, _ in LAYER:
+            tensors.append((f"blk.{li}.{names[name]}.weight", [k, n], t, shared[name]))
+        for nm, size in (("attn_norm", HIDDEN), ("ffn_norm", HIDDEN), ("attn_q_norm", 128), ("attn_k_norm", 128)):
+            tensors.append((f"blk.{li}.{nm}.weight", [size], 0, synth.gamma_numpy(size, seed=li)))
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "qwen3-8b-shaped.gguf")
+        t0 = time.perf_counter()
+        size = W.write(path, md, tensors)
+        log(f"bench gguf: wrote {size / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s")
+        del tensors, shared
+        ctx = E.AmdContext(0)
+        staged_bytes = 0
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            g = GgufFile.open(path)
+            t_open = time.perf_counter() - t0
+            all_names = qwen3_tensor_names(layers) + ["output.weight"]
+            staged = stage(ctx, g, all_names)
+            dt = time.perf_counter() - t0
+            staged_bytes = sum(g.tensor_data_range(n).stop - g.tensor_data_range(n).start for n in all_names)
+            runs.append((dt, t_open))
+            del staged
+            g.close()
+        dt, t_open = min(runs)
+        gbs = staged_bytes / dt / 1e9
+        log(f"bench gguf: open + stage {staged_bytes / 1e9:.2f} GB in {dt * 1e3:.1f} ms ({gbs:.1f} GB/s; "
+            f"open {t_open * 1e3:.2f} ms)")
+        t0 = time.perf_counter()
+        dec, cfg, g, staged = load_qwen3_decode(ctx, path)
+        t_load = time.perf_counter() - t0
+        cache = E.AmdKvCache(ctx, cfg, 8)
+        tok = dec.decode_step(cache, 7, 0)
+        log(f"bench gguf: load_qwen3_decode {t_load * 1e3:.1f} ms; first token {tok}")
+        dec.close()
+    return {
+        "metric": "GGUF open + staging into HBM, GB/s (page-cache resident file)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": 3, "warmup": 0,
+        "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bytes", "data": "synthetic",
+        "config": {"workload": "qwen3-8b-shaped-gguf-staging", "layers": layers, "file_bytes": size,
+                   "staged_bytes": staged_bytes, "open_ms": round(t_open * 1e3, 3),
+                   "load_decoder_ms": round(t_load * 1e3, 1)},
+        "roofline": None, "cpu_baseline": None,
+    }
+
+
 def bench_prefill(E, synth, torch, args):
     """M = 512 bf16 tokens against Q4_K 4096->12288 and Q6_K 12288->4096
     (weights dequantised in registers, f16 MFMA, f32 accumulation)."""
@@ -495,11 +569,12 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="issue launches eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1", "gguf"), default="decode",
                     help="decode: BASELINE config 1 (the headline line, default, which also carries the "
                          "config-4 tok/s); batched: config 2 (FFN at M = 1, 4, 16, 64); prefill: config 3 "
                          "(M = 512 bf16 matmuls); model: config 4 alone (full decoder, batch 1 and 8); q8_1: "
-                         "the Q8_1 integer-dot projections (pack + GEMV) at batch 1 and 8")
+                         "the Q8_1 integer-dot projections (pack + GEMV) at batch 1 and 8; gguf: GGUF "
+                         "open + staging of a Qwen3-8B-shaped file (--layers layers)")
     ap.add_argument("--context", type=int, default=2048, help="config 4: prompt tokens before generation")
     ap.add_argument("--gen-tokens", type=int, default=128, help="config 4: greedy tokens timed")
     ap.add_argument("--no-model", action="store_true", help="skip the config-4 full-decoder measurement")
@@ -521,8 +596,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    if args.workload in ("batched", "prefill", "q8_1"):
-        result = {"batched": bench_batched, "prefill": bench_prefill, "q8_1": bench_q8_1}[args.workload](
+    if args.workload in ("batched", "prefill", "q8_1", "gguf"):
+        result = {"batched": bench_batched, "prefill": bench_prefill, "q8_1": bench_q8_1,
+                  "gguf": bench_gguf}[args.workload](
             E, synth, torch, args)
         print(json.dumps(result), flush=True)
         return

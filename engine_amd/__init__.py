@@ -14,6 +14,7 @@ from .kquant import (  # noqa: F401
     AmdKernelError, AmdQuantizedKernelError, AmdModelKernelError, AmdWeightError,
     validate_quantized_geometry,
 )
+from .gguf import GgufError, GgufFile, TensorInfo, load_qwen3_decode, qwen3_config_from_gguf  # noqa: F401
 from .qwen3 import AmdKvCache, AmdQwen3Config, AmdQwen3Decode, QWEN3_8B, attention_decode  # noqa: F401
 
 __all__ = [
@@ -22,4 +23,6 @@ __all__ = [
     "AmdKQuantEmbedding", "AmdKernelError",
     "AmdQuantizedKernelError", "AmdModelKernelError", "AmdWeightError", "validate_quantized_geometry",
     "AmdKvCache", "AmdQwen3Config", "AmdQwen3Decode", "QWEN3_8B", "attention_decode",
+    "AmdQ8_1Quantizer", "AmdQ4KQ8_1Gemv", "AmdQ5KQ8_1Gemv", "AmdQ6KQ8_1Gemv",
+    "GgufError", "GgufFile", "TensorInfo", "load_qwen3_decode", "qwen3_config_from_gguf",
 ]

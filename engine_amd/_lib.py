@@ -19,7 +19,11 @@ STATUS_NAMES = {
     5: "ShapeOverflow", 6: "InputLength", 7: "OutputLength", 8: "ContextMismatch",
     9: "EmptyInput", 10: "WeightLength", 11: "InvalidEpsilon", 12: "InvalidArgument",
     13: "EmptyEncoding", 14: "SourceIncomplete", 15: "WorkspaceTooSmall", 16: "InvalidPlan",
-    17: "PositionOverflow", 18: "MissingTensor",
+    17: "PositionOverflow", 18: "MissingTensor", 19: "Io", 20: "InvalidMagic", 21: "UnsupportedVersion",
+    22: "InvalidUtf8", 23: "InvalidValueType", 24: "InvalidBool", 25: "InvalidLength", 26: "ArrayNestingTooDeep",
+    27: "DuplicateMetadata", 28: "InvalidDimensionCount", 29: "InvalidAlignment", 30: "Truncated",
+    31: "TensorOffsetOutOfBounds", 32: "UnsupportedTensorType", 33: "TensorByteLengthOverflow",
+    34: "QuantizationMismatch", 35: "MissingMetadata", 36: "MetadataTypeMismatch", 37: "BudgetExceeded",
 }
 
 
@@ -42,6 +46,19 @@ QWEN3_LAYER_FIELDS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "
 class Qwen3Layer(ctypes.Structure):
     """ribn_amd_qwen3_layer: seven weight handles, then four device norm vectors."""
     _fields_ = [(name, ctypes.c_void_p) for name in QWEN3_LAYER_FIELDS]
+
+
+class GgufValue(ctypes.Structure):
+    """ribn_amd_gguf_value."""
+    _fields_ = [("type", ctypes.c_uint32), ("array_type", ctypes.c_uint32), ("array_len", ctypes.c_uint64),
+                ("u", ctypes.c_uint64), ("i", ctypes.c_int64), ("f", ctypes.c_double),
+                ("str", ctypes.c_void_p), ("str_len", ctypes.c_uint64)]
+
+
+class GgufTensor(ctypes.Structure):
+    """ribn_amd_gguf_tensor."""
+    _fields_ = [("name", ctypes.c_char_p), ("n_dims", ctypes.c_uint32), ("dims", ctypes.c_uint64 * 16),
+                ("value_type", ctypes.c_uint32), ("offset", ctypes.c_uint64)]
 
 
 READ_FN = ctypes.CFUNCTYPE(ctypes.c_int64, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint8), ctypes.c_size_t)
@@ -104,6 +121,20 @@ SIGNATURES = {
     "ribn_amd_q8_1_quantize": (_i32, [_vp, _vp, _sz, _vp, _sz]),
     "ribn_amd_gemv_execute_q8_1": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
     "ribn_amd_gemv_execute_q8_1_batch": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz, _sz]),
+    "ribn_amd_gguf_open": (_i32, [ctypes.c_char_p, _pvp]),
+    "ribn_amd_gguf_close": (None, [_vp]),
+    "ribn_amd_gguf_version": (_u32, [_vp]),
+    "ribn_amd_gguf_tensor_count": (_u64, [_vp]),
+    "ribn_amd_gguf_tensor_data_offset": (_u64, [_vp]),
+    "ribn_amd_gguf_metadata_count": (_u64, [_vp]),
+    "ribn_amd_gguf_metadata_key": (ctypes.c_char_p, [_vp, _u64]),
+    "ribn_amd_gguf_metadata_get": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(GgufValue)]),
+    "ribn_amd_gguf_metadata_array_get": (_i32, [_vp, ctypes.c_char_p, _u64, ctypes.POINTER(GgufValue)]),
+    "ribn_amd_gguf_metadata_item": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64), _sz, ctypes.POINTER(GgufValue)]),
+    "ribn_amd_gguf_tensor_info": (_i32, [_vp, _u64, ctypes.POINTER(GgufTensor)]),
+    "ribn_amd_gguf_find_tensor": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]),
+    "ribn_amd_gguf_tensor_data_range": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "ribn_amd_gguf_stage": (_i32, [_vp, _vp, ctypes.POINTER(ctypes.c_char_p), _sz, _u64, _pvp]),
     "ribn_amd_kv_cache_create": (_i32, [_vp, ctypes.POINTER(Qwen3Config), _u32, _pvp]),
     "ribn_amd_kv_cache_destroy": (None, [_vp]),
     "ribn_amd_kv_cache_capacity": (_u32, [_vp]),

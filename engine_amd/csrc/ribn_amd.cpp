@@ -268,6 +268,25 @@ const char* ribn_amd_status_name(int32_t status) {
     case RIBN_AMD_INVALID_PLAN: return "InvalidPlan";
     case RIBN_AMD_POSITION_OVERFLOW: return "PositionOverflow";
     case RIBN_AMD_MISSING_TENSOR: return "MissingTensor";
+    case RIBN_AMD_GGUF_IO: return "Io";
+    case RIBN_AMD_GGUF_INVALID_MAGIC: return "InvalidMagic";
+    case RIBN_AMD_GGUF_UNSUPPORTED_VERSION: return "UnsupportedVersion";
+    case RIBN_AMD_GGUF_INVALID_UTF8: return "InvalidUtf8";
+    case RIBN_AMD_GGUF_INVALID_VALUE_TYPE: return "InvalidValueType";
+    case RIBN_AMD_GGUF_INVALID_BOOL: return "InvalidBool";
+    case RIBN_AMD_GGUF_INVALID_LENGTH: return "InvalidLength";
+    case RIBN_AMD_GGUF_ARRAY_NESTING_TOO_DEEP: return "ArrayNestingTooDeep";
+    case RIBN_AMD_GGUF_DUPLICATE_METADATA: return "DuplicateMetadata";
+    case RIBN_AMD_GGUF_INVALID_DIMENSION_COUNT: return "InvalidDimensionCount";
+    case RIBN_AMD_GGUF_INVALID_ALIGNMENT: return "InvalidAlignment";
+    case RIBN_AMD_GGUF_TRUNCATED: return "Truncated";
+    case RIBN_AMD_GGUF_TENSOR_OFFSET_OUT_OF_BOUNDS: return "TensorOffsetOutOfBounds";
+    case RIBN_AMD_GGUF_UNSUPPORTED_TENSOR_TYPE: return "UnsupportedTensorType";
+    case RIBN_AMD_GGUF_BYTE_LENGTH_OVERFLOW: return "TensorByteLengthOverflow";
+    case RIBN_AMD_GGUF_QUANTIZATION_MISMATCH: return "QuantizationMismatch";
+    case RIBN_AMD_GGUF_MISSING_METADATA: return "MissingMetadata";
+    case RIBN_AMD_GGUF_METADATA_TYPE_MISMATCH: return "MetadataTypeMismatch";
+    case RIBN_AMD_BUDGET_EXCEEDED: return "BudgetExceeded";
     default: return "Unknown";
     }
 }

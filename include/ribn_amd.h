@@ -69,7 +69,27 @@ typedef enum ribn_amd_status {
     RIBN_AMD_WORKSPACE_TOO_SMALL = 15,   /* prefill workspace not reserved (no reference twin) */
     RIBN_AMD_INVALID_PLAN = 16,          /* CudaDecodeError::InvalidPlan (decode.rs:91-93) */
     RIBN_AMD_POSITION_OVERFLOW = 17,     /* CudaDecodeError::PositionOverflow { position, capacity } */
-    RIBN_AMD_MISSING_TENSOR = 18,        /* CudaDecodeError::MissingTensor (decode.rs:86-87) */
+    RIBN_AMD_MISSING_TENSOR = 18,        /* CudaDecodeError::MissingTensor (decode.rs:86-87); GgufError::MissingTensor */
+    /* GgufError (crates/gguf/src/lib.rs:741-805) */
+    RIBN_AMD_GGUF_IO = 19,                        /* Io { path, message } (open, read, unexpected end of file) */
+    RIBN_AMD_GGUF_INVALID_MAGIC = 20,             /* InvalidMagic(u32): actual = the magic read */
+    RIBN_AMD_GGUF_UNSUPPORTED_VERSION = 21,       /* UnsupportedVersion(u32) */
+    RIBN_AMD_GGUF_INVALID_UTF8 = 22,              /* InvalidUtf8 */
+    RIBN_AMD_GGUF_INVALID_VALUE_TYPE = 23,        /* InvalidValueType(u32) */
+    RIBN_AMD_GGUF_INVALID_BOOL = 24,              /* InvalidBool(u8) */
+    RIBN_AMD_GGUF_INVALID_LENGTH = 25,            /* InvalidLength { kind, value } */
+    RIBN_AMD_GGUF_ARRAY_NESTING_TOO_DEEP = 26,    /* ArrayNestingTooDeep */
+    RIBN_AMD_GGUF_DUPLICATE_METADATA = 27,        /* DuplicateMetadata(key) */
+    RIBN_AMD_GGUF_INVALID_DIMENSION_COUNT = 28,   /* InvalidDimensionCount(u32) */
+    RIBN_AMD_GGUF_INVALID_ALIGNMENT = 29,         /* InvalidAlignment(u64) */
+    RIBN_AMD_GGUF_TRUNCATED = 30,                 /* Truncated */
+    RIBN_AMD_GGUF_TENSOR_OFFSET_OUT_OF_BOUNDS = 31, /* TensorOffsetOutOfBounds { name, offset } */
+    RIBN_AMD_GGUF_UNSUPPORTED_TENSOR_TYPE = 32,   /* UnsupportedTensorType(u32) */
+    RIBN_AMD_GGUF_BYTE_LENGTH_OVERFLOW = 33,      /* ElementCountOverflow / TensorByteLengthOverflow */
+    RIBN_AMD_GGUF_QUANTIZATION_MISMATCH = 34,     /* QuantizationDimensionMismatch / QuantizationBlockMismatch */
+    RIBN_AMD_GGUF_MISSING_METADATA = 35,          /* MissingMetadata(key) */
+    RIBN_AMD_GGUF_METADATA_TYPE_MISMATCH = 36,    /* MetadataTypeMismatch { key } */
+    RIBN_AMD_BUDGET_EXCEEDED = 37,                /* CudaWeightStagingError::BudgetExceeded (staging.rs:255-258) */
 } ribn_amd_status;
 
 typedef struct ribn_amd_error {
@@ -236,6 +256,79 @@ ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv *gemv, const 
                                                      size_t input_len, const float *gamma, size_t gamma_len,
                                                      float epsilon, float *output, size_t output_len,
                                                      size_t members);
+/* ------------------------------------------- GGUF reader and staging */
+
+/* GgufFile (crates/gguf/src/lib.rs:165-345). Parsed at open; bulk tensor data
+ * is not read until staged. */
+typedef struct ribn_amd_gguf ribn_amd_gguf;
+
+/* One metadata value (MetadataValue, lib.rs:29-46). `type` is the GGUF value
+ * type: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool, 8 string,
+ * 9 array, 10 u64, 11 i64, 12 f64. Unsigned types and bool fill `u`, signed
+ * types `i`, f32/f64 `f` (with the raw bits in `u`), strings `str`/`str_len`
+ * (owned by the file handle, not NUL-terminated by contract), arrays
+ * `array_type`/`array_len` (items via ribn_amd_gguf_metadata_array_get). */
+typedef struct ribn_amd_gguf_value {
+    uint32_t type;
+    uint32_t array_type;
+    uint64_t array_len;
+    uint64_t u;
+    int64_t i;
+    double f;
+    const char *str;
+    uint64_t str_len;
+} ribn_amd_gguf_value;
+
+/* TensorInfo (lib.rs:87-163): name (owned by the file handle), GGUF
+ * dimensions (dims[0] is the innermost, K for a weight), GGML type id, and
+ * offset relative to the aligned tensor data. */
+typedef struct ribn_amd_gguf_tensor {
+    const char *name;
+    uint32_t n_dims;
+    uint64_t dims[16];
+    uint32_t value_type;
+    uint64_t offset;
+} ribn_amd_gguf_tensor;
+
+/* GgufFile::open (lib.rs:178-272): header, metadata and tensor directory,
+ * with the reference's limits and errors (GGUF_* statuses). */
+ribn_amd_status ribn_amd_gguf_open(const char *path, ribn_amd_gguf **out);
+void ribn_amd_gguf_close(ribn_amd_gguf *g);
+/* GgufFile::{version, tensor_count, tensor_data_offset} (lib.rs:279-289, 374-377) */
+uint32_t ribn_amd_gguf_version(const ribn_amd_gguf *g);
+uint64_t ribn_amd_gguf_tensor_count(const ribn_amd_gguf *g);
+uint64_t ribn_amd_gguf_tensor_data_offset(const ribn_amd_gguf *g);
+/* GgufFile::metadata_map (lib.rs:291-299): keys in sorted order, as the
+ * reference's BTreeMap iterates. */
+uint64_t ribn_amd_gguf_metadata_count(const ribn_amd_gguf *g);
+const char *ribn_amd_gguf_metadata_key(const ribn_amd_gguf *g, uint64_t index);
+/* GgufFile::metadata (lib.rs:291-294): GGUF_MISSING_METADATA when absent. */
+ribn_amd_status ribn_amd_gguf_metadata_get(const ribn_amd_gguf *g, const char *key, ribn_amd_gguf_value *out);
+ribn_amd_status ribn_amd_gguf_metadata_array_get(const ribn_amd_gguf *g, const char *key, uint64_t index,
+                                                 ribn_amd_gguf_value *out);
+/* The item at `path` (depth indices) inside nested arrays of `key`
+ * (MetadataValue::Array nesting, lib.rs:1111-1120); depth 0 is the value itself. */
+ribn_amd_status ribn_amd_gguf_metadata_item(const ribn_amd_gguf *g, const char *key, const uint64_t *path,
+                                            size_t depth, ribn_amd_gguf_value *out);
+/* GgufFile::{tensors, tensor} (lib.rs:301-309) */
+ribn_amd_status ribn_amd_gguf_tensor_info(const ribn_amd_gguf *g, uint64_t index, ribn_amd_gguf_tensor *out);
+ribn_amd_status ribn_amd_gguf_find_tensor(const ribn_amd_gguf *g, const char *name, uint64_t *index);
+/* GgufFile::tensor_data_range (lib.rs:311-339): absolute [start, end) of a
+ * tensor's encoded bytes; MissingTensor, UnsupportedTensorType, the byte_len
+ * errors, or TensorOffsetOutOfBounds. */
+ribn_amd_status ribn_amd_gguf_tensor_data_range(const ribn_amd_gguf *g, const char *name, uint64_t *start,
+                                                uint64_t *end);
+/* CudaQwen35Weights::stage (staging.rs:238-292) over GgufFile::open_tensor
+ * readers and CudaWeightStore::materialize_quantized (cuda.rs:321-387):
+ * checks the summed encoded sizes against budget_bytes (BudgetExceeded,
+ * nothing allocated), then copies each tensor's bytes unchanged into device
+ * memory through pinned double buffers on the context stream, returning one
+ * weight handle per name (Q4_K/Q5_K/Q6_K with [K, N] geometry checks; other
+ * types as plain device bytes whose pointer ribn_amd_weight_device_ptr
+ * gives). Returns after the copies complete; on error no handle is left. */
+ribn_amd_status ribn_amd_gguf_stage(ribn_amd_context *ctx, const ribn_amd_gguf *g, const char *const *names,
+                                    size_t count, uint64_t budget_bytes, ribn_amd_quantized_weight **out);
+
 /* ------------------------------------------------- Q8_1 integer-dot path */
 
 /* CudaQ8_1Quantizer::execute (crates/nvidia/src/activation.rs:52-88,
