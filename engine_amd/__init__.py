@@ -16,6 +16,7 @@ from .kquant import (  # noqa: F401
 )
 from .gguf import GgufError, GgufFile, TensorInfo, load_qwen3_decode, qwen3_config_from_gguf  # noqa: F401
 from .qwen3 import AmdKvCache, AmdQwen3Config, AmdQwen3Decode, QWEN3_8B, attention_decode  # noqa: F401
+from .serving import AmdBackend, AmdDispatcher, AmdServingDispatcher, BackendError, plan_memory  # noqa: F401
 
 __all__ = [
     "Q4_K", "Q5_K", "Q6_K", "BLOCK_BYTES", "AmdContext", "AmdWeightStore", "AmdQuantizedWeight",
@@ -25,4 +26,5 @@ __all__ = [
     "AmdKvCache", "AmdQwen3Config", "AmdQwen3Decode", "QWEN3_8B", "attention_decode",
     "AmdQ8_1Quantizer", "AmdQ4KQ8_1Gemv", "AmdQ5KQ8_1Gemv", "AmdQ6KQ8_1Gemv",
     "GgufError", "GgufFile", "TensorInfo", "load_qwen3_decode", "qwen3_config_from_gguf",
+    "AmdBackend", "AmdDispatcher", "AmdServingDispatcher", "BackendError", "plan_memory",
 ]

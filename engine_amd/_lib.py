@@ -24,6 +24,7 @@ STATUS_NAMES = {
     27: "DuplicateMetadata", 28: "InvalidDimensionCount", 29: "InvalidAlignment", 30: "Truncated",
     31: "TensorOffsetOutOfBounds", 32: "UnsupportedTensorType", 33: "TensorByteLengthOverflow",
     34: "QuantizationMismatch", 35: "MissingMetadata", 36: "MetadataTypeMismatch", 37: "BudgetExceeded",
+    38: "Unsupported", 39: "ExecutionFailed", 40: "UnknownSubmission", 41: "DeviceFaulted", 42: "StatePosition",
 }
 
 
@@ -59,6 +60,26 @@ class GgufTensor(ctypes.Structure):
     """ribn_amd_gguf_tensor."""
     _fields_ = [("name", ctypes.c_char_p), ("n_dims", ctypes.c_uint32), ("dims", ctypes.c_uint64 * 16),
                 ("value_type", ctypes.c_uint32), ("offset", ctypes.c_uint64)]
+
+
+class ServingRow(ctypes.Structure):
+    """ribn_amd_serving_row."""
+    _fields_ = [("request", ctypes.c_uint64), ("state", ctypes.c_uint64), ("phase", ctypes.c_uint32),
+                ("state_position", ctypes.c_uint32), ("tokens", ctypes.POINTER(ctypes.c_uint32)),
+                ("token_count", ctypes.c_uint32), ("requests_sampling", ctypes.c_uint32),
+                ("temperature", ctypes.c_float), ("kv_tokens", ctypes.c_uint32),
+                ("logical_position", ctypes.c_uint32)]
+
+
+class ServingOutcome(ctypes.Structure):
+    """ribn_amd_serving_outcome."""
+    _fields_ = [("elapsed_nanos", ctypes.c_uint64), ("has_token", ctypes.c_uint32), ("token", ctypes.c_uint32)]
+
+
+class MemoryPlan(ctypes.Structure):
+    """ribn_amd_memory_plan."""
+    _fields_ = [("free_before_preparation_bytes", ctypes.c_uint64), ("weight_budget_bytes", ctypes.c_uint64),
+                ("reserved_sequence_bytes", ctypes.c_uint64)]
 
 
 READ_FN = ctypes.CFUNCTYPE(ctypes.c_int64, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint8), ctypes.c_size_t)
@@ -147,6 +168,7 @@ SIGNATURES = {
     "ribn_amd_qwen3_decode_destroy": (None, [_vp]),
     "ribn_amd_qwen3_decode_set_graphs": (_i32, [_vp, _i32]),
     "ribn_amd_qwen3_prefill_step": (_i32, [_vp, _vp, _u32, _u32]),
+    "ribn_amd_qwen3_prefill_chunk": (_i32, [_vp, _vp, ctypes.POINTER(_u32), _sz, _u32]),
     "ribn_amd_qwen3_decode_step": (_i32, [_vp, _vp, _u32, _u32, ctypes.POINTER(_u32)]),
     "ribn_amd_qwen3_decode_step_batch": (_i32, [_vp, _pvp, ctypes.POINTER(_u32), ctypes.POINTER(_u32), _sz,
                                                 ctypes.POINTER(_u32)]),
@@ -154,6 +176,24 @@ SIGNATURES = {
                                        ctypes.POINTER(_u32)]),
     "ribn_amd_qwen3_copy_hidden": (_i32, [_vp, _sz, _vp, _sz]),
     "ribn_amd_qwen3_copy_logits": (_i32, [_vp, _sz, _vp, _sz]),
+    "ribn_amd_serving_create": (_i32, [_vp, _u32, _u64, _pvp]),
+    "ribn_amd_serving_destroy": (None, [_vp]),
+    "ribn_amd_serving_set_prefill_chunk": (_i32, [_vp, _u32]),
+    "ribn_amd_serving_set_grouped_decode": (_i32, [_vp, _i32]),
+    "ribn_amd_serving_dispatch_batch": (_i32, [_vp, ctypes.POINTER(ServingRow), _sz, ctypes.POINTER(ServingOutcome)]),
+    "ribn_amd_serving_submit_batch": (_i32, [_vp, _u64, ctypes.POINTER(ServingRow), _sz]),
+    "ribn_amd_serving_poll_batch": (_i32, [_vp, _u64, ctypes.POINTER(ServingOutcome), _sz,
+                                           ctypes.POINTER(_i32)]),
+    "ribn_amd_serving_release_state": (_i32, [_vp, _u64]),
+    "ribn_amd_serving_pending": (_sz, [_vp]),
+    "ribn_amd_serving_state_count": (_sz, [_vp]),
+    "ribn_amd_serving_state_bytes": (_u64, [_vp, ctypes.POINTER(_u64)]),
+    "ribn_amd_serving_state_position": (_i32, [_vp, _u64, ctypes.POINTER(_u32)]),
+    "ribn_amd_serving_chunked_prefix_len": (_u32, [_u32, _u32, _i32]),
+    "ribn_amd_serving_decode_group": (_sz, [ctypes.POINTER(ServingRow), _sz, ctypes.POINTER(ctypes.c_uint8), _sz,
+                                            _sz, ctypes.POINTER(_sz)]),
+    "ribn_amd_plan_memory": (_i32, [_vp, _u64, _u64, _u64, _u64, _u64, ctypes.POINTER(MemoryPlan)]),
+    "ribn_amd_qwen3_kv_bytes": (_u64, [ctypes.POINTER(Qwen3Config), _u32]),
 }
 
 _lib = None

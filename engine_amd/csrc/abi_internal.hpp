@@ -16,6 +16,7 @@ struct ribn_amd_context {
     void* workspace;  // prefill activation workspace (ribn_amd_context_reserve_prefill)
     size_t workspace_bytes;
     void* act_scratch;  // packed activations of the matrix-core batched GEMV, reserved at creation
+    void* attn_members; // cache descriptors of the standalone attention call (same allocation)
 };
 
 struct ribn_amd_quantized_weight {

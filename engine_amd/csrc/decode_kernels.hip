@@ -24,7 +24,14 @@
 // (member, head) into the output (a context within one chunk is written
 // directly). The new token's K/V are computed by the
 // workgroup whose chunk holds the position: written to the cache, and used
-// from LDS by that workgroup.
+// from LDS by that workgroup. For consecutive tokens of one sequence (a
+// prefill chunk) kv_append_kernel stores every member's K/V first and the
+// attention launch reads them all from the cache ("appended"), with the same
+// values.
+//
+// Cache descriptors, positions and token ids are device memory, so one
+// captured step serves every set of caches and positions; step_inputs_kernel
+// writes them in stream order from its kernel arguments.
 //
 // argmax_kernel: greedy selection (argmax, model_ops.rs:201-258) with the
 // same ordering key, tie rule and NaN rule.
@@ -111,6 +118,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     const int grp = lane >> 4;  // token slot of this lane's row
     const int j = lane & 15;    // dims 8j..8j+7
     const AttnMember mb = a.mem[m];
+    uint16_t* const keys = mb.keys + (size_t)a.layer * mb.layer_elems;
+    uint16_t* const values = mb.values + (size_t)a.layer * mb.layer_elems;
 
     // ---- loads that do not need the position go first: this workgroup's
     // query heads and norm weight, and the new token's raw K (wave 0) and V
@@ -146,20 +155,21 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     if (t0 >= tokens) return;  // no tokens in this chunk (uniform over the workgroup)
     const int t1 = min(t0 + len, tokens);
     const int steps = (t1 - t0 + kStepTokens - 1) / kStepTokens;
-    const bool has_new = pos < t1;
+    const bool has_new = !a.appended && pos < t1;
     // a context within one chunk is finished here; the merge launch skips it
     const bool single = tokens <= len;
 
     // ---- cached K/V of this chunk: the first kRing steps are issued before
-    // anything else. The new token's slot is not read (it is written below).
+    // anything else. Unless appended, the new token's slot is not read (it is
+    // written below).
     const size_t head_elems = (size_t)mb.capacity * kHeadDim;
     const uint32_t head_bytes = (uint32_t)(head_elems * 2u);
-    const __amdgpu_buffer_rsrc_t kr = make_rsrc(mb.keys + (size_t)kvh * head_elems, head_bytes);
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(mb.values + (size_t)kvh * head_elems, head_bytes);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(keys + (size_t)kvh * head_elems, head_bytes);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(values + (size_t)kvh * head_elems, head_bytes);
     uint4 kring[kRing], vring[kRing];
     auto issue = [&](int r, int s) {
         const int t = t0 + s * kStepTokens + 4 * wave + grp;
-        const bool live = s < steps && t < t1 && t != pos;
+        const bool live = s < steps && t < t1 && (a.appended || t != pos);
         const uint32_t off = live ? ((uint32_t)t * kHeadDim + 8u * (uint32_t)j) * 2u : kOOR;
         kring[r] = load_b128(kr, off);
         vring[r] = load_b128(vr, off);
@@ -185,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         const _Float16 h0 = (_Float16)nx0;
         const _Float16 h1 = (_Float16)nx1;
         if (pos < mb.capacity) {
-            uint16_t* dst = (wave == 0 ? mb.keys : mb.values) + (size_t)kvh * head_elems + (size_t)pos * kHeadDim;
+            uint16_t* dst = (wave == 0 ? keys : values) + (size_t)kvh * head_elems + (size_t)pos * kHeadDim;
             dst[lane] = __builtin_bit_cast(uint16_t, h0);
             dst[lane + 64] = __builtin_bit_cast(uint16_t, h1);
         }
@@ -335,6 +345,36 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     }
 }
 
+// The fused kernel's new-token path on its own: wave 0 normalises and ropes
+// the member's raw K of one KV head, wave 1 takes V, both stored as f16 at
+// the member's position. Grid (KV head, member).
+__global__ __launch_bounds__(128) void kv_append_kernel(AttnArgs a) {
+    const int kvh = blockIdx.x;
+    const int m = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const AttnMember mb = a.mem[m];
+    const float* src = (wave == 0 ? a.k : a.v) + ((size_t)m * a.kv_heads + kvh) * kHeadDim;
+    float x0 = src[lane];
+    float x1 = src[lane + 64];
+    const int pos = a.positions[m];
+    if (wave == 0) norm_rope(x0, x1, a.k_norm[lane], a.k_norm[lane + 64], a.eps, (float)pos, a.rope_base, lane);
+    if (pos < 0 || pos >= mb.capacity) return;
+    const size_t head_elems = (size_t)mb.capacity * kHeadDim;
+    uint16_t* dst = (wave == 0 ? mb.keys : mb.values) + (size_t)a.layer * mb.layer_elems +
+                    (size_t)kvh * head_elems + (size_t)pos * kHeadDim;
+    dst[lane] = __builtin_bit_cast(uint16_t, (_Float16)x0);
+    dst[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16)x1);
+}
+
+__global__ __launch_bounds__(64) void step_inputs_kernel(StepInputs in) {
+    const int i = threadIdx.x;
+    if (i >= in.count) return;
+    if (in.mem_dst != nullptr) in.mem_dst[i] = in.mem[i];
+    if (in.tokens_dst != nullptr) in.tokens_dst[i] = in.tokens[i];
+    if (in.positions_dst != nullptr) in.positions_dst[i] = in.positions[i];
+}
+
 // Merges the kAttnChunks partials of one (member, query head) into the
 // attention output: o = sum_c O_c e^(m_c - M) / sum_c L_c e^(m_c - M).
 // A separate launch: the kernel boundary orders the partials' writes before
@@ -465,15 +505,17 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* log
 
 size_t attn_partials_floats(int q_heads) { return (size_t)q_heads * kAttnChunks * kPartStride; }
 
+int attn_grid_chunks(int max_capacity) {
+    // chunks a context can need: capacity / kMinChunkTokens, up to kAttnChunks
+    return std::max(1, std::min(kAttnChunks, (max_capacity + kMinChunkTokens - 1) / kMinChunkTokens));
+}
+
 hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t stream) {
-    if (members < 1 || members > kAttnMaxMembers || args.kv_heads < 1 || args.q_heads % args.kv_heads != 0) {
+    if (members < 1 || members > kAttnMaxMembers || args.kv_heads < 1 || args.q_heads % args.kv_heads != 0 ||
+        args.chunks < 1 || args.chunks > kAttnChunks || args.mem == nullptr) {
         return hipErrorInvalidValue;
     }
-    // chunks a context can need: capacity / kMinChunkTokens, up to kAttnChunks
-    int max_capacity = 1;
-    for (int m = 0; m < members; ++m) max_capacity = std::max(max_capacity, args.mem[m].capacity);
-    const int chunks = std::min(kAttnChunks, (max_capacity + kMinChunkTokens - 1) / kMinChunkTokens);
-    const dim3 grid((unsigned)chunks, (unsigned)args.kv_heads, (unsigned)members);
+    const dim3 grid((unsigned)args.chunks, (unsigned)args.kv_heads, (unsigned)members);
     switch (args.q_heads / args.kv_heads) {
     case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(kThreads), 0, stream, args); break;
     case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(kThreads), 0, stream, args); break;
@@ -485,6 +527,21 @@ hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t strea
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)args.q_heads, (unsigned)members), dim3(kHeadDim), 0, stream,
                        args);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append(const AttnArgs& args, int members, hipStream_t stream) {
+    if (members < 1 || members > kAttnMaxMembers || args.kv_heads < 1 || args.mem == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)args.kv_heads, (unsigned)members), dim3(128), 0, stream,
+                       args);
+    return hipGetLastError();
+}
+
+hipError_t launch_step_inputs(const StepInputs& in, hipStream_t stream) {
+    if (in.count < 1 || in.count > kStepInputs) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(step_inputs_kernel, dim3(1), dim3(64), 0, stream, in);
     return hipGetLastError();
 }
 

@@ -19,16 +19,22 @@ constexpr int kAttnMaxMembers = 8;
 // maximum, the running denominator, two pad words (16-byte rows).
 constexpr int kPartStride = kHeadDim + 4;
 
-// One member's cache views for one layer.
+// One member's cache, as a device-resident descriptor: the attention kernel
+// reads it from memory, so a captured step serves any set of caches.
 struct AttnMember {
-    uint16_t* keys;      // f16 [kv_heads][capacity][128]
-    uint16_t* values;    // f16 [kv_heads][capacity][128]
-    float* partials;     // [q_heads][kAttnChunks][kPartStride]
-    int capacity;        // cache tokens per (layer, KV head)
+    uint16_t* keys;       // f16 [layers][kv_heads][capacity][128]
+    uint16_t* values;     // f16 [layers][kv_heads][capacity][128]
+    float* partials;      // [q_heads][kAttnChunks][kPartStride], this member's own
+    uint64_t layer_elems; // kv_heads * capacity * 128: one layer's elements
+    int capacity;         // cache tokens per (layer, KV head)
+    int pad;
 };
 
 struct AttnArgs {
-    AttnMember mem[kAttnMaxMembers];
+    const AttnMember* mem;     // device [members] descriptors
+    int layer;
+    int chunks;                // grid chunks: ceil(max capacity / 64), at most kAttnChunks
+    int appended;              // 1: every member's K/V is already in its cache (launch_kv_append)
     const float* q;            // [members][q_heads * 128], raw projection
     const float* k;            // [members][kv_heads * 128], raw projection
     const float* v;            // [members][kv_heads * 128]
@@ -46,9 +52,36 @@ struct AttnArgs {
 // Floats of one sequence's attention partials ([q_heads][kAttnChunks][kPartStride]).
 size_t attn_partials_floats(int q_heads);
 
+// Grid chunks of an attention launch over caches of at most `max_capacity` tokens.
+int attn_grid_chunks(int max_capacity);
+
 // Two launches: the chunked attention writing partials, then their merge into
 // `out`. members <= kAttnMaxMembers; q_heads / kv_heads in {1, 2, 4, 8}.
+// Without `appended`, the workgroup whose chunk holds a member's position
+// normalises, ropes and appends that member's new K/V (members must then
+// hold distinct caches); with it the caches already hold them.
 hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t stream);
+
+// The K/V append of `members` new tokens, ahead of an `appended` attention
+// launch: per (member, KV head) the K RMSNorm + rope and the f16 store of K
+// and V at positions[m], computed as the fused attention kernel does. Members
+// may share a cache (consecutive positions of one sequence).
+hipError_t launch_kv_append(const AttnArgs& args, int members, hipStream_t stream);
+
+// Stream-ordered upload of up to kStepInputs members' step inputs through
+// kernel arguments (no host buffer outlives the call): descriptors, token
+// ids and positions; a null destination is skipped.
+constexpr int kStepInputs = 16;
+struct StepInputs {
+    AttnMember mem[kStepInputs];
+    uint32_t tokens[kStepInputs];
+    int32_t positions[kStepInputs];
+    AttnMember* mem_dst;
+    uint32_t* tokens_dst;
+    int32_t* positions_dst;
+    int count;
+};
+hipError_t launch_step_inputs(const StepInputs& in, hipStream_t stream);
 
 // Greedy selection per member over logits [members][vocab] (ties to the lowest
 // index, NaN never selected). Writes selected[m]; when `tokens` is not null

@@ -15,9 +15,16 @@
 //       the epilogue                                    (rms_norm + 2 gemv + silu_mul)
 //     down GEMV added into the stream                  (gemv + residual_add)
 //   output head: RMSNorm(output_norm) + lm_head GEMV, argmax (run_output_head, 655-677)
-// Six launches per layer (attention is two) instead of the reference's 14. Positions and token
-// ids live in device memory, so one captured graph serves every position and
-// a generation loop needs no host round trip between steps.
+// Six launches per layer (attention is two) instead of the reference's 14. Positions, token
+// ids and the members' cache descriptors live in device memory, written by one
+// small kernel from its arguments ahead of the step: one captured graph per
+// (members, head, mode, grid) serves every position and every set of caches,
+// nothing waits on the host before a launch, and a generation loop needs no
+// host round trip between steps.
+//
+// A prefill chunk runs consecutive prompt tokens of one sequence as the
+// members of one step (no output head): their K/V are appended by a separate
+// launch before the attention launch, which then reads them from the cache.
 #include "ribn_amd.h"
 
 #include <hip/hip_runtime.h>
@@ -33,6 +40,7 @@
 #include "abi_internal.hpp"
 #include "decode_launch.hpp"
 #include "kquant_launch.hpp"
+#include "qwen3_internal.hpp"
 
 using namespace ribn_amd_abi;
 
@@ -46,7 +54,7 @@ struct ribn_amd_kv_cache {
     void* block;         // one allocation: keys, values, partials
     uint16_t* keys;      // [layers][kv_heads][capacity][head_dim]
     uint16_t* values;
-    float* partials;     // attention partials ([q_heads][kAttnChunks][kPartStride])
+    float* partials;     // attention partials of the standalone attention call
 };
 
 namespace {
@@ -56,15 +64,28 @@ std::atomic<uint64_t> g_cache_ids{1};
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-struct GraphEntry {
-    std::vector<uint64_t> caches;  // cache ids, in member order
+// A captured step: the launches depend on the member count, the output head,
+// device-side advance, the append mode and the attention grid, not on which
+// caches, tokens or positions the members hold.
+struct GraphKey {
+    int members;
     bool head;
     bool advance;
+    bool appended;
+    int chunks;
+    bool operator==(const GraphKey& o) const {
+        return members == o.members && head == o.head && advance == o.advance && appended == o.appended &&
+               chunks == o.chunks;
+    }
+};
+
+struct GraphEntry {
+    GraphKey key;
     hipGraph_t graph;
     hipGraphExec_t exec;
 };
 
-constexpr size_t kMaxGraphs = 32;
+constexpr size_t kMaxGraphs = 64;
 
 ribn_amd_status check_config(const ribn_amd_qwen3_config* c) {
     if (c == nullptr) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null config");
@@ -128,6 +149,9 @@ struct ribn_amd_qwen3_decode {
     int32_t* steps;       // [members] generated-token counters
     uint32_t* history;    // [members][history_steps]
     uint32_t history_steps;
+    ribn_amd::AttnMember* members_dev;  // [members] cache descriptors of the next step
+    float* partials;      // [members][attention partials]
+    int chunks;           // attention grid of the next step (from its caches' capacities)
     hipStream_t capture;  // private stream for graph capture
     bool graphs;
     std::vector<GraphEntry> graph_cache;
@@ -188,21 +212,20 @@ hipError_t wave_shared(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_
     return hipSuccess;
 }
 
-hipError_t attention(const ribn_amd_qwen3_config& cfg, ribn_amd_kv_cache* const* caches, int members, uint32_t layer,
-                     const float* q, const float* k, const float* v, const float* q_norm, const float* k_norm,
-                     const int32_t* positions, float* out, hipStream_t stream) {
+// One layer's attention over device descriptors mem[0..members), in launches of
+// kAttnMaxMembers; `appended` first stores the launch's members' K/V.
+hipError_t attention(const ribn_amd_qwen3_config& cfg, const ribn_amd::AttnMember* mem, int chunks, bool appended,
+                     int members, uint32_t layer, const float* q, const float* k, const float* v, const float* q_norm,
+                     const float* k_norm, const int32_t* positions, float* out, hipStream_t stream) {
     const size_t qdim = (size_t)cfg.q_heads * cfg.head_dim;
     const size_t kvdim = (size_t)cfg.kv_heads * cfg.head_dim;
     for (int m0 = 0; m0 < members; m0 += ribn_amd::kAttnMaxMembers) {
         const int mc = std::min(ribn_amd::kAttnMaxMembers, members - m0);
         ribn_amd::AttnArgs a{};
-        for (int i = 0; i < mc; ++i) {
-            ribn_amd_kv_cache* c = caches[m0 + i];
-            a.mem[i].keys = c->keys + (size_t)layer * c->layer_elems;
-            a.mem[i].values = c->values + (size_t)layer * c->layer_elems;
-            a.mem[i].partials = c->partials;
-            a.mem[i].capacity = (int)c->capacity;
-        }
+        a.mem = mem + m0;
+        a.layer = (int)layer;
+        a.chunks = chunks;
+        a.appended = appended ? 1 : 0;
         a.q = q + m0 * qdim;
         a.k = k + m0 * kvdim;
         a.v = v + m0 * kvdim;
@@ -216,15 +239,19 @@ hipError_t attention(const ribn_amd_qwen3_config& cfg, ribn_amd_kv_cache* const*
         a.rope_base = cfg.rope_base;
         // softmax weights are exp2 of scores in log2 units: e^x = 2^(x log2 e)
         a.scale = 1.4426950408889634f / sqrtf((float)cfg.head_dim);
-        hipError_t e = ribn_amd::launch_attention(a, mc, stream);
+        hipError_t e = hipSuccess;
+        if (appended) e = ribn_amd::launch_kv_append(a, mc, stream);
+        if (e == hipSuccess) e = ribn_amd::launch_attention(a, mc, stream);
         if (e != hipSuccess) return e;
     }
+    // appended members in position order: a member reads only earlier
+    // positions, stored by its own launch group's append or an earlier one
     return hipSuccess;
 }
 
 // The launches of one step (see the file comment).
-hipError_t enqueue_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches, int members, bool head,
-                        bool advance, hipStream_t stream) {
+hipError_t enqueue_step(ribn_amd_qwen3_decode* d, const GraphKey& key, hipStream_t stream) {
+    const int members = key.members;
     const ribn_amd_qwen3_config& c = d->cfg;
     hipError_t e = ribn_amd::launch_embedding((int)d->token_embd->value_type, d->token_embd->data,
                                               (uint32_t)d->token_embd->encoded_bytes, d->tokens, 0, d->hidden,
@@ -236,8 +263,8 @@ hipError_t enqueue_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* cach
         float* qkv_out[3] = {d->q, d->k, d->v};
         e = wave_shared(d, qkv, qkv_out, 3, d->hidden, L.attn_norm, members, stream);
         if (e != hipSuccess) return e;
-        e = attention(c, caches, members, l, d->q, d->k, d->v, L.attn_q_norm, L.attn_k_norm, d->positions, d->attn,
-                      stream);
+        e = attention(c, d->members_dev, key.chunks, key.appended, members, l, d->q, d->k, d->v, L.attn_q_norm,
+                      L.attn_k_norm, d->positions, d->attn, stream);
         if (e != hipSuccess) return e;
         e = wave(d, &L.attn_output, 1, d->attn, nullptr, nullptr, &d->hidden, members, true, stream);
         if (e != hipSuccess) return e;
@@ -256,12 +283,12 @@ hipError_t enqueue_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* cach
         }
         if (e != hipSuccess) return e;
     }
-    if (!head) return hipSuccess;
+    if (!key.head) return hipSuccess;
     e = wave(d, &d->output, 1, d->hidden, nullptr, d->output_norm, &d->logits, members, false, stream);
     if (e != hipSuccess) return e;
     return ribn_amd::launch_argmax(d->logits, (int)c.vocab, members, d->selected, d->tokens,
-                                   advance ? d->positions : nullptr, d->steps, d->history, (int)d->history_steps,
-                                   stream);
+                                   key.advance ? d->positions : nullptr, d->steps, d->history,
+                                   (int)d->history_steps, stream);
 }
 
 void destroy_graphs(ribn_amd_qwen3_decode* d) {
@@ -272,20 +299,19 @@ void destroy_graphs(ribn_amd_qwen3_decode* d) {
     d->graph_cache.clear();
 }
 
-// Runs one step on the context stream: replays (capturing on first use) the
-// step's graph, or launches directly when graphs are off.
-ribn_amd_status run_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches, int members, bool head,
-                         bool advance) {
+// Runs one step of the uploaded members on the context stream: replays
+// (capturing on first use) the step's graph, or launches directly when graphs
+// are off.
+ribn_amd_status run_step(ribn_amd_qwen3_decode* d, int members, bool head, bool advance, bool appended = false) {
     hipStream_t stream = d->ctx->stream;
+    const GraphKey key{members, head, advance, appended, d->chunks};
     if (!d->graphs) {
-        hipError_t e = enqueue_step(d, caches, members, head, advance, stream);
+        hipError_t e = enqueue_step(d, key, stream);
         return e == hipSuccess ? ok() : driver(e, "launch decode step");
     }
-    std::vector<uint64_t> ids(members);
-    for (int m = 0; m < members; ++m) ids[m] = caches[m]->id;
     GraphEntry* hit = nullptr;
     for (GraphEntry& g : d->graph_cache) {
-        if (g.head == head && g.advance == advance && g.caches == ids) {
+        if (g.key == key) {
             hit = &g;
             break;
         }
@@ -300,7 +326,7 @@ ribn_amd_status run_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* cac
         }
         hipError_t e = hipStreamBeginCapture(d->capture, hipStreamCaptureModeRelaxed);
         if (e != hipSuccess) return driver(e, "hipStreamBeginCapture");
-        const hipError_t le = enqueue_step(d, caches, members, head, advance, d->capture);
+        const hipError_t le = enqueue_step(d, key, d->capture);
         hipGraph_t graph = nullptr;
         e = hipStreamEndCapture(d->capture, &graph);
         if (le != hipSuccess || e != hipSuccess) {
@@ -313,7 +339,7 @@ ribn_amd_status run_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* cac
             hipGraphDestroy(graph);
             return driver(e, "hipGraphInstantiate");
         }
-        d->graph_cache.push_back(GraphEntry{std::move(ids), head, advance, graph, exec});
+        d->graph_cache.push_back(GraphEntry{key, graph, exec});
         hit = &d->graph_cache.back();
     }
     hipError_t e = hipGraphLaunch(hit->exec, stream);
@@ -344,10 +370,11 @@ ribn_amd_status check_weight(const ribn_amd_context* ctx, const ribn_amd_quantiz
 }
 
 // Validates one step's members: caches of this decoder's geometry on its
-// device, distinct; tokens in the vocabulary; positions (plus `extra` further
-// steps) within each cache.
+// device, distinct unless `shared` (one sequence's consecutive tokens); tokens
+// in the vocabulary; positions (plus `extra` further steps) within each cache.
 ribn_amd_status check_members(const ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches,
-                              const uint32_t* tokens, const uint32_t* positions, size_t members, uint32_t extra) {
+                              const uint32_t* tokens, const uint32_t* positions, size_t members, uint32_t extra,
+                              bool shared = false) {
     if (members == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "a step needs at least one member");
     if (members > d->max_members) {
         return fail(RIBN_AMD_INVALID_PLAN, d->max_members, members, "the decoder was built for %u members",
@@ -363,7 +390,7 @@ ribn_amd_status check_members(const ribn_amd_qwen3_decode* d, ribn_amd_kv_cache*
         if (!same_geometry(c->cfg, d->cfg)) {
             return fail(RIBN_AMD_INVALID_PLAN, 0, 0, "member %zu's cache has another layer or head geometry", m);
         }
-        for (size_t o = 0; o < m; ++o) {
+        for (size_t o = 0; o < m && !shared; ++o) {
             if (caches[o] == c) return fail(RIBN_AMD_INVALID_PLAN, o, m, "members %zu and %zu share a cache", o, m);
         }
         if (tokens[m] >= d->cfg.vocab) {
@@ -379,21 +406,95 @@ ribn_amd_status check_members(const ribn_amd_qwen3_decode* d, ribn_amd_kv_cache*
     return RIBN_AMD_OK;
 }
 
-// Stream-ordered upload of the members' tokens and positions.
-ribn_amd_status upload_step(ribn_amd_qwen3_decode* d, const uint32_t* tokens, const uint32_t* positions,
-                            size_t members) {
-    std::vector<int32_t> pos(members);
-    for (size_t m = 0; m < members; ++m) pos[m] = (int32_t)positions[m];
-    hipError_t e = hipMemcpyAsync(d->tokens, tokens, members * sizeof(uint32_t), hipMemcpyHostToDevice, d->ctx->stream);
-    if (e == hipSuccess) {
-        e = hipMemcpyAsync(d->positions, pos.data(), members * sizeof(int32_t), hipMemcpyHostToDevice, d->ctx->stream);
+ribn_amd::AttnMember descriptor(const ribn_amd_kv_cache* c, float* partials) {
+    ribn_amd::AttnMember m{};
+    m.keys = c->keys;
+    m.values = c->values;
+    m.partials = partials;
+    m.layer_elems = c->layer_elems;
+    m.capacity = (int)c->capacity;
+    return m;
+}
+
+// Stream-ordered upload of the members' cache descriptors (with the
+// decoder's per-member partials), tokens and positions through kernel
+// arguments; records the step's attention grid. Nothing waits on the host.
+ribn_amd_status upload_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches, const uint32_t* tokens,
+                            const uint32_t* positions, size_t members) {
+    const size_t part = ribn_amd::attn_partials_floats((int)d->cfg.q_heads);
+    int max_capacity = 1;
+    for (size_t m0 = 0; m0 < members; m0 += ribn_amd::kStepInputs) {
+        ribn_amd::StepInputs in{};
+        in.count = (int)std::min<size_t>(ribn_amd::kStepInputs, members - m0);
+        for (int i = 0; i < in.count; ++i) {
+            const size_t m = m0 + i;
+            in.mem[i] = descriptor(caches[m], d->partials + m * part);
+            in.tokens[i] = tokens[m];
+            in.positions[i] = (int32_t)positions[m];
+            max_capacity = std::max(max_capacity, (int)caches[m]->capacity);
+        }
+        in.mem_dst = d->members_dev + m0;
+        in.tokens_dst = d->tokens + m0;
+        in.positions_dst = d->positions + m0;
+        hipError_t e = ribn_amd::launch_step_inputs(in, d->ctx->stream);
+        if (e != hipSuccess) return driver(e, "upload step inputs");
     }
-    // pageable sources: the copies are complete before the vectors go away
-    if (e == hipSuccess) e = hipStreamSynchronize(d->ctx->stream);
-    return e == hipSuccess ? ok() : driver(e, "upload step inputs");
+    d->chunks = ribn_amd::attn_grid_chunks(max_capacity);
+    return ok();
 }
 
 }  // namespace
+
+namespace ribn_amd_decode {
+
+ribn_amd_status enqueue_decode(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches, const uint32_t* tokens,
+                               const uint32_t* positions, size_t members) {
+    if (!d || !caches || !tokens || !positions) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    ribn_amd_status st = check_members(d, caches, tokens, positions, members, 0);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(d->ctx->device);
+    st = upload_step(d, caches, tokens, positions, members);
+    return st == RIBN_AMD_OK ? run_step(d, (int)members, true, false) : st;
+}
+
+ribn_amd_status enqueue_prefill_chunk(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* cache, const uint32_t* tokens,
+                                      size_t count, uint32_t position) {
+    if (!d || !cache || !tokens) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (count < 2) return fail(RIBN_AMD_INPUT_LENGTH, 2, count, "a prefill chunk takes at least two tokens");
+    if (count > d->max_members) {
+        return fail(RIBN_AMD_INVALID_PLAN, d->max_members, count, "the decoder was built for %u members",
+                    d->max_members);
+    }
+    if ((uint64_t)position + count > 0x7fffffffull) {
+        return fail(RIBN_AMD_POSITION_OVERFLOW, 0x7fffffffull, (uint64_t)position + count,
+                    "prefill chunk positions overflow");
+    }
+    std::vector<ribn_amd_kv_cache*> caches(count, cache);
+    std::vector<uint32_t> positions(count);
+    for (size_t m = 0; m < count; ++m) positions[m] = position + (uint32_t)m;
+    ribn_amd_status st = check_members(d, caches.data(), tokens, positions.data(), count, 0, true);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(d->ctx->device);
+    st = upload_step(d, caches.data(), tokens, positions.data(), count);
+    return st == RIBN_AMD_OK ? run_step(d, (int)count, false, false, true) : st;
+}
+
+ribn_amd_status copy_selected_async(ribn_amd_qwen3_decode* d, size_t member, uint32_t* pinned) {
+    if (!d || !pinned) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (member >= d->max_members) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, d->max_members, member, "member %zu of %u", member, d->max_members);
+    }
+    DeviceGuard guard(d->ctx->device);
+    hipError_t e = hipMemcpyAsync(pinned, d->selected + member, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                  d->ctx->stream);
+    return e == hipSuccess ? ok() : driver(e, "copy selected token into pinned memory");
+}
+
+ribn_amd_context* context(const ribn_amd_qwen3_decode* d) { return d->ctx; }
+uint32_t max_members(const ribn_amd_qwen3_decode* d) { return d->max_members; }
+const ribn_amd_qwen3_config& config(const ribn_amd_qwen3_decode* d) { return d->cfg; }
+
+}  // namespace ribn_amd_decode
 
 extern "C" {
 
@@ -493,10 +594,25 @@ ribn_amd_status ribn_amd_attention_decode(ribn_amd_context* ctx, const ribn_amd_
                     output_len, want);
     }
     DeviceGuard guard(ctx->device);
+    // the members' descriptors go to the context's descriptor array, in
+    // stream order ahead of the launches that read them
+    auto* mem = static_cast<ribn_amd::AttnMember*>(ctx->attn_members);
+    int max_capacity = 1;
+    for (size_t m0 = 0; m0 < members; m0 += ribn_amd::kStepInputs) {
+        ribn_amd::StepInputs in{};
+        in.count = (int)std::min<size_t>(ribn_amd::kStepInputs, members - m0);
+        for (int i = 0; i < in.count; ++i) {
+            in.mem[i] = descriptor(caches[m0 + i], caches[m0 + i]->partials);
+            max_capacity = std::max(max_capacity, (int)caches[m0 + i]->capacity);
+        }
+        in.mem_dst = mem + m0;
+        hipError_t e = ribn_amd::launch_step_inputs(in, ctx->stream);
+        if (e != hipSuccess) return driver(e, "upload attention descriptors");
+    }
     // Positions are device values: the kernel checks them against each cache
     // and drops an append past its capacity.
-    hipError_t e = attention(*config, caches, (int)members, layer, q, k, v, q_norm, k_norm, positions, output,
-                             ctx->stream);
+    hipError_t e = attention(*config, mem, ribn_amd::attn_grid_chunks(max_capacity), false, (int)members, layer, q, k,
+                             v, q_norm, k_norm, positions, output, ctx->stream);
     return e == hipSuccess ? ok() : driver(e, "launch attention");
 }
 
@@ -580,6 +696,10 @@ ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context* ctx, const ribn_a
         offsets[i] = bytes;
         bytes += align_up(M * sizeof(uint32_t));
     }
+    const size_t members_offset = bytes;
+    bytes += align_up(M * sizeof(ribn_amd::AttnMember));
+    const size_t partials_offset = bytes;
+    bytes += align_up(M * ribn_amd::attn_partials_floats((int)c.q_heads) * sizeof(float));
     DeviceGuard guard(ctx->device);
     auto* d = new (std::nothrow) ribn_amd_qwen3_decode{};
     if (!d) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
@@ -603,6 +723,9 @@ ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context* ctx, const ribn_a
     d->selected = reinterpret_cast<uint32_t*>(p + offsets[9]);
     d->positions = reinterpret_cast<int32_t*>(p + offsets[10]);
     d->steps = reinterpret_cast<int32_t*>(p + offsets[11]);
+    d->members_dev = reinterpret_cast<ribn_amd::AttnMember*>(p + members_offset);
+    d->partials = reinterpret_cast<float*>(p + partials_offset);
+    d->chunks = 1;
     d->history_steps = 256;
     e = hipMalloc(&d->history, M * d->history_steps * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemsetAsync(d->block, 0, bytes, ctx->stream);
@@ -644,9 +767,9 @@ ribn_amd_status ribn_amd_qwen3_decode_step_batch(ribn_amd_qwen3_decode* d, ribn_
     ribn_amd_status st = check_members(d, caches, tokens, positions, members, 0);
     if (st != RIBN_AMD_OK) return st;
     DeviceGuard guard(d->ctx->device);
-    st = upload_step(d, tokens, positions, members);
+    st = upload_step(d, caches, tokens, positions, members);
     if (st != RIBN_AMD_OK) return st;
-    st = run_step(d, caches, (int)members, true, false);
+    st = run_step(d, (int)members, true, false);
     if (st != RIBN_AMD_OK) return st;
     // the reference's blocking token readback (decode.rs:634-645)
     hipError_t e = hipMemcpyAsync(selected, d->selected, members * sizeof(uint32_t), hipMemcpyDeviceToHost,
@@ -668,9 +791,13 @@ ribn_amd_status ribn_amd_qwen3_prefill_step(ribn_amd_qwen3_decode* d, ribn_amd_k
     ribn_amd_status st = check_members(d, caches, &token, &position, 1, 0);
     if (st != RIBN_AMD_OK) return st;
     DeviceGuard guard(d->ctx->device);
-    st = upload_step(d, &token, &position, 1);
-    if (st != RIBN_AMD_OK) return st;
-    return run_step(d, caches, 1, false, false);
+    st = upload_step(d, caches, &token, &position, 1);
+    return st == RIBN_AMD_OK ? run_step(d, 1, false, false) : st;
+}
+
+ribn_amd_status ribn_amd_qwen3_prefill_chunk(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* cache,
+                                             const uint32_t* tokens, size_t count, uint32_t position) {
+    return ribn_amd_decode::enqueue_prefill_chunk(d, cache, tokens, count, position);
 }
 
 ribn_amd_status ribn_amd_qwen3_generate(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches,
@@ -696,14 +823,14 @@ ribn_amd_status ribn_amd_qwen3_generate(ribn_amd_qwen3_decode* d, ribn_amd_kv_ca
         if (e != hipSuccess) return driver(e, "hipMalloc generation history");
         d->history_steps = steps;
     }
-    st = upload_step(d, tokens, positions, members);
+    st = upload_step(d, caches, tokens, positions, members);
     if (st != RIBN_AMD_OK) return st;
     std::vector<int32_t> zeros(members, 0);
     hipError_t e = hipMemcpyAsync(d->steps, zeros.data(), members * sizeof(int32_t), hipMemcpyHostToDevice, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) return driver(e, "reset generation counters");
     for (uint32_t s = 0; s < steps; ++s) {
-        st = run_step(d, caches, (int)members, true, true);
+        st = run_step(d, (int)members, true, true);
         if (st != RIBN_AMD_OK) return st;
     }
     for (size_t m = 0; m < members; ++m) {

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "abi_internal.hpp"
+#include "decode_launch.hpp"
 #include "kquant_launch.hpp"
 
 namespace ribn_amd_abi {
@@ -219,13 +220,15 @@ ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_
     hipError_t e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return driver(e, "hipGetDeviceProperties");
     void* scratch = nullptr;
+    const size_t act_bytes = (ribn_amd::gemv_act_scratch_bytes() + 255) / 256 * 256;
     {
         DeviceGuard guard(device);
-        e = hipMalloc(&scratch, ribn_amd::gemv_act_scratch_bytes());
-        if (e != hipSuccess) return driver(e, "hipMalloc batched-GEMV activation scratch");
+        e = hipMalloc(&scratch, act_bytes + RIBN_AMD_MAX_BATCH_MEMBERS * sizeof(ribn_amd::AttnMember));
+        if (e != hipSuccess) return driver(e, "hipMalloc context scratch");
     }
-    auto* ctx =
-        new (std::nothrow) ribn_amd_context{device, stream, owns, prop.multiProcessorCount, nullptr, 0, scratch};
+    auto* ctx = new (std::nothrow) ribn_amd_context{device,  stream,  owns, prop.multiProcessorCount,
+                                                    nullptr, 0,       scratch,
+                                                    static_cast<char*>(scratch) + act_bytes};
     if (!ctx) {
         DeviceGuard guard(device);
         hipFree(scratch);
@@ -287,6 +290,11 @@ const char* ribn_amd_status_name(int32_t status) {
     case RIBN_AMD_GGUF_MISSING_METADATA: return "MissingMetadata";
     case RIBN_AMD_GGUF_METADATA_TYPE_MISMATCH: return "MetadataTypeMismatch";
     case RIBN_AMD_BUDGET_EXCEEDED: return "BudgetExceeded";
+    case RIBN_AMD_UNSUPPORTED: return "Unsupported";
+    case RIBN_AMD_EXECUTION_FAILED: return "ExecutionFailed";
+    case RIBN_AMD_UNKNOWN_SUBMISSION: return "UnknownSubmission";
+    case RIBN_AMD_DEVICE_FAULTED: return "DeviceFaulted";
+    case RIBN_AMD_STATE_POSITION: return "StatePosition";
     default: return "Unknown";
     }
 }

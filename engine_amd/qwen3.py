@@ -121,6 +121,13 @@ class AmdQwen3Decode:
         _check(self.ctx._lib.ribn_amd_qwen3_prefill_step(self.handle, cache.handle, token, position),
                AmdModelKernelError)
 
+    def prefill_chunk(self, cache: AmdKvCache, tokens, position: int):
+        """Consecutive prompt tokens of one sequence as one step's members."""
+        n = len(tokens)
+        tok = (ctypes.c_uint32 * n)(*[int(t) for t in tokens])
+        _check(self.ctx._lib.ribn_amd_qwen3_prefill_chunk(self.handle, cache.handle, tok, n, position),
+               AmdModelKernelError)
+
     def decode_step(self, cache: AmdKvCache, token: int, position: int) -> int:
         out = ctypes.c_uint32()
         _check(self.ctx._lib.ribn_amd_qwen3_decode_step(self.handle, cache.handle, token, position,

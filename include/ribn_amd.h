@@ -89,7 +89,14 @@ typedef enum ribn_amd_status {
     RIBN_AMD_GGUF_QUANTIZATION_MISMATCH = 34,     /* QuantizationDimensionMismatch / QuantizationBlockMismatch */
     RIBN_AMD_GGUF_MISSING_METADATA = 35,          /* MissingMetadata(key) */
     RIBN_AMD_GGUF_METADATA_TYPE_MISMATCH = 36,    /* MetadataTypeMismatch { key } */
-    RIBN_AMD_BUDGET_EXCEEDED = 37,                /* CudaWeightStagingError::BudgetExceeded (staging.rs:255-258) */
+    RIBN_AMD_BUDGET_EXCEEDED = 37,                /* CudaWeightStagingError::BudgetExceeded (staging.rs:255-258);
+                                                     also a KV materialization past the serving budget */
+    /* serving dispatcher (BackendError, crates/core/src/backend.rs:188-196; CudaStateError, state.rs:905-956) */
+    RIBN_AMD_UNSUPPORTED = 38,                    /* BackendError::Unsupported (non-greedy sampling, other phases) */
+    RIBN_AMD_EXECUTION_FAILED = 39,               /* BackendError::ExecutionFailed (row input, slots, duplicates) */
+    RIBN_AMD_UNKNOWN_SUBMISSION = 40,             /* BackendError::UnknownSubmission */
+    RIBN_AMD_DEVICE_FAULTED = 41,                 /* ExecutionFailed after a device failure: terminal */
+    RIBN_AMD_STATE_POSITION = 42,                 /* UnmaterializedPrefix / PositionMismatch / PositionRegression */
 } ribn_amd_status;
 
 typedef struct ribn_amd_error {
@@ -502,9 +509,19 @@ void ribn_amd_qwen3_decode_destroy(ribn_amd_qwen3_decode *decode);
  * directly. Both run the same kernels with the same arguments. */
 ribn_amd_status ribn_amd_qwen3_decode_set_graphs(ribn_amd_qwen3_decode *decode, int32_t enabled);
 /* CudaQwen35Decode::prefill_step (decode.rs:489-499): advances `cache` by
- * `token` at `position` without the output head. */
+ * `token` at `position` without the output head. Stream-ordered, not
+ * blocking: a later step or copy on the context stream observes it. */
 ribn_amd_status ribn_amd_qwen3_prefill_step(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
                                             uint32_t token, uint32_t position);
+/* CudaQwen35BatchDecode::prefill_chunk (decode.rs:1953-1977): `count`
+ * consecutive prompt tokens of one sequence (positions position ..
+ * position + count - 1, 2 <= count <= max_members) as the members of one
+ * step without the output head, so the weights are read once for the chunk.
+ * Every attention input equals the serial prefill_step sequence's; GEMV
+ * results are the batched GEMV's (bit-equal to serial on the wave path,
+ * within the GEMV tolerance on the matrix-core path). Stream-ordered. */
+ribn_amd_status ribn_amd_qwen3_prefill_chunk(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
+                                             const uint32_t *tokens, size_t count, uint32_t position);
 /* CudaQwen35Decode::decode_step (decode.rs:508-516): one forward pass and the
  * greedy token (blocking, as the reference). */
 ribn_amd_status ribn_amd_qwen3_decode_step(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
@@ -527,6 +544,137 @@ ribn_amd_status ribn_amd_qwen3_generate(ribn_amd_qwen3_decode *decode, ribn_amd_
  * residual stream [hidden] or logits [vocab] after the last step, to host. */
 ribn_amd_status ribn_amd_qwen3_copy_hidden(ribn_amd_qwen3_decode *decode, size_t member, float *host, size_t len);
 ribn_amd_status ribn_amd_qwen3_copy_logits(ribn_amd_qwen3_decode *decode, size_t member, float *host, size_t len);
+
+/* ------------------------------------------------------ serving dispatcher */
+
+/* The asynchronous serving dispatcher over one decoder
+ * (CudaQwen35ServingDispatcher, crates/nvidia/src/serving.rs:81-1038) with its
+ * physical state registry (CudaStateRegistry / CudaHybridState, state.rs:411-725;
+ * KV family only: Qwen3 has no recurrent state) and submission ownership
+ * (submissions.rs:1-47). An engine-core adapter maps ExecutionSegment /
+ * InferenceStateSet onto ribn_amd_serving_row and BackendError onto the
+ * statuses 38-42. One dispatcher per decoder; calls on one dispatcher must
+ * not overlap (the reference takes &mut self). */
+typedef struct ribn_amd_serving ribn_amd_serving;
+
+/* ExecutionPhase (crates/core/src/execution.rs); only prefill and decode run. */
+typedef enum ribn_amd_phase {
+    RIBN_AMD_PHASE_PREFILL = 0,
+    RIBN_AMD_PHASE_DECODE = 1,
+    RIBN_AMD_PHASE_SPEC_DRAFT = 2,
+    RIBN_AMD_PHASE_SPEC_VERIFY = 3,
+    RIBN_AMD_PHASE_ENCODER = 4,
+    RIBN_AMD_PHASE_MOE_EXPERT = 5
+} ribn_amd_phase;
+
+#define RIBN_AMD_NO_POSITION 0xffffffffu
+
+/* One scheduler row: an ExecutionSegment with its InferenceStateSet. */
+typedef struct ribn_amd_serving_row {
+    uint64_t request;           /* RequestId, for messages */
+    uint64_t state;             /* logical state identity (CudaStateKey::from_state_set), nonzero */
+    uint32_t phase;             /* ribn_amd_phase */
+    uint32_t state_position;    /* ExecutionSegment::state_position: the row's first position */
+    const uint32_t *tokens;     /* host: the prompt slice (prefill) or the one decode token; null = none */
+    uint32_t token_count;       /* ExecutionSegment::token_count */
+    uint32_t requests_sampling; /* nonzero: the row returns a token (sampling parameters present) */
+    float temperature;          /* SamplingParams temperature: only 0 (greedy) runs */
+    uint32_t kv_tokens;         /* the state's KvStateSpec block tokens (KV capacity); 0: no KV state */
+    uint32_t logical_position;  /* InferenceStateSet::token_position, RIBN_AMD_NO_POSITION when absent */
+} ribn_amd_serving_row;
+
+/* ExecutionOutcome: the row's wall time spent queueing and its token. */
+typedef struct ribn_amd_serving_outcome {
+    uint64_t elapsed_nanos;
+    uint32_t has_token;
+    uint32_t token;
+} ribn_amd_serving_outcome;
+
+/* CudaQwen35ServingDispatcher::new (serving.rs:281-329): `max_pending_rows`
+ * (>= 1) pinned one-token output slots (hipHostMalloc) bound the sampling
+ * rows in flight; decode rows run together in lanes of 2 ..
+ * min(max_pending_rows, the decoder's max_members) members. KV state is
+ * materialized on a state's first row, `kv_budget_bytes` bounding the
+ * device bytes held by states (0: unbounded); a released state's cache is
+ * kept for reuse by a later state of the same capacity (freed when the
+ * budget needs the room), so release never waits on the device. The decoder
+ * must outlive the dispatcher and is used on its context's stream. */
+ribn_amd_status ribn_amd_serving_create(ribn_amd_qwen3_decode *decode, uint32_t max_pending_rows,
+                                        uint64_t kv_budget_bytes, ribn_amd_serving **out);
+/* Drains the stream and frees every state, slot and event, quarantined ones
+ * included (teardown). */
+void ribn_amd_serving_destroy(ribn_amd_serving *serving);
+/* with_prefill_chunk (serving.rs:357-371): leading whole chunks of `members`
+ * prompt tokens run as one prefill-chunk step (2 <= members <= the decoder's
+ * max_members); 0 restores serial prefill. */
+ribn_amd_status ribn_amd_serving_set_prefill_chunk(ribn_amd_serving *serving, uint32_t members);
+/* with_grouped_decode (serving.rs:337-341): compatible decode rows of mixed
+ * batches are gathered into lanes (opt-in, as in the reference). */
+ribn_amd_status ribn_amd_serving_set_grouped_decode(ribn_amd_serving *serving, int32_t enabled);
+
+/* NvidiaDispatcher::dispatch_batch (serving.rs:854-882): eager execution of
+ * every row in order; returns after the stream drained. outcomes[count]. */
+ribn_amd_status ribn_amd_serving_dispatch_batch(ribn_amd_serving *serving, const ribn_amd_serving_row *rows,
+                                                size_t count, ribn_amd_serving_outcome *outcomes);
+/* NvidiaDispatcher::submit_batch (serving.rs:884-958): queues the batch
+ * without blocking (all-decode batches as one batched step unless grouped
+ * decode is on, otherwise rows in order with grouped lanes) and records one
+ * completion event. `submission` is a nonzero id, unique among pending ones.
+ * An error means nothing of the batch stays queued (or, after a device
+ * fault, its resources are quarantined). */
+ribn_amd_status ribn_amd_serving_submit_batch(ribn_amd_serving *serving, uint64_t submission,
+                                              const ribn_amd_serving_row *rows, size_t count);
+/* NvidiaDispatcher::poll_batch (serving.rs:960-1016): *ready = 0 while the
+ * completion event is pending; once complete, writes outcomes[count] (count =
+ * the submitted row count) and forgets the submission. A device fault poisons
+ * the dispatcher (RIBN_AMD_DEVICE_FAULTED on every later call). */
+ribn_amd_status ribn_amd_serving_poll_batch(ribn_amd_serving *serving, uint64_t submission,
+                                            ribn_amd_serving_outcome *outcomes, size_t count, int32_t *ready);
+/* release_inference_state (serving.rs:1018-1038): frees the state's physical
+ * KV now, or when the last pending submission using it completes. Missing
+ * state is a no-op; refused while a failed drain keeps ownership uncertain. */
+ribn_amd_status ribn_amd_serving_release_state(ribn_amd_serving *serving, uint64_t state);
+
+/* Introspection: pending submissions, materialized states, device bytes held
+ * by states (in use and kept for reuse), a state's physical position. */
+size_t ribn_amd_serving_pending(const ribn_amd_serving *serving);
+size_t ribn_amd_serving_state_count(const ribn_amd_serving *serving);
+uint64_t ribn_amd_serving_state_bytes(const ribn_amd_serving *serving, uint64_t *reusable_bytes);
+ribn_amd_status ribn_amd_serving_state_position(const ribn_amd_serving *serving, uint64_t state,
+                                                uint32_t *position);
+
+/* Host-only scheduling rules (no device access).
+ * chunked_prefix_len (serving.rs:111-118): the leading tokens of a prefill of
+ * `token_count` tokens that run as whole chunks of `members`; a sampling
+ * prefill keeps its last token serial. */
+uint32_t ribn_amd_serving_chunked_prefix_len(uint32_t token_count, uint32_t members, int32_t requests_sampling);
+/* decode_group (serving.rs:520-550): the rows, from `first` on, that run as one
+ * decode lane with row `first` (single-token sampling decode rows with a
+ * token, a logical position and a KV state of the same spec as `first`'s,
+ * not yet scheduled, at most `max_members`), in row order; just `first` when
+ * it is not eligible. Writes indices to out (capacity count), returns how
+ * many. */
+size_t ribn_amd_serving_decode_group(const ribn_amd_serving_row *rows, size_t count, const uint8_t *scheduled,
+                                     size_t first, size_t max_members, size_t *out);
+
+/* Loading-time memory plan (crates/qwen/src/loading.rs:117-132, 200-213):
+ * continuation = per_sequence_state_bytes * max_sequences (or the given
+ * override when nonzero); available = free - continuation - headroom;
+ * the weight budget is `requested_weight_budget` (0: all available), and it
+ * must be nonzero and within the available bytes. */
+typedef struct ribn_amd_memory_plan {
+    uint64_t free_before_preparation_bytes;
+    uint64_t weight_budget_bytes;
+    uint64_t reserved_sequence_bytes;
+} ribn_amd_memory_plan;
+ribn_amd_status ribn_amd_plan_memory(ribn_amd_context *ctx, uint64_t per_sequence_state_bytes,
+                                     uint64_t max_sequences, uint64_t continuation_override,
+                                     uint64_t headroom_bytes, uint64_t requested_weight_budget,
+                                     ribn_amd_memory_plan *out);
+/* KvStateSpec::byte_size (crates/core/src/state.rs:112-119) of a Qwen3
+ * sequence of `tokens`: layers * kv_heads * head_dim * tokens * 2 (K and V)
+ * * 2 bytes (f16). 147,456 bytes per token at Qwen3-8B geometry. */
+uint64_t ribn_amd_qwen3_kv_bytes(const ribn_amd_qwen3_config *config, uint32_t tokens);
 
 #ifdef __cplusplus
 }

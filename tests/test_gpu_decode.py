@@ -10,9 +10,12 @@ Bars (the oracle is oracle/kquant_oracle.c + oracle/qwen3_oracle.py):
     prompt and greedy steps (the k-quant GEMV, the f16 cache and the online
     softmax each round differently from the sequential f32 oracle), greedy
     tokens equal wherever the oracle's top-2 margin exceeds the error;
-  * graph replays bit-identical to direct launches, batch members equal to
-    single-sequence steps (bit for bit on the wave GEMV, within the GEMV bar
-    where 3+ members take the matrix cores), generate() equal to stepping.
+  * graph replays bit-identical to direct launches (one capture replayed for
+    every cache), batch members equal to single-sequence steps (bit for bit
+    on the wave GEMV, within the GEMV bar where the matrix cores serve),
+    generate() equal to stepping;
+  * a prefill chunk equal to serial prefill steps (bit for bit on the wave
+    GEMV, within the GEMV bar on the matrix cores).
 """
 import ctypes
 
@@ -369,6 +372,100 @@ def test_batch_members_equal_single_sequences(env):
             nxt_s[m] = sel_b[m]
         nxt_b = sel_b
         pos = [p + 1 for p in pos]
+
+
+def _cache_bytes(env, cache, layers, kv_heads):
+    lib, ctx = env["ctx"]._lib, env["ctx"]
+    out = []
+    for layer in range(layers):
+        for ptr in cache.layer(layer):
+            full = np.zeros((kv_heads, cache.capacity(), 128), np.uint16)
+            assert lib.ribn_amd_memcpy_dtoh(ctx.handle, full.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr),
+                                            full.nbytes) == 0
+            out.append(full)
+    return out
+
+
+@pytest.mark.parametrize("chunk", [4, 8, 12])
+def test_prefill_chunk_equals_serial_prefill(env, chunk):
+    """A prefill chunk (consecutive tokens of one sequence as one step's
+    members, K/V appended before attention) against serial prefill_step:
+    bit-equal caches and next-step logits where every GEMV takes the wave
+    path (4 members), within the GEMV bar where the matrix cores serve the
+    FFN down (8) or every GEMV (12, also two attention launch groups)."""
+    print_case(test="prefill_chunk", chunk=chunk)
+    E = env["E"]
+    w = small_weights(TINY, 310)
+    dec = build_decoder(env, TINY, w, max_members=chunk)
+    prompt = [(37 * i + 5) % TINY["vocab"] for i in range(2 * chunk + 3)]
+    a = E.AmdKvCache(env["ctx"], config(env, TINY), 96)
+    b = E.AmdKvCache(env["ctx"], config(env, TINY), 96)
+    # chunked: two whole chunks, then the remainder serially
+    for c0 in (0, chunk):
+        dec.prefill_chunk(a, prompt[c0:c0 + chunk], c0)
+    for i in range(2 * chunk, len(prompt) - 1):
+        dec.prefill_step(a, prompt[i], i)
+    for i in range(len(prompt) - 1):
+        dec.prefill_step(b, prompt[i], i)
+    last = len(prompt) - 1
+    sel_a = dec.decode_step(a, prompt[-1], last)
+    la = dec.copy_logits(0)
+    sel_b = dec.decode_step(b, prompt[-1], last)
+    lb = dec.copy_logits(0)
+    ca = _cache_bytes(env, a, TINY["layers"], TINY["kv_heads"])
+    cb = _cache_bytes(env, b, TINY["layers"], TINY["kv_heads"])
+    exact = not any(mfma_path(t, k, chunk) for t, k in ((12, TINY["hidden"]), (13, TINY["ffn"])))
+    if exact:
+        for x, y in zip(ca, cb):
+            assert np.array_equal(x[:, :len(prompt)], y[:, :len(prompt)])
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        assert sel_a == sel_b
+    else:
+        for x, y in zip(ca, cb):
+            assert _f16_err(x[:, :len(prompt)], y[:, :len(prompt)]) <= 4e-3
+        assert max_rel_err(la, lb) <= 2e-3
+        top = np.sort(lb)[-2:]
+        if top[1] - top[0] > 4e-3 * np.abs(lb).max():
+            assert sel_a == sel_b
+
+
+def test_prefill_chunk_rejects_bad_chunks(env):
+    print_case(test="prefill_chunk_errors")
+    E = env["E"]
+    w = small_weights(TINY, 311)
+    dec = build_decoder(env, TINY, w, max_members=4)
+    cache = E.AmdKvCache(env["ctx"], config(env, TINY), 8)
+    for tokens, pos, kind in (([1], 0, "InputLength"), ([1, 2, 3, 4, 5], 0, "InvalidPlan"),
+                              ([1, 2, 3, 4], 5, "PositionOverflow"), ([1, TINY["vocab"]], 0, "InvalidPlan")):
+        with pytest.raises(E.AmdKernelError) as err:
+            dec.prefill_chunk(cache, tokens, pos)
+        assert err.value.kind == kind, (tokens, pos)
+
+
+def test_one_graph_serves_every_cache(env):
+    """Captured steps hold no cache addresses: stepping several caches with
+    graphs (one capture, replayed for each cache) equals direct launches."""
+    print_case(test="graph_across_caches")
+    E = env["E"]
+    w = small_weights(TINY, 78)
+    dec = build_decoder(env, TINY, w, max_members=2)
+    g = [E.AmdKvCache(env["ctx"], config(env, TINY), 48 + 16 * i) for i in range(3)]
+    d = [E.AmdKvCache(env["ctx"], config(env, TINY), 48 + 16 * i) for i in range(3)]
+    tg, td = [5, 600, 1999], [5, 600, 1999]
+    for pos in range(5):
+        for i in range(3):
+            dec.set_graphs(True)
+            tg[i] = dec.decode_step(g[i], tg[i], pos)
+            lg = dec.copy_logits(0)
+            dec.set_graphs(False)
+            td[i] = dec.decode_step(d[i], td[i], pos)
+            ld = dec.copy_logits(0)
+            assert np.array_equal(lg.view(np.uint32), ld.view(np.uint32)), (pos, i)
+        dec.set_graphs(True)
+        pair = dec.decode_step_batch([g[2], g[0]], [tg[2], tg[0]], [pos + 1, pos + 1])
+        dec.set_graphs(False)
+        assert dec.decode_step_batch([d[2], d[0]], [td[2], td[0]], [pos + 1, pos + 1]) == pair
+    assert tg == td
 
 
 def test_generate_equals_stepping(env):
