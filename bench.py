@@ -527,6 +527,129 @@ def bench_model(E, synth, torch, ctx, step, out_gamma, args):
     }
 
 
+def _pct(values, q):
+    """Nearest-rank percentile."""
+    v = sorted(values)
+    return v[max(0, min(len(v) - 1, int(-(-q * len(v) // 100)) - 1))] if v else None
+
+
+def bench_serving(E, synth, torch, ctx, step, out_gamma, args):
+    """The serving dispatcher under a burst (the reference's qwen_serving_bench
+    burst mode): `concurrency` requests of `prompt_tokens` random prompt ids
+    arrive together; a prefill-first scheduler submits at most
+    `batch_tokens` prompt tokens per batch (prefill segments, the sampling row
+    on each prompt's last segment), then whole decode batches; every batch is
+    one submission polled to completion through AmdBackend. TTFT counts from
+    the burst's arrival; ITL between a request's successive tokens."""
+    import numpy as np
+    from engine_amd import serving as S
+
+    members = max(8, args.prefill_chunk)
+    dec, cfg = build_decoder(E, synth, torch, ctx, step, out_gamma, args.layers, args.seed, members)
+    cap = args.prompt_tokens + args.tokens
+    per_seq = S.qwen3_kv_bytes(cfg, cap)
+    disp = S.AmdServingDispatcher(dec, args.concurrency, kv_budget_bytes=per_seq * args.concurrency)
+    if args.prefill_chunk:
+        disp.with_prefill_chunk(args.prefill_chunk)
+    caps = S.BackendCapabilities("rocm", 0, "rocm", torch.cuda.get_device_properties(0).total_memory)
+    plan = S.ExecutionPlan("qwen3-8b-shaped", "rocm", 0, 1, frozenset((S.Phase.PREFILL, S.Phase.DECODE)))
+    backend = S.AmdBackend(caps, disp)
+    rng = np.random.default_rng(args.seed + 7)
+
+    def run_burst(tokens):
+        reqs = [{"id": 10_000 * (run_burst.n + 1) + i, "prompt": [int(t) for t in rng.integers(0, VOCAB, args.prompt_tokens)],
+                 "done": 0, "out": [], "times": []} for i in range(args.concurrency)]
+        run_burst.n += 1
+        for r in reqs:
+            r["state"] = S.InferenceStateSet(r["id"], kv_tokens=cap)
+        t0 = time.perf_counter()
+        batches = 0
+        while any(len(r["out"]) < tokens for r in reqs):
+            segs, states, owners, budget = [], [], [], args.batch_tokens
+            for r in reqs:
+                left = len(r["prompt"]) - r["done"]
+                if left > 0 and budget > 0:
+                    n = min(left, budget)
+                    last = n == left
+                    segs.append(S.ExecutionSegment(r["id"], S.Phase.PREFILL, n, r["done"],
+                                                   tuple(r["prompt"][r["done"]:r["done"] + n]),
+                                                   S.SamplingParams.greedy() if last else None))
+                    budget -= n
+                    states.append(r["state"])
+                    owners.append(r)
+            if not segs:
+                for r in reqs:
+                    if len(r["out"]) < tokens:
+                        pos = len(r["prompt"]) + len(r["out"]) - 1
+                        segs.append(S.ExecutionSegment(r["id"], S.Phase.DECODE, 1, pos, (r["out"][-1],),
+                                                       S.SamplingParams.greedy()))
+                        states.append(r["state"])
+                        owners.append(r)
+            batch = S.ExecutionBatch(tuple(segs))
+            ev = backend.wait(backend.submit(plan, batch, states))
+            now = time.perf_counter() - t0
+            S.commit_batch(batch, states)
+            batches += 1
+            for r, seg, e in zip(owners, segs, ev.events):
+                if seg.phase == S.Phase.PREFILL:
+                    r["done"] += seg.token_count
+                if e.output_token is not None:
+                    r["out"].append(e.output_token)
+                    r["times"].append(now)
+        wall = time.perf_counter() - t0
+        for r in reqs:
+            backend.release_inference_state(r["state"])
+        return reqs, wall, batches
+
+    run_burst.n = 0
+    log(f"bench serving: warm-up burst ({args.concurrency} x {args.prompt_tokens} prompt tokens, 2 tokens)")
+    run_burst(2)
+    log(f"bench serving: timed burst ({args.concurrency} x {args.prompt_tokens} prompt, {args.tokens} tokens, "
+        f"prefill chunk {args.prefill_chunk or 'off'})")
+    reqs, wall, batches = run_burst(args.tokens)
+    ttft = [r["times"][0] for r in reqs]
+    itl = [b - a for r in reqs for a, b in zip(r["times"], r["times"][1:])]
+    first_all = max(ttft)
+    decode_tokens = sum(len(r["out"]) - 1 for r in reqs)
+    decode_s = wall - first_all
+    out_tokens = sum(len(r["out"]) for r in reqs)
+    prompt_total = args.concurrency * args.prompt_tokens
+    used, reusable = disp.state_bytes()
+    # what 288 GB holds: sequences of the full 4096-token context beside the weights
+    full = E.AmdQwen3Config(layers=36)
+    per4k = S.qwen3_kv_bytes(full, 4096)
+    mem = S.plan_memory(ctx, per4k, 1)
+    fit = (mem.free_before_preparation_bytes - (512 << 20)) // per4k
+    result = {
+        "metric": "Qwen3-8B-shaped serving output tok/s (burst through the serving dispatcher)",
+        "value": round(out_tokens / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": batches, "warmup": 1,
+        "ms_per_step": round(wall * 1e3 / batches, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "i8dot4-f32 GEMV, f16 KV, f32 attention", "data": "synthetic",
+        "config": {"workload": "qwen3-8b-serving-burst", "layers": args.layers, "concurrency": args.concurrency,
+                   "prompt_tokens": args.prompt_tokens, "output_tokens": args.tokens,
+                   "prefill_chunk": args.prefill_chunk, "batch_tokens": args.batch_tokens,
+                   "grouped_decode": False},
+        "serving": {"wall_s": round(wall, 3), "batches": batches,
+                    "prefill_tok_s": round(prompt_total / first_all, 1),
+                    "decode_tok_s": round(decode_tokens / decode_s, 1) if decode_s > 0 else None,
+                    "ttft_ms": {"mean": round(1e3 * sum(ttft) / len(ttft), 1), "p50": round(1e3 * _pct(ttft, 50), 1),
+                                "max": round(1e3 * max(ttft), 1)},
+                    "itl_ms": {"mean": round(1e3 * sum(itl) / len(itl), 3) if itl else None,
+                               "p50": round(1e3 * _pct(itl, 50), 3) if itl else None,
+                               "p99": round(1e3 * _pct(itl, 99), 3) if itl else None,
+                               "max": round(1e3 * max(itl), 3) if itl else None},
+                    "kv_bytes_per_sequence": per_seq, "kv_state_bytes_after_release": [used, reusable]},
+        "memory_288gb": {"free_bytes_now": mem.free_before_preparation_bytes,
+                         "qwen3_8b_kv_bytes_per_token": S.qwen3_kv_bytes(full, 1),
+                         "kv_bytes_per_4096_token_sequence": per4k,
+                         "additional_4096_token_sequences_that_fit": int(fit)},
+        "roofline": None, "cpu_baseline": None,
+    }
+    disp.close()
+    dec.close()
+    return result
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_wave_q4k_gate_up_traffic.md")
 
 
@@ -569,7 +692,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="issue launches eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1", "gguf"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1", "gguf", "serving"),
+                    default="decode",
                     help="decode: BASELINE config 1 (the headline line, default, which also carries the "
                          "config-4 tok/s); batched: config 2 (FFN at M = 1, 4, 16, 64); prefill: config 3 "
                          "(M = 512 bf16 matmuls); model: config 4 alone (full decoder, batch 1 and 8); q8_1: "
@@ -578,6 +702,11 @@ def main():
     ap.add_argument("--context", type=int, default=2048, help="config 4: prompt tokens before generation")
     ap.add_argument("--gen-tokens", type=int, default=128, help="config 4: greedy tokens timed")
     ap.add_argument("--no-model", action="store_true", help="skip the config-4 full-decoder measurement")
+    ap.add_argument("--concurrency", type=int, default=8, help="serving: requests in the burst")
+    ap.add_argument("--prompt-tokens", type=int, default=257, help="serving: prompt tokens per request")
+    ap.add_argument("--tokens", type=int, default=32, help="serving: output tokens per request")
+    ap.add_argument("--prefill-chunk", type=int, default=8, help="serving: prefill chunk members (0: serial)")
+    ap.add_argument("--batch-tokens", type=int, default=128, help="serving: prompt tokens per scheduler batch")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed work, copy a MIB-MiB device buffer three times: a kernel of known "
                          "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE onto bytes")
@@ -612,6 +741,9 @@ def main():
 
     if args.workload == "model":
         print(json.dumps(bench_model(E, synth, torch, ctx, step, out_gamma, args)), flush=True)
+        return
+    if args.workload == "serving":
+        print(json.dumps(bench_serving(E, synth, torch, ctx, step, out_gamma, args)), flush=True)
         return
 
     with torch.cuda.stream(stream):
