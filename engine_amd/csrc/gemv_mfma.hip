@@ -13,14 +13,22 @@
 //    fragments in the MFMA A-operand order (lane = member + 16 * chunk, eight
 //    h bytes then eight l bytes of elements 32g + 8 chunk .. + 7), the block
 //    unscale 2^(e-14) of each member, and u * X_g (X_g = sum of v over group g)
-//    for the minimum term. A workgroup also writes its partial sum of x^2, so
+//    for the minimum term.
+//  - Up to 8 members ("HL" layout): the A operand's 16 rows hold the h digits
+//    of members 0-7 (rows 0-7) and their l digits (rows 8-15), so one MFMA per
+//    group yields both digit sums; 4 x 64 lanes x 16 bytes per block (a lane
+//    record = 8 bytes of group 2p, then 8 of group 2p + 1). The minimum term
+//    rides on the l rows. A workgroup also writes its partial sum of x^2, so
 //    the product applies RMSNorm's 1/rms per member at its output (the wave
 //    GEMV's factorisation: y = (W (x * gamma)) / rms).
 //
 // Product (mfma_gemv_kernel)
 //  - A wave owns R tiles of 16 weight rows over a contiguous range of
-//    super-blocks; the KS waves of a workgroup split K and add their results
-//    in LDS in wave order (deterministic).
+//    super-blocks, loaded through a two-slot ring refilled unconditionally
+//    (blocks past the range load zeros) with the refills pinned between the
+//    slots' MFMAs, so each wait covers one slot; the KS waves of a
+//    workgroup split K and add their results in LDS in wave order
+//    (deterministic).
 //  - Per 32-element k-quant group g, two v_mfma_i32_16x16x32_i8 (h and l
 //    planes; A = activations [member][k], B = quants [k][row]) give the exact
 //    S_g = sum(q v) for 16 members x 16 rows. With the group's scale a_g =
@@ -29,12 +37,16 @@
 //    [member][group] x [group][row] product on v_mfma_f32_16x16x4_f32.
 //  - Lane l holds output rows l % 16 for members 4 (l / 16) .. + 3, so each
 //    lane decodes the scales of one weight row per block.
-// Each member's result depends only on its own activations: a member's output
-// bits do not change with the other members of the batch.
+//  - HL: rows 0-7 and 8-15 of the result are one member's h and l sums; lane
+//    halves combine once at the end (256 h + l).
+// Each member's result depends only on its own activations and on the layout
+// (up to 8 members, or more): a member's output bits do not change with the
+// other members' values.
 #include "kquant_device.hpp"
 #include "kquant_launch.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace ribn_amd {
 
@@ -48,7 +60,7 @@ constexpr int kPackBlocks = 8;           // super-blocks one pack workgroup cove
 constexpr int kFragBlockBytes = 8 * 64 * 16;
 constexpr int kMinBlockBytes = 64 * 8;
 constexpr int kUBlockBytes = 16 * 4;
-constexpr int kMaxWaves = 8;             // K-split waves per workgroup (256 VGPRs each)
+constexpr int kMaxWaves = 4;             // K-split waves per workgroup
 
 __device__ __forceinline__ uint2 load_b64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
@@ -120,7 +132,22 @@ __global__ __launch_bounds__(256) void pack_act16_kernel(PackArgs a) {
     }
     xs += __shfl_xor(xs, 1, 64);
     xs += __shfl_xor(xs, 2, 64);  // X_g over the four chunks of group g
-    if (live) {
+    if (live && a.L.hl) {
+        const size_t blk = (size_t)b;
+        uint8_t* fr = a.act + a.L.frag + (blk * 4 + (g >> 1)) * 1024 + (g & 1) * 8;
+        *reinterpret_cast<uint2*>(fr + (m + 16 * kq) * 16) = make_uint2(hw[0], hw[1]);
+        *reinterpret_cast<uint2*>(fr + (m + 8 + 16 * kq) * 16) = make_uint2(lw[0], lw[1]);
+        if (kq == 0) {
+            float* mina = reinterpret_cast<float*>(a.act + a.L.mina);
+            mina[(blk * 64 + m + 8 + 16 * (g & 3)) * 2 + (g >> 2)] = __builtin_amdgcn_ldexpf((float)xs, ex - 14);
+            mina[(blk * 64 + m + 16 * (g & 3)) * 2 + (g >> 2)] = 0.f;
+        }
+        if (c == 0) {
+            float* ub = reinterpret_cast<float*>(a.act + a.L.ublk);
+            ub[blk * 16 + m] = __builtin_amdgcn_ldexpf(1.0f, ex - 14);
+            ub[blk * 16 + m + 8] = __builtin_amdgcn_ldexpf(1.0f, ex - 14);
+        }
+    } else if (live) {
         const int mt = m >> 4, mi = m & 15;
         const size_t blk = (size_t)mt * nb + b;
         uint4 f;
@@ -187,6 +214,62 @@ __device__ __forceinline__ void load_act(ActBlk& x, __amdgpu_buffer_rsrc_t r, co
     x.u = __builtin_bit_cast(float4, uu);
 }
 
+struct ActBlkHL {
+    uint4 f[4];   // group pairs: 8 bytes of group 2p, then 8 of group 2p + 1
+    float2 mina;  // u X of groups kq and 4 + kq (l rows; zero on h rows)
+    float4 u;     // block unscale of rows 4 kq .. 4 kq + 3
+};
+
+// Lanes whose row belongs to an absent member load nothing.
+__device__ __forceinline__ void load_act_hl(ActBlkHL& x, __amdgpu_buffer_rsrc_t r, const MfmaGemvArgs& A, bool live,
+                                            int b, int lane) {
+    const bool own = live && (lane & 7) < A.members;
+    const uint32_t fb = A.L.frag + ((uint32_t)b * 4u * 64u + (uint32_t)lane) * 16u;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) x.f[p] = load_b128(r, own ? fb + 1024u * p : kOOR);
+    const uint2 mn = load_b64(r, own ? A.L.mina + ((uint32_t)b * 64u + (uint32_t)lane) * 8u : kOOR);
+    x.mina = __builtin_bit_cast(float2, mn);
+    const uint4 uu = load_b128(r, live ? A.L.ublk + ((uint32_t)b * 16u + 4u * (uint32_t)(lane >> 4)) * 4u : kOOR);
+    x.u = __builtin_bit_cast(float4, uu);
+}
+
+// block_mma for the HL layout: one MFMA per group gives the h sums (rows
+// 0-7) and the l sums (rows 8-15) of up to 8 members.
+template <int T>
+__device__ __forceinline__ void block_mma_hl(const WRaw<T>& d, const ActBlkHL& x, int kq, v4f& acc, v4f& macc) {
+    const uint4 h = d.h;
+    const float dd = half_bits_to_float(h.x & 0xffffu);
+    const float dmin = half_bits_to_float(h.x >> 16);
+    const uint32_t lo_sc = h.y & 0x3f3f3f3fu;
+    const uint32_t lo_mn = h.z & 0x3f3f3f3fu;
+    const uint32_t hi_sc = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t hi_mn = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+    const v4i zero = {0, 0, 0, 0};
+    float accb[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        const int p = g >> 1, sh = 4 * (g & 1);
+        uint32_t q0 = (d.q[p].x >> sh) & 0x0f0f0f0fu;
+        uint32_t q1 = (d.q[p].y >> sh) & 0x0f0f0f0fu;
+        if constexpr (T == kQ5K) {
+            q0 |= ((d.qh.x >> g) & 0x01010101u) << 4;
+            q1 |= ((d.qh.y >> g) & 0x01010101u) << 4;
+        }
+        const long av = (g & 1) ? as_long(x.f[p].z, x.f[p].w) : as_long(x.f[p].x, x.f[p].y);
+        const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, as_long(q0, q1), zero, 0, 0, 0);
+        const uint32_t scw = g < 4 ? lo_sc : hi_sc;
+        const float a_g = dd * (float)((scw >> (8 * (g & 3))) & 0xffu);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) accb[t] = __builtin_fmaf(a_g, (float)c[t], accb[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = __builtin_fmaf(x.u[t], accb[t], acc[t]);
+    const float b0 = dmin * (float)((lo_mn >> (8 * kq)) & 0xffu);
+    const float b1 = dmin * (float)((hi_mn >> (8 * kq)) & 0xffu);
+    macc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.mina.x, b0, macc, 0, 0, 0);
+    macc = __builtin_amdgcn_mfma_f32_16x16x4f32(x.mina.y, b1, macc, 0, 0, 0);
+}
+
 template <int T>
 __device__ __forceinline__ void block_mma(const WRaw<T>& d, const ActBlk& x, int kq, v4f& acc, v4f& macc) {
     const uint4 h = d.h;
@@ -230,7 +313,7 @@ __device__ __forceinline__ void block_mma(const WRaw<T>& d, const ActBlk& x, int
 // the super-blocks [nb w / KS, nb (w + 1) / KS) of K with a two-slot ring of
 // (R tiles x one super-block) units, and the waves' partial sums meet in LDS
 // in wave order.
-template <int T, int R, bool PAIR>
+template <int T, int R, bool PAIR, bool HL>
 __global__ __launch_bounds__(512) void mfma_gemv_kernel(MfmaGemvArgs A) {
     constexpr int BB = BlockTraits<T>::bytes;
     constexpr int NBUF = 2;
@@ -293,23 +376,51 @@ __global__ __launch_bounds__(512) void mfma_gemv_kernel(MfmaGemvArgs A) {
         macc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
     }
     WRaw<T> ring[NBUF][R];
-    ActBlk act[NBUF];
+    using ActT = typename std::conditional<HL, ActBlkHL, ActBlk>::type;
+    ActT act[NBUF];
     auto fill = [&](int s, int b) {
         const bool lb = b < kb1;
 #pragma unroll
         for (int i = 0; i < R; ++i) load_w<T>(ring[s][i], wr[i], lb && live_row[i], rowoff[i] + (uint32_t)b * BB, kq);
-        load_act(act[s], ar, A, lb, b, lane);
+        if constexpr (HL) {
+            load_act_hl(act[s], ar, A, lb, b, lane);
+        } else {
+            load_act(act[s], ar, A, lb, b, lane);
+        }
+    };
+    auto mma = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            if constexpr (HL) {
+                block_mma_hl<T>(ring[s][i], act[s], kq, acc[i], macc[i]);
+            } else {
+                block_mma<T>(ring[s][i], act[s], kq, acc[i], macc[i]);
+            }
+        }
     };
 #pragma unroll
     for (int s = 0; s < NBUF; ++s) fill(s, kb0 + s);
-    for (int b = kb0; b < kb1; b += NBUF) {
+    // Passes of NBUF blocks. Refills are unconditional (past the range they
+    // load zeros) and pinned between the slots' MFMAs, so the loads behind a
+    // slot are always the same and its wait covers that slot only; a
+    // conditional refill made the compiler wait for every load at the top of
+    // each pass. The last pass refills nothing.
+    const int passes = (kb1 - kb0 + NBUF - 1) / NBUF;
+    int bp = kb0;
+    for (int pass = 0; pass + 1 < passes; ++pass, bp += NBUF) {
 #pragma unroll
         for (int s = 0; s < NBUF; ++s) {
-            if (b + s < kb1) {
+            mma(s);
+            __builtin_amdgcn_sched_barrier(0);
+            fill(s, bp + s + NBUF);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (passes > 0) {
+        const int left = kb1 - bp;
 #pragma unroll
-                for (int i = 0; i < R; ++i) block_mma<T>(ring[s][i], act[s], kq, acc[i], macc[i]);
-                fill(s, b + s + NBUF);
-            }
+        for (int s = 0; s < NBUF; ++s) {
+            if (s < left) mma(s);
         }
     }
 
@@ -333,12 +444,24 @@ __global__ __launch_bounds__(512) void mfma_gemv_kernel(MfmaGemvArgs A) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) v[i][t] += red[((w - 1) * R + i) * 256 + t * 64 + lane];
     }
+    // HL: lanes 0-31 hold the h sums of members 4 kq + t, lanes 32-63 the l
+    // sums of the same members
+    const bool out_lane = !HL || kq < 2;
+    if constexpr (HL) {
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float lo = __shfl_xor(v[i][t], 32, 64);
+                v[i][t] = __builtin_fmaf(256.0f, v[i][t], lo);
+            }
+    }
     float inv[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         inv[t] = 1.f;
         const int mem = 4 * kq + t;
-        if (A.has_norm && mem < A.members) {
+        if (A.has_norm && out_lane && mem < A.members) {
             const float* ssq = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(A.act) + A.L.ssq);
             float total = 0.f;
             for (int p = 0; p < A.L.parts; ++p) total += ssq[mem * A.L.parts + p];
@@ -366,7 +489,7 @@ __global__ __launch_bounds__(512) void mfma_gemv_kernel(MfmaGemvArgs A) {
                 const float up = v[i + R / 2][t] * inv[t];
                 // silu(gate) * up, in the reference's operation order (model_ops.rs:316-328)
                 const float out = (gt / (1.0f + expf(-gt))) * up;
-                const bool ok = live_row[i] && mem < A.members;
+                const bool ok = out_lane && live_row[i] && mem < A.members;
                 put(out, yr, ok ? (uint32_t)(mem * ffn + local0[i] + rl) * 4u : kOOR);
             }
         }
@@ -383,7 +506,7 @@ __global__ __launch_bounds__(512) void mfma_gemv_kernel(MfmaGemvArgs A) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int mem = 4 * kq + t;
-                const bool ok = live_row[i] && mem < A.members;
+                const bool ok = out_lane && live_row[i] && mem < A.members;
                 put(v[i][t] * inv[t], yr, ok ? (uint32_t)(mem * rows_mat[i] + local0[i] + rl) * 4u : kOOR);
             }
         }
@@ -393,8 +516,13 @@ __global__ __launch_bounds__(512) void mfma_gemv_kernel(MfmaGemvArgs A) {
 template <int T, int R, bool PAIR>
 hipError_t launch_shape(const MfmaGemvArgs& a, int groups, int ks, hipStream_t stream) {
     const size_t lds = (size_t)(ks - 1) * R * 256 * sizeof(float);
-    hipLaunchKernelGGL((mfma_gemv_kernel<T, R, PAIR>), dim3((unsigned)groups), dim3((unsigned)(64 * ks)), lds,
-                       stream, a);
+    if (a.L.hl) {
+        hipLaunchKernelGGL((mfma_gemv_kernel<T, R, PAIR, true>), dim3((unsigned)groups), dim3((unsigned)(64 * ks)),
+                           lds, stream, a);
+    } else {
+        hipLaunchKernelGGL((mfma_gemv_kernel<T, R, PAIR, false>), dim3((unsigned)groups), dim3((unsigned)(64 * ks)),
+                           lds, stream, a);
+    }
     return hipGetLastError();
 }
 
@@ -403,17 +531,16 @@ hipError_t launch_t(const MfmaGemvArgs& a, hipStream_t stream) {
     const int nb = a.K >> 8;
     const bool pair = a.pair_swiglu != 0;
     const int tiles = pair ? (a.rows_end[0] + 15) / 16 : (a.total_rows + 15) / 16;
-    const int r = pair ? 4 : (tiles >= 2048 && T == kQ4K ? 4 : 2);  // Q5_K x 4 tiles would spill
-    const int per_group = pair ? r / 2 : r;
-    const int groups = (tiles + per_group - 1) / per_group;
+    // One tile per wave (a gate tile and its up tile for pairs): from sweeps on
+    // MI355X over tiles per wave {1, 2, 4}, K splits {1, 2, 4, 8} and ring
+    // depths {2, 3, 4} at 4, 8 and 16 members, the widest grid won.
+    const int groups = tiles;
     // The K split depends on K alone, so a row's summation order (and bits)
-    // is the same in every launch shape: grouped or not, any member count.
+    // is the same in every launch shape of a layout: grouped or not, any
+    // member count up to 8, or any from 9 to 16.
     const int ks = std::min(kMaxWaves, std::max(1, nb / 2));
-    if (pair) return launch_shape<T, 4, true>(a, groups, ks, stream);
-    if constexpr (T == kQ4K) {
-        if (r == 4) return launch_shape<T, 4, false>(a, groups, ks, stream);
-    }
-    return launch_shape<T, 2, false>(a, groups, ks, stream);
+    if (pair) return launch_shape<T, 2, true>(a, groups, ks, stream);
+    return launch_shape<T, 1, false>(a, groups, ks, stream);
 }
 
 bool rows_tile_aligned(const WaveGemvArgs& a) {
@@ -432,9 +559,10 @@ Act16Layout act16_layout(int members, int K) {
     const int tiles = (members + 15) / 16;
     L.nb = nb;
     L.parts = (nb + kPackBlocks - 1) / kPackBlocks;
+    L.hl = members <= 8 ? 1 : 0;
     const uint32_t blocks = (uint32_t)tiles * (uint32_t)nb;
     L.frag = 0;
-    L.mina = L.frag + blocks * kFragBlockBytes;
+    L.mina = L.frag + blocks * (L.hl ? kFragBlockBytes / 2 : kFragBlockBytes);
     L.ublk = L.mina + blocks * kMinBlockBytes;
     L.ssq = L.ublk + blocks * kUBlockBytes;
     L.total = L.ssq + (uint32_t)members * (uint32_t)L.parts * 4u;
@@ -491,12 +619,11 @@ int gemv_launch_members(int value_type, int K, bool swiglu_prologue) {
 }
 
 hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch, int cu_count, hipStream_t stream) {
-    // Measured on MI355X: the matrix cores win where the wave GEMV would need
-    // several launches (more than kWaveMaxMembers members; K beyond one slice,
-    // where it takes two members per launch, from kMfmaMinMembers members);
-    // up to 8 members of K <= 4096 stay on the wave GEMV, which matches or
-    // beats them there.
-    const bool wanted = a.members > kWaveMaxMembers || (a.K > kSliceK && a.members >= kMfmaMinMembers);
+    // Measured on MI355X over the Qwen3-8B projections: the matrix cores win
+    // from kMfmaMinMembers members (the wave GEMV's member-serial passes are
+    // VALU-bound there), and from kMfmaMinMembersLongK where K spans several
+    // slices (the wave GEMV then takes two members per launch).
+    const bool wanted = a.members >= kMfmaMinMembers || (a.K > kSliceK && a.members >= kMfmaMinMembersLongK);
     const bool mfma = wanted && a.members <= kMfmaMaxMembers && a.x2 == nullptr && act_scratch != nullptr &&
                       gemv_mfma_supported(value_type) && a.K % 256 == 0 && a.K <= kWaveMaxK && rows_tile_aligned(a);
     if (!mfma) {

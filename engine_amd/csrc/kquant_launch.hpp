@@ -53,9 +53,11 @@ int wave_max_members(int K);
 // ---- batched GEMV on the int8 matrix cores (gemv_mfma.hip), up to 16 members
 
 constexpr int kMfmaMaxMembers = 16;
-// Below this many members a K spanning several slices stays on the wave GEMV
-// (two members per launch), which is faster there.
-constexpr int kMfmaMinMembers = 6;
+// From this many members the matrix cores beat the wave GEMV (measured on
+// MI355X over the Qwen3-8B projections); a K spanning several slices, where
+// the wave GEMV takes two members per launch, from kMfmaMinMembersLongK.
+constexpr int kMfmaMinMembers = 5;
+constexpr int kMfmaMinMembersLongK = 4;
 
 // Byte offsets of the packed activations of `members` x K (K a multiple of
 // 256): MFMA fragments, per-group minimum-term inputs, per-block unscales and
@@ -64,6 +66,7 @@ struct Act16Layout {
     uint32_t frag, mina, ublk, ssq, total;
     int nb;     // super-blocks of K
     int parts;  // pack workgroups per member (partial sums of squares)
+    int hl;     // up to 8 members: each fragment holds high digits in rows 0-7, low digits in rows 8-15
 };
 Act16Layout act16_layout(int members, int K);
 

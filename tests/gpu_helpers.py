@@ -8,9 +8,9 @@ RTOL = 1e-3
 
 def mfma_path(t, k, members):
     """Whether a batched GEMV of this shape runs on the matrix cores
-    (engine_amd/csrc/gemv_mfma.hip launch_gemv): Q4_K / Q5_K with 9..16
-    members, or 6..16 members when K spans more than one 4096 slice."""
-    return t in (12, 13) and members <= 16 and (members > 8 or (k > 4096 and members >= 6))
+    (engine_amd/csrc/gemv_mfma.hip launch_gemv): Q4_K / Q5_K with 5..16
+    members, or 4..16 members when K spans more than one 4096 slice."""
+    return t in (12, 13) and members <= 16 and (members >= 5 or (k > 4096 and members >= 4))
 
 
 def max_rel_err(got, ref):

@@ -386,13 +386,13 @@ def _cache_bytes(env, cache, layers, kv_heads):
     return out
 
 
-@pytest.mark.parametrize("chunk", [4, 8, 12])
+@pytest.mark.parametrize("chunk", [3, 4, 8, 12])
 def test_prefill_chunk_equals_serial_prefill(env, chunk):
     """A prefill chunk (consecutive tokens of one sequence as one step's
     members, K/V appended before attention) against serial prefill_step:
     bit-equal caches and next-step logits where every GEMV takes the wave
-    path (4 members), within the GEMV bar where the matrix cores serve the
-    FFN down (8) or every GEMV (12, also two attention launch groups)."""
+    path (3 members), within the GEMV bar where the matrix cores serve the
+    FFN down (4) or every GEMV (8; 12, also two attention launch groups)."""
     print_case(test="prefill_chunk", chunk=chunk)
     E = env["E"]
     w = small_weights(TINY, 310)

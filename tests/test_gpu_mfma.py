@@ -1,13 +1,16 @@
 """GPU parity tests of the batched matrix-core GEMV (engine_amd/csrc/gemv_mfma.hip),
-which serves Q4_K / Q5_K batches of 9..16 members (6..16 when K spans more
+which serves Q4_K / Q5_K batches of 5..16 members (4..16 when K spans more
 than one 4096 slice) through the same C-ABI entry points as the wave GEMV
 (execute_warp_batch, execute_rms_norm, execute_group, execute_fused,
-execute_gate_up_swiglu). Every case asserts that it takes that path.
+execute_gate_up_swiglu). Every case asserts that it takes that path. Up to 8
+members use the packed digit-plane layout (high digits in rows 0-7, low
+digits in rows 8-15 of one fragment); 9..16 the two-plane layout.
 
 Bars: every member's rows within max relative error 1e-3 (normwise,
-gpu_helpers.RTOL) of the f32-accumulated oracle; a member's output bits do not
-depend on the other members of the batch (checked by permuting and
-sub-setting batches); the residual form equals store-then-add bit for bit.
+gpu_helpers.RTOL) of the f32-accumulated oracle; within a layout, a member's
+output bits do not depend on the other members of the batch (checked by
+permuting and sub-setting batches); the residual form equals store-then-add
+bit for bit.
 """
 import numpy as np
 import pytest
@@ -55,8 +58,12 @@ def oracle_rows(t, enc, k, n, x, gamma=None):
     (12, 1024, 33, 10, True),      # partial tile (rows 32..32 live)
     (12, 4096, 1024, 12, True),
     (12, 4096, 4096, 16, False),   # a full member tile
-    (13, 12288, 4096, 8, False),   # down projection at batch 8 (48 blocks, 8-way K split)
+    (13, 12288, 4096, 8, False),   # down projection at batch 8 (48 blocks, 4-way K split, packed digits)
     (13, 12288, 300, 6, True),
+    (13, 12288, 4096, 4, False),   # four members, long K
+    (12, 4096, 6144, 5, True),     # q/k/v-sized at five members
+    (12, 4096, 4096, 8, True),     # batch 8, packed digits
+    (12, 256, 16, 7, False),       # one super-block, packed digits
     (13, 2048, 100, 13, True),
     (12, 16384, 48, 7, False),     # the largest K
     (12, 4096, 12288, 9, True),    # four-tile row groups (>= 2048 tiles)
@@ -77,6 +84,30 @@ def test_batched_matches_oracle(env, t, k, n, members, norm):
     ref = oracle_rows(t, enc, k, n, x, gamma)
     for m in range(members):
         assert max_rel_err(got[m], ref[m]) <= RTOL, m
+
+
+@pytest.mark.parametrize("t", (12, 13))
+def test_packed_digit_members_do_not_depend_on_the_batch(env, t):
+    """Up to 8 members (packed digit planes): reversed order and a 5-member
+    subset give the same bits per member."""
+    print_case(test="mfma_hl_independence", t=t)
+    k, n, members = 4096, 512, 8
+    enc = synth.kquant_numpy(t, k, n, seed=190 + t)
+    w = upload(env, t, k, n, enc)
+    x = synth.activations_numpy(k, members, seed=33)
+    y = empty_dev(members * n)
+    env["k"][t].execute_warp_batch(w, to_dev(x.reshape(-1)), y, members)
+    full = to_host(y, env["ctx"]).reshape(members, n)
+    rev = empty_dev(members * n)
+    env["k"][t].execute_warp_batch(w, to_dev(x[::-1].reshape(-1)), rev, members)
+    assert np.array_equal(to_host(rev, env["ctx"]).reshape(members, n)[::-1].view(np.uint32), full.view(np.uint32))
+    pick = [6, 0, 3, 7, 2]
+    assert mfma_path(t, k, members) and mfma_path(t, k, len(pick))
+    sub = empty_dev(len(pick) * n)
+    env["k"][t].execute_warp_batch(w, to_dev(x[pick].reshape(-1)), sub, len(pick))
+    assert np.array_equal(to_host(sub, env["ctx"]).reshape(len(pick), n).view(np.uint32), full[pick].view(np.uint32))
+    for m in range(members):
+        assert max_rel_err(full[m], O.quant_gemv(t, enc, k, n, x[m], threads=8)) <= RTOL, m
 
 
 @pytest.mark.parametrize("t", (12, 13))

@@ -9,7 +9,7 @@ same way):
     batched step, several submissions in flight) equal direct steps with the
     same member counts;
   * the prefill-chunk lane equals serial prefill (bit for bit here: every
-    GEMV of the 4-member chunk takes the wave path);
+    GEMV of the 3-member chunk takes the wave path);
   * grouped decode of a mixed batch equals the direct batched step of the
     group plus the serial row;
   * release is deferred while a submission uses the state, caches are
@@ -182,7 +182,7 @@ def test_prefill_chunk_lane_equals_serial_prefill(env):
     print_case(test="serving_prefill_chunk")
     prompt = [(53 * i + 11) % TINY["vocab"] for i in range(11)]
     got = []
-    for chunk in (0, 4):
+    for chunk in (0, 3):
         disp = S.AmdServingDispatcher(env["dec"], 4).with_prefill_chunk(chunk)
         r = Request(prompt)
         run(disp, [r], [r.prefill()], submission=1)
