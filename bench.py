@@ -268,8 +268,9 @@ def _graph_time_us(torch, stream, fn, reps):
 
 def bench_batched(E, synth, torch, args):
     """the Qwen3-8B FFN (gate/up Q4_K 4096->12288, down Q5_K 12288->4096)
-    for M tokens. M <= 8 runs the weights-read-once wave GEMV (gate/up as one grouped launch);
-    larger M the matrix-core path. Activations are synthetic f32 ~N(0,1)."""
+    for M tokens. M <= 16 runs the decode step's batched GEMV entry points (gate/up as one
+    grouped launch), which take the wave GEMV below 5 members (4 for down's long K) and the
+    matrix-core GEMV above; M = 64 the prefill matmul. Activations are synthetic f32 ~N(0,1)."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream()
     ctx = E.AmdContext(0, stream=stream)
@@ -286,12 +287,13 @@ def bench_batched(E, synth, torch, args):
     k4, k5 = E.AmdQ4KGemv.from_context(ctx), E.AmdQ5KGemv.from_context(ctx)
     wbytes = 2 * (FFN * HIDDEN // 256 * 144) + HIDDEN * FFN // 256 * 176
     per_m = {}
-    for m in (1, 4, 16, 64):
+    for m in (1, 4, 8, 16, 64):
         x = torch.randn(m, HIDDEN, device=dev, generator=gen)
         h = torch.randn(m, FFN, device=dev, generator=gen)
         g, u, d = (torch.empty(m * n, device=dev) for n in (FFN, FFN, HIDDEN))
-        if m <= 8:
-            path = "wave GEMV (weights read once per launch)"
+        if m <= 16:
+            path = ("wave GEMV" if m < 4 else "wave GEMV gate/up, matrix-core GEMV down" if m < 5
+                    else "matrix-core GEMV") + " (weights read once per launch)"
 
             def fn():
                 for ly in layers:
@@ -315,7 +317,8 @@ def bench_batched(E, synth, torch, args):
         "metric": "batched decode FFN throughput (BASELINE config 2), tokens/s at M=64",
         "value": top["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(top["us_per_ffn"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "i8dot4-f32 (M<=8), f16-mfma-f32 (M>8)", "data": "synthetic",
+        "vs_baseline": None, "dtype": "i8dot4-f32 (M<5), i8-mfma-i32/f32 (5<=M<=16), f16-mfma-f32 (M=64)",
+        "data": "synthetic",
         "config": {"workload": "qwen3-8b-ffn-batched", "ffn_weight_bytes": wbytes, "layers_cycled": n_layers,
                    "per_m": per_m},
         "roofline": {"bound": "hbm", "achieved": per_m[1]["weight_GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
