@@ -176,12 +176,25 @@ __global__ __launch_bounds__(256) void pack_act16_kernel(PackArgs a) {
 template <int T> struct WRaw;
 template <> struct WRaw<kQ4K> { uint4 h; uint2 q[4]; };
 template <> struct WRaw<kQ5K> { uint4 h; uint2 qh; uint2 q[4]; };
+// Q6_K: the 16 int8 scales, d, and for each half n the 8 low-nibble bytes of
+// both 32-byte quadrant pairs (ql[2n], ql[2n + 1]) and the 8 qh bytes.
+template <> struct WRaw<kQ6K> { uint4 sc; uint32_t d16; uint2 ql[4]; uint2 qh[2]; };
 
 // One lane's bytes of a 16-row tile's super-block: the 16-byte header (d,
 // dmin, packed scales) and, for each group pair p, the 8 quant bytes of
 // elements 8 kq .. 8 kq + 7 (low nibbles: group 2p, high: 2p + 1).
 template <int T>
 __device__ __forceinline__ void load_w(WRaw<T>& d, __amdgpu_buffer_rsrc_t r, bool live, uint32_t base, int kq) {
+    if constexpr (T == kQ6K) {
+        // block: ql[128] at 0, qh[64] at 128, scales[16] at 192, d at 208
+        d.sc = load_b128(r, live ? base + 192u : kOOR);
+        d.d16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, live ? (int)(base + 208u) : (int)kOOR, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d.ql[i] = load_b64(r, live ? base + 32u * i + 8u * kq : kOOR);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) d.qh[n] = load_b64(r, live ? base + 128u + 32u * n + 8u * kq : kOOR);
+        return;
+    } else {
     d.h = load_b128(r, live ? base : kOOR);
     if constexpr (T == kQ5K) {
         d.qh = load_b64(r, live ? base + 16u + 8u * kq : kOOR);
@@ -191,6 +204,76 @@ __device__ __forceinline__ void load_w(WRaw<T>& d, __amdgpu_buffer_rsrc_t r, boo
 #pragma unroll
         for (int p = 0; p < 4; ++p) d.q[p] = load_b64(r, live ? base + 16u + 32u * p + 8u * kq : kOOR);
     }
+    }
+}
+
+// Q6_K quants of 32-element group g (half n = g / 4, quadrant t = g % 4,
+// elements l = 8 kq .. 8 kq + 7 of the quadrant, crates/gguf/src/lib.rs
+// 627-661): low nibble of ql[64 n + 32 (t & 1) + l] (high nibble for t >= 2)
+// and bits 2t, 2t + 1 of qh[32 n + l], minus 32, as signed bytes. The
+// subtraction is carry-free per byte: x = q ^ 32 is q - 32 for q >= 32, and
+// q - 32 + 64 otherwise, which setting bits 6-7 turns into q - 32.
+__device__ __forceinline__ long q6_group(const WRaw<kQ6K>& d, int g) {
+    const int n = g >> 2, t = g & 3;
+    const uint2 lo = d.ql[2 * n + (t & 1)];
+    const uint2 hi = d.qh[n];
+    const int sl = (t >> 1) * 4, sh = 2 * t;
+    uint32_t w[2] = {lo.x, lo.y}, h2[2] = {hi.x, hi.y}, out[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t q = ((w[i] >> sl) & 0x0f0f0f0fu) | (((h2[i] >> sh) & 0x03030303u) << 4);
+        const uint32_t x = q ^ 0x20202020u;
+        out[i] = x | ((x & 0x20202020u) * 6u);
+    }
+    return as_long(out[0], out[1]);
+}
+
+// Q6_K over one super-block: per 32-element group, two MFMAs whose A operand
+// keeps only lanes of one 16-element scale group (k 0..15: lanes kq 0-1;
+// 16..31: kq 2-3), scaled by d * scale in f32. No minimum term. With `hl`,
+// one A plane per MFMA (packed digits); otherwise the h and l planes.
+template <bool HL, class Act>
+__device__ __forceinline__ void block_mma_q6(const WRaw<kQ6K>& d, const Act& x, int kq, v4f& acc) {
+    const float dd = half_bits_to_float(d.d16 & 0xffffu);
+    const uint32_t scw[4] = {d.sc.x, d.sc.y, d.sc.z, d.sc.w};
+    const v4i zero = {0, 0, 0, 0};
+    const bool low_half = kq < 2;
+    float accb[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        const long bq = q6_group(d, g);
+        // scale index 8 n + 2 t + (l / 16): bytes 2g and 2g + 1 of the scales
+        const uint32_t sw = scw[g >> 1] >> (16 * (g & 1));
+        const float s0 = dd * (float)(int8_t)(sw & 0xffu);
+        const float s1 = dd * (float)(int8_t)((sw >> 8) & 0xffu);
+        long a_h, a_l;
+        if constexpr (HL) {
+            const int p = g >> 1;
+            a_h = (g & 1) ? as_long(x.f[p].z, x.f[p].w) : as_long(x.f[p].x, x.f[p].y);
+            a_l = 0;
+        } else {
+            a_h = as_long(x.f[g].x, x.f[g].y);
+            a_l = as_long(x.f[g].z, x.f[g].w);
+        }
+        const long h0 = low_half ? a_h : 0, h1 = low_half ? 0 : a_h;
+        const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(h0, bq, zero, 0, 0, 0);
+        const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(h1, bq, zero, 0, 0, 0);
+        if constexpr (HL) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) accb[t] = __builtin_fmaf(s1, (float)c1[t], __builtin_fmaf(s0, (float)c0[t], accb[t]));
+        } else {
+            const long l0 = low_half ? a_l : 0, l1 = low_half ? 0 : a_l;
+            const v4i e0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(l0, bq, zero, 0, 0, 0);
+            const v4i e1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(l1, bq, zero, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                accb[t] = __builtin_fmaf(s0, (float)(c0[t] * 256 + e0[t]), accb[t]);
+                accb[t] = __builtin_fmaf(s1, (float)(c1[t] * 256 + e1[t]), accb[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = __builtin_fmaf(x.u[t], accb[t], acc[t]);
 }
 
 struct ActBlk {
@@ -391,7 +474,9 @@ __global__ __launch_bounds__(512) void mfma_gemv_kernel(MfmaGemvArgs A) {
     auto mma = [&](int s) {
 #pragma unroll
         for (int i = 0; i < R; ++i) {
-            if constexpr (HL) {
+            if constexpr (T == kQ6K) {
+                block_mma_q6<HL>(ring[s][i], act[s], kq, acc[i]);
+            } else if constexpr (HL) {
                 block_mma_hl<T>(ring[s][i], act[s], kq, acc[i], macc[i]);
             } else {
                 block_mma<T>(ring[s][i], act[s], kq, acc[i], macc[i]);
@@ -569,7 +654,7 @@ Act16Layout act16_layout(int members, int K) {
     return L;
 }
 
-bool gemv_mfma_supported(int value_type) { return value_type == kQ4K || value_type == kQ5K; }
+bool gemv_mfma_supported(int value_type) { return value_type == kQ4K || value_type == kQ5K || value_type == kQ6K; }
 
 hipError_t launch_pack_act16(const float* x, const float* gamma, int members, int K, void* act,
                              hipStream_t stream) {
@@ -601,6 +686,7 @@ hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& a, int /*cu_coun
     switch (value_type) {
     case kQ4K: return launch_t<kQ4K>(a, stream);
     case kQ5K: return launch_t<kQ5K>(a, stream);
+    case kQ6K: return launch_t<kQ6K>(a, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -625,7 +711,8 @@ hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch,
     // slices (the wave GEMV then takes two members per launch).
     const bool wanted = a.members >= kMfmaMinMembers || (a.K > kSliceK && a.members >= kMfmaMinMembersLongK);
     const bool mfma = wanted && a.members <= kMfmaMaxMembers && a.x2 == nullptr && act_scratch != nullptr &&
-                      gemv_mfma_supported(value_type) && a.K % 256 == 0 && a.K <= kWaveMaxK && rows_tile_aligned(a);
+                      gemv_mfma_supported(value_type) && a.K % 256 == 0 && a.K <= kWaveMaxK &&
+                      (rows_tile_aligned(a) || !a.pair_swiglu);
     if (!mfma) {
         // the wave GEMV, in launch groups of as many members as it stages
         int per = std::min(wave_max_members(a.K), kWaveMaxMembers);
@@ -665,7 +752,22 @@ hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch,
     m.eps = a.eps;
     m.accumulate = a.accumulate;
     m.pair_swiglu = a.pair_swiglu;
-    return launch_gemv_mfma(value_type, m, cu_count, stream);
+    if (rows_tile_aligned(a)) return launch_gemv_mfma(value_type, m, cu_count, stream);
+    // a group whose matrices do not end on whole tiles: one launch per matrix
+    // over the shared packed activations, each as its single-matrix call
+    for (int i = 0; i < a.count; ++i) {
+        MfmaGemvArgs one = m;
+        const int start = i > 0 ? a.rows_end[i - 1] : 0;
+        one.w[0] = a.w[i];
+        one.wbytes[0] = a.wbytes[i];
+        one.y[0] = a.y[i];
+        one.rows_end[0] = a.rows_end[i] - start;
+        one.total_rows = one.rows_end[0];
+        one.count = 1;
+        e = launch_gemv_mfma(value_type, one, cu_count, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace ribn_amd

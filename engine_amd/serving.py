@@ -24,7 +24,7 @@ from enum import IntEnum
 from typing import Optional
 
 from . import _lib
-from .kquant import AmdKernelError
+from .kquant import AmdKernelError, _live
 
 NO_POSITION = 0xFFFFFFFF
 
@@ -282,7 +282,9 @@ class AmdServingDispatcher(AmdDispatcher):
         return int(pos.value)
 
     def close(self):
-        if self.handle:
+        # at interpreter exit the handle is leaked, like every other handle of
+        # the package: the HIP runtime may already be torn down
+        if self.handle and _live():
             self._lib.ribn_amd_serving_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 

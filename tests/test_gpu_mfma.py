@@ -1,5 +1,5 @@
 """GPU parity tests of the batched matrix-core GEMV (engine_amd/csrc/gemv_mfma.hip),
-which serves Q4_K / Q5_K batches of 5..16 members (4..16 when K spans more
+which serves Q4_K / Q5_K / Q6_K batches of 5..16 members (4..16 when K spans more
 than one 4096 slice) through the same C-ABI entry points as the wave GEMV
 (execute_warp_batch, execute_rms_norm, execute_group, execute_fused,
 execute_gate_up_swiglu). Every case asserts that it takes that path. Up to 8
@@ -30,7 +30,7 @@ def env():
     assert torch.cuda.is_available(), "GPU tests need a ROCm device"
     ctx = E.AmdContext(0)
     store = E.AmdWeightStore(ctx)
-    kernels = {t: E.QwenGemvKernel.from_value_type(ctx, t) for t in (12, 13)}
+    kernels = {t: E.QwenGemvKernel.from_value_type(ctx, t) for t in (12, 13, 14)}
     return {"E": E, "ctx": ctx, "store": store, "k": kernels, "n": [0]}
 
 
@@ -64,6 +64,9 @@ def oracle_rows(t, enc, k, n, x, gamma=None):
     (12, 4096, 6144, 5, True),     # q/k/v-sized at five members
     (12, 4096, 4096, 8, True),     # batch 8, packed digits
     (12, 256, 16, 7, False),       # one super-block, packed digits
+    (14, 4096, 1024, 8, True),     # Q6_K lm_head-shaped at batch 8, packed digits
+    (14, 4096, 300, 12, False),    # Q6_K, two planes, partial last tile
+    (14, 256, 16, 5, True),        # Q6_K, one super-block
     (13, 2048, 100, 13, True),
     (12, 16384, 48, 7, False),     # the largest K
     (12, 4096, 12288, 9, True),    # four-tile row groups (>= 2048 tiles)
@@ -86,7 +89,7 @@ def test_batched_matches_oracle(env, t, k, n, members, norm):
         assert max_rel_err(got[m], ref[m]) <= RTOL, m
 
 
-@pytest.mark.parametrize("t", (12, 13))
+@pytest.mark.parametrize("t", (12, 13, 14))
 def test_packed_digit_members_do_not_depend_on_the_batch(env, t):
     """Up to 8 members (packed digit planes): reversed order and a 5-member
     subset give the same bits per member."""

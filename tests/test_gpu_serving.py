@@ -330,3 +330,32 @@ def test_memory_plan(env):
     with pytest.raises(S.BackendError) as e:
         S.plan_memory(env["ctx"], 1 << 50, 1)
     assert e.value.status == 37
+
+
+def test_handles_alive_at_interpreter_exit(env):
+    """A dispatcher, decoder and context still referenced when the
+    interpreter exits are leaked, not destroyed after the HIP runtime's own
+    teardown: the process exits cleanly."""
+    import os
+    import subprocess
+    import sys
+    print_case(test="serving_exit")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = "\n".join([
+        "import engine_amd as E",
+        "from engine_amd import serving as S",
+        "from tests.decode_helpers import small_weights",
+        "from tests.test_gpu_serving import TINY, Request, build_decoder, run",
+        "ctx = E.AmdContext(0)",
+        "env = {'E': E, 'ctx': ctx, 'store': E.AmdWeightStore(ctx), 'n': [0]}",
+        "dec = build_decoder(env, small_weights(TINY, 5), max_members=2)",
+        "disp = S.AmdServingDispatcher(dec, 2)",
+        "r = Request([1, 2, 3])",
+        "run(disp, [r], [r.prefill()], submission=1)",
+        "KEEP = (disp, dec, env)",
+        "print('served', r.generated, flush=True)",
+    ])
+    out = subprocess.run([sys.executable, "-c", script], cwd=root, capture_output=True, text=True, timeout=180)
+    assert out.returncode == 0, (out.returncode, out.stdout[-500:], out.stderr[-2000:])
+    assert "served" in out.stdout
+
