@@ -15,7 +15,7 @@ import ctypes
 from dataclasses import dataclass
 
 from . import _lib
-from .kquant import AmdContext, AmdKernelError, AmdQuantizedWeight, _check
+from .kquant import RANK_RESOURCE, AmdContext, AmdKernelError, AmdQuantizedWeight, _check, _own
 
 DEFAULT_BUDGET = 1 << 62
 
@@ -71,6 +71,7 @@ class GgufFile:
         self._lib = _lib.load()
         self.handle = handle
         self._path = path
+        _own(self, RANK_RESOURCE)
 
     @classmethod
     def open(cls, path: str) -> "GgufFile":

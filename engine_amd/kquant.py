@@ -19,6 +19,8 @@ from __future__ import annotations
 
 import atexit
 import ctypes
+import gc
+import weakref
 
 from . import _lib
 
@@ -51,14 +53,36 @@ class AmdWeightError(AmdKernelError):
 
 _SHUTTING_DOWN = [False]
 
+# Live owners of library handles, released in rank order at exit: serving
+# dispatchers, then decoders, KV caches, weights / kernels / GGUF files, and
+# contexts last (each destroy may synchronise its context's stream).
+RANK_DISPATCHER, RANK_DECODER, RANK_CACHE, RANK_RESOURCE, RANK_CONTEXT = range(5)
+_OWNERS = weakref.WeakSet()
 
-def _mark_shutdown():
-    # Handles still alive at interpreter exit are leaked on purpose: releasing
-    # them while the HIP runtime and torch tear down is not ordered.
+
+def _own(obj, rank: int):
+    obj._release_rank = rank
+    _OWNERS.add(obj)
+
+
+def _release_all():
+    """Runs at exit before interpreter finalization, while torch and the HIP
+    runtime are whole. Owners held only by reference cycles (a frame kept by
+    an exception's traceback, say) would otherwise survive to the runtime's
+    own teardown with live graphs, events, streams and pinned memory, which is
+    not ordered against this library's code objects. The collection finalizes
+    those; every owner still referenced is then released in rank order. After
+    this, finalizers no longer call into the library."""
+    gc.collect()
+    for obj in sorted(list(_OWNERS), key=lambda o: o._release_rank):
+        try:
+            obj.close()
+        except Exception:
+            pass
     _SHUTTING_DOWN[0] = True
 
 
-atexit.register(_mark_shutdown)
+atexit.register(_release_all)
 
 
 def _live() -> bool:
@@ -92,6 +116,7 @@ class AmdContext:
         self._lib = lib
         self.handle = handle
         self.device = device
+        _own(self, RANK_CONTEXT)
 
     def synchronize(self):
         _check(self._lib.ribn_amd_context_synchronize(self.handle))
@@ -119,6 +144,7 @@ class AmdQuantizedWeight:
     def __init__(self, ctx: AmdContext, handle, name: str, dims, value_type: int):
         self.ctx = ctx
         self.handle = handle
+        _own(self, RANK_RESOURCE)
         self.name = name
         self.dims = tuple(dims)
         self._value_type = value_type
@@ -221,6 +247,7 @@ class _AmdQuantizedGemv:
         self._lib = ctx._lib
         self.handle = ctypes.c_void_p()
         _check(self._lib.ribn_amd_gemv_create(ctx.handle, value_type, ctypes.byref(self.handle)))
+        _own(self, RANK_RESOURCE)
 
     @classmethod
     def from_context(cls, ctx: AmdContext):
@@ -383,6 +410,7 @@ class _AmdEmbedding:
         self._lib = ctx._lib
         self.handle = ctypes.c_void_p()
         _check(self._lib.ribn_amd_embedding_create(ctx.handle, value_type, ctypes.byref(self.handle)))
+        _own(self, RANK_RESOURCE)
 
     @classmethod
     def from_context(cls, ctx: AmdContext):

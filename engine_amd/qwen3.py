@@ -19,7 +19,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from .kquant import AmdModelKernelError, _check, _live, _ptr
+from .kquant import RANK_CACHE, RANK_DECODER, AmdModelKernelError, _check, _live, _own, _ptr
 
 
 @dataclass(frozen=True)
@@ -52,6 +52,7 @@ class AmdKvCache:
         self.handle = ctypes.c_void_p()
         _check(ctx._lib.ribn_amd_kv_cache_create(ctx.handle, ctypes.byref(self._cfg), capacity,
                                                  ctypes.byref(self.handle)), AmdModelKernelError)
+        _own(self, RANK_CACHE)
 
     def capacity(self) -> int:
         return int(self.ctx._lib.ribn_amd_kv_cache_capacity(self.handle))
@@ -113,6 +114,7 @@ class AmdQwen3Decode:
         _check(ctx._lib.ribn_amd_qwen3_decode_create(ctx.handle, ctypes.byref(self._cfg), token_embd.handle,
                                                      output.handle, _ptr(output_norm), arr, max_members,
                                                      ctypes.byref(self.handle)), AmdModelKernelError)
+        _own(self, RANK_DECODER)
 
     def set_graphs(self, enabled: bool):
         _check(self.ctx._lib.ribn_amd_qwen3_decode_set_graphs(self.handle, 1 if enabled else 0))

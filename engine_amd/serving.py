@@ -24,7 +24,7 @@ from enum import IntEnum
 from typing import Optional
 
 from . import _lib
-from .kquant import AmdKernelError, _live
+from .kquant import RANK_DISPATCHER, AmdKernelError, _live, _own
 
 NO_POSITION = 0xFFFFFFFF
 
@@ -218,6 +218,7 @@ class AmdServingDispatcher(AmdDispatcher):
         self.handle = ctypes.c_void_p()
         _call(self._lib.ribn_amd_serving_create(decoder.handle, max_pending_rows, kv_budget_bytes,
                                                 ctypes.byref(self.handle)))
+        _own(self, RANK_DISPATCHER)
         self._rows = {}
 
     def with_prefill_chunk(self, members: int) -> "AmdServingDispatcher":
@@ -282,8 +283,6 @@ class AmdServingDispatcher(AmdDispatcher):
         return int(pos.value)
 
     def close(self):
-        # at interpreter exit the handle is leaked, like every other handle of
-        # the package: the HIP runtime may already be torn down
         if self.handle and _live():
             self._lib.ribn_amd_serving_destroy(self.handle)
             self.handle = ctypes.c_void_p()
