@@ -11,7 +11,7 @@
 //
 // Work split (split-T "flash decoding"): the grid is (chunk, KV head,
 // member). A workgroup takes one contiguous chunk (at least kMinChunkTokens,
-// at most kAttnChunks chunks per context) of the member's tokens for one KV
+// at most the launch's grid chunks per context) of the member's tokens for one KV
 // head and all q_per_kv query heads that share it, so each K/V byte is read
 // once; workgroups past the context exit. Within the workgroup a 16-lane row
 // of a wave owns one token per step (lane j of the row holds dims 8j..8j+7:
@@ -57,10 +57,21 @@ constexpr int kStepTokens = kWaves * 4;   // tokens a workgroup covers per step
 constexpr int kMinChunkTokens = 64;
 static_assert(kMinChunkTokens % kStepTokens == 0, "chunks are whole steps");
 
-// Tokens per chunk for a context of `tokens`: kMinChunkTokens, or more when
-// the context needs more than kAttnChunks chunks of that size.
-__device__ __forceinline__ int chunk_tokens(int tokens) {
-    int len = (tokens + kAttnChunks - 1) / kAttnChunks;
+// Workgroups an attention launch aims at (a sweep on MI355X over 256, 512,
+// 1024 and 2048 at 1 and 8 members, 2048-token context: 512 was fastest at
+// 8 members, 1 member is unaffected). Past it, a workgroup's fixed work (query
+// norm and rope, the row and wave merges) outweighs its share of the K/V
+// stream and the launch turns VALU-bound.
+constexpr int kAttnTargetGroups = 512;
+// Batches from this size take the batch-dependent chunking (the size from
+// which the matrix-core GEMVs serve the projections as well).
+constexpr int kAttnSplitMembers = 5;
+
+// Tokens per chunk for a context of `tokens` in a launch of `chunks` grid
+// chunks: kMinChunkTokens, or more when the context needs more than `chunks`
+// chunks of that size.
+__device__ __forceinline__ int chunk_tokens(int tokens, int chunks) {
+    int len = (tokens + chunks - 1) / chunks;
     len = len < kMinChunkTokens ? kMinChunkTokens : len;
     return (len + kStepTokens - 1) / kStepTokens * kStepTokens;
 }
@@ -150,7 +161,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 
     const int pos = a.positions[m];
     const int tokens = pos + 1;
-    const int len = chunk_tokens(tokens);
+    const int len = chunk_tokens(tokens, a.chunks);
     const int t0 = chunk * len;
     if (t0 >= tokens) return;  // no tokens in this chunk (uniform over the workgroup)
     const int t1 = min(t0 + len, tokens);
@@ -393,11 +404,11 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(AttnArgs a) {
     const float* part = a.mem[m].partials + (size_t)qh * kAttnChunks * kPartStride;
     float o[kAttnChunks];
 #pragma unroll
-    for (int c = 0; c < kAttnChunks; ++c) o[c] = part[c * kPartStride + d];
-    const float mcv = d < kAttnChunks ? part[d * kPartStride + kHeadDim] : 0.f;
-    const float lcv = d < kAttnChunks ? part[d * kPartStride + kHeadDim + 1] : 0.f;
+    for (int c = 0; c < kAttnChunks; ++c) o[c] = c < a.chunks ? part[c * kPartStride + d] : 0.f;
+    const float mcv = d < a.chunks ? part[d * kPartStride + kHeadDim] : 0.f;
+    const float lcv = d < a.chunks ? part[d * kPartStride + kHeadDim + 1] : 0.f;
     const int tokens = a.positions[m] + 1;
-    const int len = chunk_tokens(tokens);
+    const int len = chunk_tokens(tokens, a.chunks);
     const int chunks = (tokens + len - 1) / len;
     if (chunks <= 1) return;  // the attention launch wrote the output
     if (d < kAttnChunks) {
@@ -515,18 +526,25 @@ hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t strea
         args.chunks < 1 || args.chunks > kAttnChunks || args.mem == nullptr) {
         return hipErrorInvalidValue;
     }
-    const dim3 grid((unsigned)args.chunks, (unsigned)args.kv_heads, (unsigned)members);
-    switch (args.q_heads / args.kv_heads) {
-    case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(kThreads), 0, stream, args); break;
-    case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(kThreads), 0, stream, args); break;
-    case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(kThreads), 0, stream, args); break;
-    case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(kThreads), 0, stream, args); break;
+    // From kAttnSplitMembers members, fewer, longer chunks when (KV heads x
+    // members) already fill the chip. Below it the chunking depends on the
+    // caches' capacity only, so a member's bits equal its single-sequence step.
+    AttnArgs b = args;
+    const int fill = members < kAttnSplitMembers ? kAttnChunks
+                                                 : std::max(1, kAttnTargetGroups / (args.kv_heads * members));
+    b.chunks = std::min(args.chunks, fill);
+    const dim3 grid((unsigned)b.chunks, (unsigned)b.kv_heads, (unsigned)members);
+    switch (b.q_heads / b.kv_heads) {
+    case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(kThreads), 0, stream, b); break;
+    case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(kThreads), 0, stream, b); break;
+    case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(kThreads), 0, stream, b); break;
+    case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(kThreads), 0, stream, b); break;
     default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)args.q_heads, (unsigned)members), dim3(kHeadDim), 0, stream,
-                       args);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)b.q_heads, (unsigned)members), dim3(kHeadDim), 0, stream,
+                       b);
     return hipGetLastError();
 }
 

@@ -9,9 +9,10 @@ namespace ribn_amd {
 
 // Head geometry the attention kernel is built for (Qwen3: 128-wide heads).
 constexpr int kHeadDim = 128;
-// Token chunks per (member, KV head): the work of one workgroup. The count is
-// fixed, so a member's arithmetic does not depend on the batch it runs in and
-// a captured step serves every position.
+// Token chunks per (member, KV head): the work of one workgroup, at most
+// this many. Below 5 members the count depends on the caches' capacity only,
+// so a member's arithmetic does not depend on the batch it runs in; a
+// captured step serves every position either way.
 constexpr int kAttnChunks = 32;
 // Members one attention launch serves (the host splits larger batches).
 constexpr int kAttnMaxMembers = 8;
@@ -33,7 +34,8 @@ struct AttnMember {
 struct AttnArgs {
     const AttnMember* mem;     // device [members] descriptors
     int layer;
-    int chunks;                // grid chunks: ceil(max capacity / 64), at most kAttnChunks
+    int chunks;                // grid chunks: ceil(max capacity / 64), at most kAttnChunks (the launch
+                               // lowers it further when KV heads x members fill the chip)
     int appended;              // 1: every member's K/V is already in its cache (launch_kv_append)
     const float* q;            // [members][q_heads * 128], raw projection
     const float* k;            // [members][kv_heads * 128], raw projection

@@ -197,55 +197,66 @@ def _f16_err(a_bits, b_bits):
 
 @pytest.mark.parametrize("qh,kvh", [(32, 8), (8, 2), (4, 4), (16, 2)])
 def test_attention_matches_oracle(env, qh, kvh):
+    positions = [0, 1, 15, 16, 33, 300, 2047, 2100]
+    for i0 in range(0, len(positions), 3):
+        _check_attention(env, qh, kvh, positions[i0:i0 + 3], i0)
+
+
+@pytest.mark.parametrize("qh,kvh", [(32, 8), (8, 8)])
+def test_attention_eight_members_long_chunks(env, qh, kvh):
+    """Eight members over 8 KV heads fill the chip, so the launch splits each
+    context into at most 8 chunks (272 tokens at position 2100) instead of
+    64-token ones."""
+    _check_attention(env, qh, kvh, [2100, 0, 511, 512, 1000, 63, 2047, 64], 99)
+
+
+def _check_attention(env, qh, kvh, pos_list, seed):
     E = env["E"]
     cfg = dict(layers=1, hidden=qh * 128, q_heads=qh, kv_heads=kvh, head_dim=128, ffn=256, vocab=1,
                rope_base=1.0e6, epsilon=1.0e-6)
     cap = 2200
-    positions = [0, 1, 15, 16, 33, 300, 2047, 2100]
-    for i0 in range(0, len(positions), 3):
-        pos_list = positions[i0:i0 + 3]
-        members = len(pos_list)
-        print_case(test="attention", qh=qh, kvh=kvh, positions=pos_list)
-        caches, orc = [], []
-        qs, ks, vs = [], [], []
-        rng = np.random.default_rng(qh * 1000 + i0)
-        qn = synth.gamma_numpy(128, qh + 1)
-        kn = synth.gamma_numpy(128, qh + 2)
-        for m, pos in enumerate(pos_list):
-            c = E.AmdKvCache(env["ctx"], config(env, cfg), cap)
-            keys = rng.standard_normal((cap, kvh, 128)).astype(np.float16).view(np.uint16)
-            values = rng.standard_normal((cap, kvh, 128)).astype(np.float16).view(np.uint16)
-            _fill_cache(env, c, 0, keys[:pos], values[:pos])
-            caches.append(c)
-            orc.append((keys, values))
-            qs.append(rng.standard_normal(qh * 128).astype(np.float32))
-            ks.append(rng.standard_normal(kvh * 128).astype(np.float32))
-            vs.append(rng.standard_normal(kvh * 128).astype(np.float32) * 4)
-        out = to_dev(np.full(members * qh * 128, np.nan, np.float32))
-        posd = to_dev(np.array(pos_list, np.int32))
-        args = (to_dev(np.concatenate(qs)), to_dev(np.concatenate(ks)), to_dev(np.concatenate(vs)), to_dev(qn),
-                to_dev(kn), posd)
-        E.attention_decode(env["ctx"], config(env, cfg), caches, 0, *args, out)
-        got = to_host(out, env["ctx"]).reshape(members, -1)
-        # a second launch at the same positions repeats the result bit for bit
-        out2 = to_dev(np.full(members * qh * 128, np.nan, np.float32))
-        E.attention_decode(env["ctx"], config(env, cfg), caches, 0, *args, out2)
-        assert np.array_equal(to_host(out2, env["ctx"]).reshape(members, -1).view(np.uint32), got.view(np.uint32))
-        for m, pos in enumerate(pos_list):
-            keys, values = orc[m]
-            kk = np.ascontiguousarray(keys[:pos + 1]).reshape(pos + 1, -1)
-            vv = np.ascontiguousarray(values[:pos + 1]).reshape(pos + 1, -1)
-            ref = O.qwen3_attention(qs[m], ks[m], vs[m], qn, kn, 1e-6, 1e6, qh, kvh, 128, pos, kk, vv)
-            bad = ~np.isfinite(got[m].reshape(qh, 128))
-            assert max_rel_err(got[m], ref) <= RTOL, (m, pos, int(bad.sum()), sorted(set(np.where(bad)[0].tolist())),
-                                                     sorted(set(np.where(bad)[1].tolist()))[:16])
-            krow, vrow = _read_cache_row(env, caches[m], 0, pos, kvh)
-            # V is stored as f16(v) of the same input: bit-exact. K passes
-            # through the norm and the rope, whose angle pos * base^(-2p/128)
-            # moves by an f32 ulp (1.2e-4 rad near pos 2048) between pow
-            # implementations: normwise bound, as for the outputs.
-            assert np.array_equal(vrow.reshape(-1), vv[pos])
-            assert _f16_err(krow.reshape(-1), kk[pos]) <= RTOL, pos
+    members = len(pos_list)
+    print_case(test="attention", qh=qh, kvh=kvh, positions=pos_list)
+    caches, orc = [], []
+    qs, ks, vs = [], [], []
+    rng = np.random.default_rng(qh * 1000 + seed)
+    qn = synth.gamma_numpy(128, qh + 1)
+    kn = synth.gamma_numpy(128, qh + 2)
+    for m, pos in enumerate(pos_list):
+        c = E.AmdKvCache(env["ctx"], config(env, cfg), cap)
+        keys = rng.standard_normal((cap, kvh, 128)).astype(np.float16).view(np.uint16)
+        values = rng.standard_normal((cap, kvh, 128)).astype(np.float16).view(np.uint16)
+        _fill_cache(env, c, 0, keys[:pos], values[:pos])
+        caches.append(c)
+        orc.append((keys, values))
+        qs.append(rng.standard_normal(qh * 128).astype(np.float32))
+        ks.append(rng.standard_normal(kvh * 128).astype(np.float32))
+        vs.append(rng.standard_normal(kvh * 128).astype(np.float32) * 4)
+    out = to_dev(np.full(members * qh * 128, np.nan, np.float32))
+    posd = to_dev(np.array(pos_list, np.int32))
+    args = (to_dev(np.concatenate(qs)), to_dev(np.concatenate(ks)), to_dev(np.concatenate(vs)), to_dev(qn),
+            to_dev(kn), posd)
+    E.attention_decode(env["ctx"], config(env, cfg), caches, 0, *args, out)
+    got = to_host(out, env["ctx"]).reshape(members, -1)
+    # a second launch at the same positions repeats the result bit for bit
+    out2 = to_dev(np.full(members * qh * 128, np.nan, np.float32))
+    E.attention_decode(env["ctx"], config(env, cfg), caches, 0, *args, out2)
+    assert np.array_equal(to_host(out2, env["ctx"]).reshape(members, -1).view(np.uint32), got.view(np.uint32))
+    for m, pos in enumerate(pos_list):
+        keys, values = orc[m]
+        kk = np.ascontiguousarray(keys[:pos + 1]).reshape(pos + 1, -1)
+        vv = np.ascontiguousarray(values[:pos + 1]).reshape(pos + 1, -1)
+        ref = O.qwen3_attention(qs[m], ks[m], vs[m], qn, kn, 1e-6, 1e6, qh, kvh, 128, pos, kk, vv)
+        bad = ~np.isfinite(got[m].reshape(qh, 128))
+        assert max_rel_err(got[m], ref) <= RTOL, (m, pos, int(bad.sum()), sorted(set(np.where(bad)[0].tolist())),
+                                                 sorted(set(np.where(bad)[1].tolist()))[:16])
+        krow, vrow = _read_cache_row(env, caches[m], 0, pos, kvh)
+        # V is stored as f16(v) of the same input: bit-exact. K passes
+        # through the norm and the rope, whose angle pos * base^(-2p/128)
+        # moves by an f32 ulp (1.2e-4 rad near pos 2048) between pow
+        # implementations: normwise bound, as for the outputs.
+        assert np.array_equal(vrow.reshape(-1), vv[pos])
+        assert _f16_err(krow.reshape(-1), kk[pos]) <= RTOL, pos
 
 
 # ---------------------------------------------------------------- argmax
