@@ -77,9 +77,10 @@ def build_model(E, synth, torch, layers, seed):
 class DecodeGemvStep:
     """Issues one step's launches through the C ABI on ctx's stream."""
 
-    def __init__(self, E, torch, ctx, weights, head, out_gamma, acts):
+    def __init__(self, E, torch, ctx, weights, head, out_gamma, acts, mode=0):
         self.store = E.AmdWeightStore(ctx)
         self.kern = {t: E.QwenGemvKernel.from_value_type(ctx, t) for t in (12, 13, 14)}
+        self.set_mode(mode)
         self.layers = []
         for li, lw in enumerate(weights):
             entry = {}
@@ -101,6 +102,10 @@ class DecodeGemvStep:
         gate_up = 2 * (launch_bytes(12, HIDDEN, FFN) - 4 * HIDDEN) + 4 * HIDDEN
         per_layer = qkv + launch_bytes(12, Q_OUT, HIDDEN) + gate_up + launch_bytes(13, FFN, HIDDEN)
         self.bytes_per_step = per_layer * len(weights) + launch_bytes(14, HIDDEN, VOCAB)
+
+    def set_mode(self, mode):
+        for k in self.kern.values():
+            k.set_mode(mode)
 
     def layer(self, entry):
         # q/k/v share the attention-normed input and gate/up the FFN-normed
@@ -179,6 +184,8 @@ def cpu_baseline(seconds_budget=12.0):
 
 
 PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense f16/bf16
+# GEMV arithmetic (include/ribn_amd.h RIBN_AMD_GEMV_*)
+GEMV_MODES = {"warp": 0, "fixed16": 1}
 KV_BYTES_PER_TOKEN = 36 * 8 * 128 * 2 * 2  # f16 K and V of every layer: 147,456 B
 
 
@@ -202,8 +209,9 @@ def build_decoder(E, synth, torch, ctx, step, out_gamma, layers, seed, members):
         lw["attn_k_norm"] = 1.0 + 0.02 * torch.randn(128, device=dev, generator=gen)
         plan.append(lw)
     cfg = E.AmdQwen3Config(layers=layers)
-    return E.AmdQwen3Decode(ctx, cfg, step.store.quantized_tensor("token_embd"), step.head, out_gamma, plan,
-                            members), cfg
+    dec = E.AmdQwen3Decode(ctx, cfg, step.store.quantized_tensor("token_embd"), step.head, out_gamma, plan, members)
+    dec.set_gemv_mode(GEMV_MODES[getattr(build_decoder, "mode", "warp")])
+    return dec, cfg
 
 
 def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed):
@@ -694,6 +702,8 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-graph", action="store_true", help="issue launches eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemv-mode", choices=tuple(GEMV_MODES), default="warp",
+                    help="GEMV arithmetic: warp (f32 activations, default) or fixed16 (opt-in block fixed point)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1", "gguf", "serving"),
                     default="decode",
@@ -739,7 +749,8 @@ def main():
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     ctx = E.AmdContext(0, stream=stream)
-    step = DecodeGemvStep(E, torch, ctx, weights, head, out_gamma, acts)
+    step = DecodeGemvStep(E, torch, ctx, weights, head, out_gamma, acts, GEMV_MODES[args.gemv_mode])
+    build_decoder.mode = args.gemv_mode
     log(f"bench: {step.bytes_per_step / 1e9:.3f} GB of algorithmic traffic per step")
 
     if args.workload == "model":

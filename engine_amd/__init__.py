@@ -7,7 +7,7 @@ host-side mirror of the reference's operator API (kquant.py).
 from . import _lib  # noqa: F401
 from .kquant import (  # noqa: F401
     AmdQ4KQ8_1Gemv, AmdQ5KQ8_1Gemv, AmdQ6KQ8_1Gemv, AmdQ8_1Quantizer,
-    Q4_K, Q5_K, Q6_K, BLOCK_BYTES,
+    Q4_K, Q5_K, Q6_K, BLOCK_BYTES, GEMV_WARP, GEMV_FIXED16,
     AmdContext, AmdWeightStore, AmdQuantizedWeight,
     AmdQ4KGemv, AmdQ5KGemv, AmdQ6KGemv, QwenGemvKernel, AmdQwenOps,
     AmdQ4KEmbedding, AmdKQuantEmbedding,
@@ -19,7 +19,7 @@ from .qwen3 import AmdKvCache, AmdQwen3Config, AmdQwen3Decode, QWEN3_8B, attenti
 from .serving import AmdBackend, AmdDispatcher, AmdServingDispatcher, BackendError, plan_memory  # noqa: F401
 
 __all__ = [
-    "Q4_K", "Q5_K", "Q6_K", "BLOCK_BYTES", "AmdContext", "AmdWeightStore", "AmdQuantizedWeight",
+    "Q4_K", "Q5_K", "Q6_K", "BLOCK_BYTES", "GEMV_WARP", "GEMV_FIXED16", "AmdContext", "AmdWeightStore", "AmdQuantizedWeight",
     "AmdQ4KGemv", "AmdQ5KGemv", "AmdQ6KGemv", "QwenGemvKernel", "AmdQwenOps", "AmdQ4KEmbedding",
     "AmdKQuantEmbedding", "AmdKernelError",
     "AmdQuantizedKernelError", "AmdModelKernelError", "AmdWeightError", "validate_quantized_geometry",

@@ -121,6 +121,8 @@ SIGNATURES = {
     "ribn_amd_gemv_create": (_i32, [_vp, _u32, _pvp]),
     "ribn_amd_gemv_destroy": (None, [_vp]),
     "ribn_amd_gemv_value_type": (_u32, [_vp]),
+    "ribn_amd_gemv_set_mode": (_i32, [_vp, _u32]),
+    "ribn_amd_gemv_mode": (_u32, [_vp]),
     "ribn_amd_gemv_execute": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
     "ribn_amd_gemv_execute_warp": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz]),
     "ribn_amd_gemv_execute_warp_batch": (_i32, [_vp, _vp, _vp, _sz, _vp, _sz, _sz]),
@@ -167,6 +169,8 @@ SIGNATURES = {
                                             ctypes.POINTER(Qwen3Layer), _u32, _pvp]),
     "ribn_amd_qwen3_decode_destroy": (None, [_vp]),
     "ribn_amd_qwen3_decode_set_graphs": (_i32, [_vp, _i32]),
+    "ribn_amd_qwen3_decode_set_gemv_mode": (_i32, [_vp, _u32]),
+    "ribn_amd_qwen3_decode_gemv_mode": (_u32, [_vp]),
     "ribn_amd_qwen3_prefill_step": (_i32, [_vp, _vp, _u32, _u32]),
     "ribn_amd_qwen3_prefill_chunk": (_i32, [_vp, _vp, ctypes.POINTER(_u32), _sz, _u32]),
     "ribn_amd_qwen3_decode_step": (_i32, [_vp, _vp, _u32, _u32, ctypes.POINTER(_u32)]),

@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+
+#include <atomic>
 #include <stdint.h>
 
 #include "ribn_amd.h"
@@ -17,6 +19,10 @@ struct ribn_amd_context {
     size_t workspace_bytes;
     void* act_scratch;  // packed activations of the matrix-core batched GEMV, reserved at creation
     void* attn_members; // cache descriptors of the standalone attention call (same allocation)
+    // Owner handle plus every decoder and dispatcher built on the context: the
+    // device resources are released when the last of them lets go, so handles
+    // may be destroyed in any order (e.g. by a garbage collector).
+    std::atomic<int> refs{1};
 };
 
 struct ribn_amd_quantized_weight {
@@ -33,7 +39,13 @@ struct ribn_amd_quantized_weight {
 struct ribn_amd_gemv {
     ribn_amd_context* ctx;
     uint32_t value_type;
+    uint32_t mode;  // RIBN_AMD_GEMV_WARP or RIBN_AMD_GEMV_FIXED16
 };
+
+namespace ribn_amd_abi {
+// Launch arithmetic (ribn_amd::kArith*) of a GEMV mode.
+inline int arith_of_mode(uint32_t mode) { return mode == RIBN_AMD_GEMV_FIXED16 ? 1 : 0; }
+}  // namespace ribn_amd_abi
 
 struct ribn_amd_embedding {
     ribn_amd_context* ctx;
@@ -57,6 +69,11 @@ ribn_amd_status check_device_ptr(const ribn_amd_context* ctx, const void* ptr, c
 ribn_amd_status validate_geometry(uint32_t kernel_type, const ribn_amd_quantized_weight* w, uint64_t* k,
                                   uint64_t* n);
 ribn_amd_status check_epsilon(float epsilon);
+
+// Context lifetime: dependents retain the context they use and release it
+// when destroyed; the last release frees the stream, scratch and workspace.
+void context_retain(ribn_amd_context* ctx);
+void context_release(ribn_amd_context* ctx);
 
 struct DeviceGuard {
     int previous = -1;

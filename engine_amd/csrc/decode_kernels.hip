@@ -57,15 +57,6 @@ constexpr int kStepTokens = kWaves * 4;   // tokens a workgroup covers per step
 constexpr int kMinChunkTokens = 64;
 static_assert(kMinChunkTokens % kStepTokens == 0, "chunks are whole steps");
 
-// Workgroups an attention launch aims at (a sweep on MI355X over 256, 512,
-// 1024 and 2048 at 1 and 8 members, 2048-token context: 512 was fastest at
-// 8 members, 1 member is unaffected). Past it, a workgroup's fixed work (query
-// norm and rope, the row and wave merges) outweighs its share of the K/V
-// stream and the launch turns VALU-bound.
-constexpr int kAttnTargetGroups = 512;
-// Batches from this size take the batch-dependent chunking (the size from
-// which the matrix-core GEMVs serve the projections as well).
-constexpr int kAttnSplitMembers = 5;
 
 // Tokens per chunk for a context of `tokens` in a launch of `chunks` grid
 // chunks: kMinChunkTokens, or more when the context needs more than `chunks`
@@ -526,13 +517,11 @@ hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t strea
         args.chunks < 1 || args.chunks > kAttnChunks || args.mem == nullptr) {
         return hipErrorInvalidValue;
     }
-    // From kAttnSplitMembers members, fewer, longer chunks when (KV heads x
-    // members) already fill the chip. Below it the chunking depends on the
-    // caches' capacity only, so a member's bits equal its single-sequence step.
-    AttnArgs b = args;
-    const int fill = members < kAttnSplitMembers ? kAttnChunks
-                                                 : std::max(1, kAttnTargetGroups / (args.kv_heads * members));
-    b.chunks = std::min(args.chunks, fill);
+    // The chunking depends on the caches' capacity only, never on the member
+    // count, so every member's bits equal its single-sequence step (the
+    // reference qualifies batched rows bit for bit against batch-1 rows,
+    // cuda_reference.rs:5322-5334).
+    const AttnArgs& b = args;
     const dim3 grid((unsigned)b.chunks, (unsigned)b.kv_heads, (unsigned)members);
     switch (b.q_heads / b.kv_heads) {
     case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(kThreads), 0, stream, b); break;

@@ -695,7 +695,12 @@ hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& a, int /*cu_coun
 
 size_t gemv_act_scratch_bytes() { return act16_layout(kMfmaMaxMembers, kWaveMaxK).total; }
 
-int gemv_launch_members(int value_type, int K, bool swiglu_prologue) {
+int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith) {
+    if (arith == kArithF32) {
+        int per = f32_max_members(K);
+        if (swiglu_prologue) per = std::min(per, kSwigluMaxMembers);
+        return per;
+    }
     if (!swiglu_prologue && gemv_mfma_supported(value_type) && K % 256 == 0 && K <= kWaveMaxK) {
         return kMfmaMaxMembers;
     }
@@ -705,6 +710,26 @@ int gemv_launch_members(int value_type, int K, bool swiglu_prologue) {
 }
 
 hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch, int cu_count, hipStream_t stream) {
+    if (a.arith == kArithF32) {
+        // the f32 wave GEMV, in launch groups of as many members as it stages
+        int per = f32_max_members(a.K);
+        if (a.x2 != nullptr) per = std::min(per, kSwigluMaxMembers);
+        if (per <= 0) return hipErrorInvalidValue;
+        for (int m0 = 0; m0 < a.members; m0 += per) {
+            WaveGemvArgs c = a;
+            c.members = std::min(per, a.members - m0);
+            c.x = a.x + (size_t)m0 * a.K;
+            c.x2 = a.x2 != nullptr ? a.x2 + (size_t)m0 * a.K : nullptr;
+            for (int i = 0; i < a.count; ++i) {
+                const int n = a.rows_end[i] - (i > 0 ? a.rows_end[i - 1] : 0);
+                c.y[i] = a.y[i] + (size_t)m0 * (a.pair_swiglu ? a.rows_end[0] : n);
+            }
+            hipError_t e = launch_gemv_f32(value_type, c, cu_count, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    if (a.arith != kArithFixed16) return hipErrorInvalidValue;
     // Measured on MI355X over the Qwen3-8B projections: the matrix cores win
     // from kMfmaMinMembers members (the wave GEMV's member-serial passes are
     // VALU-bound there), and from kMfmaMinMembersLongK where K spans several

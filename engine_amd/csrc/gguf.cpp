@@ -571,6 +571,7 @@ ribn_amd_status ribn_amd_gguf_stage(ribn_amd_context* ctx, const ribn_amd_gguf* 
                 result = fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
                 break;
             }
+            context_retain(ctx);  // released by ribn_amd_weight_destroy
             out[k] = w;
             if (kquant) {
                 uint64_t vk, vn;

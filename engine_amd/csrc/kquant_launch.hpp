@@ -45,7 +45,18 @@ struct WaveGemvArgs {
     // nonzero: w[0] / w[1] are gate / up of equal shape, and y[0] [members][N]
     // receives silu(gate . x') * (up . x') (K <= 4096; y[1] unused)
     int pair_swiglu;
+    // Arithmetic: kArithF32 (f32 activations, the default) or kArithFixed16
+    // (block fixed-point activations with integer dot products, opt-in).
+    int arith;
 };
+
+constexpr int kArithF32 = 0;
+constexpr int kArithFixed16 = 1;
+
+// Largest member count one f32 wave-GEMV launch stages for this K (0 if none).
+int f32_max_members(int K);
+// The f32-activation wave GEMV (gemv_f32.hip); members <= f32_max_members(K).
+hipError_t launch_gemv_f32(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
 
 // Largest member count one wave launch can stage for this K (0 if none).
 int wave_max_members(int K);
@@ -107,13 +118,13 @@ hipError_t launch_gemv_q8_1(int value_type, const uint8_t* w, uint32_t wbytes, c
 
 // Device scratch (bytes) a context reserves for launch_gemv's packed activations.
 size_t gemv_act_scratch_bytes();
-// Members one launch_gemv call may carry for this shape.
-int gemv_launch_members(int value_type, int K, bool swiglu_prologue);
-// Q4_K / Q5_K without the SwiGLU prologue (and with tiles not straddling
-// grouped weights) run packed activations through the matrix-core GEMV (two
-// launches) for 9..16 members, or 6..16 members when K spans more than one
-// slice; every other call runs the wave GEMV, split into the launch groups it
-// stages.
+// Members one launch_gemv call may carry for this shape and arithmetic.
+int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith);
+// kArithF32: the f32 wave GEMV, split into the launch groups it stages.
+// kArithFixed16: the block fixed-point wave GEMV, or from kMfmaMinMembers
+// (kMfmaMinMembersLongK for K spanning several slices) up to 16 members
+// without the SwiGLU prologue, packed activations through the matrix-core
+// GEMV (two launches).
 hipError_t launch_gemv(int value_type, const WaveGemvArgs& args, void* act_scratch, int cu_count,
                        hipStream_t stream);
 

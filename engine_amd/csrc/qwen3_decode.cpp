@@ -154,6 +154,7 @@ struct ribn_amd_qwen3_decode {
     int chunks;           // attention grid of the next step (from its caches' capacities)
     hipStream_t capture;  // private stream for graph capture
     bool graphs;
+    uint32_t gemv_mode;   // RIBN_AMD_GEMV_WARP (f32 activations) or RIBN_AMD_GEMV_FIXED16
     std::vector<GraphEntry> graph_cache;
 };
 
@@ -166,7 +167,8 @@ hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight*
                 const float* x, const float* x2, const float* gamma, float* const* ys, int members, bool accumulate,
                 hipStream_t stream, bool pair = false) {
     const int K = (int)ws[0]->input_size;
-    const int per = ribn_amd::gemv_launch_members((int)ws[0]->value_type, K, x2 != nullptr);
+    const int arith = arith_of_mode(d->gemv_mode);
+    const int per = ribn_amd::gemv_launch_members((int)ws[0]->value_type, K, x2 != nullptr, arith);
     if (per <= 0) return hipErrorInvalidValue;
     for (int m0 = 0; m0 < members; m0 += per) {
         const int mc = std::min(per, members - m0);
@@ -190,6 +192,7 @@ hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight*
         a.members = mc;
         a.accumulate = accumulate ? 1 : 0;
         a.pair_swiglu = pair ? 1 : 0;
+        a.arith = arith;
         hipError_t e = ribn_amd::launch_gemv((int)ws[0]->value_type, a, d->ctx->act_scratch, d->ctx->cu_count,
                                              stream);
         if (e != hipSuccess) return e;
@@ -711,6 +714,7 @@ ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context* ctx, const ribn_a
     d->output_norm = output_norm;
     d->layers.assign(layers, layers + c.layers);
     d->graphs = true;
+    d->gemv_mode = RIBN_AMD_GEMV_WARP;
     hipError_t e = hipMalloc(&d->block, bytes);
     if (e != hipSuccess) {
         delete d;
@@ -737,6 +741,7 @@ ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context* ctx, const ribn_a
         delete d;
         return driver(e, "set up decode buffers");
     }
+    context_retain(ctx);
     *out = d;
     return ok();
 }
@@ -749,13 +754,34 @@ void ribn_amd_qwen3_decode_destroy(ribn_amd_qwen3_decode* d) {
     hipStreamDestroy(d->capture);
     hipFree(d->history);
     hipFree(d->block);
+    ribn_amd_context* ctx = d->ctx;
     delete d;
+    context_release(ctx);
 }
 
 ribn_amd_status ribn_amd_qwen3_decode_set_graphs(ribn_amd_qwen3_decode* d, int32_t enabled) {
     if (!d) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null decoder");
     d->graphs = enabled != 0;
     return ok();
+}
+
+ribn_amd_status ribn_amd_qwen3_decode_set_gemv_mode(ribn_amd_qwen3_decode* d, uint32_t mode) {
+    if (!d) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null decoder");
+    if (mode != RIBN_AMD_GEMV_WARP && mode != RIBN_AMD_GEMV_FIXED16) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, RIBN_AMD_GEMV_FIXED16, mode, "unknown GEMV mode %u", mode);
+    }
+    if (mode != d->gemv_mode) {
+        DeviceGuard guard(d->ctx->device);
+        hipError_t e = hipStreamSynchronize(d->ctx->stream);
+        if (e != hipSuccess) return driver(e, "synchronize before a GEMV mode change");
+        destroy_graphs(d);  // captured with the other mode's kernels
+        d->gemv_mode = mode;
+    }
+    return ok();
+}
+
+uint32_t ribn_amd_qwen3_decode_gemv_mode(const ribn_amd_qwen3_decode* d) {
+    return d ? d->gemv_mode : RIBN_AMD_GEMV_WARP;
 }
 
 ribn_amd_status ribn_amd_qwen3_decode_step_batch(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches,

@@ -171,7 +171,7 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
         }
         return ok();
     }
-    per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, up != nullptr);
+    per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, up != nullptr, arith_of_mode(g->mode));
     for (size_t m0 = 0; m0 < members; m0 += (size_t)per_launch) {
         const size_t mc = std::min<size_t>((size_t)per_launch, members - m0);
         ribn_amd::WaveGemvArgs a{};
@@ -193,6 +193,7 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
         a.eps = eps;
         a.K = (int)k;
         a.members = (int)mc;
+        a.arith = arith_of_mode(g->mode);
         hipError_t e = ribn_amd::launch_gemv((int)g->value_type, a, g->ctx->act_scratch, g->ctx->cu_count,
                                              g->ctx->stream);
         if (e != hipSuccess) return driver(e, "launch GEMV");
@@ -341,6 +342,16 @@ ribn_amd_status ribn_amd_context_wrap_stream(int32_t device, void* hip_stream, r
 
 void ribn_amd_context_destroy(ribn_amd_context* ctx) {
     if (!ctx) return;
+    context_release(ctx);
+}
+
+extern "C++" {
+namespace ribn_amd_abi {
+
+void context_retain(ribn_amd_context* ctx) { ctx->refs.fetch_add(1, std::memory_order_relaxed); }
+
+void context_release(ribn_amd_context* ctx) {
+    if (ctx->refs.fetch_sub(1, std::memory_order_acq_rel) != 1) return;
     DeviceGuard guard(ctx->device);
     if (ctx->workspace || ctx->act_scratch) hipStreamSynchronize(ctx->stream);
     if (ctx->workspace) hipFree(ctx->workspace);
@@ -351,6 +362,9 @@ void ribn_amd_context_destroy(ribn_amd_context* ctx) {
     }
     delete ctx;
 }
+
+}  // namespace ribn_amd_abi
+}  // extern "C++"
 
 size_t ribn_amd_gemm_workspace_bytes(size_t tokens, size_t k, size_t n) {
     return ribn_amd::gemm_workspace_bytes(tokens, k, n);
@@ -498,6 +512,7 @@ static ribn_amd_status new_weight(ribn_amd_context* ctx, uint32_t value_type, ui
         delete w;
         return driver(e, "hipMalloc weight");
     }
+    context_retain(ctx);  // released by ribn_amd_weight_destroy
     *out = w;
     return RIBN_AMD_OK;
 }
@@ -572,6 +587,7 @@ ribn_amd_status ribn_amd_weight_wrap_device(ribn_amd_context* ctx, uint32_t valu
         ctx, ctx->device, value_type, input_size, output_size, encoded_bytes,
         const_cast<uint8_t*>(static_cast<const uint8_t*>(device_bytes)), false};
     if (!w) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    context_retain(ctx);
     *out = w;
     return ok();
 }
@@ -592,7 +608,9 @@ void ribn_amd_weight_destroy(ribn_amd_quantized_weight* weight) {
         DeviceGuard guard(weight->device);
         hipFree(weight->data);  // synchronises with outstanding work on the device
     }
+    ribn_amd_context* ctx = weight->ctx;
     delete weight;
+    context_release(ctx);
 }
 
 uint32_t ribn_amd_weight_value_type(const ribn_amd_quantized_weight* w) { return w ? w->value_type : 0; }
@@ -607,14 +625,31 @@ ribn_amd_status ribn_amd_gemv_create(ribn_amd_context* ctx, uint32_t value_type,
         return fail(RIBN_AMD_UNSUPPORTED_VALUE_TYPE, RIBN_AMD_Q4_K, value_type,
                     "GGML value type %u has no MI355X GEMV kernel", value_type);
     }
-    auto* g = new (std::nothrow) ribn_amd_gemv{ctx, value_type};
+    auto* g = new (std::nothrow) ribn_amd_gemv{ctx, value_type, RIBN_AMD_GEMV_WARP};
     if (!g) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    context_retain(ctx);
     *out = g;
     return ok();
 }
 
-void ribn_amd_gemv_destroy(ribn_amd_gemv* gemv) { delete gemv; }
+void ribn_amd_gemv_destroy(ribn_amd_gemv* gemv) {
+    if (!gemv) return;
+    ribn_amd_context* ctx = gemv->ctx;
+    delete gemv;
+    context_release(ctx);
+}
 uint32_t ribn_amd_gemv_value_type(const ribn_amd_gemv* gemv) { return gemv ? gemv->value_type : 0; }
+
+ribn_amd_status ribn_amd_gemv_set_mode(ribn_amd_gemv* gemv, uint32_t mode) {
+    if (!gemv) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null GEMV");
+    if (mode != RIBN_AMD_GEMV_WARP && mode != RIBN_AMD_GEMV_FIXED16) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, RIBN_AMD_GEMV_FIXED16, mode, "unknown GEMV mode %u", mode);
+    }
+    gemv->mode = mode;
+    return ok();
+}
+
+uint32_t ribn_amd_gemv_mode(const ribn_amd_gemv* gemv) { return gemv ? gemv->mode : RIBN_AMD_GEMV_WARP; }
 
 ribn_amd_status ribn_amd_gemv_execute(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const float* input,
                                       size_t input_len, float* output, size_t output_len) {
@@ -768,7 +803,7 @@ ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv* g, const rib
         if (st != RIBN_AMD_OK) return st;
     }
     DeviceGuard guard(g->ctx->device);
-    const int per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, false);
+    const int per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, false, arith_of_mode(g->mode));
     for (size_t m0 = 0; m0 < members; m0 += (size_t)per_launch) {
         const size_t mc = std::min<size_t>((size_t)per_launch, members - m0);
         ribn_amd::WaveGemvArgs a{};
@@ -788,6 +823,7 @@ ribn_amd_status ribn_amd_gemv_execute_gate_up_swiglu(ribn_amd_gemv* g, const rib
         a.K = (int)k;
         a.members = (int)mc;
         a.pair_swiglu = 1;
+        a.arith = arith_of_mode(g->mode);
         hipError_t e = ribn_amd::launch_gemv((int)g->value_type, a, g->ctx->act_scratch, g->ctx->cu_count,
                                              g->ctx->stream);
         if (e != hipSuccess) return driver(e, "launch gate/up GEMV");
@@ -954,11 +990,17 @@ ribn_amd_status ribn_amd_embedding_create(ribn_amd_context* ctx, uint32_t value_
     }
     auto* e = new (std::nothrow) ribn_amd_embedding{ctx, value_type};
     if (!e) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
+    context_retain(ctx);
     *out = e;
     return ok();
 }
 
-void ribn_amd_embedding_destroy(ribn_amd_embedding* e) { delete e; }
+void ribn_amd_embedding_destroy(ribn_amd_embedding* e) {
+    if (!e) return;
+    ribn_amd_context* ctx = e->ctx;
+    delete e;
+    context_release(ctx);
+}
 
 namespace {
 

@@ -557,6 +557,7 @@ ribn_amd_status ribn_amd_serving_create(ribn_amd_qwen3_decode* decode, uint32_t 
     s->pinned = static_cast<uint32_t*>(pinned);
     s->slots = max_pending_rows;
     for (uint32_t i = max_pending_rows; i > 0; --i) s->free_slots.push_back((int32_t)(i - 1));
+    context_retain(ctx);
     *out = s;
     return ok();
 }
@@ -574,7 +575,9 @@ void ribn_amd_serving_destroy(ribn_amd_serving* s) {
         for (ribn_amd_kv_cache* c : kv.second) ribn_amd_kv_cache_destroy(c);
     }
     hipHostFree(s->pinned);
+    ribn_amd_context* ctx = s->ctx;
     delete s;
+    context_release(ctx);
 }
 
 ribn_amd_status ribn_amd_serving_set_prefill_chunk(ribn_amd_serving* s, uint32_t members) {

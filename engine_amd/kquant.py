@@ -26,6 +26,9 @@ from . import _lib
 
 Q4_K, Q5_K, Q6_K = 12, 13, 14
 BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210}
+# GEMV arithmetic (the reference's GemvMode, decode.rs:285-307): GEMV_WARP is
+# f32 activations (default); GEMV_FIXED16 the opt-in block fixed-point mode.
+GEMV_WARP, GEMV_FIXED16 = 0, 1
 
 
 class AmdKernelError(Exception):
@@ -259,6 +262,13 @@ class _AmdQuantizedGemv:
 
     def value_type(self) -> int:
         return int(self._lib.ribn_amd_gemv_value_type(self.handle))
+
+    def set_mode(self, mode: int):
+        """GEMV_WARP (f32 activations, default) or GEMV_FIXED16 (opt-in, lossy)."""
+        _check(self._lib.ribn_amd_gemv_set_mode(self.handle, mode))
+
+    def mode(self) -> int:
+        return int(self._lib.ribn_amd_gemv_mode(self.handle))
 
     def execute(self, weight, input, output):
         _check(self._lib.ribn_amd_gemv_execute(self.handle, weight.handle, _ptr(input), input.numel(),

@@ -37,7 +37,7 @@ from collections import defaultdict
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 # The decode GEMV's sources (the kernel the roofline and traffic figures are about).
-KERNEL_SOURCES = ("csrc/gemv_wave.hip", "csrc/kquant_device.hpp", "csrc/kquant_launch.hpp")
+KERNEL_SOURCES = ("csrc/gemv_f32.hip", "csrc/wave_rows.hpp", "csrc/kquant_device.hpp", "csrc/kquant_launch.hpp")
 
 
 def source_hash() -> str:

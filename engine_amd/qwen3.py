@@ -100,7 +100,9 @@ class AmdQwen3Decode:
         self.ctx = ctx
         self.config = config
         self._cfg = config.to_c()
-        self._keep = [output_norm]
+        # The decoder reads these every step: weight handles and norm tensors
+        # stay referenced for its lifetime (the C side does not own them).
+        self._keep = [output_norm, token_embd, output]
         arr = (_lib.Qwen3Layer * len(layers))()
         for i, lw in enumerate(layers):
             for name in _lib.QWEN3_LAYER_FIELDS:
@@ -109,7 +111,7 @@ class AmdQwen3Decode:
                     setattr(arr[i], name, obj.handle.value)
                 else:
                     setattr(arr[i], name, obj.data_ptr())
-                    self._keep.append(obj)
+                self._keep.append(obj)
         self.handle = ctypes.c_void_p()
         _check(ctx._lib.ribn_amd_qwen3_decode_create(ctx.handle, ctypes.byref(self._cfg), token_embd.handle,
                                                      output.handle, _ptr(output_norm), arr, max_members,
@@ -118,6 +120,14 @@ class AmdQwen3Decode:
 
     def set_graphs(self, enabled: bool):
         _check(self.ctx._lib.ribn_amd_qwen3_decode_set_graphs(self.handle, 1 if enabled else 0))
+
+    def set_gemv_mode(self, mode: int):
+        """CudaQwen35Decode::set_gemv_mode (decode.rs:738-741): GEMV_WARP (f32
+        activations, default) or GEMV_FIXED16 (opt-in block fixed point)."""
+        _check(self.ctx._lib.ribn_amd_qwen3_decode_set_gemv_mode(self.handle, mode))
+
+    def gemv_mode(self) -> int:
+        return int(self.ctx._lib.ribn_amd_qwen3_decode_gemv_mode(self.handle))
 
     def prefill_step(self, cache: AmdKvCache, token: int, position: int):
         _check(self.ctx._lib.ribn_amd_qwen3_prefill_step(self.handle, cache.handle, token, position),

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define RIBN_AMD_ABI_VERSION 1
+#define RIBN_AMD_ABI_VERSION 2
 
 /* GGML value types served by this library (quantized.rs:25-27). */
 #define RIBN_AMD_Q4_K 12u
@@ -131,6 +131,11 @@ ribn_amd_status ribn_amd_context_create(int32_t device, ribn_amd_context **out);
 /* CudaQ4KGemv::from_context(&ctx, stream) (quantized.rs:1588-1610): wraps a
  * caller-owned HIP stream; the caller keeps ownership and must outlive the context. */
 ribn_amd_status ribn_amd_context_wrap_stream(int32_t device, void *hip_stream, ribn_amd_context **out);
+/* Releases the caller's reference. Weights, kernel objects, decoders and
+ * serving dispatchers built on the context hold references of their own (as
+ * the reference's operators hold an Arc<CudaContext>), so handles may be
+ * destroyed in any order: the stream (when owned), scratch and workspace go
+ * with the last reference. */
 void ribn_amd_context_destroy(ribn_amd_context *ctx);
 /* CudaStream::synchronize. */
 ribn_amd_status ribn_amd_context_synchronize(ribn_amd_context *ctx);
@@ -198,13 +203,33 @@ ribn_amd_status ribn_amd_gemv_create(ribn_amd_context *ctx, uint32_t value_type,
 void ribn_amd_gemv_destroy(ribn_amd_gemv *gemv);
 uint32_t ribn_amd_gemv_value_type(const ribn_amd_gemv *gemv);
 
+/* GEMV arithmetic of the warp-family calls below (execute_warp, _warp_batch,
+ * _rms_norm, _group, _fused, _gate_up_swiglu); the reference's GemvMode
+ * (crates/nvidia/src/decode.rs:285-307).
+ *   RIBN_AMD_GEMV_WARP (default; GemvMode::Warp): f32 activations against
+ *     weights dequantised in registers, f32 accumulation. Up to 8 members
+ *     (2 when K > 4096) share one weight stream; every row is bit-identical
+ *     to the single-member call.
+ *   RIBN_AMD_GEMV_FIXED16 (opt-in, lossy; no reference twin, used like
+ *     GemvMode::IntegerDot for throughput comparison): activations rounded to
+ *     block fixed point (16-bit per scale group in the wave kernel, 15-bit per
+ *     super-block on the int8 matrix cores from 5 members) with integer dot
+ *     products. Never bit-identical to WARP. */
+#define RIBN_AMD_GEMV_WARP 0u
+#define RIBN_AMD_GEMV_FIXED16 1u
+/* set_gemv_mode / gemv_mode (decode.rs:711-741) at the operator level: an
+ * unknown mode is InvalidArgument. */
+ribn_amd_status ribn_amd_gemv_set_mode(ribn_amd_gemv *gemv, uint32_t mode);
+uint32_t ribn_amd_gemv_mode(const ribn_amd_gemv *gemv);
+
 /* execute (quantized.rs:368-388): y[N] = W x[K]. Exact-order kernel: per row,
  * elements in K order, each product and sum rounded separately, so results
  * equal the host decoder + sequential f32 dot bit for bit. Correctness oracle;
  * slow. */
 ribn_amd_status ribn_amd_gemv_execute(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
                                       const float *input, size_t input_len, float *output, size_t output_len);
-/* execute_warp (quantized.rs:401-435): the wave64 bandwidth kernel (default decode path). */
+/* execute_warp (quantized.rs:401-435): the wave64 bandwidth kernel (default
+ * decode path), in the kernel object's GEMV mode. */
 ribn_amd_status ribn_amd_gemv_execute_warp(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
                                            const float *input, size_t input_len, float *output,
                                            size_t output_len);
@@ -508,6 +533,12 @@ void ribn_amd_qwen3_decode_destroy(ribn_amd_qwen3_decode *decode);
  * graphs and replayed (default); disabled, every step launches its kernels
  * directly. Both run the same kernels with the same arguments. */
 ribn_amd_status ribn_amd_qwen3_decode_set_graphs(ribn_amd_qwen3_decode *decode, int32_t enabled);
+/* CudaQwen35Decode::set_gemv_mode / gemv_mode (decode.rs:711-741): the
+ * arithmetic of every projection of later steps (RIBN_AMD_GEMV_WARP by
+ * default, or RIBN_AMD_GEMV_FIXED16); an unknown mode is InvalidArgument.
+ * Captured graphs of the other mode are dropped. */
+ribn_amd_status ribn_amd_qwen3_decode_set_gemv_mode(ribn_amd_qwen3_decode *decode, uint32_t mode);
+uint32_t ribn_amd_qwen3_decode_gemv_mode(const ribn_amd_qwen3_decode *decode);
 /* CudaQwen35Decode::prefill_step (decode.rs:489-499): advances `cache` by
  * `token` at `position` without the output head. Stream-ordered, not
  * blocking: a later step or copy on the context stream observes it. */

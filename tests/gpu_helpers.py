@@ -7,9 +7,11 @@ RTOL = 1e-3
 
 
 def mfma_path(t, k, members):
-    """Whether a batched GEMV of this shape runs on the matrix cores
-    (engine_amd/csrc/gemv_mfma.hip launch_gemv): Q4_K / Q5_K / Q6_K with 5..16
-    members, or 4..16 members when K spans more than one 4096 slice."""
+    """Whether a batched GEMV of this shape runs on the matrix cores in the
+    opt-in GEMV_FIXED16 mode (engine_amd/csrc/gemv_mfma.hip launch_gemv):
+    Q4_K / Q5_K / Q6_K with 5..16 members, or 4..16 members when K spans more
+    than one 4096 slice. The default GEMV_WARP mode never takes that path:
+    every batched row is bit-identical to its single-member call."""
     return t in (12, 13, 14) and members <= 16 and (members >= 5 or (k > 4096 and members >= 4))
 
 

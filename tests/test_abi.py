@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_names():
     lib = _lib.load()
-    assert lib.ribn_amd_abi_version() == 1
+    assert lib.ribn_amd_abi_version() == 2
     for code, name in _lib.STATUS_NAMES.items():
         assert lib.ribn_amd_status_name(code).decode() == name
 

@@ -17,7 +17,7 @@ import pytest
 from engine_amd import synth
 from oracle import kquant_oracle as O
 
-from .gpu_helpers import RTOL, empty_dev, max_rel_err, mfma_path, to_dev, to_host
+from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -174,20 +174,12 @@ def test_batch_matches_oracle_and_single_bitwise(env, t, members):
     got = to_host(y, env["ctx"]).reshape(members, n)
     ref = O.quant_gemv(t, enc, k, n, x.reshape(-1), members=members).reshape(members, n)
     assert max_rel_err(got, ref) <= RTOL
-    if not mfma_path(t, k, members):
-        # the wave GEMV's weights-read-once batching keeps every row
-        # bit-identical to the single path
-        for m in range(members):
-            ys = empty_dev(n)
-            env["k"][t].execute_warp(w, to_dev(x[m]), ys)
-            assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
-    else:
-        # matrix-core batches: a member's bits do not depend on the batch
-        # (here: the batch in reverse order)
-        yr = empty_dev(members * n)
-        env["k"][t].execute_warp_batch(w, to_dev(x[::-1].reshape(-1)), yr, members)
-        rev = to_host(yr, env["ctx"]).reshape(members, n)[::-1]
-        assert np.array_equal(rev.view(np.uint32), got.view(np.uint32))
+    # GEMV_WARP batching (weights read once for up to 8 members) keeps every
+    # row bit-identical to the single path (cuda_reference.rs:5322-5334)
+    for m in range(members):
+        ys = empty_dev(n)
+        env["k"][t].execute_warp(w, to_dev(x[m]), ys)
+        assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
 
 
 @pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096), (14, 4096, 4096)])
@@ -337,3 +329,159 @@ def test_grouped_launch_matches_separate(env, t, k, ns, members, norm):
             src = O.rms_norm_raw(x[m], gam, 1e-6) if norm else x[m]
             ref = O.quant_gemv(t, e, k, n, src, threads=8)
             assert max_rel_err(got.reshape(members, n)[m], ref) <= RTOL
+
+
+# ------------------------------------------- shapes the decode step runs
+
+def _row_sample(n, count, seed):
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([[0, 1, n // 2, n - 2, n - 1], rng.integers(0, n, count)]))
+    return rows[rows < n]
+
+
+def _oracle_rows(t, enc, k, n, x, rows):
+    row_bytes = k // 256 * O.BLOCK_BYTES[t]
+    sub = enc.reshape(n, row_bytes)[rows].reshape(-1)
+    return O.quant_gemv(t, sub, k, len(rows), x, threads=8)
+
+
+@pytest.mark.parametrize("t,n,norm", [(14, 151936, True), (12, 32768, True), (13, 32768, False),
+                                      (14, 32768, False)])
+def test_long_stream_launch_shape(env, t, n, norm):
+    """The batch-1 launch shape of long one-slice streams (>= 128 rows per CU):
+    the Qwen3-8B lm_head (Q6_K 4096 -> 151936, RMSNorm fused) that every decode
+    step runs, and Q4_K / Q5_K / Q6_K at 32768 rows; checked on a row sample."""
+    k = 4096
+    print_case(test="long_stream", t=t, n=n, norm=norm)
+    enc = synth.kquant_numpy(t, k, n, seed=77 + t)
+    x = synth.activations_numpy(k, 1, seed=t)[0]
+    gam = synth.gamma_numpy(k, seed=5)
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(n)
+    if norm:
+        env["k"][t].execute_rms_norm(w, to_dev(x), to_dev(gam), 1e-6, y, 1)
+        src = O.rms_norm_raw(x, gam, 1e-6)
+    else:
+        env["k"][t].execute_warp(w, to_dev(x), y)
+        src = x
+    got = to_host(y, env["ctx"])
+    rows = _row_sample(n, 3000, seed=n)
+    ref = _oracle_rows(t, enc, k, n, src, rows)
+    err = max_rel_err(got[rows], ref)
+    print(f"max_rel_err={err:.3e}", flush=True)
+    assert err <= RTOL
+    assert np.all(np.isfinite(got))
+    del w, y
+
+
+def wide_range_activations(k, seed):
+    """N(0,1) activations with a few x3000 outlier channels, whole scale groups
+    at 2^-20, and groups whose elements spread over 2^-16..1 in magnitude."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(k)
+    x[rng.choice(k, 8, replace=False)] *= 3000.0
+    groups = k // 32
+    for g in rng.choice(groups, groups // 8, replace=False):
+        x[32 * g:32 * g + 32] *= 2.0 ** -20
+    for g in rng.choice(groups, groups // 8, replace=False):
+        x[32 * g:32 * g + 32] *= 2.0 ** rng.uniform(-16, 0, 32)
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("mode", ["warp", "fixed16"])
+@pytest.mark.parametrize("t,k,n,members,norm", [(12, 4096, 1024, 1, True), (13, 12288, 512, 1, False),
+                                                (14, 4096, 512, 1, False), (12, 4096, 512, 3, False),
+                                                (12, 4096, 512, 8, True), (13, 4096, 256, 6, False),
+                                                (14, 4096, 256, 16, True)])
+def test_wide_dynamic_range_activations(env, mode, t, k, n, members, norm):
+    """Outlier channels and wide dynamic range inside scale groups and blocks,
+    the case where block fixed point drops the small values. GEMV_WARP holds
+    f32-level agreement with the oracle (normwise 5e-5); GEMV_FIXED16 (wave
+    kernel below 5 members, matrix cores from 5) the 1e-3 bar. (The f32
+    paths differ from the oracle only in summation order; Q6_K's (q - 32)
+    offset enters as S - 32 X per 16-element group, which cancels more.)"""
+    print_case(test="wide_range", mode=mode, t=t, k=k, n=n, m=members, norm=norm)
+    E = env["E"]
+    kern = env["k"][t]
+    enc = synth.kquant_numpy(t, k, n, seed=3 * k + n + t)
+    x = np.stack([wide_range_activations(k, seed=m + 10 * t) for m in range(members)])
+    gam = synth.gamma_numpy(k, seed=9)
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(members * n)
+    kern.set_mode(E.GEMV_FIXED16 if mode == "fixed16" else E.GEMV_WARP)
+    try:
+        if norm:
+            kern.execute_rms_norm(w, to_dev(x.reshape(-1)), to_dev(gam), 1e-6, y, members)
+        else:
+            kern.execute_warp_batch(w, to_dev(x.reshape(-1)), y, members)
+    finally:
+        kern.set_mode(E.GEMV_WARP)
+    got = to_host(y, env["ctx"]).reshape(members, n)
+    for m in range(members):
+        src = O.rms_norm_raw(x[m], gam, 1e-6) if norm else x[m]
+        ref = O.quant_gemv(t, enc, k, n, src, threads=8)
+        err = max_rel_err(got[m], ref)
+        print(f"member {m} max_rel_err={err:.3e}", flush=True)
+        assert err <= (5e-5 if mode == "warp" else RTOL), (m, err)
+
+
+@pytest.mark.parametrize("t,k,ns", [(12, 4096, (4096, 1024, 1024)), (12, 4096, (12288,)), (13, 12288, (4096,)),
+                                    (14, 4096, (151936,))])
+def test_eight_members_bit_identical_at_qwen3_shapes(env, t, k, ns):
+    """Eight members (the reference's batch cap) at the decode step's shapes:
+    every row bit-identical to its single-member call (q/k/v group, gate or up,
+    the 12288-wide down projection, the lm_head), and a row sample within the
+    bar of the oracle."""
+    members = 8
+    print_case(test="eight_members", t=t, k=k, ns=ns)
+    encs = [synth.kquant_numpy(t, k, n, seed=n + 3) for n in ns]
+    ws = [upload(env, t, k, n, e) for n, e in zip(ns, encs)]
+    x = synth.activations_numpy(k, members, seed=11)
+    gam = synth.gamma_numpy(k, seed=12)
+    xd, gd = to_dev(x.reshape(-1)), to_dev(gam)
+    outs = [empty_dev(members * n) for n in ns]
+    env["k"][t].execute_group(ws, xd, outs, members, gd, 1e-6)
+    for w, n, o, e in zip(ws, ns, outs, encs):
+        got = to_host(o, env["ctx"]).reshape(members, n)
+        rows = _row_sample(n, 400, seed=n)
+        for m in (0, members - 1):
+            single = empty_dev(n)
+            env["k"][t].execute_rms_norm(w, to_dev(x[m]), gd, 1e-6, single, 1)
+            assert np.array_equal(to_host(single, env["ctx"]).view(np.uint32), got[m].view(np.uint32)), m
+            ref = _oracle_rows(t, e, k, n, O.rms_norm_raw(x[m], gam, 1e-6), rows)
+            assert max_rel_err(got[m][rows], ref) <= RTOL
+
+
+@pytest.mark.parametrize("t,k,n,members", [(12, 4096, 4096, 1), (13, 12288, 4096, 2), (14, 4096, 1024, 4),
+                                           (12, 2048, 333, 3)])
+def test_fixed16_wave_gemv_against_oracle(env, t, k, n, members):
+    """The opt-in GEMV_FIXED16 mode on its wave kernel (below the matrix-core
+    member counts): within the bar of the oracle, rows bit-identical to the
+    single-member call."""
+    E = env["E"]
+    kern = env["k"][t]
+    print_case(test="fixed16_wave", t=t, k=k, n=n, m=members)
+    enc = synth.kquant_numpy(t, k, n, seed=k + n)
+    x = synth.activations_numpy(k, members, seed=2)
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(members * n)
+    one = empty_dev(n)
+    kern.set_mode(E.GEMV_FIXED16)
+    try:
+        assert kern.mode() == E.GEMV_FIXED16
+        kern.execute_warp_batch(w, to_dev(x.reshape(-1)), y, members)
+        kern.execute_warp(w, to_dev(x[members - 1]), one)
+    finally:
+        kern.set_mode(E.GEMV_WARP)
+    got = to_host(y, env["ctx"]).reshape(members, n)
+    assert np.array_equal(to_host(one, env["ctx"]).view(np.uint32), got[members - 1].view(np.uint32))
+    for m in range(members):
+        assert max_rel_err(got[m], O.quant_gemv(t, enc, k, n, x[m], threads=8)) <= RTOL
+
+
+def test_gemv_mode_errors(env):
+    E = env["E"]
+    with pytest.raises(E.AmdQuantizedKernelError) as e:
+        env["k"][12].set_mode(7)
+    assert e.value.kind == "InvalidArgument" and e.value.actual == 7
+    assert env["k"][12].mode() == E.GEMV_WARP

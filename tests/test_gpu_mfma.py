@@ -1,5 +1,5 @@
 """GPU parity tests of the batched matrix-core GEMV (engine_amd/csrc/gemv_mfma.hip),
-which serves Q4_K / Q5_K / Q6_K batches of 5..16 members (4..16 when K spans more
+which, in the opt-in GEMV_FIXED16 mode, serves Q4_K / Q5_K / Q6_K batches of 5..16 members (4..16 when K spans more
 than one 4096 slice) through the same C-ABI entry points as the wave GEMV
 (execute_warp_batch, execute_rms_norm, execute_group, execute_fused,
 execute_gate_up_swiglu). Every case asserts that it takes that path. Up to 8
@@ -31,6 +31,8 @@ def env():
     ctx = E.AmdContext(0)
     store = E.AmdWeightStore(ctx)
     kernels = {t: E.QwenGemvKernel.from_value_type(ctx, t) for t in (12, 13, 14)}
+    for kern in kernels.values():
+        kern.set_mode(E.GEMV_FIXED16)  # the matrix cores serve the opt-in fixed-point mode
     return {"E": E, "ctx": ctx, "store": store, "k": kernels, "n": [0]}
 
 

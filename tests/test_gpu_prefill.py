@@ -104,6 +104,44 @@ def test_prefill_config3_full_size(env, t, k, n):
     assert np.all(np.isfinite(got))
 
 
+@pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096)])
+def test_batched_ffn_m64_full_size(env, t, k, n):
+    """BASELINE config 2 at M = 64 on the Qwen3-8B FFN shapes (gate/up Q4_K
+    4096 -> 12288, down Q5_K 12288 -> 4096, f32 activations, RMSNorm fused on
+    gate/up): the f16 matrix-core matmul and the batched GEMV (GEMV_WARP,
+    launch groups of 8 or 2 members) against the oracle on a token sample,
+    and batched rows bit-identical to single-member calls."""
+    m = 64
+    print("CASE batched m64", t, k, n, flush=True)
+    enc = synth.kquant_numpy(t, k, n, seed=640 + t)
+    w = upload(env, t, k, n, enc)
+    x = synth.activations_numpy(k, m, seed=64)
+    gamma = synth.gamma_numpy(k, seed=65) if t == 12 else None
+    xd = to_dev(x)
+    y = empty_dev(m * n)
+    env["k"][t].gemm_prefill(w, xd, y, m, gamma=to_dev(gamma) if gamma is not None else None, epsilon=1e-6)
+    got = to_host(y, env["ctx"]).reshape(m, n)
+    yb = empty_dev(m * n)
+    if gamma is not None:
+        env["k"][t].execute_rms_norm(w, xd, to_dev(gamma), 1e-6, yb, m)
+    else:
+        env["k"][t].execute_warp_batch(w, xd, yb, m)
+    batched = to_host(yb, env["ctx"]).reshape(m, n)
+    sample = [0, 1, 7, 8, 31, 40, 63]
+    for i in sample:
+        src = O.rms_norm_raw(x[i], gamma, 1e-6) if gamma is not None else x[i]
+        ref = O.quant_gemv(t, enc, k, n, src, threads=16)
+        assert max_rel_err(got[i], ref) <= RTOL, ("matmul", i)
+        assert max_rel_err(batched[i], ref) <= RTOL, ("batched", i)
+    for i in (0, 63):
+        one = empty_dev(n)
+        if gamma is not None:
+            env["k"][t].execute_rms_norm(w, to_dev(x[i]), to_dev(gamma), 1e-6, one, 1)
+        else:
+            env["k"][t].execute_warp(w, to_dev(x[i]), one)
+        assert np.array_equal(to_host(one, env["ctx"]).view(np.uint32), batched[i].view(np.uint32))
+
+
 def test_prefill_matches_wave_gemv_rows(env):
     # the two paths agree on the same tokens (both within tolerance of f32)
     k, n, m = 4096, 512, 8

@@ -16,7 +16,9 @@ same way):
     reused, the KV budget and the reference's error cases hold, and the
     dispatcher stays usable after each rejected submission;
   * the adapter (AmdBackend) over the dispatcher produces completion events;
-  * the loading-time memory plan.
+  * the loading-time memory plan;
+  * handles destroyed in any order (the context first, or by the cycle
+    collector) leave serving working and every destroy safe.
 """
 import numpy as np
 import pytest
@@ -66,7 +68,6 @@ def build_decoder(env, w, max_members):
                 "attn_q_norm", "attn_k_norm", "ffn_norm")} for l in range(TINY["layers"])]
     dec = E.AmdQwen3Decode(env["ctx"], E.AmdQwen3Config(**TINY), handles["token_embd"], handles["output"],
                            handles["output_norm"], layers, max_members)
-    dec._handles = handles
     return dec
 
 
@@ -332,32 +333,38 @@ def test_memory_plan(env):
     assert e.value.status == 37
 
 
-@pytest.mark.skip(reason="a child process started by the test process reports no ROCm device "
-                         "(hipGetDeviceCount) on the GPU box, so the exit cannot be observed there")
-def test_handles_alive_at_interpreter_exit(env):
-    """A dispatcher, decoder and context still referenced when the
-    interpreter exits are leaked, not destroyed after the HIP runtime's own
-    teardown: the process exits cleanly."""
-    import os
-    import subprocess
-    import sys
-    print_case(test="serving_exit")
-    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    script = "\n".join([
-        "import engine_amd as E",
-        "from engine_amd import serving as S",
-        "from tests.decode_helpers import small_weights",
-        "from tests.test_gpu_serving import TINY, Request, build_decoder, run",
-        "ctx = E.AmdContext(0)",
-        "env = {'E': E, 'ctx': ctx, 'store': E.AmdWeightStore(ctx), 'n': [0]}",
-        "dec = build_decoder(env, small_weights(TINY, 5), max_members=2)",
-        "disp = S.AmdServingDispatcher(dec, 2)",
-        "r = Request([1, 2, 3])",
-        "run(disp, [r], [r.prefill()], submission=1)",
-        "KEEP = (disp, dec, env)",
-        "print('served', r.generated, flush=True)",
-    ])
-    out = subprocess.run([sys.executable, "-c", script], cwd=root, capture_output=True, text=True, timeout=180)
-    assert out.returncode == 0, (out.returncode, out.stdout[-500:], out.stderr[-2000:])
-    assert "served" in out.stdout
+def test_handles_destroyed_in_any_order(env):
+    """The context handle may go first: weights, kernels, the decoder and the
+    dispatcher keep its stream and scratch alive (reference-counted in the C
+    library), so serving continues and every later destroy is safe. Then the
+    same objects are dropped inside a reference cycle and collected, which
+    finalizes them in no particular order (as an exit-time collection
+    does)."""
+    import gc
+    print_case(test="destroy_order")
+    E = env["E"]
+    ctx = E.AmdContext(0, own_stream=True)
+    mine = {"E": E, "ctx": ctx, "store": E.AmdWeightStore(ctx), "n": [0]}
+    dec = build_decoder(mine, small_weights(TINY, 5), max_members=2)
+    disp = S.AmdServingDispatcher(dec, 4)
+    r = Request([1, 2, 3])
+    run(disp, [r], [r.prefill()], submission=1)
+    first = list(r.generated)
+    ctx.close()  # the caller's reference goes first
+    run(disp, [r], [r.decode()], submission=2)
+    run(disp, [r], [r.decode()])
+    assert len(r.generated) == len(first) + 2
+    disp.close()
+    dec.close()
+    mine["store"] = None
+    # a second set, left to the cycle collector
+    ctx2 = E.AmdContext(0, own_stream=True)
+    env2 = {"E": E, "ctx": ctx2, "store": E.AmdWeightStore(ctx2), "n": [0]}
+    dec2 = build_decoder(env2, small_weights(TINY, 6), max_members=1)
+    disp2 = S.AmdServingDispatcher(dec2, 2)
+    cycle = [ctx2, env2, dec2, disp2]
+    cycle.append(cycle)
+    del ctx2, env2, dec2, disp2, cycle
+    gc.collect()
+    env["ctx"].synchronize()
 
