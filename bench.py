@@ -19,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -136,49 +137,70 @@ def capture(torch, stream, fn):
     return g
 
 
+def _time_median(fn, budget_s, max_runs=20, min_runs=5, warmup=3):
+    """Median and minimum seconds of fn() after `warmup` runs: up to max_runs
+    runs within budget_s (at least min_runs)."""
+    for _ in range(warmup):
+        fn()
+    samples = []
+    t_end = time.perf_counter() + budget_s
+    while len(samples) < max_runs and (time.perf_counter() < t_end or len(samples) < min_runs):
+        t0 = time.perf_counter()
+        fn()
+        samples.append(time.perf_counter() - t0)
+    samples.sort()
+    return samples[len(samples) // 2], samples[0], len(samples)
+
+
 def cpu_baseline(seconds_budget=12.0):
-    """Reference CPU path (dequantize_block + sequential f32 dot) on one Qwen3-8B layer."""
+    """The reference's CPU path restated in C (oracle/kquant_oracle.c, built
+    -O2 -ffp-contract=off): dequantize_block per super-block, then the
+    sequential f32 dot (crates/gguf/src/lib.rs:520-661,
+    crates/nvidia/src/qwen_reference.rs:31-40). Primary input BASELINE
+    config 0 (one 4096x4096 Q4_K matvec) on 1 thread, as the reference runs
+    it; also on every host core (rows split across threads) and the config-1
+    layer (RMSNorm + the seven projections) on 1 thread."""
     import numpy as np
 
     from engine_amd import synth
     from oracle import kquant_oracle as O
 
-    mats = [(t, k, n, synth.kquant_numpy(t, k, n, seed=500 + i)) for i, (_, t, k, n, _) in enumerate(LAYER)]
+    nproc = os.cpu_count() or 1
+    threads_all = min(16, nproc)  # the GPU box grants 16 host threads per GPU
+    k0 = n0 = 4096
+    enc0 = synth.kquant_numpy(12, k0, n0, seed=500)
+    x0 = synth.activations_numpy(k0, 1, seed=501)[0]
+    bytes0 = launch_bytes(12, k0, n0)
+    med1, min1, runs1 = _time_median(lambda: O.quant_gemv(12, enc0, k0, n0, x0, threads=1), seconds_budget / 3)
+    med_all, _, runs_all = _time_median(lambda: O.quant_gemv(12, enc0, k0, n0, x0, threads=threads_all),
+                                        seconds_budget / 6)
+
+    mats = [(t, k, n, synth.kquant_numpy(t, k, n, seed=510 + i)) for i, (_, t, k, n, _) in enumerate(LAYER)]
     x = {k: synth.activations_numpy(k, 1, seed=k)[0] for k in (HIDDEN, FFN)}
     gamma = synth.gamma_numpy(HIDDEN, seed=9)
     layer_bytes = sum(launch_bytes(t, k, n) for t, k, n, _ in mats)
 
-    def one_layer(threads):
+    def one_layer():
         normed = O.rms_norm_raw(x[HIDDEN], gamma, EPS)
         for t, k, n, enc in mats:
-            src = normed if k == HIDDEN else x[FFN]
-            O.quant_gemv(t, enc, k, n, src, threads=threads)
+            O.quant_gemv(t, enc, k, n, normed if k == HIDDEN else x[FFN], threads=1)
 
-    results = {}
-    for threads in (1, min(16, os.cpu_count() or 1)):
-        for _ in range(2):
-            one_layer(threads)
-        samples = []
-        t_end = time.perf_counter() + seconds_budget / 2
-        while len(samples) < 20 and (time.perf_counter() < t_end or len(samples) < 5):
-            t0 = time.perf_counter()
-            one_layer(threads)
-            samples.append(time.perf_counter() - t0)
-        samples.sort()
-        med = samples[len(samples) // 2]
-        results[threads] = (med, samples[0], len(samples))
-    med1, min1, n1 = results[1]
-    threads_all = max(results)
-    med_all, _, _ = results[threads_all]
+    med_layer, _, runs_layer = _time_median(one_layer, seconds_budget / 2, max_runs=20, min_runs=3, warmup=1)
     return {
-        "value": layer_bytes / med1 / 1e9,
+        "value": round(bytes0 / med1 / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"one Qwen3-8B layer (RMSNorm + q,k,v,o,gate,up Q4_K + down Q5_K, {layer_bytes} B), "
-                   f"oracle/kquant_oracle.c -O2 -ffp-contract=off, median of {n1} runs "
-                   f"(min {layer_bytes / min1 / 1e9:.3f} GB/s); {1.0 / (36 * med1):.3f} layer-stacks/s"),
-        "all_cores": {"value": layer_bytes / med_all / 1e9, "cores": threads_all},
+        "sample": (f"BASELINE config 0: Q4_K 4096x4096 matvec ({bytes0} algorithmic bytes, "
+                   f"{2 * k0 * n0} flop), oracle/kquant_oracle.c -O2 -ffp-contract=off, 1 thread, "
+                   f"median of {runs1} runs after 3 warm-ups ({med1 * 1e3:.2f} ms; min {min1 * 1e3:.2f} ms)"),
+        "gflop_s": round(2 * k0 * n0 / med1 / 1e9, 3),
+        "all_cores": {"value": round(bytes0 / med_all / 1e9, 3), "unit": "GB/s", "cores": threads_all,
+                      "ms": round(med_all * 1e3, 3), "runs": runs_all},
+        "layer_1_thread": {"value": round(layer_bytes / med_layer / 1e9, 4), "unit": "GB/s", "bytes": layer_bytes,
+                           "ms": round(med_layer * 1e3, 2), "runs": runs_layer,
+                           "sample": "BASELINE config 1: RMSNorm + q,k,v,o,gate,up Q4_K + down Q5_K"},
+        "nproc": nproc,
         "host_cpu": _cpu_model(),
     }
 
@@ -299,39 +321,52 @@ def bench_batched(E, synth, torch, args):
         x = torch.randn(m, HIDDEN, device=dev, generator=gen)
         h = torch.randn(m, FFN, device=dev, generator=gen)
         g, u, d = (torch.empty(m * n, device=dev) for n in (FFN, FFN, HIDDEN))
+        runs = []
         if m <= 16:
-            path = ("wave GEMV" if m < 4 else "wave GEMV gate/up, matrix-core GEMV down" if m < 5
-                    else "matrix-core GEMV") + " (weights read once per launch)"
+            for mode in ("warp", "fixed16"):
+                if mode == "warp":
+                    path = ("f32 wave GEMV, weights read once per 8 members (2 for down's K = 12288)")
+                else:
+                    path = ("block fixed-point " + ("wave GEMV" if m < 4 else
+                            "wave GEMV gate/up, matrix-core GEMV down" if m < 5 else "matrix-core GEMV") +
+                            ", weights read once per launch")
 
-            def fn():
-                for ly in layers:
-                    k4.execute_group([ly["gate"], ly["up"]], x, [g, u], m)
-                    k5.execute_warp_batch(ly["down"], h, d, m)
+                def fn():
+                    for ly in layers:
+                        k4.execute_group([ly["gate"], ly["up"]], x, [g, u], m)
+                        k5.execute_warp_batch(ly["down"], h, d, m)
+                runs.append((mode, path, fn))
         else:
-            path = "matrix-core matmul (f16 MFMA)"
-
             def fn():
                 for ly in layers:
                     k4.gemm_prefill(ly["gate"], x, g, m)
                     k4.gemm_prefill(ly["up"], x, u, m)
                     k5.gemm_prefill(ly["down"], h, d, m)
-        us = _graph_time_us(torch, stream, fn, max(2, args.steps // 10)) / n_layers
-        per_m[m] = {"us_per_ffn": round(us, 2), "tokens_per_s": round(m * 1e6 / us, 1),
-                    "weight_GBps": round(wbytes / us / 1e3, 1),
-                    "tflops": round(2.0 * m * 3 * FFN * HIDDEN / us / 1e6, 2), "path": path}
-        log(f"bench batched: M={m} {us:.2f} us per FFN ({path})")
-    top = per_m[64]
+            runs.append(("f16-mfma", "matrix-core matmul (f16 MFMA, f32 accumulation)", fn))
+        per_m[m] = {}
+        for mode, path, fn in runs:
+            for kern in (k4, k5):
+                kern.set_mode(GEMV_MODES.get(mode, 0))
+            us = _graph_time_us(torch, stream, fn, max(2, args.steps // 10)) / n_layers
+            per_m[m][mode] = {"us_per_ffn": round(us, 2), "tokens_per_s": round(m * 1e6 / us, 1),
+                              "weight_GBps": round(wbytes / us / 1e3, 1),
+                              "tflops": round(2.0 * m * 3 * FFN * HIDDEN / us / 1e6, 2), "path": path}
+            log(f"bench batched: M={m} {mode}: {us:.2f} us per FFN ({path})")
+        for kern in (k4, k5):
+            kern.set_mode(0)
+    top = per_m[64]["f16-mfma"]
     return {
         "metric": "batched decode FFN throughput (BASELINE config 2), tokens/s at M=64",
         "value": top["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(top["us_per_ffn"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "i8dot4-f32 (M<5), i8-mfma-i32/f32 (5<=M<=16), f16-mfma-f32 (M=64)",
+        "vs_baseline": None,
+        "dtype": "f16-mfma-f32 (M=64); per_m also holds f32 (warp) and i8dot4 / i8-mfma (fixed16) for M<=16",
         "data": "synthetic",
         "config": {"workload": "qwen3-8b-ffn-batched", "ffn_weight_bytes": wbytes, "layers_cycled": n_layers,
                    "per_m": per_m},
-        "roofline": {"bound": "hbm", "achieved": per_m[1]["weight_GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(per_m[1]["weight_GBps"] / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "M=1 FFN (gate/up group + down)"},
+        "roofline": {"bound": "hbm", "achieved": per_m[1]["warp"]["weight_GBps"], "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(per_m[1]["warp"]["weight_GBps"] / PEAK_HBM_GBS, 4),
+                     "traffic": None, "kernel": "M=1 FFN (gate/up group + down), f32 wave GEMV"},
         "cpu_baseline": None,
     }
 
@@ -528,7 +563,8 @@ def bench_model(E, synth, torch, ctx, step, out_gamma, args):
         "metric": "Qwen3-8B-shaped Q4_K batch-1 decode tok/s (BASELINE config 4)",
         "value": b1["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.gen_tokens, "warmup": 1,
         "ms_per_step": b1["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "i8dot4-f32 GEMV, f16 KV, f32 attention", "data": "synthetic",
+        "dtype": ("f32" if args.gemv_mode == "warp" else "i8dot4-f32") + " GEMV, f16 KV, f32 attention",
+        "data": "synthetic",
         "config": {"workload": "qwen3-8b-decode-model", "layers": args.layers, "context": args.context,
                    "generated": args.gen_tokens, "batches": res},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -635,7 +671,8 @@ def bench_serving(E, synth, torch, ctx, step, out_gamma, args):
         "metric": "Qwen3-8B-shaped serving output tok/s (burst through the serving dispatcher)",
         "value": round(out_tokens / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": batches, "warmup": 1,
         "ms_per_step": round(wall * 1e3 / batches, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "i8dot4-f32 GEMV, f16 KV, f32 attention", "data": "synthetic",
+        "vs_baseline": None, "data": "synthetic",
+        "dtype": ("f32" if args.gemv_mode == "warp" else "i8dot4-f32") + " GEMV, f16 KV, f32 attention",
         "config": {"workload": "qwen3-8b-serving-burst", "layers": args.layers, "concurrency": args.concurrency,
                    "prompt_tokens": args.prompt_tokens, "output_tokens": args.tokens,
                    "prefill_chunk": args.prefill_chunk, "batch_tokens": args.batch_tokens,
@@ -683,6 +720,14 @@ def measured_traffic():
 
 
 def _cpu_model():
+    """`lscpu` model name of the host (falls back to /proc/cpuinfo)."""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -760,53 +805,56 @@ def main():
         print(json.dumps(bench_serving(E, synth, torch, ctx, step, out_gamma, args)), flush=True)
         return
 
-    with torch.cuda.stream(stream):
-        step.run()  # eager warm-up (and validation of every launch)
-    torch.cuda.synchronize()
-    graph = None if args.no_graph else capture(torch, stream, step.run)
-    graph_gu = None if args.no_graph else capture(torch, stream, step.run_gate_up)
-
-    def one():
-        if graph is not None:
-            graph.replay()
-        else:
-            step.run()
-
-    with torch.cuda.stream(stream):
-        for _ in range(args.warmup):
-            one()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        for _ in range(args.steps):
-            one()
-        end.record(stream)
-    torch.cuda.synchronize()
-    ms_total = start.elapsed_time(end)
-    ms_step = ms_total / args.steps
-    gbs = step.bytes_per_step / (ms_step * 1e-3) / 1e9
-    log(f"bench: {ms_step:.4f} ms/step, {gbs:.1f} GB/s")
-
-    # Dominant kernel: the RMSNorm-fused Q4_K gate+up group launch (4096 -> 2x12288),
-    # timed live with HIP events over back-to-back launches on the stream it runs on.
-    reps = 5
-    gate_up = graph_gu.replay if graph_gu is not None else step.run_gate_up
-    with torch.cuda.stream(stream):
-        gate_up()
-        s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s2.record(stream)
-        for _ in range(reps):
-            gate_up()
-        e2.record(stream)
-    torch.cuda.synchronize()
-    launches = reps * args.layers
-    us_launch = s2.elapsed_time(e2) * 1e3 / launches
     gu_bytes = 2 * (launch_bytes(12, HIDDEN, FFN) - 4 * HIDDEN) + 4 * HIDDEN
+
+    def measure(mode):
+        """ms per step of the 36-layer + lm_head GEMV chain, and mean us per
+        gate+up group launch (timed live with HIP events over back-to-back
+        launches on the stream they run on), in one GEMV mode."""
+        step.set_mode(GEMV_MODES[mode])
+        with torch.cuda.stream(stream):
+            step.run()  # eager warm-up (and validation of every launch)
+        torch.cuda.synchronize()
+        graph = None if args.no_graph else capture(torch, stream, step.run)
+        graph_gu = None if args.no_graph else capture(torch, stream, step.run_gate_up)
+        one = graph.replay if graph is not None else step.run
+        with torch.cuda.stream(stream):
+            for _ in range(args.warmup):
+                one()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            for _ in range(args.steps):
+                one()
+            end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / args.steps
+        reps = 5
+        gate_up = graph_gu.replay if graph_gu is not None else step.run_gate_up
+        with torch.cuda.stream(stream):
+            gate_up()
+            s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s2.record(stream)
+            for _ in range(reps):
+                gate_up()
+            e2.record(stream)
+        torch.cuda.synchronize()
+        return ms, s2.elapsed_time(e2) * 1e3 / (reps * args.layers), graph is not None
+
+    # The opt-in fixed-point mode first (for comparison), then the headline mode.
+    other = "fixed16" if args.gemv_mode == "warp" else "warp"
+    ms_o, us_o, _ = measure(other)
+    log(f"bench: {other} GEMV mode (comparison): {ms_o:.4f} ms/step, "
+        f"{step.bytes_per_step / (ms_o * 1e-3) / 1e9:.1f} GB/s, gate+up {us_o:.3f} us")
+    ms_step, us_launch, graphed = measure(args.gemv_mode)
+    gbs = step.bytes_per_step / (ms_step * 1e-3) / 1e9
+    log(f"bench: {args.gemv_mode} GEMV mode: {ms_step:.4f} ms/step, {gbs:.1f} GB/s, gate+up {us_launch:.3f} us")
     achieved = gu_bytes / (us_launch * 1e-6) / 1e9
     roofline = {
         "bound": "hbm",
-        "kernel": "gemv_wave_kernel<Q4_K, 1 member, fused RMSNorm>: gate+up group, 4096->2x12288",
+        "kernel": ("gemv_f32_kernel<Q4_K, 1 member, fused RMSNorm>" if args.gemv_mode == "warp" else
+                   "gemv_wave_kernel<Q4_K, 1 member, fused RMSNorm>") + ": gate+up group, 4096->2x12288",
         "achieved": round(achieved, 1),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
@@ -843,8 +891,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        # products: 4..6-bit quants x 16-bit fixed-point activations (v_dot4, int32); scales and sums f32
-        "dtype": "i8dot4-f32",
+        # warp: f32 activations x weights dequantised to f32 in registers, f32 FMAs;
+        # fixed16: 4..6-bit quants x 16-bit fixed-point activations (v_dot4, int32), scales f32
+        "dtype": "f32" if args.gemv_mode == "warp" else "i8dot4-f32",
         "data": "synthetic",
         "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
         # the full decoder (embedding, 36 layers with attention
@@ -853,6 +902,10 @@ def main():
         "decode_tok_s_b8": model[8]["tok_s"] if model else None,
         "decode_model": model,
         "gemv_chain_tok_s": round(1000.0 / ms_step, 2),
+        "gemv_mode": args.gemv_mode,
+        "comparison_mode": {"gemv_mode": other, "dtype": "i8dot4-f32" if other == "fixed16" else "f32",
+                            "value": round(step.bytes_per_step / (ms_o * 1e-3) / 1e9, 2), "unit": "GB/s",
+                            "ms_per_step": round(ms_o, 5), "gate_up_us": round(us_o, 3)},
         "config": {
             "workload": "qwen3-8b-decode-gemv-b1",
             "layers": args.layers,
@@ -862,7 +915,7 @@ def main():
             "rmsnorm": "fused into the q/k/v group, gate/up group and lm_head activation load, eps 1e-6",
             "bytes_per_step": step.bytes_per_step,
             "launches_per_step": 4 * args.layers + 1,
-            "hip_graph": graph is not None,
+            "hip_graph": graphed,
             "batch": 1,
         },
         "roofline": roofline,

@@ -664,9 +664,12 @@ hipError_t launch_few(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
         return F32Instance<T, MT, PRO, false, 2, 8, 2>::launch(a, cu_count, 1, stream);
     } else {
         if constexpr (MT == 1) {
+            // Long streams (the lm_head): a three-unit ring over 8-wave
+            // workgroups, one per CU (MI355X sweep over ring {2,3,4,6,8} x
+            // waves {4,8} x workgroups per CU {1,2,4}: 97 us for the Q6_K
+            // 4096 -> 151936 head, against 124 us for ring 8 x 4 waves).
             if (per_cu >= 128) {
-                if constexpr (T == kQ6K) return F32Instance<T, 1, PRO, true, 8, 4, 1, PAIR>::launch(a, cu_count, 1, stream);
-                return F32Instance<T, 1, PRO, true, 4, 8, 1, PAIR>::launch(a, cu_count, 4, stream);
+                return F32Instance<T, 1, PRO, true, (PAIR ? 4 : 3), 8, 1, PAIR>::launch(a, cu_count, 1, stream);
             }
         }
         return F32Instance<T, MT, PRO, true, 2, 8, 1, PAIR>::launch(a, cu_count, per_cu > 48 ? 2 : 1, stream);
