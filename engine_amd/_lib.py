@@ -133,6 +133,7 @@ SIGNATURES = {
     "ribn_amd_gemm_workspace_bytes": (_sz, [_sz, _sz, _sz]),
     "ribn_amd_context_reserve_prefill": (_i32, [_vp, _sz, _sz, _sz]),
     "ribn_amd_gemm_prefill": (_i32, [_vp, _vp, _vp, _u32, _sz, _sz, _vp, _sz, _f32, _vp, _sz]),
+    "ribn_amd_gemm_prefill_static": (_i32, [_vp, _vp, _vp, _u32, _sz, _sz, _vp, _sz, _f32, _vp, _sz]),
     "ribn_amd_embedding_create": (_i32, [_vp, _u32, _pvp]),
     "ribn_amd_embedding_destroy": (None, [_vp]),
     "ribn_amd_embedding_execute": (_i32, [_vp, _vp, _u32, _vp, _sz]),

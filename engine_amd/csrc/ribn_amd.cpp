@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -216,23 +217,58 @@ ribn_amd_status check_epsilon(float epsilon) {
     return RIBN_AMD_OK;
 }
 
+// ---- device scratch of the allocation-free prefill (ribn_amd_gemm_prefill_static)
+//
+// One file-scope array per device, resolved to its device address once per
+// device when a context is created there. Every call on a device shares it.
+constexpr size_t kStaticScratchBytes = (size_t)8 << 20;
+constexpr int kStaticScratchDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[kStaticScratchDevices];  // device address of `scratch` per device
+
+// With `device` current: looks up the device address of `scratch` (once).
+ribn_amd_status resolve_static_scratch(int device) {
+    if (device < 0 || device >= kStaticScratchDevices) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, kStaticScratchDevices, (uint64_t)device,
+                    "device %d is beyond the %d devices the static scratch table covers", device,
+                    kStaticScratchDevices);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device] != nullptr) return RIBN_AMD_OK;
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return driver(e, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) return fail(RIBN_AMD_DRIVER, 0, 0, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[device] = ptr;
+    return RIBN_AMD_OK;
+}
+
+void* static_scratch(int device) {
+    if (device < 0 || device >= kStaticScratchDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    return g_scratch_ptr[device];
+}
+
 ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_context** out) {
     hipDeviceProp_t prop;
     hipError_t e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return driver(e, "hipGetDeviceProperties");
-    void* scratch = nullptr;
+    void* ctx_scratch = nullptr;
     const size_t act_bytes = (ribn_amd::gemv_act_scratch_bytes() + 255) / 256 * 256;
     {
         DeviceGuard guard(device);
-        e = hipMalloc(&scratch, act_bytes + RIBN_AMD_MAX_BATCH_MEMBERS * sizeof(ribn_amd::AttnMember));
+        ribn_amd_status st = resolve_static_scratch(device);
+        if (st != RIBN_AMD_OK) return st;
+        e = hipMalloc(&ctx_scratch, act_bytes + RIBN_AMD_MAX_BATCH_MEMBERS * sizeof(ribn_amd::AttnMember));
         if (e != hipSuccess) return driver(e, "hipMalloc context scratch");
     }
     auto* ctx = new (std::nothrow) ribn_amd_context{device,  stream,  owns, prop.multiProcessorCount,
-                                                    nullptr, 0,       scratch,
-                                                    static_cast<char*>(scratch) + act_bytes};
+                                                    nullptr, 0,       ctx_scratch,
+                                                    static_cast<char*>(ctx_scratch) + act_bytes};
     if (!ctx) {
         DeviceGuard guard(device);
-        hipFree(scratch);
+        hipFree(ctx_scratch);
         return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
     }
     *out = ctx;
@@ -242,6 +278,47 @@ ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_
 }  // namespace ribn_amd_abi
 
 using namespace ribn_amd_abi;
+
+namespace {
+
+// Argument checks of the prefill entry points, in the order of the other
+// execute calls (quantized.rs:1755-1804), then the prefill limits.
+ribn_amd_status validate_prefill(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const void* input,
+                                 uint32_t input_dtype, size_t input_len, size_t members, const float* gamma,
+                                 size_t gamma_len, float epsilon, float* output, size_t output_len, uint64_t* k_out,
+                                 uint64_t* n_out) {
+    if (input_dtype != RIBN_AMD_F32 && input_dtype != RIBN_AMD_BF16) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, RIBN_AMD_BF16, input_dtype, "input dtype %u is neither f32 nor bf16",
+                    input_dtype);
+    }
+    uint64_t k, n;
+    // Pointer checks take f32 alignment for either dtype; rows of bf16 input
+    // are read one element at a time.
+    ribn_amd_status st = validate_launch(g, w, static_cast<const float*>(input), input_len, output, output_len,
+                                         members, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    if (members == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "prefill needs at least one token");
+    if (gamma != nullptr) {
+        st = check_device_ptr(g->ctx, gamma, "gamma");
+        if (st != RIBN_AMD_OK) return st;
+        if (gamma_len != k) {
+            return fail(RIBN_AMD_WEIGHT_LENGTH, k, gamma_len, "RMSNorm weight has %zu values, expected %llu",
+                        gamma_len, (unsigned long long)k);
+        }
+        st = check_epsilon(epsilon);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    if (k > (uint64_t)ribn_amd::kGemmMaxK || members > (size_t)std::numeric_limits<int>::max() / k ||
+        n > (uint64_t)std::numeric_limits<int>::max() || w->encoded_bytes > 0xffffffffull) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kGemmMaxK, k,
+                    "prefill supports K up to %d and tokens*K < 2^31", ribn_amd::kGemmMaxK);
+    }
+    *k_out = k;
+    *n_out = n;
+    return RIBN_AMD_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -935,32 +1012,10 @@ ribn_amd_status ribn_amd_dequantize(ribn_amd_gemv* g, const ribn_amd_quantized_w
 ribn_amd_status ribn_amd_gemm_prefill(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const void* input,
                                       uint32_t input_dtype, size_t input_len, size_t members, const float* gamma,
                                       size_t gamma_len, float epsilon, float* output, size_t output_len) {
-    if (input_dtype != RIBN_AMD_F32 && input_dtype != RIBN_AMD_BF16) {
-        return fail(RIBN_AMD_INVALID_ARGUMENT, RIBN_AMD_BF16, input_dtype, "input dtype %u is neither f32 nor bf16",
-                    input_dtype);
-    }
     uint64_t k, n;
-    // Pointer checks take f32 alignment for either dtype; rows of bf16 input
-    // are read one element at a time.
-    ribn_amd_status st = validate_launch(g, w, static_cast<const float*>(input), input_len, output, output_len,
-                                         members, &k, &n);
+    ribn_amd_status st = validate_prefill(g, w, input, input_dtype, input_len, members, gamma, gamma_len, epsilon,
+                                          output, output_len, &k, &n);
     if (st != RIBN_AMD_OK) return st;
-    if (members == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "prefill needs at least one token");
-    if (gamma != nullptr) {
-        st = check_device_ptr(g->ctx, gamma, "gamma");
-        if (st != RIBN_AMD_OK) return st;
-        if (gamma_len != k) {
-            return fail(RIBN_AMD_WEIGHT_LENGTH, k, gamma_len, "RMSNorm weight has %zu values, expected %llu",
-                        gamma_len, (unsigned long long)k);
-        }
-        st = check_epsilon(epsilon);
-        if (st != RIBN_AMD_OK) return st;
-    }
-    if (k > (uint64_t)ribn_amd::kGemmMaxK || members > (size_t)std::numeric_limits<int>::max() / k ||
-        n > (uint64_t)std::numeric_limits<int>::max() || w->encoded_bytes > 0xffffffffull) {
-        return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kGemmMaxK, k,
-                    "prefill supports K up to %d and tokens*K < 2^31", ribn_amd::kGemmMaxK);
-    }
     // the activation stage's part is required; split-K room is used as far as reserved
     const size_t need = ribn_amd::gemm_workspace_bytes(members, k, 0);
     if (need > g->ctx->workspace_bytes) {
@@ -976,6 +1031,34 @@ ribn_amd_status ribn_amd_gemm_prefill(ribn_amd_gemv* g, const ribn_amd_quantized
     e = ribn_amd::launch_qgemm((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, g->ctx->workspace,
                                g->ctx->workspace_bytes, output, (int)members, (int)n, (int)k, g->ctx->cu_count,
                                g->ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch prefill matmul");
+    return ok();
+}
+
+ribn_amd_status ribn_amd_gemm_prefill_static(ribn_amd_gemv* g, const ribn_amd_quantized_weight* w, const void* input,
+                                             uint32_t input_dtype, size_t input_len, size_t members,
+                                             const float* gamma, size_t gamma_len, float epsilon, float* output,
+                                             size_t output_len) {
+    uint64_t k, n;
+    ribn_amd_status st = validate_prefill(g, w, input, input_dtype, input_len, members, gamma, gamma_len, epsilon,
+                                          output, output_len, &k, &n);
+    if (st != RIBN_AMD_OK) return st;
+    // the f16 activations and per-token unscales must fit; split-K partials use what is left
+    const size_t need = ribn_amd::gemm_workspace_bytes(members, k, 0);
+    if (need > kStaticScratchBytes) {
+        return fail(RIBN_AMD_WORKSPACE_TOO_SMALL, kStaticScratchBytes, need,
+                    "allocation-free prefill of %zu tokens x K=%llu needs %zu scratch bytes; the static scratch "
+                    "holds %zu (use ribn_amd_gemm_prefill with a reserved workspace)",
+                    members, (unsigned long long)k, need, kStaticScratchBytes);
+    }
+    void* ptr = static_scratch(g->ctx->device);
+    if (ptr == nullptr) return fail(RIBN_AMD_DRIVER, 0, 0, "static scratch of device %d is unresolved", g->ctx->device);
+    DeviceGuard guard(g->ctx->device);
+    hipError_t e = ribn_amd::launch_act_f16(input_dtype == RIBN_AMD_BF16, input, gamma, epsilon, (int)members, (int)k,
+                                            ptr, g->ctx->stream);
+    if (e != hipSuccess) return driver(e, "launch prefill activation stage");
+    e = ribn_amd::launch_qgemm((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, ptr, kStaticScratchBytes,
+                               output, (int)members, (int)n, (int)k, g->ctx->cu_count, g->ctx->stream);
     if (e != hipSuccess) return driver(e, "launch prefill matmul");
     return ok();
 }

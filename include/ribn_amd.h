@@ -415,6 +415,22 @@ ribn_amd_status ribn_amd_gemm_prefill(ribn_amd_gemv *gemv, const ribn_amd_quanti
                                       const void *input, uint32_t input_dtype, size_t input_len, size_t members,
                                       const float *gamma, size_t gamma_len, float epsilon, float *output,
                                       size_t output_len);
+/* Allocation-free variant of ribn_amd_gemm_prefill. It has no counterpart in
+ * the reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, validation and kernels, but the f16 activations
+ * and split-K partials live in a static 8 MiB device array per GPU instead of
+ * the context's reserved workspace (no reserve call is needed). Limit: the
+ * activation stage, align256(members * K * 2) + align256(members * 4) bytes,
+ * must fit 8 MiB (e.g. 1024 tokens at K = 4096, 256 at K = 16384); larger
+ * calls return WorkspaceTooSmall { expected: 8 MiB, actual: bytes needed }
+ * before any launch. Split K uses what is left. Every call on a GPU shares
+ * that GPU's array (whatever the context or stream): calls that overlap in
+ * time on one GPU race; order them on one stream or synchronise. */
+ribn_amd_status ribn_amd_gemm_prefill_static(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
+                                             const void *input, uint32_t input_dtype, size_t input_len,
+                                             size_t members, const float *gamma, size_t gamma_len, float epsilon,
+                                             float *output, size_t output_len);
 
 /* ------------------------------------------------------------- embedding */
 
