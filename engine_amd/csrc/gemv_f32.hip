@@ -287,9 +287,14 @@ __device__ __forceinline__ void rows_dot(const RowData<T> (&d)[NR], int p, XF xf
 
 // ------------------------------------------------------------------ kernel
 
-template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP, bool PAIR>
+// SPLIT: K spans several slices and each workgroup takes one of them
+// (blockIdx.y); it stores each row's slice total P_s (before any RMSNorm
+// factor) to args.partial[s][members][rows], and f32_split_reduce_kernel adds
+// the slices in order. The result equals the one-launch form bit for bit.
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP, bool PAIR, bool SPLIT = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args) {
     static_assert(NBUF % GROUP == 0, "the ring holds whole row groups");
+    static_assert(!SPLIT || (ONE_SLICE && !PAIR && PRO == kProPlain), "slice splits are plain one-slice passes");
     static_assert(!PAIR || (ONE_SLICE && NBUF % 2 == 0), "pairs are whole ring slots of one-slice rows");
     static_assert(MT <= 2 || ONE_SLICE, "several members stage one slice");
     constexpr bool NORM = PRO == kProNorm;
@@ -308,6 +313,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
     const int K = args.K;
     const int nb = K >> 8;
     const int slices = ONE_SLICE ? 1 : (nb + 15) >> 4;
+    const int slice0 = SPLIT ? (int)blockIdx.y : 0;  // the slice this workgroup covers (SPLIT)
     const int members = args.members;
     const int p = lane & 3;
     const int bs = lane >> 2;
@@ -373,7 +379,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
     float4 uv[SWIGLU ? NBW : 1][SWIGLU ? MT : 1];
 #pragma unroll
     for (int k = 0; k < NBW; ++k) {
-        const int b = wave + WAVES * k;
+        const int b = 16 * slice0 + wave + WAVES * k;
         const int e = 256 * b + 4 * lane;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
@@ -396,7 +402,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
         int mat, local;
         locate(live_row ? row : r_begin, mat, local);
         const __amdgpu_buffer_rsrc_t rs = pick_w(mat);
-        const int b = lslice * 16 + bs;
+        const int b = (SPLIT ? slice0 : lslice) * 16 + bs;
         const bool live = live_row && b < nb;
         load_row<T>(dst, rs, live ? (uint32_t)local * row_bytes + (uint32_t)b * BB : kOutOfRange, p);
         if constexpr (ONE_SLICE) {
@@ -413,11 +419,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
     // per-block sums of squares for RMSNorm.
 #pragma unroll
     for (int k = 0; k < NBW; ++k) {
-        const int b = wave + WAVES * k;
+        const int b = 16 * slice0 + wave + WAVES * k;
         const int e = 256 * b + 4 * lane;
-        const int slice = b >> 4;
+        const int slice = (b >> 4) - slice0;  // staged slice (LDS index)
         int rec, pos;
-        f32_slot<T>(e - slice * kSliceElems, rec, pos);
+        f32_slot<T>(e - (b >> 4) * kSliceElems, rec, pos);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             float4 v = xv[k][m];
@@ -440,7 +446,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
             const float gsum = group_sum_f<T>(((v.x + v.y) + v.z) + v.w);
             // Blocks past K inside the last slice are staged as zeros: their
             // lanes multiply zero weights, and 0 * (stale LDS) could be NaN.
-            if (b < 16 * slices && m < members) {
+            if (b < 16 * (slice0 + slices) && m < members) {
                 float* dst = xs + ((m * slices + slice) * 64 + rec) * STRIDE;
                 *reinterpret_cast<float4*>(dst + pos) = v;
                 if ((lane & (F32Rec<T>::group / 4 - 1)) == 0) dst[64 + pos / F32Rec<T>::group] = gsum;
@@ -471,6 +477,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
     };
     // silu(gate) * up of one output row (model_ops.rs:316-328)
     auto swiglu = [](float g, float u) { return (g / (1.0f + expf(-g))) * u; };
+    const __amdgpu_buffer_rsrc_t partial_r =
+        make_rsrc(args.partial, SPLIT ? (uint32_t)gridDim.y * (uint32_t)members * (uint32_t)args.total_rows * 4u : 0u);
 
     if constexpr (!XREG) {
         // ---- several members, one slice: passes over the whole ring. Each
@@ -501,6 +509,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
                 const __amdgpu_buffer_rsrc_t yr = pick_y(PAIR ? 0 : mat, rows_mat);
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
+                    if constexpr (SPLIT) {
+                        const float ps = wave_sum_uniform(part[r][m]);
+                        const uint32_t off =
+                            (live && lane == 0 && m < members)
+                                ? (uint32_t)((slice0 * members + m) * args.total_rows + row) * 4u
+                                : kOutOfRange;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ps), partial_r, (int)off, 0, 0);
+                        continue;
+                    }
                     const float total = wave_sum_uniform(part[r][m]) * inv[m];
                     const uint32_t off = (live && lane == 0 && m < members)
                                              ? (uint32_t)(m * rows_mat + local) * 4u
@@ -621,12 +638,13 @@ size_t f32_lds_bytes(int members, int K) {
     return (size_t)members * slices * 64 * F32Rec<T>::stride * sizeof(float);
 }
 
-template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP = 1, bool PAIR = false>
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP = 1, bool PAIR = false,
+          bool SPLIT = false>
 struct F32Instance {
     static std::atomic<int> occupancy;  // resident workgroups per CU at the largest LDS size (0: not queried)
     static hipError_t launch(const WaveGemvArgs& a, int cu_count, int per_cu, hipStream_t stream) {
-        auto kern = gemv_f32_kernel<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP, PAIR>;
-        const size_t lds = f32_lds_bytes<T>(MT, a.K);
+        auto kern = gemv_f32_kernel<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP, PAIR, SPLIT>;
+        const size_t lds = f32_lds_bytes<T>(MT, ONE_SLICE ? std::min(a.K, (int)kSliceElems) : a.K);
         int occ = occupancy.load(std::memory_order_relaxed);
         if (occ == 0) {
             const int max_lds = (int)f32_lds_bytes<T>(MT, ONE_SLICE ? kSliceElems : kWaveMaxK);
@@ -647,12 +665,44 @@ struct F32Instance {
                                                                (long long)per_cu});
         }
         if (grid < 1) grid = 1;
-        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WAVES * 64), lds, stream, a);
+        unsigned gy = 1;
+        if constexpr (SPLIT) {
+            // one slice per grid row; about one workgroup per CU in all
+            gy = (unsigned)(((a.K >> 8) + 15) >> 4);
+            grid = std::max<long long>(1, std::min<long long>(want, cu_count / (long long)gy));
+        }
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid, gy), dim3(WAVES * 64), lds, stream, a);
         return hipGetLastError();
     }
 };
-template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP, bool PAIR>
-std::atomic<int> F32Instance<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP, PAIR>::occupancy{0};
+template <int T, int MT, int PRO, bool ONE_SLICE, int NBUF, int WAVES, int GROUP, bool PAIR, bool SPLIT>
+std::atomic<int> F32Instance<T, MT, PRO, ONE_SLICE, NBUF, WAVES, GROUP, PAIR, SPLIT>::occupancy{0};
+
+// y[m][row] (+)= ((P_0 + P_1) + P_2) ... over the slices of a SPLIT launch,
+// in slice order: the slice totals of the one-launch form, added the same way.
+__global__ __launch_bounds__(256) void f32_split_reduce_kernel(WaveGemvArgs a, int slices) {
+    const int total = a.members * a.total_rows;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+        const int m = i / a.total_rows;
+        const int row = i - m * a.total_rows;
+        float t = a.partial[(size_t)m * a.total_rows + row];
+        for (int s = 1; s < slices; ++s) t = t + a.partial[((size_t)s * a.members + m) * a.total_rows + row];
+        int mat = 0, start = 0;
+        for (int g = 0; g + 1 < a.count; ++g) {
+            if (row >= a.rows_end[g]) {
+                mat = g + 1;
+                start = a.rows_end[g];
+            }
+        }
+        float* y = a.y[0];
+        for (int g = 1; g < kMaxGroup; ++g) {
+            if (mat == g) y = a.y[g];
+        }
+        const int rows_mat = a.rows_end[mat] - start;
+        float* dst = y + (size_t)m * rows_mat + (row - start);
+        *dst = a.accumulate ? *dst + t : t;
+    }
+}
 
 // One or two members.
 template <int T, int MT, int PRO, bool ONE_SLICE, bool PAIR = false>
@@ -725,7 +775,41 @@ hipError_t launch_type(const WaveGemvArgs& a, int cu_count, hipStream_t stream) 
     return launch_plain<T, kProPlain>(a, cu_count, stream);
 }
 
+// Three to eight members over a K of several slices: one workgroup per
+// (row range, slice), then the ordered slice reduction.
+template <int T>
+hipError_t launch_split(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
+    hipError_t e = (a.members <= 4)
+                       ? F32Instance<T, 4, kProPlain, true, 4, 8, 1, false, true>::launch(a, cu_count, 1, stream)
+                       : F32Instance<T, 8, kProPlain, true, (T == kQ4K ? 4 : 2), 8, 1, false, true>::launch(
+                             a, cu_count, 1, stream);
+    if (e != hipSuccess) return e;
+    const int slices = ((a.K >> 8) + 15) >> 4;
+    const long long total = (long long)a.members * a.total_rows;
+    const unsigned grid = (unsigned)std::min<long long>((total + 255) / 256, (long long)cu_count * 4);
+    hipLaunchKernelGGL(f32_split_reduce_kernel, dim3(grid), dim3(256), 0, stream, a, slices);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+size_t f32_split_partial_bytes(int members, int K, int total_rows) {
+    const int slices = ((K >> 8) + 15) >> 4;
+    return (size_t)slices * members * total_rows * sizeof(float);
+}
+
+hipError_t launch_gemv_f32_split(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream) {
+    if (args.members < 3 || args.members > kWaveMaxMembers || args.K <= kSliceElems || args.K > kWaveMaxK ||
+        args.gamma != nullptr || args.x2 != nullptr || args.pair_swiglu || args.partial == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    switch (value_type) {
+    case kQ4K: return launch_split<kQ4K>(args, cu_count, stream);
+    case kQ5K: return launch_split<kQ5K>(args, cu_count, stream);
+    case kQ6K: return launch_split<kQ6K>(args, cu_count, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
 
 int f32_max_members(int K) {
     if (K < 256 || K > kWaveMaxK) return 0;

@@ -693,13 +693,18 @@ hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& a, int /*cu_coun
 
 // ------------------------------------------------------------ dispatcher
 
-size_t gemv_act_scratch_bytes() { return act16_layout(kMfmaMaxMembers, kWaveMaxK).total; }
+// The context scratch serves either the packed activations of the matrix-core
+// GEMV or the slice totals of a split f32 launch (never both in one call).
+constexpr size_t kF32SplitScratchBytes = (size_t)2 << 20;
+size_t gemv_act_scratch_bytes() {
+    return std::max<size_t>(act16_layout(kMfmaMaxMembers, kWaveMaxK).total, kF32SplitScratchBytes);
+}
 
 int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith) {
     if (arith == kArithF32) {
-        int per = f32_max_members(K);
-        if (swiglu_prologue) per = std::min(per, kSwigluMaxMembers);
-        return per;
+        if (K < 256 || K > kWaveMaxK) return 0;
+        // launch_gemv splits larger calls into the launch groups each form stages
+        return swiglu_prologue ? kSwigluMaxMembers : kWaveMaxMembers;
     }
     if (!swiglu_prologue && gemv_mfma_supported(value_type) && K % 256 == 0 && K <= kWaveMaxK) {
         return kMfmaMaxMembers;
@@ -711,10 +716,16 @@ int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith) 
 
 hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch, int cu_count, hipStream_t stream) {
     if (a.arith == kArithF32) {
-        // the f32 wave GEMV, in launch groups of as many members as it stages
+        // the f32 wave GEMV, in launch groups of as many members as it stages;
+        // 3..8 members over a K of several slices split by slice when the
+        // context scratch holds their slice totals
         int per = f32_max_members(a.K);
         if (a.x2 != nullptr) per = std::min(per, kSwigluMaxMembers);
         if (per <= 0) return hipErrorInvalidValue;
+        const bool splittable = a.K > kSliceK && a.x2 == nullptr && a.gamma == nullptr && !a.pair_swiglu &&
+                                act_scratch != nullptr &&
+                                f32_split_partial_bytes(kWaveMaxMembers, a.K, a.total_rows) <= kF32SplitScratchBytes;
+        if (splittable) per = kWaveMaxMembers;
         for (int m0 = 0; m0 < a.members; m0 += per) {
             WaveGemvArgs c = a;
             c.members = std::min(per, a.members - m0);
@@ -724,7 +735,26 @@ hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch,
                 const int n = a.rows_end[i] - (i > 0 ? a.rows_end[i - 1] : 0);
                 c.y[i] = a.y[i] + (size_t)m0 * (a.pair_swiglu ? a.rows_end[0] : n);
             }
-            hipError_t e = launch_gemv_f32(value_type, c, cu_count, stream);
+            hipError_t e;
+            if (splittable && c.members > 2) {
+                c.partial = static_cast<float*>(act_scratch);
+                e = launch_gemv_f32_split(value_type, c, cu_count, stream);
+            } else if (c.members > f32_max_members(a.K)) {
+                // two-member groups of the one-launch form
+                e = hipSuccess;
+                for (int j = 0; j < c.members && e == hipSuccess; j += 2) {
+                    WaveGemvArgs d = c;
+                    d.members = std::min(2, c.members - j);
+                    d.x = c.x + (size_t)j * a.K;
+                    for (int i = 0; i < a.count; ++i) {
+                        const int n = a.rows_end[i] - (i > 0 ? a.rows_end[i - 1] : 0);
+                        d.y[i] = c.y[i] + (size_t)j * n;
+                    }
+                    e = launch_gemv_f32(value_type, d, cu_count, stream);
+                }
+            } else {
+                e = launch_gemv_f32(value_type, c, cu_count, stream);
+            }
             if (e != hipSuccess) return e;
         }
         return hipSuccess;

@@ -48,6 +48,8 @@ struct WaveGemvArgs {
     // Arithmetic: kArithF32 (f32 activations, the default) or kArithFixed16
     // (block fixed-point activations with integer dot products, opt-in).
     int arith;
+    // f32 launches split by slice: [slices][members][total_rows] slice totals
+    float* partial;
 };
 
 constexpr int kArithF32 = 0;
@@ -57,6 +59,11 @@ constexpr int kArithFixed16 = 1;
 int f32_max_members(int K);
 // The f32-activation wave GEMV (gemv_f32.hip); members <= f32_max_members(K).
 hipError_t launch_gemv_f32(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
+// Its slice-split form for 3..8 members over K spanning several slices (plain
+// prologue, no pairs): args.partial holds f32_split_partial_bytes of slice
+// totals, which a second launch adds in slice order into y.
+size_t f32_split_partial_bytes(int members, int K, int total_rows);
+hipError_t launch_gemv_f32_split(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
 
 // Largest member count one wave launch can stage for this K (0 if none).
 int wave_max_members(int K);

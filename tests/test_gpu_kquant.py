@@ -425,30 +425,36 @@ def test_wide_dynamic_range_activations(env, mode, t, k, n, members, norm):
         assert err <= (5e-5 if mode == "warp" else RTOL), (m, err)
 
 
-@pytest.mark.parametrize("t,k,ns", [(12, 4096, (4096, 1024, 1024)), (12, 4096, (12288,)), (13, 12288, (4096,)),
-                                    (14, 4096, (151936,))])
-def test_eight_members_bit_identical_at_qwen3_shapes(env, t, k, ns):
-    """Eight members (the reference's batch cap) at the decode step's shapes:
-    every row bit-identical to its single-member call (q/k/v group, gate or up,
-    the 12288-wide down projection, the lm_head), and a row sample within the
-    bar of the oracle."""
-    members = 8
-    print_case(test="eight_members", t=t, k=k, ns=ns)
+@pytest.mark.parametrize("t,k,ns,members,norm", [(12, 4096, (4096, 1024, 1024), 8, True), (12, 4096, (12288,), 8, True),
+                                                  (13, 12288, (4096,), 8, True), (13, 12288, (4096,), 8, False),
+                                                  (13, 12288, (4096, 100), 5, False), (12, 8192, (700,), 3, False),
+                                                  (14, 4096, (151936,), 8, True)])
+def test_eight_members_bit_identical_at_qwen3_shapes(env, t, k, ns, members, norm):
+    """Up to eight members (the reference's batch cap) at the decode step's
+    shapes: every row bit-identical to its single-member call (q/k/v group,
+    gate or up, the 12288-wide down projection with and without RMSNorm --
+    plain long-K batches split by slice -- the lm_head), and a row sample
+    within the bar of the oracle."""
+    print_case(test="eight_members", t=t, k=k, ns=ns, m=members, norm=norm)
     encs = [synth.kquant_numpy(t, k, n, seed=n + 3) for n in ns]
     ws = [upload(env, t, k, n, e) for n, e in zip(ns, encs)]
     x = synth.activations_numpy(k, members, seed=11)
     gam = synth.gamma_numpy(k, seed=12)
     xd, gd = to_dev(x.reshape(-1)), to_dev(gam)
     outs = [empty_dev(members * n) for n in ns]
-    env["k"][t].execute_group(ws, xd, outs, members, gd, 1e-6)
+    env["k"][t].execute_group(ws, xd, outs, members, gd if norm else None, 1e-6)
     for w, n, o, e in zip(ws, ns, outs, encs):
         got = to_host(o, env["ctx"]).reshape(members, n)
         rows = _row_sample(n, 400, seed=n)
         for m in (0, members - 1):
             single = empty_dev(n)
-            env["k"][t].execute_rms_norm(w, to_dev(x[m]), gd, 1e-6, single, 1)
+            if norm:
+                env["k"][t].execute_rms_norm(w, to_dev(x[m]), gd, 1e-6, single, 1)
+            else:
+                env["k"][t].execute_warp(w, to_dev(x[m]), single)
             assert np.array_equal(to_host(single, env["ctx"]).view(np.uint32), got[m].view(np.uint32)), m
-            ref = _oracle_rows(t, e, k, n, O.rms_norm_raw(x[m], gam, 1e-6), rows)
+            src = O.rms_norm_raw(x[m], gam, 1e-6) if norm else x[m]
+            ref = _oracle_rows(t, e, k, n, src, rows)
             assert max_rel_err(got[m][rows], ref) <= RTOL
 
 
