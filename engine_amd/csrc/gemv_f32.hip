@@ -368,6 +368,28 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
         return make_rsrc(y, (uint32_t)members * (uint32_t)rows_mat * 4u);
     };
 
+    // Rows only move forward in one-slice launches, so the matrix of the
+    // current row (and its weight / output resources) is tracked by cursors
+    // that change only at matrix boundaries instead of being selected per unit.
+    struct Cursor {
+        int mat, start, end;
+        __amdgpu_buffer_rsrc_t rs;
+        int rows_mat;
+    };
+    auto cursor_at = [&](int row, bool out) {
+        Cursor c;
+        int local;
+        locate(row, c.mat, local);
+        c.start = row - local;
+        const __amdgpu_buffer_rsrc_t yr = pick_y(c.mat, c.rows_mat);
+        c.end = c.start + c.rows_mat;
+        c.rs = out ? yr : pick_w(c.mat);
+        return c;
+    };
+    auto seek = [&](Cursor& c, int row, bool out) {
+        if (row >= c.end && c.mat + 1 < args.count) c = cursor_at(row, out);
+    };
+
     // ---- activation loads first (vector memory returns in order, so the
     // staging waits for these, not for the weight loads issued after them).
     // Wave w stages super-blocks w, w + WAVES, ... of every member.
@@ -396,12 +418,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
     // exactly the unit reduced next.
     RowData<T> ring[NBUF];
     int lrow = r_begin, lslice = 0;
+    constexpr bool kCursor = ONE_SLICE && !PAIR;
+    Cursor lcur = cursor_at(r_begin, false);
+    Cursor ccur = cursor_at(r_begin, true);
+    // gate/up pairs: the two weights alternate row by row into one output
+    const __amdgpu_buffer_rsrc_t pair_w0 = make_rsrc(args.w[0], PAIR ? args.wbytes[0] : 0u);
+    const __amdgpu_buffer_rsrc_t pair_w1 = make_rsrc(args.w[1], PAIR ? args.wbytes[1] : 0u);
+    const int pair_rows = args.rows_end[0];
+    const __amdgpu_buffer_rsrc_t pair_y =
+        make_rsrc(args.y[0], PAIR ? (uint32_t)members * (uint32_t)pair_rows * 4u : 0u);
     auto load_next = [&](RowData<T>& dst, int r) {
         const int row = ONE_SLICE ? lrow : lrow + r % GROUP;
         const bool live_row = row < r_end;
         int mat, local;
-        locate(live_row ? row : r_begin, mat, local);
-        const __amdgpu_buffer_rsrc_t rs = pick_w(mat);
+        __amdgpu_buffer_rsrc_t rs;
+        if constexpr (kCursor) {
+            if (live_row) seek(lcur, row, false);
+            rs = lcur.rs;
+            local = row - lcur.start;
+        } else if constexpr (PAIR) {
+            rs = (row & 1) ? pair_w1 : pair_w0;
+            local = row >> 1;
+        } else {
+            locate(live_row ? row : r_begin, mat, local);
+            rs = pick_w(mat);
+        }
         const int b = (SPLIT ? slice0 : lslice) * 16 + bs;
         const bool live = live_row && b < nb;
         load_row<T>(dst, rs, live ? (uint32_t)local * row_bytes + (uint32_t)b * BB : kOutOfRange, p);
@@ -505,8 +546,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
                 const int row = crow + r;
                 const bool live = r < left && row < r_end;
                 int mat, local, rows_mat;
-                locate(live ? row : r_begin, mat, local);
-                const __amdgpu_buffer_rsrc_t yr = pick_y(PAIR ? 0 : mat, rows_mat);
+                __amdgpu_buffer_rsrc_t yr;
+                if constexpr (kCursor) {
+                    if (live) seek(ccur, row, true);
+                    yr = ccur.rs;
+                    local = row - ccur.start;
+                    rows_mat = ccur.rows_mat;
+                } else if constexpr (PAIR) {
+                    yr = pair_y;
+                    local = row >> 1;
+                    rows_mat = pair_rows;
+                } else {
+                    locate(live ? row : r_begin, mat, local);
+                    yr = pick_y(mat, rows_mat);
+                }
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     if constexpr (SPLIT) {
@@ -580,8 +633,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
             const int row = ONE_SLICE ? crow : crow + r % GROUP;
             const bool last = ONE_SLICE || cslice == slices - 1;
             int mat, local, rows_mat;
-            locate(row < r_end ? row : r_begin, mat, local);
-            const __amdgpu_buffer_rsrc_t yr = pick_y(PAIR ? 0 : mat, rows_mat);
+            __amdgpu_buffer_rsrc_t yr;
+            if constexpr (kCursor) {
+                if (row < r_end) seek(ccur, row, true);
+                yr = ccur.rs;
+                local = row - ccur.start;
+                rows_mat = ccur.rows_mat;
+            } else if constexpr (PAIR) {
+                yr = pair_y;
+                local = row >> 1;
+                rows_mat = pair_rows;
+            } else {
+                locate(row < r_end ? row : r_begin, mat, local);
+                yr = pick_y(mat, rows_mat);
+            }
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 const float ps = wave_sum_uniform(part[0][m]);
@@ -714,11 +779,14 @@ hipError_t launch_few(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
         return F32Instance<T, MT, PRO, false, 2, 8, 2>::launch(a, cu_count, 1, stream);
     } else {
         if constexpr (MT == 1) {
-            // Long streams (the lm_head): a three-unit ring over 8-wave
-            // workgroups, one per CU (MI355X sweep over ring {2,3,4,6,8} x
-            // waves {4,8} x workgroups per CU {1,2,4}: 97 us for the Q6_K
-            // 4096 -> 151936 head, against 124 us for ring 8 x 4 waves).
-            if (per_cu >= 128) {
+            // Streams of more than 48 units per CU (gate/up, the lm_head): a
+            // three-unit ring (four for gate/up pairs) over 8-wave workgroups,
+            // one per CU. MI355X sweep over ring {2,3,4,6,8} x waves {4,8,16} x
+            // workgroups per CU {1,2,4}: 13.3 us for the gate+up group
+            // (Q4_K 4096 -> 2 x 12288) against 14.3 us for ring 2 x 2 per CU,
+            // and 97 us for the Q6_K 4096 -> 151936 head against 124 us for
+            // ring 8 x 4 waves.
+            if (per_cu > 48) {
                 return F32Instance<T, 1, PRO, true, (PAIR ? 4 : 3), 8, 1, PAIR>::launch(a, cu_count, 1, stream);
             }
         }
