@@ -698,7 +698,7 @@ def bench_serving(E, synth, torch, ctx, step, out_gamma, args):
     return result
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_wave_q4k_gate_up_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_f32_q4k_gate_up_traffic.md")
 
 
 def measured_traffic():
