@@ -18,11 +18,11 @@
 // one 16-byte load of K and one of V, kRing steps in flight), and keeps an
 // online-softmax state (running max, denominator and output sums) per query
 // head, rescaled once per kRing-step block, with scores in log2 units so each
-// weight is one exp2. The 16 states of a workgroup are merged across
-// rows with lane shuffles and across waves in LDS into one partial per
+// weight is one exp2. The 16 row states of a workgroup meet in LDS and are
+// merged, in row order, into one partial per
 // (chunk, head); attn_combine_kernel then merges the chunks' partials of each
-// (member, head) into the output (a context within one chunk is written
-// directly). The new token's K/V are computed by the
+// (member, head) into the output (for a context within one chunk it divides
+// the one partial by its denominator). The new token's K/V are computed by the
 // workgroup whose chunk holds the position: written to the cache, and used
 // from LDS by that workgroup. For consecutive tokens of one sequence (a
 // prefill chunk) kv_append_kernel stores every member's K/V first and the
@@ -51,6 +51,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kRing = 4;                  // steps of K/V loads in flight per wave
 constexpr int kStepTokens = kWaves * 4;   // tokens a workgroup covers per step
+constexpr int kRows = kWaves * 4;         // 16-lane rows of a workgroup, one softmax state each
 // A chunk spans at least this many tokens (sweep on MI355X over workgroups of
 // 256/512 threads and 16-256-token minimum chunks: batch 1 at 2048 tokens is
 // fastest here, and short contexts need fewer chunks and merges).
@@ -85,21 +86,34 @@ __device__ __forceinline__ void unpack_f16x8(uint4 w, float (&f)[8]) {
     }
 }
 
+// NEOX rope angle of lane l's pair (l, l + 64): pos * base^(-2l/128)
+// (model_ops.rs:393-425). The frequency does not depend on the position, so a
+// kernel computes it while the position is still in flight; every head of a
+// lane shares the angle, so its sine and cosine are computed once.
+__device__ __forceinline__ float rope_freq(float base, int lane) {
+    return powf(base, -(2.0f * (float)lane) / (float)kHeadDim);
+}
+
+struct Rot {
+    float s, c;
+};
+
+__device__ __forceinline__ Rot rope_rot(float pos, float freq) {
+    Rot r;
+    sincosf(pos * freq, &r.s, &r.c);
+    return r;
+}
+
 // One 128-wide head held by a wave as lane l: x0 = dim l, x1 = dim l + 64.
 // RMSNorm with the shared per-head weight (x * inv * w, model_ops.rs:660-685),
-// then the NEOX rotation of the pair (l, l + 64) by pos * base^(-2l/128)
-// (model_ops.rs:393-425).
-__device__ __forceinline__ void norm_rope(float& x0, float& x1, float w0, float w1, float eps, float pos,
-                                          float base, int lane) {
+// then the rotation of the pair (l, l + 64) by the lane's angle.
+__device__ __forceinline__ void norm_rope(float& x0, float& x1, float w0, float w1, float eps, Rot r) {
     const float ssq = wave_sum(x0 * x0 + x1 * x1);
     const float inv = 1.0f / sqrtf(ssq / (float)kHeadDim + eps);
     const float y0 = x0 * inv * w0;
     const float y1 = x1 * inv * w1;
-    const float theta = pos * powf(base, -(2.0f * (float)lane) / (float)kHeadDim);
-    float s, c;
-    sincosf(theta, &s, &c);
-    x0 = y0 * c - y1 * s;
-    x1 = y0 * s + y1 * c;
+    x0 = y0 * r.c - y1 * r.s;
+    x1 = y0 * r.s + y1 * r.c;
 }
 
 template <int QPK>
@@ -107,9 +121,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     constexpr int kHeadsPerWave = (QPK + kWaves - 1) / kWaves;
     __shared__ float qs[QPK][kHeadDim];
     __shared__ float kv_new[2][kHeadDim];
-    __shared__ float st_m[kWaves][QPK];
-    __shared__ float st_l[kWaves][QPK];
-    __shared__ float st_o[kWaves][QPK][kHeadDim];
+    __shared__ float2 st_ml[kRows][QPK];  // each row's running maximum and denominator
+    __shared__ float st_o[kRows][QPK][kHeadDim];
 
     const int chunk = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -119,13 +132,14 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = lane >> 4;  // token slot of this lane's row
     const int j = lane & 15;    // dims 8j..8j+7
+    // the member's descriptor and position: two scalar loads, waited for
+    // together below
     const AttnMember mb = a.mem[m];
-    uint16_t* const keys = mb.keys + (size_t)a.layer * mb.layer_elems;
-    uint16_t* const values = mb.values + (size_t)a.layer * mb.layer_elems;
+    const int pos = a.positions[m];
 
-    // ---- loads that do not need the position go first: this workgroup's
-    // query heads and norm weight, and the new token's raw K (wave 0) and V
-    // (wave 1) with the K norm weight
+    // ---- work that does not need them goes first: this workgroup's query
+    // heads and norm weight, the new token's raw K (wave 0) and V (wave 1)
+    // with the K norm weight, and the lane's rope frequency
     const float* qm = a.q + ((size_t)m * a.q_heads + (size_t)kvh * QPK) * kHeadDim;
     float qx[kHeadsPerWave][2];
 #pragma unroll
@@ -139,6 +153,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     }
     const float qw0 = a.q_norm[lane];
     const float qw1 = a.q_norm[lane + 64];
+    const float freq = rope_freq(a.rope_base, lane);
     float nx0 = 0.f, nx1 = 0.f, kw0 = 0.f, kw1 = 0.f;
     if (wave < 2) {
         const float* src = (wave == 0 ? a.k : a.v) + ((size_t)m * a.kv_heads + kvh) * kHeadDim;
@@ -150,7 +165,12 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
         }
     }
 
-    const int pos = a.positions[m];
+    // Both scalar loads are needed from here on; without this use the compiler
+    // sinks the descriptor's load past the early exit below and waits twice.
+    asm volatile("" ::"s"(mb.keys), "s"(mb.values), "s"(mb.partials), "s"(mb.layer_elems), "s"(mb.capacity),
+                 "s"(pos), "v"(freq));
+    uint16_t* const keys = mb.keys + (size_t)a.layer * mb.layer_elems;
+    uint16_t* const values = mb.values + (size_t)a.layer * mb.layer_elems;
     const int tokens = pos + 1;
     const int len = chunk_tokens(tokens, a.chunks);
     const int t0 = chunk * len;
@@ -158,8 +178,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     const int t1 = min(t0 + len, tokens);
     const int steps = (t1 - t0 + kStepTokens - 1) / kStepTokens;
     const bool has_new = !a.appended && pos < t1;
-    // a context within one chunk is finished here; the merge launch skips it
-    const bool single = tokens <= len;
 
     // ---- cached K/V of this chunk: the first kRing steps are issued before
     // anything else. Unless appended, the new token's slot is not read (it is
@@ -181,18 +199,18 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
 
     // ---- query heads (and the new K/V): norm + rope into LDS
     const bool new_wave = has_new && wave < 2;  // wave 0: K, wave 1: V
-    const float fpos = (float)pos;
+    const Rot rot = rope_rot((float)pos, freq);
 #pragma unroll
     for (int i = 0; i < kHeadsPerWave; ++i) {
         const int h = wave + kWaves * i;
         if (h < QPK) {
-            norm_rope(qx[i][0], qx[i][1], qw0, qw1, a.eps, fpos, a.rope_base, lane);
+            norm_rope(qx[i][0], qx[i][1], qw0, qw1, a.eps, rot);
             qs[h][lane] = qx[i][0];
             qs[h][lane + 64] = qx[i][1];
         }
     }
     if (new_wave) {
-        if (wave == 0) norm_rope(nx0, nx1, kw0, kw1, a.eps, fpos, a.rope_base, lane);
+        if (wave == 0) norm_rope(nx0, nx1, kw0, kw1, a.eps, rot);
         // f16 round to nearest even, as kv_append_f16 stores it
         const _Float16 h0 = (_Float16)nx0;
         const _Float16 h1 = (_Float16)nx1;
@@ -284,66 +302,62 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
                 for (int i = 0; i < 8; ++i) o[h][i] = __builtin_fmaf(p, vf[i], o[h][i]);
             }
         }
+        // the next block's loads; none past the chunk, whose registers the
+        // merge below would otherwise wait for
+        if (s0 + kRing < steps) {
 #pragma unroll
-        for (int r = 0; r < kRing; ++r) issue(r, s0 + r + kRing);
+            for (int r = 0; r < kRing; ++r) issue(r, s0 + r + kRing);
+        }
     }
 
-    // ---- merge the four row states of each wave (lane xor 16, xor 32), then
-    // the waves' states through LDS into this chunk's partial
+    // ---- merge the workgroup's 16 row states (one per 16-lane row) through
+    // LDS into this chunk's partial: each row's maximum, denominator and
+    // output sums are scaled to the workgroup maximum and summed in row order
+    const int row = wave * 4 + grp;
 #pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
-#pragma unroll
-        for (int h = 0; h < QPK; ++h) {
-            const float m2 = __shfl_xor(mrun[h], off, 64);
-            const float l2 = __shfl_xor(lrun[h], off, 64);
-            const float mx = fmaxf(mrun[h], m2);
-            const float f1 = __builtin_amdgcn_exp2f(mrun[h] - mx);
-            const float f2 = __builtin_amdgcn_exp2f(m2 - mx);
-            lrun[h] = lrun[h] * f1 + l2 * f2;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float o2 = __shfl_xor(o[h][i], off, 64);
-                o[h][i] = o[h][i] * f1 + o2 * f2;
-            }
-            mrun[h] = mx;
-        }
-    }
-    if (grp == 0) {
-#pragma unroll
-        for (int h = 0; h < QPK; ++h) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) st_o[wave][h][8 * j + i] = o[h][i];
-            if (j == 0) {
-                st_m[wave][h] = mrun[h];
-                st_l[wave][h] = lrun[h];
-            }
-        }
+    for (int h = 0; h < QPK; ++h) {
+        float4* dst = reinterpret_cast<float4*>(&st_o[row][h][8 * j]);
+        dst[0] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+        dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+        if (j == 0) st_ml[row][h] = make_float2(mrun[h], lrun[h]);
     }
     __syncthreads();
-    float* outm = a.out + ((size_t)m * a.q_heads + (size_t)kvh * QPK) * kHeadDim;
-    for (int idx = tid; idx < QPK * kHeadDim; idx += kThreads) {
-        const int h = idx / kHeadDim;
-        const int d = idx - h * kHeadDim;
-        float* part = mb.partials + ((size_t)(kvh * QPK + h) * kAttnChunks + chunk) * kPartStride;
-        float mx = -FLT_MAX;
+    // A thread finishes kOut outputs of one head (d0 + kSpan * u): the rows'
+    // maxima and denominators are read once for all of them, and every LDS
+    // read is issued before the first is used.
+    constexpr int kOut = (QPK * kHeadDim + kThreads - 1) / kThreads;
+    constexpr int kSpan = kHeadDim / kOut;
+    const int h = tid / kSpan;
+    const int d0 = tid - h * kSpan;
+    if (h >= QPK) return;
+    float2 ml[kRows];
+    float ov[kOut][kRows];
 #pragma unroll
-        for (int q = 0; q < kWaves; ++q) mx = fmaxf(mx, st_m[q][h]);
-        float l = 0.f, acc = 0.f;
+    for (int q = 0; q < kRows; ++q) {
+        ml[q] = st_ml[q][h];
 #pragma unroll
-        for (int q = 0; q < kWaves; ++q) {
-            const float f = __builtin_amdgcn_exp2f(st_m[q][h] - mx);
-            l = __builtin_fmaf(st_l[q][h], f, l);
-            acc = __builtin_fmaf(st_o[q][h][d], f, acc);
-        }
-        if (single) {
-            outm[h * kHeadDim + d] = acc / l;
-        } else {
-            part[d] = acc;
-            if (d == 0) {
-                part[kHeadDim] = mx;
-                part[kHeadDim + 1] = l;
-            }
-        }
+        for (int u = 0; u < kOut; ++u) ov[u][q] = st_o[q][h][d0 + kSpan * u];
+    }
+    float mx = -FLT_MAX;
+#pragma unroll
+    for (int q = 0; q < kRows; ++q) mx = fmaxf(mx, ml[q].x);
+    float l = 0.f, acc[kOut];
+#pragma unroll
+    for (int u = 0; u < kOut; ++u) acc[u] = 0.f;
+#pragma unroll
+    for (int q = 0; q < kRows; ++q) {
+        const float f = __builtin_amdgcn_exp2f(ml[q].x - mx);
+        l = __builtin_fmaf(ml[q].y, f, l);
+#pragma unroll
+        for (int u = 0; u < kOut; ++u) acc[u] = __builtin_fmaf(ov[u][q], f, acc[u]);
+    }
+    float* const own = a.partials != nullptr ? a.partials + (size_t)m * a.partial_floats : mb.partials;
+    float* part = own + ((size_t)(kvh * QPK + h) * kAttnChunks + chunk) * kPartStride;
+#pragma unroll
+    for (int u = 0; u < kOut; ++u) part[d0 + kSpan * u] = acc[u];
+    if (d0 == 0) {
+        part[kHeadDim] = mx;
+        part[kHeadDim + 1] = l;
     }
 }
 
@@ -360,7 +374,9 @@ __global__ __launch_bounds__(128) void kv_append_kernel(AttnArgs a) {
     float x0 = src[lane];
     float x1 = src[lane + 64];
     const int pos = a.positions[m];
-    if (wave == 0) norm_rope(x0, x1, a.k_norm[lane], a.k_norm[lane + 64], a.eps, (float)pos, a.rope_base, lane);
+    if (wave == 0) {
+        norm_rope(x0, x1, a.k_norm[lane], a.k_norm[lane + 64], a.eps, rope_rot((float)pos, rope_freq(a.rope_base, lane)));
+    }
     if (pos < 0 || pos >= mb.capacity) return;
     const size_t head_elems = (size_t)mb.capacity * kHeadDim;
     uint16_t* dst = (wave == 0 ? mb.keys : mb.values) + (size_t)a.layer * mb.layer_elems +
@@ -377,46 +393,55 @@ __global__ __launch_bounds__(64) void step_inputs_kernel(StepInputs in) {
     if (in.positions_dst != nullptr) in.positions_dst[i] = in.positions[i];
 }
 
-// Merges the kAttnChunks partials of one (member, query head) into the
-// attention output: o = sum_c O_c e^(m_c - M) / sum_c L_c e^(m_c - M).
+// Merges the chunk partials of one (member, query head) into the attention
+// output: o = sum_c O_c e^(m_c - M) / sum_c L_c e^(m_c - M), in chunk order.
 // A separate launch: the kernel boundary orders the partials' writes before
 // these reads, where an in-kernel hand-off would need a device-scope release
-// (an L2 write-back) in every attention workgroup.
-static_assert(kAttnChunks <= kHeadDim, "one combine thread per chunk loads its maximum");
-__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(AttnArgs a) {
+// (an L2 write-back) in every attention workgroup, which costs far more.
+// Every thread loads each chunk's maximum and denominator itself (the
+// threads of a workgroup read the same words), and every slot the launch can
+// hold is loaded before the position says which are live, so the launch
+// waits on memory once. One chunk is the same arithmetic: o = O_0 / L_0.
+// The store is unconditional: a branch on the position would let the
+// compiler sink the loads past its arrival.
+// (A few workgroups per CU at most: the occupancy hint lets the compiler keep
+// all of a thread's loads in flight instead of trading them for registers.)
+__global__ __launch_bounds__(kHeadDim) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_combine_kernel(AttnArgs a) {
     const int qh = blockIdx.x;
     const int m = blockIdx.y;
     const int d = threadIdx.x;
-    __shared__ float mc[kAttnChunks], lc[kAttnChunks];
-    // every chunk slot is requested together with the position. Slots past
-    // the context's chunks hold stale memory (possibly NaN bit patterns): they
-    // are replaced by a neutral state (sum 0, maximum -FLT_MAX, denominator 0)
-    // before any arithmetic, so no guard on later operations is needed.
-    const float* part = a.mem[m].partials + (size_t)qh * kAttnChunks * kPartStride;
+    const float* own = a.partials != nullptr ? a.partials + (size_t)m * a.partial_floats : a.mem[m].partials;
+    // Slots past the launch's chunks are never read (out of the buffer
+    // range: zero); slots past this context's chunks hold stale memory
+    // (possibly NaN bit patterns) and are replaced by a neutral state (sum 0,
+    // maximum -FLT_MAX, denominator 0) before any arithmetic.
+    const __amdgpu_buffer_rsrc_t pr =
+        make_rsrc(own + (size_t)qh * kAttnChunks * kPartStride, (uint32_t)(a.chunks * kPartStride * 4));
     float o[kAttnChunks];
+    float2 ml[kAttnChunks];
 #pragma unroll
-    for (int c = 0; c < kAttnChunks; ++c) o[c] = c < a.chunks ? part[c * kPartStride + d] : 0.f;
-    const float mcv = d < a.chunks ? part[d * kPartStride + kHeadDim] : 0.f;
-    const float lcv = d < a.chunks ? part[d * kPartStride + kHeadDim + 1] : 0.f;
+    for (int c = 0; c < kAttnChunks; ++c) {
+        const uint32_t row = (uint32_t)(c * kPartStride) * 4u;
+        o[c] = __builtin_bit_cast(float, load_b32(pr, row + (uint32_t)d * 4u));
+        ml[c] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (int)(row + kHeadDim * 4), 0, 0));
+    }
     const int tokens = a.positions[m] + 1;
     const int len = chunk_tokens(tokens, a.chunks);
     const int chunks = (tokens + len - 1) / len;
-    if (chunks <= 1) return;  // the attention launch wrote the output
-    if (d < kAttnChunks) {
-        mc[d] = d < chunks ? mcv : -FLT_MAX;
-        lc[d] = d < chunks ? lcv : 0.f;
-    }
-#pragma unroll
-    for (int c = 0; c < kAttnChunks; ++c) o[c] = c < chunks ? o[c] : 0.f;
-    __syncthreads();
     float mx = -FLT_MAX;
 #pragma unroll
-    for (int c = 0; c < kAttnChunks; ++c) mx = fmaxf(mx, mc[c]);
+    for (int c = 0; c < kAttnChunks; ++c) {
+        const bool live = c < chunks;
+        ml[c].x = live ? ml[c].x : -FLT_MAX;
+        ml[c].y = live ? ml[c].y : 0.f;
+        o[c] = live ? o[c] : 0.f;
+        mx = fmaxf(mx, ml[c].x);
+    }
     float l = 0.f, acc = 0.f;
 #pragma unroll
     for (int c = 0; c < kAttnChunks; ++c) {
-        const float f = __builtin_amdgcn_exp2f(mc[c] - mx);
-        l = __builtin_fmaf(lc[c], f, l);
+        const float f = __builtin_amdgcn_exp2f(ml[c].x - mx);
+        l = __builtin_fmaf(ml[c].y, f, l);
         acc = __builtin_fmaf(o[c], f, acc);
     }
     a.out[((size_t)m * a.q_heads + qh) * kHeadDim + d] = acc / l;

@@ -10,9 +10,9 @@ namespace ribn_amd {
 // Head geometry the attention kernel is built for (Qwen3: 128-wide heads).
 constexpr int kHeadDim = 128;
 // Token chunks per (member, KV head): the work of one workgroup, at most
-// this many. Below 5 members the count depends on the caches' capacity only,
-// so a member's arithmetic does not depend on the batch it runs in; a
-// captured step serves every position either way.
+// this many. The count depends on the caches' capacity only, so a member's
+// arithmetic does not depend on the batch it runs in, and a captured step
+// serves every position.
 constexpr int kAttnChunks = 32;
 // Members one attention launch serves (the host splits larger batches).
 constexpr int kAttnMaxMembers = 8;
@@ -34,8 +34,7 @@ struct AttnMember {
 struct AttnArgs {
     const AttnMember* mem;     // device [members] descriptors
     int layer;
-    int chunks;                // grid chunks: ceil(max capacity / 64), at most kAttnChunks (the launch
-                               // lowers it further when KV heads x members fill the chip)
+    int chunks;                // grid chunks: ceil(max capacity / 64), at most kAttnChunks
     int appended;              // 1: every member's K/V is already in its cache (launch_kv_append)
     const float* q;            // [members][q_heads * 128], raw projection
     const float* k;            // [members][kv_heads * 128], raw projection
@@ -44,6 +43,9 @@ struct AttnArgs {
     const float* k_norm;       // [128]
     const int32_t* positions;  // [members] device positions of the new token
     float* out;                // [members][q_heads * 128]
+    float* partials;           // when set, member m's partials start at partials + m * partial_floats
+                               // (the merge launch then needs no descriptor); else the descriptors'
+    uint64_t partial_floats;
     int q_heads;
     int kv_heads;
     float eps;

@@ -217,9 +217,13 @@ hipError_t wave_shared(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_
 
 // One layer's attention over device descriptors mem[0..members), in launches of
 // kAttnMaxMembers; `appended` first stores the launch's members' K/V.
+// With `partials` set, member m's attention partials live at partials +
+// m * attn_partials_floats (the decoder's own buffer, whose address the merge
+// launch then takes from its arguments); else in the descriptors.
 hipError_t attention(const ribn_amd_qwen3_config& cfg, const ribn_amd::AttnMember* mem, int chunks, bool appended,
                      int members, uint32_t layer, const float* q, const float* k, const float* v, const float* q_norm,
-                     const float* k_norm, const int32_t* positions, float* out, hipStream_t stream) {
+                     const float* k_norm, const int32_t* positions, float* out, float* partials, hipStream_t stream) {
+    const size_t part = ribn_amd::attn_partials_floats((int)cfg.q_heads);
     const size_t qdim = (size_t)cfg.q_heads * cfg.head_dim;
     const size_t kvdim = (size_t)cfg.kv_heads * cfg.head_dim;
     for (int m0 = 0; m0 < members; m0 += ribn_amd::kAttnMaxMembers) {
@@ -236,6 +240,8 @@ hipError_t attention(const ribn_amd_qwen3_config& cfg, const ribn_amd::AttnMembe
         a.k_norm = k_norm;
         a.positions = positions + m0;
         a.out = out + m0 * qdim;
+        a.partials = partials != nullptr ? partials + m0 * part : nullptr;
+        a.partial_floats = part;
         a.q_heads = (int)cfg.q_heads;
         a.kv_heads = (int)cfg.kv_heads;
         a.eps = cfg.epsilon;
@@ -267,7 +273,7 @@ hipError_t enqueue_step(ribn_amd_qwen3_decode* d, const GraphKey& key, hipStream
         e = wave_shared(d, qkv, qkv_out, 3, d->hidden, L.attn_norm, members, stream);
         if (e != hipSuccess) return e;
         e = attention(c, d->members_dev, key.chunks, key.appended, members, l, d->q, d->k, d->v, L.attn_q_norm,
-                      L.attn_k_norm, d->positions, d->attn, stream);
+                      L.attn_k_norm, d->positions, d->attn, d->partials, stream);
         if (e != hipSuccess) return e;
         e = wave(d, &L.attn_output, 1, d->attn, nullptr, nullptr, &d->hidden, members, true, stream);
         if (e != hipSuccess) return e;
@@ -615,7 +621,7 @@ ribn_amd_status ribn_amd_attention_decode(ribn_amd_context* ctx, const ribn_amd_
     // Positions are device values: the kernel checks them against each cache
     // and drops an append past its capacity.
     hipError_t e = attention(*config, mem, ribn_amd::attn_grid_chunks(max_capacity), false, (int)members, layer, q, k,
-                             v, q_norm, k_norm, positions, output, ctx->stream);
+                             v, q_norm, k_norm, positions, output, nullptr, ctx->stream);
     return e == hipSuccess ? ok() : driver(e, "launch attention");
 }
 
