@@ -33,8 +33,8 @@
 // captured step serves every set of caches and positions; step_inputs_kernel
 // writes them in stream order from its kernel arguments.
 //
-// argmax_kernel: greedy selection (argmax, model_ops.rs:201-258) with the
-// same ordering key, tie rule and NaN rule.
+// argmax_slice_kernel + argmax_final_kernel: greedy selection (argmax,
+// model_ops.rs:201-258) with the same ordering key, tie rule and NaN rule.
 #include "decode_launch.hpp"
 #include "kquant_device.hpp"
 
@@ -460,19 +460,27 @@ __device__ __forceinline__ void take_better(uint32_t& key, uint32_t& idx, uint32
     }
 }
 
-constexpr int kArgmaxThreads = 1024;
+// Greedy selection in two stages: argmax_slice_kernel
+// reduces one contiguous slice of a member's logits per workgroup (grid:
+// slices x members) to its best (key, index); argmax_final_kernel reduces a
+// member's slice results and applies the step's updates. The result is the
+// largest key, the lowest index among equal keys, and 0 when every value is
+// NaN (the reference's strict comparisons): each stage keeps the lowest index
+// on ties. One workgroup per member would read a 151,936-value row at a
+// single CU's bandwidth.
+constexpr int kSliceThreads = 256;
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* logits, int vocab, uint32_t* selected,
-                                                               uint32_t* tokens, int32_t* positions, int32_t* steps,
-                                                               uint32_t* history, int history_stride) {
-    __shared__ uint32_t wkey[kArgmaxThreads / 64];
-    __shared__ uint32_t widx[kArgmaxThreads / 64];
-    const int m = blockIdx.x;
+__global__ __launch_bounds__(kSliceThreads) void argmax_slice_kernel(const float* logits, int vocab, int slice,
+                                                                     uint2* part) {
+    __shared__ uint32_t wkey[kSliceThreads / 64];
+    __shared__ uint32_t widx[kSliceThreads / 64];
+    const int b = blockIdx.x;
+    const int m = blockIdx.y;
     const int tid = threadIdx.x;
     const float* row = logits + (size_t)m * vocab;
+    const int lo = b * slice;
+    const int hi = min(lo + slice, vocab);
     uint32_t key = 0u, idx = 0u;
-    // v == v rejects NaN like the scalar reference's strict comparisons; each
-    // thread visits its indices in increasing order, so `>` keeps the first
     auto consider = [&](float v, int p) {
         const uint32_t k = logit_key(v);
         if (v == v && k > key) {
@@ -480,28 +488,31 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* log
             idx = (uint32_t)p;
         }
     };
-    // 16-byte loads, eight in flight per thread
-    constexpr int U = 8;
-    const bool wide = (vocab & 3) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
-    const int vec = wide ? vocab / 4 : 0;
-    const float4* row4 = reinterpret_cast<const float4*>(row);
-    for (int base = 0; base < vec; base += kArgmaxThreads * U) {
-        float4 v[U];
+    // slices are whole float4s when the row allows it (16-byte aligned rows
+    // of a multiple of 4 values); all of a thread's loads are in flight at once
+    const bool wide = (vocab & 3) == 0 && (slice & 3) == 0 && ((reinterpret_cast<uintptr_t>(row) & 15) == 0);
+    if (wide) {
+        constexpr int U = 4;
+        const float4* row4 = reinterpret_cast<const float4*>(row);
+        for (int base = lo / 4; base < hi / 4; base += kSliceThreads * U) {
+            float4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = base + u * kArgmaxThreads + tid;
-            v[u] = i < vec ? row4[i] : make_float4(NAN, NAN, NAN, NAN);
-        }
+            for (int u = 0; u < U; ++u) {
+                const int i = base + u * kSliceThreads + tid;
+                v[u] = i < hi / 4 ? row4[i] : make_float4(NAN, NAN, NAN, NAN);
+            }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int p = 4 * (base + u * kArgmaxThreads + tid);
-            consider(v[u].x, p);
-            consider(v[u].y, p + 1);
-            consider(v[u].z, p + 2);
-            consider(v[u].w, p + 3);
+            for (int u = 0; u < U; ++u) {
+                const int p = 4 * (base + u * kSliceThreads + tid);
+                consider(v[u].x, p);
+                consider(v[u].y, p + 1);
+                consider(v[u].z, p + 2);
+                consider(v[u].w, p + 3);
+            }
         }
+    } else {
+        for (int p = lo + tid; p < hi; p += kSliceThreads) consider(row[p], p);
     }
-    for (int p = 4 * vec + tid; p < vocab; p += kArgmaxThreads) consider(row[p], p);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const uint32_t ok = (uint32_t)__shfl_xor((int)key, off, 64);
@@ -516,7 +527,28 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* log
     if (tid == 0) {
         key = wkey[0];
         idx = widx[0];
-        for (int w = 1; w < kArgmaxThreads / 64; ++w) take_better(key, idx, wkey[w], widx[w]);
+        for (int w = 1; w < kSliceThreads / 64; ++w) take_better(key, idx, wkey[w], widx[w]);
+        part[(size_t)m * gridDim.x + b] = make_uint2(key, idx);
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const uint2* part, int slices, uint32_t* selected,
+                                                         uint32_t* tokens, int32_t* positions, int32_t* steps,
+                                                         uint32_t* history, int history_stride) {
+    const int m = blockIdx.x;
+    const int lane = threadIdx.x;
+    uint32_t key = 0u, idx = 0u;
+    for (int b = lane; b < slices; b += 64) {
+        const uint2 r = part[(size_t)m * slices + b];
+        take_better(key, idx, r.x, r.y);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t ok = (uint32_t)__shfl_xor((int)key, off, 64);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)idx, off, 64);
+        take_better(key, idx, ok, oi);
+    }
+    if (lane == 0) {
         selected[m] = idx;
         if (tokens != nullptr) tokens[m] = idx;
         if (positions != nullptr) {
@@ -578,11 +610,20 @@ hipError_t launch_step_inputs(const StepInputs& in, hipStream_t stream) {
 }
 
 hipError_t launch_argmax(const float* logits, int vocab, int members, uint32_t* selected, uint32_t* tokens,
-                         int32_t* positions, int32_t* steps, uint32_t* history, int history_stride,
+                         int32_t* positions, int32_t* steps, uint32_t* history, int history_stride, uint64_t* part,
                          hipStream_t stream) {
-    if (members < 1 || vocab < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)members), dim3(kArgmaxThreads), 0, stream, logits, vocab,
-                       selected, tokens, positions, steps, history, history_stride);
+    if (members < 1 || vocab < 1 || part == nullptr) return hipErrorInvalidValue;
+    // slices of at least 1024 values, a multiple of 4, at most kArgmaxSlices of them
+    int slice = (vocab + kArgmaxSlices - 1) / kArgmaxSlices;
+    slice = std::max(1024, (slice + 3) / 4 * 4);
+    const int slices = (vocab + slice - 1) / slice;
+    uint2* p = reinterpret_cast<uint2*>(part);
+    hipLaunchKernelGGL(argmax_slice_kernel, dim3((unsigned)slices, (unsigned)members), dim3(kSliceThreads), 0, stream,
+                       logits, vocab, slice, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)members), dim3(64), 0, stream, p, slices, selected, tokens,
+                       positions, steps, history, history_stride);
     return hipGetLastError();
 }
 

@@ -87,13 +87,17 @@ struct StepInputs {
 };
 hipError_t launch_step_inputs(const StepInputs& in, hipStream_t stream);
 
+// Slice results a two-stage greedy selection keeps per member.
+constexpr int kArgmaxSlices = 64;
+
 // Greedy selection per member over logits [members][vocab] (ties to the lowest
 // index, NaN never selected). Writes selected[m]; when `tokens` is not null
 // also tokens[m] (the next step's input). When `positions` is not null the
 // member's generation advances on the device: history[m * history_stride +
-// steps[m]] = selected, then steps[m] and positions[m] grow by one.
+// steps[m]] = selected, then steps[m] and positions[m] grow by one. `part`
+// holds [members][kArgmaxSlices] scratch words for the slice results.
 hipError_t launch_argmax(const float* logits, int vocab, int members, uint32_t* selected, uint32_t* tokens,
-                         int32_t* positions, int32_t* steps, uint32_t* history, int history_stride,
+                         int32_t* positions, int32_t* steps, uint32_t* history, int history_stride, uint64_t* part,
                          hipStream_t stream);
 
 }  // namespace ribn_amd

@@ -151,6 +151,7 @@ struct ribn_amd_qwen3_decode {
     uint32_t history_steps;
     ribn_amd::AttnMember* members_dev;  // [members] cache descriptors of the next step
     float* partials;      // [members][attention partials]
+    uint64_t* argmax_part;  // [members][kArgmaxSlices] slice results of the greedy selection
     int chunks;           // attention grid of the next step (from its caches' capacities)
     hipStream_t capture;  // private stream for graph capture
     bool graphs;
@@ -297,7 +298,7 @@ hipError_t enqueue_step(ribn_amd_qwen3_decode* d, const GraphKey& key, hipStream
     if (e != hipSuccess) return e;
     return ribn_amd::launch_argmax(d->logits, (int)c.vocab, members, d->selected, d->tokens,
                                    key.advance ? d->positions : nullptr, d->steps, d->history,
-                                   (int)d->history_steps, stream);
+                                   (int)d->history_steps, d->argmax_part, stream);
 }
 
 void destroy_graphs(ribn_amd_qwen3_decode* d) {
@@ -642,9 +643,17 @@ ribn_amd_status ribn_amd_argmax(ribn_amd_context* ctx, const float* logits, size
         return fail(RIBN_AMD_SHAPE_OVERFLOW, 0, 0, "argmax shape exceeds launch limits");
     }
     DeviceGuard guard(ctx->device);
-    hipError_t e = ribn_amd::launch_argmax(logits, (int)length, (int)members, selected, nullptr, nullptr, nullptr,
-                                           nullptr, 0, ctx->stream);
-    return e == hipSuccess ? ok() : driver(e, "launch argmax");
+    // The slice results live in the context's activation scratch (stream
+    // ordered with every other user of it), in groups of members that fit.
+    const size_t group = ribn_amd::gemv_act_scratch_bytes() / (ribn_amd::kArgmaxSlices * sizeof(uint64_t));
+    auto* part = static_cast<uint64_t*>(ctx->act_scratch);
+    for (size_t m0 = 0; m0 < members; m0 += group) {
+        const int mc = (int)std::min(group, members - m0);
+        hipError_t e = ribn_amd::launch_argmax(logits + m0 * length, (int)length, mc, selected + m0, nullptr, nullptr,
+                                               nullptr, nullptr, 0, part, ctx->stream);
+        if (e != hipSuccess) return driver(e, "launch argmax");
+    }
+    return ok();
 }
 
 ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context* ctx, const ribn_amd_qwen3_config* config,
@@ -709,6 +718,8 @@ ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context* ctx, const ribn_a
     bytes += align_up(M * sizeof(ribn_amd::AttnMember));
     const size_t partials_offset = bytes;
     bytes += align_up(M * ribn_amd::attn_partials_floats((int)c.q_heads) * sizeof(float));
+    const size_t argmax_offset = bytes;
+    bytes += align_up(M * ribn_amd::kArgmaxSlices * sizeof(uint64_t));
     DeviceGuard guard(ctx->device);
     auto* d = new (std::nothrow) ribn_amd_qwen3_decode{};
     if (!d) return fail(RIBN_AMD_DRIVER, 0, 0, "host allocation failed");
@@ -735,6 +746,7 @@ ribn_amd_status ribn_amd_qwen3_decode_create(ribn_amd_context* ctx, const ribn_a
     d->steps = reinterpret_cast<int32_t*>(p + offsets[11]);
     d->members_dev = reinterpret_cast<ribn_amd::AttnMember*>(p + members_offset);
     d->partials = reinterpret_cast<float*>(p + partials_offset);
+    d->argmax_part = reinterpret_cast<uint64_t*>(p + argmax_offset);
     d->chunks = 1;
     d->history_steps = 256;
     e = hipMalloc(&d->history, M * d->history_steps * sizeof(uint32_t));

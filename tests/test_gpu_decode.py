@@ -279,6 +279,27 @@ def test_argmax_matches_oracle(env):
     assert list(got) == [O.argmax(logits[m]) for m in range(3)] == [17, 6, 151935]
 
 
+@pytest.mark.parametrize("vocab", [300, 1024, 4097, 65537])
+def test_argmax_slices_match_oracle(env, vocab):
+    """Row lengths that give one slice, an exact slice, ragged slices and rows
+    that are not whole float4s; ties across slices, NaN runs, an all-NaN row."""
+    E = env["E"]
+    rng = np.random.default_rng(vocab)
+    logits = rng.standard_normal((5, vocab)).astype(np.float32)
+    logits[0, 3] = logits[0, vocab - 2] = 7.5          # first index wins across slices
+    logits[1, : vocab // 2] = np.nan
+    logits[1, vocab - 1] = -np.inf                      # every other value beats -inf
+    logits[2, :] = np.nan                               # all NaN: index 0
+    logits[3, :] = -np.inf
+    logits[3, vocab // 3] = -1e30
+    logits[4, :] = 1.0                                  # all equal: index 0
+    sel = to_dev(np.zeros(5, np.int32))
+    ops = E.AmdQwenOps(env["ctx"])
+    ops.argmax_into_batch(to_dev(logits.reshape(-1)), vocab, sel)
+    got = to_host(sel, env["ctx"])
+    assert list(got) == [O.argmax(logits[m]) for m in range(5)]
+
+
 # ------------------------------------------------------------- decoder
 
 
