@@ -325,7 +325,8 @@ def bench_batched(E, synth, torch, args):
         if m <= 16:
             for mode in ("warp", "fixed16"):
                 if mode == "warp":
-                    path = ("f32 wave GEMV, weights read once per 8 members (2 for down's K = 12288)")
+                    path = ("f32 wave GEMV, weights read once per 8 members (down's K = 12288 split by "
+                            "slice from 3 members, with an ordered slice reduction)")
                 else:
                     path = ("block fixed-point " + ("wave GEMV" if m < 4 else
                             "wave GEMV gate/up, matrix-core GEMV down" if m < 5 else "matrix-core GEMV") +

@@ -16,8 +16,9 @@ in the run (a device-to-device copy of N bytes reads N and writes N bytes) and
 prints the scale factor that maps the counter onto true bytes.
 
 `decode-steps` summarises the last N generation steps of each batch size in
-a trace of the decoder: a step ends with its argmax dispatch, and the argmax
-grid (one workgroup per member) tells the batch sizes apart. Per kernel and
+a trace of the decoder: a step ends with its greedy-selection dispatch
+(`argmax_final_kernel`, one 64-thread workgroup per member; `argmax_kernel`
+in traces of the one-launch form), whose grid tells the batch sizes apart. Per kernel and
 grid it prints launches per step, mean duration and time per step, and per
 batch size the span and busy time of the window.
 
@@ -126,7 +127,7 @@ def decode_steps_summary(path: str, steps: int = 32) -> list[dict]:
     rows = _dispatches(path)
     ends: dict[int, list[int]] = defaultdict(list)
     for i, (name, grid, _, _) in enumerate(rows):
-        if name.startswith("argmax_kernel"):
+        if name.startswith(("argmax_final_kernel", "argmax_kernel")):
             ends[grid].append(i)
     out = []
     for grid in sorted(ends):

@@ -425,6 +425,35 @@ def test_wide_dynamic_range_activations(env, mode, t, k, n, members, norm):
         assert err <= (5e-5 if mode == "warp" else RTOL), (m, err)
 
 
+@pytest.mark.parametrize("t,k,members,norm", [(12, 4096, 1, False), (13, 12288, 1, True), (14, 4096, 3, False),
+                                            (12, 4096, 8, True)])
+def test_nan_activation_propagates(env, t, k, members, norm):
+    """GEMV_WARP: one NaN activation makes every output row of its member NaN,
+    as the oracle's sequential f32 sum does; the other members stay finite
+    and within 1e-3."""
+    print_case(test="nan_activation", t=t, k=k, m=members, norm=norm)
+    kern = env["k"][t]
+    n = 256
+    enc = synth.kquant_numpy(t, k, n, seed=11 * k + t)
+    x = synth.activations_numpy(k, members, seed=t + members)
+    x[0, k // 3] = np.nan
+    gam = synth.gamma_numpy(k, seed=4)
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(members * n)
+    if norm:
+        kern.execute_rms_norm(w, to_dev(x.reshape(-1)), to_dev(gam), 1e-6, y, members)
+    else:
+        kern.execute_warp_batch(w, to_dev(x.reshape(-1)), y, members)
+    got = to_host(y, env["ctx"]).reshape(members, n)
+    for m in range(members):
+        src = O.rms_norm_raw(x[m], gam, 1e-6) if norm else x[m]
+        ref = O.quant_gemv(t, enc, k, n, src, threads=8)
+        if m == 0:
+            assert np.isnan(ref).all() and np.isnan(got[m]).all()
+        else:
+            assert np.isfinite(got[m]).all() and max_rel_err(got[m], ref) <= RTOL, m
+
+
 @pytest.mark.parametrize("t,k,ns,members,norm", [(12, 4096, (4096, 1024, 1024), 8, True), (12, 4096, (12288,), 8, True),
                                                   (13, 12288, (4096,), 8, True), (13, 12288, (4096,), 8, False),
                                                   (13, 12288, (4096, 100), 5, False), (12, 8192, (700,), 3, False),

@@ -1,9 +1,10 @@
 """GPU tests of the serving dispatcher (engine_amd/csrc/serving.cpp) through the C ABI.
 
 The decode step itself is pinned to the oracle by test_gpu_decode.py; here
-every dispatcher result is compared with direct decoder calls on separate
-caches (the reference's serving tests compare with the batch-1 executor the
-same way):
+the dispatcher's greedy tokens are checked against the oracle's decode step
+on the same sequence, and every dispatcher result is compared with direct
+decoder calls on separate caches (the reference's serving tests compare with
+the batch-1 executor the same way):
   * eager dispatch equals serial prefill + decode steps, token for token;
   * asynchronous submissions (serial prefill rows, all-decode batches as one
     batched step, several submissions in flight) equal direct steps with the
@@ -24,6 +25,8 @@ import numpy as np
 import pytest
 
 from engine_amd import serving as S
+
+from oracle.qwen3_oracle import OracleQwen3
 
 from .decode_helpers import small_weights
 from .gpu_helpers import to_dev
@@ -135,6 +138,35 @@ def test_eager_dispatch_equals_direct_steps(env):
     assert r.generated == want
     assert disp.state_position(r.state) == len(r.prompt) + 4
     disp.close()
+
+
+def test_dispatcher_tokens_match_the_oracle(env):
+    """Eager dispatch of a prompt and eight greedy steps, against the oracle's
+    decode step (oracle/qwen3_oracle.py) teacher-forced on the dispatcher's
+    own tokens: wherever the oracle's top-2 logit margin exceeds four times
+    the decoder's 1e-3 normwise bound, the dispatcher picked the oracle's
+    token."""
+    print_case(test="serving_oracle")
+    disp = S.AmdServingDispatcher(env["dec"], 4)
+    r = Request([5, 1500, 77, 2047, 9])
+    run(disp, [r], [r.prefill()])
+    for _ in range(8):
+        run(disp, [r], [r.decode()])
+    disp.close()
+    orc = OracleQwen3(TINY, small_weights(TINY, 4242), CAP)
+    for i, t in enumerate(r.prompt[:-1]):
+        orc.step(t, i, head=False)
+    seq = r.prompt + r.generated
+    checked = 0
+    for k, got in enumerate(r.generated):
+        pos = len(r.prompt) - 1 + k
+        ref = orc.step(seq[pos], pos)
+        top2 = np.sort(orc.logits.astype(np.float64))[-2:]
+        margin = (top2[1] - top2[0]) / np.abs(orc.logits).max()
+        if margin > 4e-3:
+            assert got == ref, (k, got, ref, margin)
+            checked += 1
+    assert checked >= 4, checked
 
 
 def test_async_submissions_equal_direct_steps(env):

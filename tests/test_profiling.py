@@ -56,3 +56,19 @@ def test_decode_steps_windows_by_argmax_grid(tmp_path):
     assert b8["kernels"][0] == ("gemv<8>", 8, 1.0, 5.0, 5.0)
     # more steps than the trace holds: that batch size is left out
     assert [r["argmax_grid"] for r in P.decode_steps_summary(str(tmp_path), steps=2)] == [1024]
+
+
+def test_decode_steps_end_at_the_final_selection_launch(tmp_path):
+    # the two-launch greedy selection: slices (not a step boundary), then the
+    # final merge (64 threads per member) ends the step
+    rows, t = [], 0
+    for _ in range(2):
+        rows.append(("void ribn_amd::gemv<1>(int)", (4096, 1, 1), t, t + 2000))
+        rows.append(("ribn_amd::(anonymous namespace)::argmax_slice_kernel(float const*, int, int, uint2*)",
+                     (16384, 1, 1), t + 2000, t + 2500))
+        rows.append(("ribn_amd::(anonymous namespace)::argmax_final_kernel(uint2 const*, int)", (64, 1, 1),
+                     t + 2500, t + 3000))
+        t += 3000
+    _write_trace(tmp_path / "x_kernel_trace.csv", rows)
+    (w,) = P.decode_steps_summary(str(tmp_path), steps=1)
+    assert w["argmax_grid"] == 64 and w["dispatches"] == 3 and w["busy_us"] == 3.0
