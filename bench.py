@@ -239,10 +239,12 @@ def build_decoder(E, synth, torch, ctx, step, out_gamma, layers, seed, members):
 def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed):
     """Prefills `context` prompt tokens per member, then times `gen_tokens`
     greedy steps of the graph-replayed generation loop (wall clock, which
-    includes the step's host work)."""
+    includes the step's host work). Member m's prompt depends on the seed and
+    m only, so member 0 has the same prompt at every batch size. Returns the
+    result line, the generated tokens and member 0's last logits."""
     import numpy as np
     rng = np.random.default_rng(seed)
-    prompts = rng.integers(0, VOCAB, size=(members, context))
+    prompts = rng.integers(0, VOCAB, size=(8, context))[:members]
     caches = [E.AmdKvCache(ctx, cfg, context + gen_tokens) for _ in range(members)]
     t0 = time.perf_counter()
     for p in range(context - 1):
@@ -259,20 +261,31 @@ def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed):
     out = dec.generate(caches, last, start, gen_tokens)
     dt = time.perf_counter() - t0
     kv_read = sum((context + s) * KV_BYTES_PER_TOKEN * cfg.layers // 36 for s in range(gen_tokens)) / gen_tokens
-    return {"members": members, "context": context, "generated": gen_tokens,
+    line = {"members": members, "context": context, "generated": gen_tokens,
             "tok_s": round(members * gen_tokens / dt, 1), "ms_per_step": round(dt * 1e3 / gen_tokens, 4),
             "prefill_s": round(prefill_s, 2), "kv_bytes_per_step": int(kv_read * members),
             "distinct_tokens": int(len(set(out.reshape(-1).tolist())))}
+    return line, out, dec.copy_logits(0)
 
 
 def model_decode_results(E, synth, torch, ctx, step, out_gamma, args):
+    """Batch 1, then batch 8 whose member 0 has batch 1's prompt. In the f32
+    GEMV mode member 0's tokens and last logits equal batch 1's bit for bit
+    (`b8_member0_bitwise_equal_b1`): a check on the timed run itself, since
+    random weights make the greedy output settle on one token."""
+    import numpy as np
     dec, cfg = build_decoder(E, synth, torch, ctx, step, out_gamma, args.layers, args.seed, 8)
-    res = {}
+    res, runs = {}, {}
     for members in (1, 8):
-        r = time_model_decode(E, dec, cfg, ctx, members, args.context, args.gen_tokens, args.seed + members)
+        r, toks, logits = time_model_decode(E, dec, cfg, ctx, members, args.context, args.gen_tokens, args.seed)
         log(f"bench model: batch {members}: {r['tok_s']} tok/s ({r['ms_per_step']} ms/step, "
             f"prefill {r['prefill_s']} s)")
         res[members] = r
+        runs[members] = (toks[0], logits)
+    res["b8_member0_bitwise_equal_b1"] = bool(np.array_equal(runs[1][0], runs[8][0]) and
+                                              np.array_equal(runs[1][1].view(np.uint32),
+                                                             runs[8][1].view(np.uint32)))
+    log(f"bench model: batch-8 member 0 bit-identical to batch 1: {res['b8_member0_bitwise_equal_b1']}")
     dec.close()
     return res
 
