@@ -848,20 +848,23 @@ def main():
         gate_up = graph_gu.replay if graph_gu is not None else step.run_gate_up
         with torch.cuda.stream(stream):
             gate_up()
-            s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s2.record(stream)
-            for _ in range(reps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+            ev[0].record(stream)
+            for r in range(reps):
                 gate_up()
-            e2.record(stream)
+                ev[r + 1].record(stream)
         torch.cuda.synchronize()
-        return ms, s2.elapsed_time(e2) * 1e3 / (reps * args.layers), graph is not None
+        # mean us per gate+up launch over each replay of the 36 launches
+        per = sorted(ev[r].elapsed_time(ev[r + 1]) * 1e3 / args.layers for r in range(reps))
+        mean = ev[0].elapsed_time(ev[reps]) * 1e3 / (reps * args.layers)
+        return ms, mean, graph is not None, per[reps // 2], per[0]
 
     # The opt-in fixed-point mode first (for comparison), then the headline mode.
     other = "fixed16" if args.gemv_mode == "warp" else "warp"
-    ms_o, us_o, _ = measure(other)
+    ms_o, us_o, _, _, _ = measure(other)
     log(f"bench: {other} GEMV mode (comparison): {ms_o:.4f} ms/step, "
         f"{step.bytes_per_step / (ms_o * 1e-3) / 1e9:.1f} GB/s, gate+up {us_o:.3f} us")
-    ms_step, us_launch, graphed = measure(args.gemv_mode)
+    ms_step, us_launch, graphed, us_median, us_min = measure(args.gemv_mode)
     gbs = step.bytes_per_step / (ms_step * 1e-3) / 1e9
     log(f"bench: {args.gemv_mode} GEMV mode: {ms_step:.4f} ms/step, {gbs:.1f} GB/s, gate+up {us_launch:.3f} us")
     achieved = gu_bytes / (us_launch * 1e-6) / 1e9
@@ -875,6 +878,8 @@ def main():
         "frac": round(achieved / PEAK_HBM_GBS, 4),
         "traffic": measured_traffic(),
         "avg_launch_us": round(us_launch, 3),
+        "median_launch_us": round(us_median, 3),  # of the 5 replays' means
+        "min_launch_us": round(us_min, 3),
         "bytes_per_launch": gu_bytes,
     }
 
