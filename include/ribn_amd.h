@@ -530,7 +530,8 @@ ribn_amd_status ribn_amd_attention_decode(ribn_amd_context *ctx, const ribn_amd_
 
 /* CudaQwen35Ops::argmax_into / argmax_into_batch (model_ops.rs:1583-1674):
  * selected[m] = the first index of the largest non-NaN value of
- * logits[m*length .. (m+1)*length) (device u32 array). */
+ * logits[m*length .. (m+1)*length) (device u32 array), 0 when every value is
+ * NaN. Its slice results use the context's scratch, in stream order. */
 ribn_amd_status ribn_amd_argmax(ribn_amd_context *ctx, const float *logits, size_t logits_len, size_t length,
                                 uint32_t *selected);
 
