@@ -443,6 +443,409 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restri
     }
 }
 
+// ------------------------------------------------------------- wide tiles
+//
+// qgemm_tile_kernel<T, RB> (M > 64): four waves, one per SIMD, one workgroup
+// per CU. The workgroup owns 64*RB weight rows and 128 tokens; wave w owns
+// rows [16*RB*w, 16*RB*(w+1)) as RB blocks of 16 and all 8 token blocks, so
+// each dequantised A fragment feeds 8 MFMAs and each B fragment read from LDS
+// feeds RB. v_mfma_f32_16x16x32_f16: lane l holds A[l%16][8(l/16)+j],
+// B[8(l/16)+j][l%16] and C[4(l/16)+i][l%16]. K advances a super-block (256
+// elements, 8 chunks of 32) per step; the x tile [128][256] f16 is staged in
+// LDS (padded rows, double-buffered, loaded into registers a step ahead), and
+// each lane loads its weight bytes a step ahead.
+//
+// Chunk c of a super-block and k-piece q = l/16 select 8 consecutive k:
+//   Q4_K/Q5_K: c = 4L + 2h + p -> k0 = 128L + 64(q>>1) + 32h + 16(q&1) + 8p,
+//              payload bytes 16q + 8p.. of qs half L (64 B), nibble h, scale
+//              group 4L + 2(q>>1) + h;
+//   Q6_K:      c = 2Q + p -> k0 = 128(q>>1) + 32Q + 16(q&1) + 8p, ql window
+//              (Q & 1), nibble Q >> 1, qh bits 2Q, scale 8(q>>1) + 2Q + (q&1).
+// (lib.rs:596-661 element order.) Each 16-byte weight load serves 4 chunks.
+
+constexpr int kTileTok = 128;                      // tokens per workgroup (8 blocks of 16)
+constexpr int kTileThreads = 256;
+constexpr int kTileLoads = kTileTok * 512 / 1024 / (kTileThreads / 64);  // 1 KB LDS loads per wave per super-block
+
+typedef float float4_v __attribute__((ext_vector_type(4)));
+
+template <int T> struct SbW;
+template <> struct SbW<kQ4K> { uint4 h, p0, p1; };
+template <> struct SbW<kQ5K> { uint4 h, qh, p0, p1; };
+template <> struct SbW<kQ6K> {
+    uint4 a, b, qh, sc;                // dword-aligned-down windows: ql (two), qh, scales
+    uint32_t at, bt, qht, sct;         // the dword after each window
+    uint32_t d16, shift;
+};
+
+template <int T>
+__device__ __forceinline__ void load_sb(SbW<T>& s, __amdgpu_buffer_rsrc_t r, uint32_t blk, int q) {
+    if constexpr (T == kQ4K) {
+        s.h = load_b128(r, blk);
+        s.p0 = load_b128(r, blk + 16 + 16 * q);
+        s.p1 = load_b128(r, blk + 80 + 16 * q);
+    } else if constexpr (T == kQ5K) {
+        s.h = load_b128(r, blk);
+        s.qh = load_b128(r, blk + 16 + 16 * (q & 1));
+        s.p0 = load_b128(r, blk + 48 + 16 * q);
+        s.p1 = load_b128(r, blk + 112 + 16 * q);
+    } else {
+        const uint32_t base = blk & ~3u;
+        s.shift = (blk & 3u) * 8u;
+        const uint32_t oa = base + 16 * q + 32 * (q >> 1);
+        const uint32_t oh = base + 128 + 16 * q;
+        s.a = load_b128(r, oa);
+        s.at = load_b32(r, oa + 16);
+        s.b = load_b128(r, oa + 32);
+        s.bt = load_b32(r, oa + 48);
+        s.qh = load_b128(r, oh);
+        s.qht = load_b32(r, oh + 16);
+        s.sc = load_b128(r, base + 192);
+        s.sct = load_b32(r, base + 208);
+        s.d16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)(blk + 208), 0, kStreamPolicy);
+    }
+}
+
+// Weights are dequantised in packed f16 (two per instruction, no conversion
+// instructions): a quant byte q becomes the f16 1024 + q (bits 0x6400 | q,
+// or 1024 + 16q for a high nibble left in place), and
+//   Q4_K/Q5_K: qs = fma(1024 + q, sc, -1024 sc) = q*sc exactly (every value
+//              involved is an f16 integer, q*sc <= 1953), then
+//              w = fma(qs, d, -f16(dmin*m)): one rounding of d*sc*q - dmin*m
+//              besides that of the minimum term;
+//   Q6_K:      qm = (1024 + q) - 1056 = q - 32 exactly, then
+//              w = fma(qm, a_hi, qm * a_lo) with a = d*sc split into two f16
+//              parts: one rounding of a*(q - 32).
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+__device__ __forceinline__ uint32_t as_u(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ half2_t splat_h2(float v) {
+    const _Float16 h = (_Float16)v;
+    return half2_t{h, h};
+}
+// bytes (b0, b1, b2, b3) -> (b0, b2, b1, b3): the halves of x & 0x00ff00ff
+// are then elements (0, 1) and those of (x >> 8) elements (2, 3)
+__device__ __forceinline__ uint32_t pair_order(uint32_t x) { return __builtin_amdgcn_perm(x, x, 0x03010200u); }
+
+// A super-block's per-lane constants: Q4_K/Q5_K for groups 4L + 2(q>>1) + h
+// (s, c as above, d, and -f16(dmin*m)); Q6_K a_hi, a_lo per quarter Q (and the
+// realigned windows).
+template <int T> struct SbDec;
+template <> struct SbDec<kQ4K> { half2_t s[2][2], c[2][2], nb[2][2], d; };
+template <> struct SbDec<kQ5K> { half2_t s[2][2], c[2][2], nb[2][2], d; };
+template <> struct SbDec<kQ6K> { half2_t ahi[4], alo[4]; uint4 la, lb, qh; };
+
+template <int T>
+__device__ __forceinline__ void decode_sb(const SbW<T>& s, int q, SbDec<T>& o) {
+    if constexpr (T == kQ4K || T == kQ5K) {
+        const float dmin = half_bits_to_float(s.h.x >> 16);
+        o.d = as_h2((s.h.x & 0xffffu) * 0x10001u);
+        const int sh = 16 * (q >> 1);
+        const uint32_t sc[2] = {(s.h.y & 0x3f3f3f3fu) >> sh,
+                                ((s.h.w & 0x0f0f0f0fu) | ((s.h.y >> 2) & 0x30303030u)) >> sh};
+        const uint32_t mn[2] = {(s.h.z & 0x3f3f3f3fu) >> sh,
+                                (((s.h.w >> 4) & 0x0f0f0f0fu) | ((s.h.z >> 2) & 0x30303030u)) >> sh};
+#pragma unroll
+        for (int L = 0; L < 2; ++L) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float scf = (float)((sc[L] >> (8 * h)) & 0xffu);
+                o.s[L][h] = splat_h2(h ? scf * 0.0625f : scf);
+                o.c[L][h] = splat_h2(h ? -64.0f * scf : -1024.0f * scf);
+                o.nb[L][h] = splat_h2(-(dmin * (float)((mn[L] >> (8 * h)) & 0xffu)));
+            }
+        }
+    } else {
+        o.la = funnel4(s.a, s.at, s.shift);
+        o.lb = funnel4(s.b, s.bt, s.shift);
+        o.qh = funnel4(s.qh, s.qht, s.shift);
+        const uint4 scw = funnel4(s.sc, s.sct, s.shift);
+        const float d = half_bits_to_float(s.d16);
+        // scale 8n + 2Q + (q&1), n = q>>1: byte 2(Q&1) + (q&1) of dword 2n + (Q>>1)
+        const uint32_t w0 = ((q >> 1) ? scw.z : scw.x) >> (8 * (q & 1));
+        const uint32_t w1 = ((q >> 1) ? scw.w : scw.y) >> (8 * (q & 1));
+        const float a[4] = {d * (float)(int8_t)(w0 & 0xffu), d * (float)(int8_t)((w0 >> 16) & 0xffu),
+                            d * (float)(int8_t)(w1 & 0xffu), d * (float)(int8_t)((w1 >> 16) & 0xffu)};
+#pragma unroll
+        for (int Q = 0; Q < 4; ++Q) {
+            const _Float16 hi = (_Float16)a[Q];
+            o.ahi[Q] = half2_t{hi, hi};
+            o.alo[Q] = splat_h2(a[Q] - (float)hi);
+        }
+    }
+}
+
+// Four packed f16 weights from one word of quant bytes (elements j..j+3)
+// whose values, after `mask`, sit in the low bits of each byte (plus `extra`
+// bits already placed: the Q5_K high bit).
+// 0x64006400 in a vector register, so (x & mask) | it is one v_and_or_b32
+// (a three-operand instruction takes no literal and reads at most one scalar
+// register on gfx9: the mask goes in the scalar register)
+__device__ __forceinline__ uint32_t f16_magic() {
+    uint32_t k;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(k));
+    return k;
+}
+
+template <int T>
+__device__ __forceinline__ void tile_word(uint32_t x, uint32_t mask, uint32_t extra_a, uint32_t extra_b, half2_t s,
+                                          half2_t c, half2_t d, half2_t nb, uint32_t& oa, uint32_t& ob) {
+    const uint32_t xp = pair_order(x);
+    const uint32_t k = f16_magic();
+    const half2_t pa = as_h2((xp & mask) | (extra_a | k));
+    const half2_t pb = as_h2(((xp >> 8) & mask) | (extra_b | k));
+    oa = as_u(__builtin_elementwise_fma(__builtin_elementwise_fma(pa, s, c), d, nb));
+    ob = as_u(__builtin_elementwise_fma(__builtin_elementwise_fma(pb, s, c), d, nb));
+}
+
+__device__ __forceinline__ void tile_word6(uint32_t x, half2_t ahi, half2_t alo, uint32_t& oa, uint32_t& ob) {
+    const uint32_t xp = pair_order(x);
+    const uint32_t k = f16_magic();
+    const half2_t off = half2_t{(_Float16)-1056.0f, (_Float16)-1056.0f};
+    const half2_t qa = as_h2((xp & 0x003f003fu) | k) + off;
+    const half2_t qb = as_h2(((xp >> 8) & 0x003f003fu) | k) + off;
+    oa = as_u(__builtin_elementwise_fma(qa, ahi, qa * alo));
+    ob = as_u(__builtin_elementwise_fma(qb, ahi, qb * alo));
+}
+
+// Chunk C's A fragment (8 f16 weights of the lane's row).
+template <int T, int C>
+__device__ __forceinline__ half8_t tile_chunk(const SbW<T>& s, const SbDec<T>& dec, int q) {
+    uint32_t o[4];
+    if constexpr (T == kQ4K || T == kQ5K) {
+        constexpr int L = C >> 2, h = (C >> 1) & 1, p = C & 1;
+        const uint4 P = L ? s.p1 : s.p0;
+        const uint32_t mask = h ? 0x00f000f0u : 0x000f000fu;
+        uint32_t ea0 = 0, eb0 = 0, ea1 = 0, eb1 = 0;
+        if constexpr (T == kQ5K) {
+            // bit g of each qh byte -> bit 4 (low nibble) or 8 (high nibble, 16x) of its f16 half
+            const int g = 4 * L + 2 * (q >> 1) + h;
+            const uint32_t hm = h ? 0x01000100u : 0x00100010u;
+            const int ra = (g + (h ? 24 : 28)) & 31, rb = (g + (h ? 0 : 4)) & 31;
+            const uint32_t q0 = pair_order(p ? s.qh.z : s.qh.x), q1 = pair_order(p ? s.qh.w : s.qh.y);
+            ea0 = __builtin_amdgcn_alignbit(q0, q0, ra) & hm;
+            eb0 = __builtin_amdgcn_alignbit(q0, q0, rb) & hm;
+            ea1 = __builtin_amdgcn_alignbit(q1, q1, ra) & hm;
+            eb1 = __builtin_amdgcn_alignbit(q1, q1, rb) & hm;
+        }
+        tile_word<T>(p ? P.z : P.x, mask, ea0, eb0, dec.s[L][h], dec.c[L][h], dec.d, dec.nb[L][h], o[0], o[1]);
+        tile_word<T>(p ? P.w : P.y, mask, ea1, eb1, dec.s[L][h], dec.c[L][h], dec.d, dec.nb[L][h], o[2], o[3]);
+    } else {
+        constexpr int Q = C >> 1, p = C & 1;
+        const uint4 W = (Q & 1) ? dec.lb : dec.la;
+        // 6-bit bytes: low nibble | (2 high bits << 4); the high bits sit at
+        // bits 2Q of each qh byte and move to bits 4-5 in one shift
+        auto up = [](uint32_t v) { return Q < 2 ? v << (4 - 2 * Q) : v >> (2 * Q - 4); };
+        const uint32_t lo = (((p ? W.z : W.x) >> (4 * (Q >> 1))) & 0x0f0f0f0fu) |
+                            (up(p ? dec.qh.z : dec.qh.x) & 0x30303030u);
+        const uint32_t hi = (((p ? W.w : W.y) >> (4 * (Q >> 1))) & 0x0f0f0f0fu) |
+                            (up(p ? dec.qh.w : dec.qh.y) & 0x30303030u);
+        tile_word6(lo, dec.ahi[Q], dec.alo[Q], o[0], o[1]);
+        tile_word6(hi, dec.ahi[Q], dec.alo[Q], o[2], o[3]);
+    }
+    return __builtin_bit_cast(half8_t, uint4{o[0], o[1], o[2], o[3]});
+}
+
+template <int T, int C>
+__device__ __forceinline__ int tile_k0(int q) {
+    if constexpr (T == kQ4K || T == kQ5K) {
+        constexpr int L = C >> 2, h = (C >> 1) & 1, p = C & 1;
+        return 128 * L + 64 * (q >> 1) + 32 * h + 16 * (q & 1) + 8 * p;
+    } else {
+        constexpr int Q = C >> 1, p = C & 1;
+        return 128 * (q >> 1) + 32 * Q + 16 * (q & 1) + 8 * p;
+    }
+}
+
+template <int T, int RB>
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void qgemm_tile_kernel(
+    const uint8_t* __restrict__ w, uint32_t wbytes, const _Float16* __restrict__ xh, const float* __restrict__ unscale,
+    float* __restrict__ y, int M, int N, int K) {
+    constexpr int BB = BlockTraits<T>::bytes;
+    // two x slots as separate objects: the compiler can then tell that the
+    // reads of one slot do not alias the loads into the other in flight
+    __shared__ __attribute__((aligned(16))) _Float16 xs0[kTileTok * 256];
+    __shared__ __attribute__((aligned(16))) _Float16 xs1[kTileTok * 256];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int q = lane >> 4;
+    const int r16 = lane & 15;
+    const int n0 = blockIdx.x * 64 * RB + 16 * RB * wave;
+    const int m0 = blockIdx.y * kTileTok;
+    const int nb = K >> 8;
+    const int sb_begin = 0;
+    const int sb_end = nb;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, wbytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
+    uint32_t row_off[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int row = min(n0 + 16 * rb + r16, N - 1);  // rows past N repeat the last (not stored)
+        row_off[rb] = (uint32_t)row * (uint32_t)(nb * BB);
+    }
+
+    // x tile of a super-block, loaded straight into LDS (1 KB per wave load,
+    // 16 bytes per lane): load i of wave w fills tokens t = 32w + 2i, +1
+    // (lanes 0-31 and 32-63), 512 bytes each. LDS slot u of token t holds the
+    // 16-byte piece u ^ (t & 15), so the B reads of 16 tokens at one piece
+    // fall in distinct banks (measured conflict-free on gfx950). A lane's
+    // offset for load i (token and swizzled piece) is fixed; the super-block
+    // goes in the uniform offset. Tokens past M read past the activations
+    // (zeros) through the lane offset alone.
+    uint32_t xoff[kTileLoads];
+#pragma unroll
+    for (int i = 0; i < kTileLoads; ++i) {
+        const int t = 32 * wave + 2 * i + (lane >> 5);
+        xoff[i] = ((uint32_t)(m0 + t) * (uint32_t)K + (uint32_t)((lane & 31) ^ (t & 15)) * 8u) * 2u;
+    }
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    auto load_x = [&](_Float16* xs, int sb) {
+#pragma unroll
+        for (int i = 0; i < kTileLoads; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void*)&xs[(32 * wave_u + 2 * i) * 256], 16, (int)xoff[i],
+                sb * 512, 0, 0);
+        // the tile is written behind the compiler's back: LDS reads must not
+        // be folded or moved across this point
+        asm volatile("" ::: "memory");
+    };
+    auto load_w = [&](SbW<T> (&ring)[RB], int sb) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) load_sb<T>(ring[rb], wr, row_off[rb] + (uint32_t)sb * BB, q);
+    };
+
+    float4_v acc[RB][8];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int tb = 0; tb < 8; ++tb) acc[rb][tb] = float4_v{};
+
+    // Prologue: x and weights of the first super-block.
+    SbW<T> wring[2][RB];
+    load_x(xs0, sb_begin);
+    load_w(wring[0], sb_begin);
+    __syncthreads();
+
+    // One super-block; slot r (static) holds its x tile and weights.
+    // PREFETCH: x of sb+1 into the other LDS slot (every wave finished
+    // reading it before the last barrier) and the weights of sb+1, a whole
+    // step ahead of their use (the barrier below waits for the x tile). The
+    // loads are unconditional within the loop, so the compiler's wait counts
+    // stay exact; a prefetch of sb+1 = sb_end <= nb reads in-bounds data that
+    // is not used (or zeros past the tensors).
+    auto step = [&](auto r_const, auto prefetch_const, int sb) {
+        constexpr int r = decltype(r_const)::value;
+        _Float16* const xcur = r ? xs1 : xs0;
+        _Float16* const xnext = r ? xs0 : xs1;
+        if constexpr (decltype(prefetch_const)::value) {
+            load_x(xnext, sb + 1);
+            load_w(wring[r ^ 1], sb + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            const SbW<T>(&wcur)[RB] = wring[r];
+            SbDec<T> dec[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) decode_sb<T>(wcur[rb], q, dec[rb]);
+            const _Float16* xt0 = &xcur[r16 * 256];
+            // Software pipeline over the 8 chunks: the next chunk's A fragments
+            // are dequantised while the current chunk's MFMAs run, and the B
+            // fragments (LDS) are read three token blocks ahead (the next
+            // chunk's first three at the end of the current one).
+            half8_t acur[RB], anext[RB], bq[3];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acur[rb] = tile_chunk<T, 0>(wcur[rb], dec[rb], q);
+            // token 16tb + r16, piece k0/8: LDS slot (k0/8) ^ r16
+            auto bsrc = [&](int k0) { return xt0 + 8 * ((k0 >> 3) ^ r16); };
+#pragma unroll
+            for (int tb = 0; tb < 3; ++tb)
+                bq[tb] = *reinterpret_cast<const half8_t*>(bsrc(tile_k0<T, 0>(q)) + tb * 16 * 256);
+            constexpr int kValu = (BlockTraits<T>::bytes == 144 ? 24 : 30) / RB;  // dequant instructions per MFMA
+            auto chunk = [&](auto c_const) {
+                constexpr int C = decltype(c_const)::value;
+                if constexpr (C < 7) {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) anext[rb] = tile_chunk<T, C + 1>(wcur[rb], dec[rb], q);
+                }
+                const _Float16* src = bsrc(tile_k0<T, C>(q));
+#pragma unroll
+                for (int tb = 0; tb < 8; ++tb) {
+                    const half8_t b = tb < 3 ? bq[tb] : *reinterpret_cast<const half8_t*>(src + tb * 16 * 256);
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+                        acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(acur[rb], b, acc[rb][tb], 0, 0, 0);
+                }
+                if constexpr (C < 7) {
+                    const _Float16* nsrc = bsrc(tile_k0<T, C + 1>(q));
+#pragma unroll
+                    for (int tb = 0; tb < 3; ++tb)
+                        bq[tb] = *reinterpret_cast<const half8_t*>(nsrc + tb * 16 * 256);
+                }
+                // issue order: per token block its MFMAs, the B read three
+                // blocks ahead, and a share of the next chunk's dequantisation
+#pragma unroll
+                for (int tb = 0; tb < 8; ++tb) {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (C < 7) {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) acur[rb] = anext[rb];
+                }
+            };
+            chunk(std::integral_constant<int, 0>{});
+            chunk(std::integral_constant<int, 1>{});
+            chunk(std::integral_constant<int, 2>{});
+            chunk(std::integral_constant<int, 3>{});
+            chunk(std::integral_constant<int, 4>{});
+            chunk(std::integral_constant<int, 5>{});
+            chunk(std::integral_constant<int, 6>{});
+            chunk(std::integral_constant<int, 7>{});
+        }
+        __syncthreads();
+    };
+    // pairs of steps, then an odd last one (no conditional work inside a step)
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using Yes = std::true_type;
+    int sb = sb_begin;
+    for (; sb + 1 < sb_end; sb += 2) {
+        step(I0{}, Yes{}, sb);
+        step(I1{}, Yes{}, sb + 1);
+    }
+    if (sb < sb_end) step(I0{}, std::false_type{}, sb);
+
+    // epilogue: C[n][m] -> y[m][n] * unscale[m]
+    float* out = y;
+    const bool vec = (N & 3) == 0;
+#pragma unroll
+    for (int tb = 0; tb < 8; ++tb) {
+        const int m = m0 + 16 * tb + r16;
+        if (m >= M) continue;
+        const float us = unscale[m];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int n = n0 + 16 * rb + 4 * q;
+            const float4_v o = acc[rb][tb] * us;
+            float* dst = out + (size_t)m * N + n;
+            if (vec && n + 3 < N) {
+                *reinterpret_cast<float4_v*>(dst) = o;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (n + i < N) dst[i] = o[i];
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- launchers
 
 constexpr int kMaxSplits = 8;
@@ -506,6 +909,34 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, void* worksp
     return hipGetLastError();
 }
 
+// Wide tiles (M > 64) run when their grid of 192-row x 128-token
+// workgroups fills at least 90% of its last round of CUs (e.g. Q4_K
+// 4096 -> 12288 at M = 512: 64 x 4 = 256 workgroups); other shapes keep
+// qgemm_kernel, whose split K and 256-row tiles balance them better. Each
+// wave's 48 rows keep its B reads (the whole x tile per wave) within the
+// LDS bandwidth (about 90 B/clk per CU measured); fewer rows per wave are
+// LDS-bound.
+constexpr int kTileRb = 3;
+
+static bool use_tile(int M, int N, int cu_count) {
+    const long long wgs = (long long)((N + 64 * kTileRb - 1) / (64 * kTileRb)) * ((M + kTileTok - 1) / kTileTok);
+    const long long cus = std::max(1, cu_count);
+    const long long rounds = (wgs + cus - 1) / cus;
+    return wgs * 10 >= rounds * cus * 9;
+}
+
+template <int T>
+static hipError_t launch_qgemm_tile(void* workspace, const uint8_t* w, uint32_t wbytes, float* y, int M, int N, int K,
+                                    hipStream_t stream) {
+    uint8_t* base = static_cast<uint8_t*>(workspace);
+    const _Float16* xh = reinterpret_cast<const _Float16*>(base);
+    const float* us = reinterpret_cast<const float*>(base + align256((size_t)M * K * 2));
+    const dim3 grid((N + 64 * kTileRb - 1) / (64 * kTileRb), (M + kTileTok - 1) / kTileTok);
+    hipLaunchKernelGGL((qgemm_tile_kernel<T, kTileRb>), grid, dim3(kTileThreads), 0, stream, w, wbytes, xh, us, y, M,
+                       N, K);
+    return hipGetLastError();
+}
+
 // Tile by token count: few tokens take small tiles (more workgroups for the
 // weight stream); many tokens take 256-row x 128-token tiles (each
 // dequantised weight fragment feeds four MFMAs, 8 waves share each activation
@@ -517,6 +948,9 @@ static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, void* worksp
                                  int M, int N, int K, int cu_count, hipStream_t stream) {
     if (M <= 32) return launch_qgemm_t<T, 1, 1>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
     if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
+    // (the tile kernel's activation offsets of its last token tile must stay below 2^32)
+    if (use_tile(M, N, cu_count) && (uint64_t)(M + kTileTok) * (uint64_t)K * 2u < (1ull << 32))
+        return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, stream);
     return launch_qgemm_t<T, 4, 8>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
 }
 

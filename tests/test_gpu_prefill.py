@@ -104,6 +104,37 @@ def test_prefill_config3_full_size(env, t, k, n):
     assert np.all(np.isfinite(got))
 
 
+@pytest.mark.parametrize("t,k,n,m,dtype", [
+    (12, 1024, 11000, 450, "bf16"),   # last row tile 56 of 192 rows, last token tile 66 of 128
+    (13, 768, 12288, 512, "f32"),     # three super-blocks: one pair of steps and the odd one
+    (14, 256, 11520, 400, "bf16"),    # one super-block (the odd step alone), 2-byte aligned rows
+    (14, 2048, 12288, 500, "f32"),
+])
+def test_prefill_wide_tiles(env, t, k, n, m, dtype):
+    """Shapes whose 192-row x 128-token grid fills a 256-CU MI355X (the
+    wide-tile matmul with packed-f16 dequantisation): rows of a token sample
+    against the oracle, every output finite."""
+    import torch
+    print("CASE prefill wide", t, k, n, m, dtype, flush=True)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(k + n + t)
+    enc_dev = synth.kquant_torch(t, k, n, gen, torch.device("cuda:0"))
+    w = upload(env, t, k, n, enc_dev)
+    x = synth.activations_numpy(k, m, seed=m + 11)
+    if dtype == "bf16":
+        xd, x = bf16_values(x)
+    else:
+        xd = to_dev(x)
+    y = empty_dev(m * n)
+    env["k"][t].gemm_prefill(w, xd, y, m)
+    got = to_host(y, env["ctx"]).reshape(m, n)
+    enc = enc_dev.cpu().numpy()
+    sample = sorted({0, 1, 15, 16, 127, 128, m // 2, m - 1})
+    ref = np.stack([O.quant_gemv(t, enc, k, n, x[i], threads=16) for i in sample])
+    assert max_rel_err(got[sample], ref) <= RTOL
+    assert np.all(np.isfinite(got))
+
+
 @pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096)])
 def test_batched_ffn_m64_full_size(env, t, k, n):
     """BASELINE config 2 at M = 64 on the Qwen3-8B FFN shapes (gate/up Q4_K
