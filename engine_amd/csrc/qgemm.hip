@@ -750,41 +750,37 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) decode_sb<T>(wcur[rb], q, dec[rb]);
             const _Float16* xt0 = &xcur[r16 * 256];
-            // Software pipeline over the 8 chunks: the next chunk's A fragments
-            // are dequantised while the current chunk's MFMAs run, and the B
-            // fragments (LDS) are read three token blocks ahead (the next
-            // chunk's first three at the end of the current one).
-            half8_t acur[RB], anext[RB], bq[3];
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) acur[rb] = tile_chunk<T, 0>(wcur[rb], dec[rb], q);
+            // Software pipeline over the 8 chunks: while chunk C's 8*RB MFMAs
+            // run, chunk C+1's A fragments are dequantised (a few VALU
+            // instructions after each MFMA, which its 16 cycles hide) and its
+            // 8 B fragments are read from LDS (one per token block, a whole
+            // chunk ahead of use).
             // token 16tb + r16, piece k0/8: LDS slot (k0/8) ^ r16
             auto bsrc = [&](int k0) { return xt0 + 8 * ((k0 >> 3) ^ r16); };
+            half8_t acur[RB], anext[RB], bcur[8], bnext[8];
 #pragma unroll
-            for (int tb = 0; tb < 3; ++tb)
-                bq[tb] = *reinterpret_cast<const half8_t*>(bsrc(tile_k0<T, 0>(q)) + tb * 16 * 256);
-            constexpr int kValu = (BlockTraits<T>::bytes == 144 ? 24 : 30) / RB;  // dequant instructions per MFMA
+            for (int rb = 0; rb < RB; ++rb) acur[rb] = tile_chunk<T, 0>(wcur[rb], dec[rb], q);
+#pragma unroll
+            for (int tb = 0; tb < 8; ++tb)
+                bcur[tb] = *reinterpret_cast<const half8_t*>(bsrc(tile_k0<T, 0>(q)) + tb * 16 * 256);
+            constexpr int kValu = T == kQ5K ? 4 : 3;  // dequant instructions per MFMA
             auto chunk = [&](auto c_const) {
                 constexpr int C = decltype(c_const)::value;
                 if constexpr (C < 7) {
+                    const _Float16* nsrc = bsrc(tile_k0<T, C + 1>(q));
+#pragma unroll
+                    for (int tb = 0; tb < 8; ++tb)
+                        bnext[tb] = *reinterpret_cast<const half8_t*>(nsrc + tb * 16 * 256);
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) anext[rb] = tile_chunk<T, C + 1>(wcur[rb], dec[rb], q);
                 }
-                const _Float16* src = bsrc(tile_k0<T, C>(q));
 #pragma unroll
-                for (int tb = 0; tb < 8; ++tb) {
-                    const half8_t b = tb < 3 ? bq[tb] : *reinterpret_cast<const half8_t*>(src + tb * 16 * 256);
+                for (int tb = 0; tb < 8; ++tb)
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb)
-                        acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(acur[rb], b, acc[rb][tb], 0, 0, 0);
-                }
-                if constexpr (C < 7) {
-                    const _Float16* nsrc = bsrc(tile_k0<T, C + 1>(q));
-#pragma unroll
-                    for (int tb = 0; tb < 3; ++tb)
-                        bq[tb] = *reinterpret_cast<const half8_t*>(nsrc + tb * 16 * 256);
-                }
-                // issue order: per token block its MFMAs, the B read three
-                // blocks ahead, and a share of the next chunk's dequantisation
+                        acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(acur[rb], bcur[tb], acc[rb][tb], 0, 0, 0);
+                // issue order: each MFMA followed by a share of the next
+                // chunk's dequantisation, one B read per token block
 #pragma unroll
                 for (int tb = 0; tb < 8; ++tb) {
 #pragma unroll
@@ -798,6 +794,8 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
                 if constexpr (C < 7) {
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) acur[rb] = anext[rb];
+#pragma unroll
+                    for (int tb = 0; tb < 8; ++tb) bcur[tb] = bnext[tb];
                 }
             };
             chunk(std::integral_constant<int, 0>{});
