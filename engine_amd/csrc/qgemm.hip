@@ -1,9 +1,8 @@
 // Prefill / large-batch matmul for Q4_K / Q5_K / Q6_K on gfx950: y[M][N] =
 // x[M][K] . W^T with the weights dequantised in registers straight into MFMA
-// operand layout and multiplied on the matrix cores (v_mfma_f32_32x32x16_f16),
-// accumulating in f32.
+// operand layout and multiplied on the matrix cores, accumulating in f32.
 //
-// Two kernels:
+// Kernels:
 //  - act_f16_kernel: one workgroup per token. Optional RMSNorm
 //    (x * 1/sqrt(sum(x^2)/K + eps) * gamma, qwen_reference.rs:550-556), then
 //    conversion to f16 after a power-of-two scale that maps the token's
@@ -17,7 +16,10 @@
 //    registers two steps ahead and written to LDS one step ahead), weights are
 //    loaded per lane straight from HBM (three steps ahead) and dequantised in
 //    f32, (d*sc)*q - dmin*m, then rounded once to f16 (RNE) in the A-operand
-//    layout. Each A fragment feeds CB MFMAs.
+//    layout. Each A fragment feeds CB MFMAs (v_mfma_f32_32x32x16_f16).
+//  - qgemm_tile_kernel: 192-row x 128-token workgroups of four waves on
+//    v_mfma_f32_16x16x32_f16 with packed-f16 dequantisation, for grids that
+//    fill the CUs (described where it is defined).
 //
 // MFMA 32x32x16 operand layout (measured on gfx950): lane l holds
 // A[l%32][8*(l/32)+j], B[8*(l/32)+j][l%32] (j = 0..7) and
