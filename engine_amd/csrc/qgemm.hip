@@ -465,9 +465,8 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restri
 //              (Q & 1), nibble Q >> 1, qh bits 2Q, scale 8(q>>1) + 2Q + (q&1).
 // (lib.rs:596-661 element order.) Each 16-byte weight load serves 4 chunks.
 
-constexpr int kTileTok = 128;                      // tokens per workgroup (8 blocks of 16)
+constexpr int kTileTokMax = 128;                   // most tokens per workgroup (8 blocks of 16)
 constexpr int kTileThreads = 256;
-constexpr int kTileLoads = kTileTok * 512 / 1024 / (kTileThreads / 64);  // 1 KB LDS loads per wave per super-block
 
 typedef float float4_v __attribute__((ext_vector_type(4)));
 
@@ -660,25 +659,32 @@ __device__ __forceinline__ int tile_k0(int q) {
     }
 }
 
-template <int T, int RB>
+// RB row blocks of 16 per wave, TB token blocks of 16 per workgroup. Split
+// K: workgroup z covers super-blocks [z*split_sb, (z+1)*split_sb); with
+// partial != null it writes its raw tile to partial[z][M][N] and
+// qgemm_reduce_kernel adds the splits in order.
+template <int T, int RB, int TB>
 __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void qgemm_tile_kernel(
     const uint8_t* __restrict__ w, uint32_t wbytes, const _Float16* __restrict__ xh, const float* __restrict__ unscale,
-    float* __restrict__ y, int M, int N, int K) {
+    float* __restrict__ y, float* __restrict__ partial, int M, int N, int K, int split_sb) {
+    constexpr int kTok = 16 * TB;                        // tokens per workgroup
+    constexpr int kWaveTok = kTok / (kTileThreads / 64);  // x tile tokens each wave loads
+    constexpr int kLoads = kWaveTok / 2;                  // its 1 KB loads per super-block
     constexpr int BB = BlockTraits<T>::bytes;
     // two x slots as separate objects: the compiler can then tell that the
     // reads of one slot do not alias the loads into the other in flight
-    __shared__ __attribute__((aligned(16))) _Float16 xs0[kTileTok * 256];
-    __shared__ __attribute__((aligned(16))) _Float16 xs1[kTileTok * 256];
+    __shared__ __attribute__((aligned(16))) _Float16 xs0[kTok * 256];
+    __shared__ __attribute__((aligned(16))) _Float16 xs1[kTok * 256];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int q = lane >> 4;
     const int r16 = lane & 15;
     const int n0 = blockIdx.x * 64 * RB + 16 * RB * wave;
-    const int m0 = blockIdx.y * kTileTok;
+    const int m0 = blockIdx.y * kTok;
     const int nb = K >> 8;
-    const int sb_begin = 0;
-    const int sb_end = nb;
+    const int sb_begin = blockIdx.z * split_sb;
+    const int sb_end = min(nb, sb_begin + split_sb);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, wbytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(xh, (uint32_t)M * (uint32_t)K * 2u);
     uint32_t row_off[RB];
@@ -696,18 +702,18 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
     // offset for load i (token and swizzled piece) is fixed; the super-block
     // goes in the uniform offset. Tokens past M read past the activations
     // (zeros) through the lane offset alone.
-    uint32_t xoff[kTileLoads];
+    uint32_t xoff[kLoads];
 #pragma unroll
-    for (int i = 0; i < kTileLoads; ++i) {
-        const int t = 32 * wave + 2 * i + (lane >> 5);
+    for (int i = 0; i < kLoads; ++i) {
+        const int t = kWaveTok * wave + 2 * i + (lane >> 5);
         xoff[i] = ((uint32_t)(m0 + t) * (uint32_t)K + (uint32_t)((lane & 31) ^ (t & 15)) * 8u) * 2u;
     }
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     auto load_x = [&](_Float16* xs, int sb) {
 #pragma unroll
-        for (int i = 0; i < kTileLoads; ++i)
+        for (int i = 0; i < kLoads; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                xr, (__attribute__((address_space(3))) void*)&xs[(32 * wave_u + 2 * i) * 256], 16, (int)xoff[i],
+                xr, (__attribute__((address_space(3))) void*)&xs[(kWaveTok * wave_u + 2 * i) * 256], 16, (int)xoff[i],
                 sb * 512, 0, 0);
         // the tile is written behind the compiler's back: LDS reads must not
         // be folded or moved across this point
@@ -718,11 +724,11 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
         for (int rb = 0; rb < RB; ++rb) load_sb<T>(ring[rb], wr, row_off[rb] + (uint32_t)sb * BB, q);
     };
 
-    float4_v acc[RB][8];
+    float4_v acc[RB][TB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int tb = 0; tb < 8; ++tb) acc[rb][tb] = float4_v{};
+        for (int tb = 0; tb < TB; ++tb) acc[rb][tb] = float4_v{};
 
     // Prologue: x and weights of the first super-block.
     SbW<T> wring[2][RB];
@@ -759,11 +765,11 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
             // chunk ahead of use).
             // token 16tb + r16, piece k0/8: LDS slot (k0/8) ^ r16
             auto bsrc = [&](int k0) { return xt0 + 8 * ((k0 >> 3) ^ r16); };
-            half8_t acur[RB], anext[RB], bcur[8], bnext[8];
+            half8_t acur[RB], anext[RB], bcur[TB], bnext[TB];
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) acur[rb] = tile_chunk<T, 0>(wcur[rb], dec[rb], q);
 #pragma unroll
-            for (int tb = 0; tb < 8; ++tb)
+            for (int tb = 0; tb < TB; ++tb)
                 bcur[tb] = *reinterpret_cast<const half8_t*>(bsrc(tile_k0<T, 0>(q)) + tb * 16 * 256);
             constexpr int kValu = T == kQ5K ? 4 : 3;  // dequant instructions per MFMA
             auto chunk = [&](auto c_const) {
@@ -771,20 +777,20 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
                 if constexpr (C < 7) {
                     const _Float16* nsrc = bsrc(tile_k0<T, C + 1>(q));
 #pragma unroll
-                    for (int tb = 0; tb < 8; ++tb)
+                    for (int tb = 0; tb < TB; ++tb)
                         bnext[tb] = *reinterpret_cast<const half8_t*>(nsrc + tb * 16 * 256);
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) anext[rb] = tile_chunk<T, C + 1>(wcur[rb], dec[rb], q);
                 }
 #pragma unroll
-                for (int tb = 0; tb < 8; ++tb)
+                for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb)
                         acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(acur[rb], bcur[tb], acc[rb][tb], 0, 0, 0);
                 // issue order: each MFMA followed by a share of the next
                 // chunk's dequantisation, one B read per token block
 #pragma unroll
-                for (int tb = 0; tb < 8; ++tb) {
+                for (int tb = 0; tb < TB; ++tb) {
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) {
                         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -797,7 +803,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) acur[rb] = anext[rb];
 #pragma unroll
-                    for (int tb = 0; tb < 8; ++tb) bcur[tb] = bnext[tb];
+                    for (int tb = 0; tb < TB; ++tb) bcur[tb] = bnext[tb];
                 }
             };
             chunk(std::integral_constant<int, 0>{});
@@ -822,14 +828,14 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
     }
     if (sb < sb_end) step(I0{}, std::false_type{}, sb);
 
-    // epilogue: C[n][m] -> y[m][n] * unscale[m]
-    float* out = y;
+    // epilogue: C[n][m] -> y[m][n] * unscale[m], or the raw split tile
+    float* out = partial ? partial + (size_t)blockIdx.z * M * N : y;
     const bool vec = (N & 3) == 0;
 #pragma unroll
-    for (int tb = 0; tb < 8; ++tb) {
+    for (int tb = 0; tb < TB; ++tb) {
         const int m = m0 + 16 * tb + r16;
         if (m >= M) continue;
-        const float us = unscale[m];
+        const float us = partial ? 1.0f : unscale[m];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             const int n = n0 + 16 * rb + 4 * q;
@@ -909,32 +915,91 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, void* worksp
     return hipGetLastError();
 }
 
-// Wide tiles (M > 64) run when their grid of 192-row x 128-token
-// workgroups fills at least 90% of its last round of CUs (e.g. Q4_K
-// 4096 -> 12288 at M = 512: 64 x 4 = 256 workgroups); other shapes keep
-// qgemm_kernel, whose split K and 256-row tiles balance them better. Each
-// wave's 48 rows keep its B reads (the whole x tile per wave) within the
-// LDS bandwidth (about 90 B/clk per CU measured); fewer rows per wave are
-// LDS-bound.
+// Wide tiles. M > 128 runs 192-row x 128-token workgroups when their grid
+// fills at least 90% of its last round of CUs (e.g. Q4_K 4096 -> 12288 at
+// M = 512: 64 x 4 = 256 workgroups); other shapes keep qgemm_kernel, whose
+// split K and 256-row tiles balance them better. Each wave's 48 rows keep its
+// B reads (the whole x tile per wave) within the LDS bandwidth (about 90
+// B/clk per CU measured); 32-row waves over 128 tokens are LDS-bound.
+// 32 < M <= 128 picks (rows per wave, tokens per workgroup, K split) among
+// the grids that fill 90-100% of one round, by an estimate fitted to
+// measured calls: about 3 us per super-block step plus 0.05 us per MFMA
+// tile block, plus the split's partial tiles (written, read, reduced).
 constexpr int kTileRb = 3;
+constexpr int kTileTb = 8;
 
 static bool use_tile(int M, int N, int cu_count) {
-    const long long wgs = (long long)((N + 64 * kTileRb - 1) / (64 * kTileRb)) * ((M + kTileTok - 1) / kTileTok);
+    const long long wgs = (long long)((N + 64 * kTileRb - 1) / (64 * kTileRb)) * ((M + 16 * kTileTb - 1) / (16 * kTileTb));
     const long long cus = std::max(1, cu_count);
     const long long rounds = (wgs + cus - 1) / cus;
     return wgs * 10 >= rounds * cus * 9;
 }
 
-template <int T>
-static hipError_t launch_qgemm_tile(void* workspace, const uint8_t* w, uint32_t wbytes, float* y, int M, int N, int K,
-                                    hipStream_t stream) {
+struct TileChoice {
+    int rb = 0, tb = 0, splits = 0;  // rb == 0: none fits
+};
+
+static TileChoice choose_tile_small(int M, int N, int K, size_t room_bytes, int cu_count) {
+    TileChoice best;
+    const long long cus = std::max(1, cu_count);
+    const int nb = K >> 8;
+    const size_t tile_bytes = (size_t)M * N * 4;
+    const int room_splits = (int)std::min<size_t>(16, tile_bytes ? room_bytes / tile_bytes : 0);
+    double best_t = 1e30;
+    const int shapes[3][2] = {{3, 8}, {3, 4}, {2, 4}};
+    for (const auto& sh : shapes) {
+        const int rb = sh[0], tb = sh[1];
+        if (tb == 8 && M <= 64) continue;  // a mostly empty token tile
+        const long long tn = (N + 64 * rb - 1) / (64 * rb), tm = (M + 16 * tb - 1) / (16 * tb);
+        for (int s = 1; s <= 16 && s <= nb; ++s) {
+            if (s > 1 && s > room_splits) break;
+            const int split_sb = (nb + s - 1) / s;
+            const int splits = (nb + split_sb - 1) / split_sb;
+            const long long wgs = tn * tm * splits;
+            if (wgs > cus || wgs * 10 < cus * 9) continue;
+            double t = split_sb * (3.0 + 0.05 * rb * tb);
+            if (splits > 1) t += 1.0 + (double)(2 * splits + 1) * (double)tile_bytes / 4.0e6;
+            if (t < best_t - 1e-9) {
+                best_t = t;
+                best.rb = rb;
+                best.tb = tb;
+                best.splits = splits;
+            }
+        }
+    }
+    return best;
+}
+
+template <int T, int RB, int TB>
+static hipError_t launch_tile_t(void* workspace, const uint8_t* w, uint32_t wbytes, float* y, int M, int N, int K,
+                                int splits, int cu_count, hipStream_t stream) {
     uint8_t* base = static_cast<uint8_t*>(workspace);
     const _Float16* xh = reinterpret_cast<const _Float16*>(base);
-    const float* us = reinterpret_cast<const float*>(base + align256((size_t)M * K * 2));
-    const dim3 grid((N + 64 * kTileRb - 1) / (64 * kTileRb), (M + kTileTok - 1) / kTileTok);
-    hipLaunchKernelGGL((qgemm_tile_kernel<T, kTileRb>), grid, dim3(kTileThreads), 0, stream, w, wbytes, xh, us, y, M,
-                       N, K);
+    const size_t us_off = align256((size_t)M * K * 2);
+    const float* us = reinterpret_cast<const float*>(base + us_off);
+    float* part = reinterpret_cast<float*>(base + us_off + align256((size_t)M * 4));
+    const int nb = K >> 8;
+    const int split_sb = (nb + splits - 1) / splits;
+    splits = (nb + split_sb - 1) / split_sb;
+    const dim3 grid((N + 64 * RB - 1) / (64 * RB), (M + 16 * TB - 1) / (16 * TB), splits);
+    hipLaunchKernelGGL((qgemm_tile_kernel<T, RB, TB>), grid, dim3(kTileThreads), 0, stream, w, wbytes, xh, us, y,
+                       splits > 1 ? part : nullptr, M, N, K, split_sb);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
+    const size_t total = (size_t)M * N;
+    const int rgrid = (int)std::min<size_t>((total + 255) / 256, (size_t)std::max(1, cu_count) * 8);
+    hipLaunchKernelGGL(qgemm_reduce_kernel, dim3(rgrid), dim3(256), 0, stream, part, us, y, M, N, splits);
     return hipGetLastError();
+}
+
+template <int T>
+static hipError_t launch_qgemm_tile(void* workspace, const uint8_t* w, uint32_t wbytes, float* y, int M, int N, int K,
+                                    int rb, int tb, int splits, int cu_count, hipStream_t stream) {
+    if (rb == 3 && tb == 8) return launch_tile_t<T, 3, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
+    if (rb == 3 && tb == 4) return launch_tile_t<T, 3, 4>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
+    if (rb == 2 && tb == 8) return launch_tile_t<T, 2, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
+    if (rb == 2 && tb == 4) return launch_tile_t<T, 2, 4>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
+    return hipErrorInvalidValue;
 }
 
 // Tile by token count: few tokens take small tiles (more workgroups for the
@@ -947,10 +1012,17 @@ template <int T>
 static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, void* workspace, size_t workspace_bytes, float* y,
                                  int M, int N, int K, int cu_count, hipStream_t stream) {
     if (M <= 32) return launch_qgemm_t<T, 1, 1>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
-    if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
     // (the tile kernel's activation offsets of its last token tile must stay below 2^32)
-    if (use_tile(M, N, cu_count) && (uint64_t)(M + kTileTok) * (uint64_t)K * 2u < (1ull << 32))
-        return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, stream);
+    const bool tile_ok = (uint64_t)(M + kTileTokMax) * (uint64_t)K * 2u < (1ull << 32);
+    if (tile_ok && M <= 128) {
+        const size_t part_off = align256((size_t)M * K * 2) + align256((size_t)M * 4);
+        const TileChoice c =
+            choose_tile_small(M, N, K, workspace_bytes > part_off ? workspace_bytes - part_off : 0, cu_count);
+        if (c.rb) return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, c.rb, c.tb, c.splits, cu_count, stream);
+    }
+    if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
+    if (tile_ok && M > 128 && use_tile(M, N, cu_count))
+        return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, kTileRb, kTileTb, 1, cu_count, stream);
     return launch_qgemm_t<T, 4, 8>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
 }
 

@@ -109,11 +109,15 @@ def test_prefill_config3_full_size(env, t, k, n):
     (13, 768, 12288, 512, "f32"),     # three super-blocks: one pair of steps and the odd one
     (14, 256, 11520, 400, "bf16"),    # one super-block (the odd step alone), 2-byte aligned rows
     (14, 2048, 12288, 500, "f32"),
+    (12, 4096, 12288, 128, "bf16"),   # 64 x 1 tiles of 128 tokens, K split in 4 (partials reduced in order)
+    (14, 4096, 12288, 48, "f32"),     # 64 x 1 tiles of 64 tokens, K split in 4, last token tile 48 of 64
+    (14, 4096, 4096, 100, "bf16"),    # 32-row waves: 32 x 2 tiles of 64 tokens, K split in 4
+    (13, 12288, 4096, 64, "f32"),     # 32 x 1 tiles of 64 tokens, K split in 8
 ])
 def test_prefill_wide_tiles(env, t, k, n, m, dtype):
-    """Shapes whose 192-row x 128-token grid fills a 256-CU MI355X (the
-    wide-tile matmul with packed-f16 dequantisation): rows of a token sample
-    against the oracle, every output finite."""
+    """Shapes whose wide-tile grid fills a 256-CU MI355X (the wide-tile
+    matmul with packed-f16 dequantisation, with K split for 32 < M <= 128):
+    rows of a token sample against the oracle, every output finite."""
     import torch
     print("CASE prefill wide", t, k, n, m, dtype, flush=True)
     gen = torch.Generator(device="cuda:0")
@@ -129,7 +133,7 @@ def test_prefill_wide_tiles(env, t, k, n, m, dtype):
     env["k"][t].gemm_prefill(w, xd, y, m)
     got = to_host(y, env["ctx"]).reshape(m, n)
     enc = enc_dev.cpu().numpy()
-    sample = sorted({0, 1, 15, 16, 127, 128, m // 2, m - 1})
+    sample = sorted(i for i in {0, 1, 15, 16, 127, 128, m // 2, m - 1} if i < m)
     ref = np.stack([O.quant_gemv(t, enc, k, n, x[i], threads=16) for i in sample])
     assert max_rel_err(got[sample], ref) <= RTOL
     assert np.all(np.isfinite(got))
