@@ -709,9 +709,11 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
         xoff[i] = ((uint32_t)(m0 + t) * (uint32_t)K + (uint32_t)((lane & 31) ^ (t & 15)) * 8u) * 2u;
     }
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    auto load_x = [&](_Float16* xs, int sb) {
+    // loads [part*kLoads/4, (part+1)*kLoads/4) of the tile
+    auto load_x = [&](_Float16* xs, int sb, auto part_const) {
+        constexpr int part = decltype(part_const)::value;
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i)
+        for (int i = part * kLoads / 4; i < (part + 1) * kLoads / 4; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 xr, (__attribute__((address_space(3))) void*)&xs[(kWaveTok * wave_u + 2 * i) * 256], 16, (int)xoff[i],
                 sb * 512, 0, 0);
@@ -732,25 +734,26 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
 
     // Prologue: x and weights of the first super-block.
     SbW<T> wring[2][RB];
-    load_x(xs0, sb_begin);
+    load_x(xs0, sb_begin, std::integral_constant<int, 0>{});
+    load_x(xs0, sb_begin, std::integral_constant<int, 1>{});
+    load_x(xs0, sb_begin, std::integral_constant<int, 2>{});
+    load_x(xs0, sb_begin, std::integral_constant<int, 3>{});
     load_w(wring[0], sb_begin);
     __syncthreads();
 
     // One super-block; slot r (static) holds its x tile and weights.
     // PREFETCH: x of sb+1 into the other LDS slot (every wave finished
-    // reading it before the last barrier) and the weights of sb+1, a whole
-    // step ahead of their use (the barrier below waits for the x tile). The
-    // loads are unconditional within the loop, so the compiler's wait counts
-    // stay exact; a prefetch of sb+1 = sb_end <= nb reads in-bounds data that
-    // is not used (or zeros past the tensors).
+    // reading it before the last barrier; a quarter in each of the first four
+    // chunks) and the weights of sb+1 (a row block in each of the first RB
+    // chunks), most of a step ahead of their use (the barrier below waits
+    // for the x tile). The loads are unconditional within the loop, so the
+    // compiler's wait counts stay exact; a prefetch of sb+1 = sb_end <= nb
+    // reads in-bounds data that is not used (or zeros past the tensors).
     auto step = [&](auto r_const, auto prefetch_const, int sb) {
         constexpr int r = decltype(r_const)::value;
         _Float16* const xcur = r ? xs1 : xs0;
         _Float16* const xnext = r ? xs0 : xs1;
-        if constexpr (decltype(prefetch_const)::value) {
-            load_x(xnext, sb + 1);
-            load_w(wring[r ^ 1], sb + 1);
-        }
+        constexpr bool kNext = decltype(prefetch_const)::value;
         __builtin_amdgcn_sched_barrier(0);
         {
             const SbW<T>(&wcur)[RB] = wring[r];
@@ -774,6 +777,11 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(1,
             constexpr int kValu = T == kQ5K ? 4 : 3;  // dequant instructions per MFMA
             auto chunk = [&](auto c_const) {
                 constexpr int C = decltype(c_const)::value;
+                // the next step's loads, spread over the first chunks so the
+                // wave never queues them all at once
+                if constexpr (kNext && C < 4) load_x(xnext, sb + 1, c_const);
+                if constexpr (kNext && C < RB)
+                    load_sb<T>(wring[r ^ 1][C], wr, row_off[C] + (uint32_t)(sb + 1) * BB, q);
                 if constexpr (C < 7) {
                     const _Float16* nsrc = bsrc(tile_k0<T, C + 1>(q));
 #pragma unroll
