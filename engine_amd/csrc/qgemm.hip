@@ -15,8 +15,8 @@
 //    in LDS (padded rows, double-buffered; a step's tile is loaded into
 //    registers two steps ahead and written to LDS one step ahead), weights are
 //    loaded per lane straight from HBM (three steps ahead) and dequantised in
-//    f32, (d*sc)*q - dmin*m, then rounded once to f16 (RNE) in the A-operand
-//    layout. Each A fragment feeds CB MFMAs (v_mfma_f32_32x32x16_f16).
+//    packed f16 (below) in the A-operand layout. Each A fragment feeds CB
+//    MFMAs (v_mfma_f32_32x32x16_f16).
 //  - qgemm_tile_kernel: 192-row x 128-token workgroups of four waves on
 //    v_mfma_f32_16x16x32_f16 with packed-f16 dequantisation, for grids that
 //    fill the CUs (described where it is defined).
@@ -196,49 +196,97 @@ __device__ __forceinline__ uint4 funnel4(uint4 a, uint32_t t, uint32_t sh) {
     return o;
 }
 
-// Eight f16 weights (a*q_j - b), q_j = byte j of (lo, hi) after masking
-// (byte-to-float converts are single v_cvt_f32_ubyteN instructions).
-__device__ __forceinline__ half8_t dequant8(uint32_t lo, uint32_t hi, float a, float b) {
-    // Opaque to the optimiser, so each byte converts with one v_cvt_f32_ubyteN
-    // instead of a bit-field extract plus a convert.
-    asm volatile("" : "+v"(lo), "+v"(hi));
-    float w[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        w[j] = __builtin_fmaf(a, (float)((lo >> (8 * j)) & 0xffu), -b);
-        w[4 + j] = __builtin_fmaf(a, (float)((hi >> (8 * j)) & 0xffu), -b);
-    }
-    half8_t h;
-#pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-        const float2_v f = {w[j], w[j + 1]};
-        const half2_v p = __builtin_convertvector(f, half2_v);
-        h[j] = p[0];
-        h[j + 1] = p[1];
-    }
-    return h;
+// Weights are dequantised in packed f16 (two per instruction, no conversion
+// instructions): a quant byte q becomes the f16 1024 + q (bits 0x6400 | q,
+// or 1024 + 16q for a high nibble left in place), and
+//   Q4_K/Q5_K: qs = fma(1024 + q, sc, -1024 sc) = q*sc exactly (every value
+//              involved is an f16 integer, q*sc <= 1953), then
+//              w = fma(qs, d, -f16(dmin*m)): one rounding of d*sc*q - dmin*m
+//              besides that of the minimum term;
+//   Q6_K:      qm = (1024 + q) - 1056 = q - 32 exactly, then
+//              w = fma(qm, a_hi, qm * a_lo) with a = d*sc split into two f16
+//              parts: one rounding of a*(q - 32).
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+__device__ __forceinline__ uint32_t as_u(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ half2_t splat_h2(float v) {
+    const _Float16 h = (_Float16)v;
+    return half2_t{h, h};
+}
+// bytes (b0, b1, b2, b3) -> (b0, b2, b1, b3): the halves of x & 0x00ff00ff
+// are then elements (0, 1) and those of (x >> 8) elements (2, 3)
+__device__ __forceinline__ uint32_t pair_order(uint32_t x) { return __builtin_amdgcn_perm(x, x, 0x03010200u); }
+
+// 0x64006400 in a vector register, so (x & mask) | it is one v_and_or_b32
+// (a three-operand instruction takes no literal and reads at most one scalar
+// register on gfx9: the mask goes in the scalar register)
+__device__ __forceinline__ uint32_t f16_magic() {
+    uint32_t k;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(k));
+    return k;
+}
+
+template <int T>
+__device__ __forceinline__ void tile_word(uint32_t x, uint32_t mask, uint32_t extra_a, uint32_t extra_b, half2_t s,
+                                          half2_t c, half2_t d, half2_t nb, uint32_t& oa, uint32_t& ob) {
+    const uint32_t xp = pair_order(x);
+    const uint32_t k = f16_magic();
+    const half2_t pa = as_h2((xp & mask) | (extra_a | k));
+    const half2_t pb = as_h2(((xp >> 8) & mask) | (extra_b | k));
+    oa = as_u(__builtin_elementwise_fma(__builtin_elementwise_fma(pa, s, c), d, nb));
+    ob = as_u(__builtin_elementwise_fma(__builtin_elementwise_fma(pb, s, c), d, nb));
+}
+
+__device__ __forceinline__ void tile_word6(uint32_t x, half2_t ahi, half2_t alo, uint32_t& oa, uint32_t& ob) {
+    const uint32_t xp = pair_order(x);
+    const uint32_t k = f16_magic();
+    const half2_t off = half2_t{(_Float16)-1056.0f, (_Float16)-1056.0f};
+    const half2_t qa = as_h2((xp & 0x003f003fu) | k) + off;
+    const half2_t qb = as_h2(((xp >> 8) & 0x003f003fu) | k) + off;
+    oa = as_u(__builtin_elementwise_fma(qa, ahi, qa * alo));
+    ob = as_u(__builtin_elementwise_fma(qb, ahi, qb * alo));
+}
+
+// Eight f16 weights from byte quants q_j (byte j of lo, then of hi):
+// Q4_K/Q5_K w = f16(d*sc*q - f16(dmin*m)), Q6_K w = f16(a*(q - 32)), as above.
+__device__ __forceinline__ half8_t dequant8_qs(uint32_t lo, uint32_t hi, half2_t s, half2_t c, half2_t d,
+                                               half2_t nb) {
+    uint32_t o[4];
+    tile_word<kQ4K>(lo, 0x00ff00ffu, 0, 0, s, c, d, nb, o[0], o[1]);
+    tile_word<kQ4K>(hi, 0x00ff00ffu, 0, 0, s, c, d, nb, o[2], o[3]);
+    return __builtin_bit_cast(half8_t, uint4{o[0], o[1], o[2], o[3]});
+}
+
+__device__ __forceinline__ half8_t dequant8_q6(uint32_t lo, uint32_t hi, half2_t ahi, half2_t alo) {
+    uint32_t o[4];
+    tile_word6(lo, ahi, alo, o[0], o[1]);
+    tile_word6(hi, ahi, alo, o[2], o[3]);
+    return __builtin_bit_cast(half8_t, uint4{o[0], o[1], o[2], o[3]});
 }
 
 // A step's weights decoded once: scale and offset of each scale group the
 // lane touches, and (Q6_K) the payload windows realigned.
 template <int T> struct StepDec;
-template <> struct StepDec<kQ4K> { float a[4], b[4]; };
-template <> struct StepDec<kQ5K> { float a[4], b[4]; };
-template <> struct StepDec<kQ6K> { float a[4]; uint4 l0, l1, qh; };
+template <> struct StepDec<kQ4K> { half2_t s[4], c[4], nb[4], d; };
+template <> struct StepDec<kQ5K> { half2_t s[4], c[4], nb[4], d; };
+template <> struct StepDec<kQ6K> { half2_t ahi[4], alo[4]; uint4 l0, l1, qh; };
 
 template <int T, int HALF>
 __device__ __forceinline__ void decode_step(const StepW<T>& s, int hl, StepDec<T>& o) {
     if constexpr (T == kQ4K || T == kQ5K) {
         // groups 4*HALF + i, i = 2t' + p; six-bit scales/minima (lib.rs:573-587)
-        const float d = half_bits_to_float(s.h.x & 0xffffu);
         const float dmin = half_bits_to_float(s.h.x >> 16);
+        o.d = as_h2((s.h.x & 0xffffu) * 0x10001u);
         const uint32_t scw = HALF ? ((s.h.w & 0x0f0f0f0fu) | ((s.h.y >> 2) & 0x30303030u)) : (s.h.y & 0x3f3f3f3fu);
         const uint32_t mnw = HALF ? (((s.h.w >> 4) & 0x0f0f0f0fu) | ((s.h.z >> 2) & 0x30303030u))
                                   : (s.h.z & 0x3f3f3f3fu);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            o.a[i] = d * (float)((scw >> (8 * i)) & 0xffu);
-            o.b[i] = dmin * (float)((mnw >> (8 * i)) & 0xffu);
+            const float scf = (float)((scw >> (8 * i)) & 0xffu);
+            o.s[i] = splat_h2(scf);
+            o.c[i] = splat_h2(-1024.0f * scf);
+            o.nb[i] = splat_h2(-(dmin * (float)((mnw >> (8 * i)) & 0xffu)));
         }
     } else {
         o.l0 = funnel4(s.l0, s.l0t, s.shift);
@@ -249,10 +297,14 @@ __device__ __forceinline__ void decode_step(const StepW<T>& s, int hl, StepDec<T
         // scale 8*HALF + 2v + hl: bytes hl and hl+2 of dwords 2*HALF (v = 0, 1) and 2*HALF+1 (v = 2, 3)
         const uint32_t w0 = (HALF ? scw.z : scw.x) >> (8 * hl);
         const uint32_t w1 = (HALF ? scw.w : scw.y) >> (8 * hl);
-        o.a[0] = d * (float)(int8_t)(w0 & 0xffu);
-        o.a[1] = d * (float)(int8_t)((w0 >> 16) & 0xffu);
-        o.a[2] = d * (float)(int8_t)(w1 & 0xffu);
-        o.a[3] = d * (float)(int8_t)((w1 >> 16) & 0xffu);
+        const float a[4] = {d * (float)(int8_t)(w0 & 0xffu), d * (float)(int8_t)((w0 >> 16) & 0xffu),
+                            d * (float)(int8_t)(w1 & 0xffu), d * (float)(int8_t)((w1 >> 16) & 0xffu)};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const _Float16 h = (_Float16)a[v];
+            o.ahi[v] = half2_t{h, h};
+            o.alo[v] = splat_h2(a[v] - (float)h);
+        }
     }
 }
 
@@ -274,7 +326,7 @@ __device__ __forceinline__ half8_t chunk_weights(const StepW<T>& s, const StepDe
             lo |= (((ss ? s.qh.z : s.qh.x) >> g) & 0x01010101u) << 4;
             hi |= (((ss ? s.qh.w : s.qh.y) >> g) & 0x01010101u) << 4;
         }
-        return dequant8(lo, hi, dec.a[2 * tp + p], dec.b[2 * tp + p]);
+        return dequant8_qs(lo, hi, dec.s[2 * tp + p], dec.c[2 * tp + p], dec.d, dec.nb[2 * tp + p]);
     } else {
         constexpr int v = C >> 1, ss = C & 1;
         koff = 32 * v + 16 * hl + 8 * ss;
@@ -285,7 +337,7 @@ __device__ __forceinline__ half8_t chunk_weights(const StepW<T>& s, const StepDe
         const uint32_t hhi = ss ? dec.qh.w : dec.qh.y;
         lo = ((lo >> (4 * (v >> 1))) & 0x0f0f0f0fu) | (((hlo >> (2 * v)) & 0x03030303u) << 4);
         hi = ((hi >> (4 * (v >> 1))) & 0x0f0f0f0fu) | (((hhi >> (2 * v)) & 0x03030303u) << 4);
-        return dequant8(lo, hi, dec.a[v], 32.f * dec.a[v]);
+        return dequant8_q6(lo, hi, dec.ahi[v], dec.alo[v]);
     }
 }
 
@@ -507,28 +559,6 @@ __device__ __forceinline__ void load_sb(SbW<T>& s, __amdgpu_buffer_rsrc_t r, uin
     }
 }
 
-// Weights are dequantised in packed f16 (two per instruction, no conversion
-// instructions): a quant byte q becomes the f16 1024 + q (bits 0x6400 | q,
-// or 1024 + 16q for a high nibble left in place), and
-//   Q4_K/Q5_K: qs = fma(1024 + q, sc, -1024 sc) = q*sc exactly (every value
-//              involved is an f16 integer, q*sc <= 1953), then
-//              w = fma(qs, d, -f16(dmin*m)): one rounding of d*sc*q - dmin*m
-//              besides that of the minimum term;
-//   Q6_K:      qm = (1024 + q) - 1056 = q - 32 exactly, then
-//              w = fma(qm, a_hi, qm * a_lo) with a = d*sc split into two f16
-//              parts: one rounding of a*(q - 32).
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
-__device__ __forceinline__ uint32_t as_u(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
-__device__ __forceinline__ half2_t splat_h2(float v) {
-    const _Float16 h = (_Float16)v;
-    return half2_t{h, h};
-}
-// bytes (b0, b1, b2, b3) -> (b0, b2, b1, b3): the halves of x & 0x00ff00ff
-// are then elements (0, 1) and those of (x >> 8) elements (2, 3)
-__device__ __forceinline__ uint32_t pair_order(uint32_t x) { return __builtin_amdgcn_perm(x, x, 0x03010200u); }
-
 // A super-block's per-lane constants: Q4_K/Q5_K for groups 4L + 2(q>>1) + h
 // (s, c as above, d, and -f16(dmin*m)); Q6_K a_hi, a_lo per quarter Q (and the
 // realigned windows).
@@ -580,36 +610,6 @@ __device__ __forceinline__ void decode_sb(const SbW<T>& s, int q, SbDec<T>& o) {
 // Four packed f16 weights from one word of quant bytes (elements j..j+3)
 // whose values, after `mask`, sit in the low bits of each byte (plus `extra`
 // bits already placed: the Q5_K high bit).
-// 0x64006400 in a vector register, so (x & mask) | it is one v_and_or_b32
-// (a three-operand instruction takes no literal and reads at most one scalar
-// register on gfx9: the mask goes in the scalar register)
-__device__ __forceinline__ uint32_t f16_magic() {
-    uint32_t k;
-    asm("v_mov_b32 %0, 0x64006400" : "=v"(k));
-    return k;
-}
-
-template <int T>
-__device__ __forceinline__ void tile_word(uint32_t x, uint32_t mask, uint32_t extra_a, uint32_t extra_b, half2_t s,
-                                          half2_t c, half2_t d, half2_t nb, uint32_t& oa, uint32_t& ob) {
-    const uint32_t xp = pair_order(x);
-    const uint32_t k = f16_magic();
-    const half2_t pa = as_h2((xp & mask) | (extra_a | k));
-    const half2_t pb = as_h2(((xp >> 8) & mask) | (extra_b | k));
-    oa = as_u(__builtin_elementwise_fma(__builtin_elementwise_fma(pa, s, c), d, nb));
-    ob = as_u(__builtin_elementwise_fma(__builtin_elementwise_fma(pb, s, c), d, nb));
-}
-
-__device__ __forceinline__ void tile_word6(uint32_t x, half2_t ahi, half2_t alo, uint32_t& oa, uint32_t& ob) {
-    const uint32_t xp = pair_order(x);
-    const uint32_t k = f16_magic();
-    const half2_t off = half2_t{(_Float16)-1056.0f, (_Float16)-1056.0f};
-    const half2_t qa = as_h2((xp & 0x003f003fu) | k) + off;
-    const half2_t qb = as_h2(((xp >> 8) & 0x003f003fu) | k) + off;
-    oa = as_u(__builtin_elementwise_fma(qa, ahi, qa * alo));
-    ob = as_u(__builtin_elementwise_fma(qb, ahi, qb * alo));
-}
-
 // Chunk C's A fragment (8 f16 weights of the lane's row).
 template <int T, int C>
 __device__ __forceinline__ half8_t tile_chunk(const SbW<T>& s, const SbDec<T>& dec, int q) {
