@@ -80,3 +80,44 @@ def test_package_fails_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _lib.load()
+
+
+def test_decoder_keeps_its_weights_and_norms_alive():
+    """AmdQwen3Decode holds every weight handle and norm tensor it is given:
+    the C decoder reads them at every step and does not own them, so dropping
+    the caller's references must not free them while the decoder lives, and
+    dropping the decoder releases them. (A stand-in library answers the
+    create call; nothing reaches the device.)"""
+    import gc
+    import weakref
+
+    from engine_amd import qwen3
+
+    class FakeLib:
+        def ribn_amd_qwen3_decode_create(self, *args):
+            return 0
+
+    class FakeCtx:
+        def __init__(self):
+            self._lib = FakeLib()
+            self.handle = ctypes.c_void_p(1)
+
+    class Weight:
+        def __init__(self):
+            self.handle = ctypes.c_void_p(0x1000)
+
+    class Tensor:
+        def data_ptr(self):
+            return 0x2000
+
+    weights = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"}
+    layers = [{n: (Weight() if n in weights else Tensor()) for n in _lib.QWEN3_LAYER_FIELDS} for _ in range(2)]
+    emb, out, norm = Weight(), Weight(), Tensor()
+    refs = [weakref.ref(o) for lw in layers for o in lw.values()] + [weakref.ref(o) for o in (emb, out, norm)]
+    dec = qwen3.AmdQwen3Decode(FakeCtx(), qwen3.AmdQwen3Config(layers=2), emb, out, norm, layers)
+    del layers, emb, out, norm
+    gc.collect()
+    assert all(r() is not None for r in refs)
+    del dec
+    gc.collect()
+    assert all(r() is None for r in refs)
