@@ -15,6 +15,20 @@ def mfma_path(t, k, members):
     return t in (12, 13, 14) and members <= 16 and (members >= 5 or (k > 4096 and members >= 4))
 
 
+def wide_range_activations(k, seed):
+    """N(0,1) activations with a few x3000 outlier channels, whole scale groups
+    at 2^-20, and groups whose elements spread over 2^-16..1 in magnitude."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(k)
+    x[rng.choice(k, 8, replace=False)] *= 3000.0
+    groups = k // 32
+    for g in rng.choice(groups, groups // 8, replace=False):
+        x[32 * g:32 * g + 32] *= 2.0 ** -20
+    for g in rng.choice(groups, groups // 8, replace=False):
+        x[32 * g:32 * g + 32] *= 2.0 ** rng.uniform(-16, 0, 32)
+    return x.astype(np.float32)
+
+
 def max_rel_err(got, ref):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)

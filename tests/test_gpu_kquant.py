@@ -17,7 +17,7 @@ import pytest
 from engine_amd import synth
 from oracle import kquant_oracle as O
 
-from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host
+from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host, wide_range_activations
 
 pytestmark = pytest.mark.gpu
 
@@ -372,20 +372,6 @@ def test_long_stream_launch_shape(env, t, n, norm):
     assert err <= RTOL
     assert np.all(np.isfinite(got))
     del w, y
-
-
-def wide_range_activations(k, seed):
-    """N(0,1) activations with a few x3000 outlier channels, whole scale groups
-    at 2^-20, and groups whose elements spread over 2^-16..1 in magnitude."""
-    rng = np.random.default_rng(seed)
-    x = rng.standard_normal(k)
-    x[rng.choice(k, 8, replace=False)] *= 3000.0
-    groups = k // 32
-    for g in rng.choice(groups, groups // 8, replace=False):
-        x[32 * g:32 * g + 32] *= 2.0 ** -20
-    for g in rng.choice(groups, groups // 8, replace=False):
-        x[32 * g:32 * g + 32] *= 2.0 ** rng.uniform(-16, 0, 32)
-    return x.astype(np.float32)
 
 
 @pytest.mark.parametrize("mode", ["warp", "fixed16"])

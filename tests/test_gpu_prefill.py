@@ -12,7 +12,7 @@ import pytest
 from engine_amd import synth
 from oracle import kquant_oracle as O
 
-from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host
+from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host, wide_range_activations
 
 pytestmark = pytest.mark.gpu
 
@@ -136,6 +136,43 @@ def test_prefill_wide_tiles(env, t, k, n, m, dtype):
     sample = sorted(i for i in {0, 1, 15, 16, 127, 128, m // 2, m - 1} if i < m)
     ref = np.stack([O.quant_gemv(t, enc, k, n, x[i], threads=16) for i in sample])
     assert max_rel_err(got[sample], ref) <= RTOL
+    assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("t,k,n,m,dtype,norm", [
+    (12, 4096, 1024, 40, "f32", False),     # 32x32 kernel, 2 token blocks
+    (13, 4096, 12288, 128, "bf16", False),  # wide tiles, K split
+    (14, 4096, 512, 200, "f32", True),      # 32x32 kernel, 4 token blocks x 8 waves
+    (12, 4096, 12288, 256, "bf16", True),   # wide tiles, one round
+])
+def test_prefill_wide_dynamic_range(env, t, k, n, m, dtype, norm):
+    """Outlier channels (x3000), whole scale groups at 2^-20 and groups spread
+    over 2^-16..1: the per-token power-of-two scale maps each token's maximum
+    just below 2^15 before the f16 conversion, so small values keep their
+    relative precision down to f16's subnormal step (2^-24 of 2^15). Token
+    sample against the oracle at the 1e-3 bar, every output finite."""
+    import torch
+    print("CASE prefill wide range", t, k, n, m, dtype, norm, flush=True)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(7 * k + n + t)
+    enc_dev = synth.kquant_torch(t, k, n, gen, torch.device("cuda:0"))
+    w = upload(env, t, k, n, enc_dev)
+    x = np.stack([wide_range_activations(k, seed=1000 + i) for i in range(m)])
+    if dtype == "bf16":
+        xd, x = bf16_values(x)
+    else:
+        xd = to_dev(x)
+    gamma = synth.gamma_numpy(k, seed=17) if norm else None
+    y = empty_dev(m * n)
+    env["k"][t].gemm_prefill(w, xd, y, m, gamma=to_dev(gamma) if norm else None, epsilon=1e-6)
+    got = to_host(y, env["ctx"]).reshape(m, n)
+    enc = enc_dev.cpu().numpy()
+    for i in sorted({0, 1, 31, m // 2, m - 1}):
+        src = O.rms_norm_raw(x[i], gamma, 1e-6) if norm else x[i]
+        ref = O.quant_gemv(t, enc, k, n, src, threads=16)
+        err = max_rel_err(got[i], ref)
+        print(f"token {i} max_rel_err={err:.3e}", flush=True)
+        assert err <= RTOL, (i, err)
     assert np.all(np.isfinite(got))
 
 
