@@ -561,7 +561,7 @@ def bench_prefill(E, synth, torch, args):
         "config": {"workload": "prefill-m512", "shapes": out},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_MFMA_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None,
-                     "kernel": "qgemm_kernel (activation stage + matmul) over both shapes"},
+                     "kernel": "act_f16_kernel + qgemm_tile_kernel (Q4_K 192-row tiles; Q6_K 256-row tiles, K split in 4, + qgemm_reduce_kernel), per call over both shapes"},
         "cpu_baseline": None,
     }
 

@@ -19,7 +19,8 @@
 //    MFMAs (v_mfma_f32_32x32x16_f16).
 //  - qgemm_tile_kernel: 192-row x 128-token workgroups of four waves on
 //    v_mfma_f32_16x16x32_f16 with packed-f16 dequantisation, for grids that
-//    fill the CUs (described where it is defined).
+//    fill the CUs (described where it is defined); 256-row tiles with split K
+//    for Q6_K shapes whose 192-row grid does not fill them.
 //
 // MFMA 32x32x16 operand layout (measured on gfx950): lane l holds
 // A[l%32][8*(l/32)+j], B[8*(l/32)+j][l%32] (j = 0..7) and
@@ -933,6 +934,8 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, void* worksp
 // the grids that fill 90-100% of one round, by an estimate fitted to
 // measured calls: about 3 us per super-block step plus 0.05 us per MFMA
 // tile block, plus the split's partial tiles (written, read, reduced).
+// Q6_K shapes with M > 128 that the 192-row grid does not fill take 256-row
+// tiles with split K where those fill one round (q6k_wide_splits).
 constexpr int kTileRb = 3;
 constexpr int kTileTb = 8;
 
@@ -1000,6 +1003,29 @@ static hipError_t launch_tile_t(void* workspace, const uint8_t* w, uint32_t wbyt
     return hipGetLastError();
 }
 
+// Q6_K with M > 128 where the 192-row tiles do not fill the CUs (e.g.
+// 12288 -> 4096): 256-row x 128-token tiles of four 64-row waves with K
+// split so that the grid fills 90-100% of one round. 64-row waves read a
+// quarter less LDS per MFMA than 48-row ones; measured at 12288 -> 4096
+// against the 32x32 kernel with split K: 104.5 against 110.3 us at M = 512
+// (split 4), 60.1 against 65.3 us at M = 256 (split 8). Q5_K measured level
+// (88.4 us both) and stays on the 32x32 kernel. Returns 0 when none fits.
+static int q6k_wide_splits(int M, int N, int K, size_t room_bytes, int cu_count) {
+    const long long cus = std::max(1, cu_count);
+    const int nb = K >> 8;
+    const size_t tile_bytes = (size_t)M * N * 4;
+    const long long tiles = (long long)((N + 255) / 256) * ((M + 127) / 128);
+    for (int s = 1; s <= kMaxSplits && s <= nb; ++s) {
+        const int split_sb = (nb + s - 1) / s;
+        const int splits = (nb + split_sb - 1) / split_sb;
+        if (splits > 1 && (size_t)splits * tile_bytes > room_bytes) break;
+        const long long wgs = tiles * splits;
+        if (wgs > cus) break;
+        if (wgs * 10 >= cus * 9) return splits;
+    }
+    return 0;
+}
+
 template <int T>
 static hipError_t launch_qgemm_tile(void* workspace, const uint8_t* w, uint32_t wbytes, float* y, int M, int N, int K,
                                     int rb, int tb, int splits, int cu_count, hipStream_t stream) {
@@ -1007,6 +1033,9 @@ static hipError_t launch_qgemm_tile(void* workspace, const uint8_t* w, uint32_t 
     if (rb == 3 && tb == 4) return launch_tile_t<T, 3, 4>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
     if (rb == 2 && tb == 8) return launch_tile_t<T, 2, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
     if (rb == 2 && tb == 4) return launch_tile_t<T, 2, 4>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
+    if constexpr (T == kQ6K) {
+        if (rb == 4 && tb == 8) return launch_tile_t<T, 4, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
+    }
     return hipErrorInvalidValue;
 }
 
@@ -1031,6 +1060,14 @@ static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, void* worksp
     if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
     if (tile_ok && M > 128 && use_tile(M, N, cu_count))
         return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, kTileRb, kTileTb, 1, cu_count, stream);
+    if constexpr (T == kQ6K) {
+        if (tile_ok && M > 128) {
+            const size_t part_off = align256((size_t)M * K * 2) + align256((size_t)M * 4);
+            const int s =
+                q6k_wide_splits(M, N, K, workspace_bytes > part_off ? workspace_bytes - part_off : 0, cu_count);
+            if (s) return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, 4, 8, s, cu_count, stream);
+        }
+    }
     return launch_qgemm_t<T, 4, 8>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
 }
 

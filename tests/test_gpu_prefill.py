@@ -113,6 +113,8 @@ def test_prefill_config3_full_size(env, t, k, n):
     (14, 4096, 12288, 48, "f32"),     # 64 x 1 tiles of 64 tokens, K split in 4, last token tile 48 of 64
     (14, 4096, 4096, 100, "bf16"),    # 32-row waves: 32 x 2 tiles of 64 tokens, K split in 4
     (13, 12288, 4096, 64, "f32"),     # 32 x 1 tiles of 64 tokens, K split in 8
+    (14, 12288, 4096, 384, "bf16"),   # Q6_K 256-row tiles: 16 x 3, K split in 5 (10, 10, 10, 10, 8 blocks)
+    (14, 6144, 4000, 200, "f32"),     # Q6_K 256-row tiles: 16 x 2, K split in 8 (3 blocks each), last row tile 160 of 256
 ])
 def test_prefill_wide_tiles(env, t, k, n, m, dtype):
     """Shapes whose wide-tile grid fills a 256-CU MI355X (the wide-tile
@@ -144,6 +146,7 @@ def test_prefill_wide_tiles(env, t, k, n, m, dtype):
     (13, 4096, 12288, 128, "bf16", False),  # wide tiles, K split
     (14, 4096, 512, 200, "f32", True),      # 32x32 kernel, 4 token blocks x 8 waves
     (12, 4096, 12288, 256, "bf16", True),   # wide tiles, one round
+    (14, 12288, 4096, 256, "f32", True),    # Q6_K 256-row tiles, K split in 8
 ])
 def test_prefill_wide_dynamic_range(env, t, k, n, m, dtype, norm):
     """Outlier channels (x3000), whole scale groups at 2^-20 and groups spread
