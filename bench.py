@@ -212,26 +212,45 @@ KV_BYTES_PER_TOKEN = 36 * 8 * 128 * 2 * 2  # f16 K and V of every layer: 147,456
 
 
 def build_decoder(E, synth, torch, ctx, step, out_gamma, layers, seed, members):
-    """The full Qwen3-8B-shaped decoder over the step's weights:
-    adds a Q4_K token_embd table and per-head q/k norms; random-init, seeded."""
+    """The full Qwen3-8B-shaped decoder, random-init and
+    seeded: its own weights of the step's shapes (Q4_K q/k/v/o/gate/up, Q5_K
+    down, Q6_K lm_head, a Q4_K token_embd table), drawn centered (zero-mean
+    weights, so greedy decoding does not settle on one token; the same bytes
+    and kernels as the GEMV chain), the step's RMSNorm gammas and per-head q/k
+    norms. Built once and cached on the step."""
+    cached = getattr(step, "decoder_weights", None)
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed + 1)
-    if step.store.quantized_tensor("token_embd") is None:
-        step.store.materialize_quantized("token_embd", [HIDDEN, VOCAB], 12,
-                                         synth.kquant_torch(12, HIDDEN, VOCAB, gen, dev))
+    if cached is None:
+        store = E.AmdWeightStore(ctx)
+        store.materialize_quantized("token_embd", [HIDDEN, VOCAB], 12,
+                                    synth.kquant_torch(12, HIDDEN, VOCAB, gen, dev, centered=True))
+        store.materialize_quantized("output", [HIDDEN, VOCAB], 14,
+                                    synth.kquant_torch(14, HIDDEN, VOCAB, gen, dev, centered=True))
+        per_layer = []
+        for li in range(len(step.layers)):
+            lw = {}
+            for name, t, k, n, _ in LAYER:
+                store.materialize_quantized(f"blk.{li}.{name}", [k, n], t,
+                                            synth.kquant_torch(t, k, n, gen, dev, centered=True))
+                lw[name] = store.quantized_tensor(f"blk.{li}.{name}")
+            per_layer.append(lw)
+        cached = step.decoder_weights = (store, per_layer)
+    store, per_layer = cached
     names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
              "up": "ffn_up", "down": "ffn_down"}
     plan = []
-    for entry in step.layers[:layers]:
-        lw = {names[n]: entry[n][0] for n in names}
+    for entry, lwq in zip(step.layers[:layers], per_layer):
+        lw = {names[n]: lwq[n] for n in names}
         lw["attn_norm"] = entry["attn_gamma"]
         lw["ffn_norm"] = entry["ffn_gamma"]
         lw["attn_q_norm"] = 1.0 + 0.02 * torch.randn(128, device=dev, generator=gen)
         lw["attn_k_norm"] = 1.0 + 0.02 * torch.randn(128, device=dev, generator=gen)
         plan.append(lw)
     cfg = E.AmdQwen3Config(layers=layers)
-    dec = E.AmdQwen3Decode(ctx, cfg, step.store.quantized_tensor("token_embd"), step.head, out_gamma, plan, members)
+    dec = E.AmdQwen3Decode(ctx, cfg, store.quantized_tensor("token_embd"), store.quantized_tensor("output"),
+                           out_gamma, plan, members)
     dec.set_gemv_mode(GEMV_MODES[getattr(build_decoder, "mode", "warp")])
     return dec, cfg
 
@@ -271,8 +290,8 @@ def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed):
 def model_decode_results(E, synth, torch, ctx, step, out_gamma, args):
     """Batch 1, then batch 8 whose member 0 has batch 1's prompt. In the f32
     GEMV mode member 0's tokens and last logits equal batch 1's bit for bit
-    (`b8_member0_bitwise_equal_b1`): a check on the timed run itself, since
-    random weights make the greedy output settle on one token."""
+    (`b8_member0_bitwise_equal_b1`): a check on the timed run itself, beside
+    `distinct_tokens` (the centered random weights give varied greedy tokens)."""
     import numpy as np
     dec, cfg = build_decoder(E, synth, torch, ctx, step, out_gamma, args.layers, args.seed, 8)
     res, runs = {}, {}

@@ -54,8 +54,20 @@ def gamma_numpy(k: int, seed: int) -> np.ndarray:
     return (1.0 + 0.02 * rng.standard_normal(k)).astype(np.float32)
 
 
-def kquant_torch(value_type: int, k: int, n: int, generator, device):
-    """Device-side generator (same distributions) returning a flat uint8 tensor."""
+# Mean quant of a uniform Q4_K nibble / Q5_K 5-bit value.
+_MEAN_Q = {Q4_K: 7.5, Q5_K: 15.5}
+
+
+def kquant_torch(value_type: int, k: int, n: int, generator, device, centered: bool = False):
+    """Device-side generator (same distributions) returning a flat uint8 tensor.
+
+    centered=True (Q4_K / Q5_K): dmin = f16(d * mean quant) instead of an
+    independent draw, so the minimum term cancels the quants' mean on average
+    (d*sc*q - dmin*m has mean 0 over independent uniform sc, m, q). Weights of
+    the BASELINE distribution all share a positive mean, which makes every
+    output of a random-weight decoder nearly a multiple of sum(x); a decoder
+    built on centered weights produces varied greedy tokens. Block layout and
+    sizes are unchanged."""
     import torch
 
     if k % 256:
@@ -64,14 +76,17 @@ def kquant_torch(value_type: int, k: int, n: int, generator, device):
     bb = BLOCK_BYTES[value_type]
     blocks = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device=device, generator=generator)
 
-    def f16_bytes(count):
-        vals = torch.empty(count, dtype=torch.float32, device=device).uniform_(
-            0.001, 0.02, generator=generator)
+    def f16_vals(count):
+        return torch.empty(count, dtype=torch.float32, device=device).uniform_(0.001, 0.02, generator=generator)
+
+    def f16_bytes(count, vals=None):
+        vals = f16_vals(count) if vals is None else vals
         return vals.to(torch.float16).view(torch.uint8).view(count, 2)
 
     if value_type in (Q4_K, Q5_K):
-        blocks[:, 0:2] = f16_bytes(nb)
-        blocks[:, 2:4] = f16_bytes(nb)
+        d = f16_vals(nb).to(torch.float16).to(torch.float32)
+        blocks[:, 0:2] = f16_bytes(nb, d)
+        blocks[:, 2:4] = f16_bytes(nb, d * _MEAN_Q[value_type] if centered else None)
     else:
         sc = torch.randint(-32, 32, (nb, 16), dtype=torch.int8, device=device, generator=generator)
         blocks[:, 192:208] = sc.view(torch.uint8)
