@@ -524,27 +524,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
     if constexpr (!XREG) {
         // ---- several members, one slice: passes over the whole ring. Each
         // pass reads every 4-element piece of a member's record once and
-        // applies it to all NBUF rows; then the ring is refilled.
+        // applies it to the ring's rows; then the ring is refilled. The last
+        // pass reduces only the wave's remaining NR rows (a wave's share of a
+        // short launch is often fewer rows than the ring holds).
         const float* rec_base = xs + lane * STRIDE;
         auto xf = [&](int m, int i) { return *reinterpret_cast<const float4*>(rec_base + m * 64 * STRIDE + 4 * i); };
         auto sf = [&](int m, int g) { return rec_base[m * 64 * STRIDE + 64 + g]; };
         int crow = r_begin;
-        auto pass = [&](auto refill_const, int left) {
+        auto pass = [&](auto refill_const, auto nr_const) {
             constexpr bool REFILL = decltype(refill_const)::value;
+            constexpr int NR = decltype(nr_const)::value;
+            static_assert(NR >= 1 && NR <= NBUF && (REFILL ? NR == NBUF : true), "full passes reduce the whole ring");
             // The records never change, but keeping all of them in registers
             // across passes would spill: re-read them every pass.
             asm volatile("" ::: "memory");
-            float part[NBUF][MT];
-            rows_dot<T, NBUF, MT>(ring, p, xf, sf, part);
+            float part[NR][MT];
+            rows_dot<T, NR, MT>(reinterpret_cast<const RowData<T>(&)[NR]>(ring), p, xf, sf, part);
             if constexpr (REFILL) {
 #pragma unroll
                 for (int r = 0; r < NBUF; ++r) load_next(ring[r], r);
             }
             float gk[MT];
 #pragma unroll
-            for (int r = 0; r < NBUF; ++r) {
+            for (int r = 0; r < NR; ++r) {
                 const int row = crow + r;
-                const bool live = r < left && row < r_end;
+                const bool live = row < r_end;
                 int mat, local, rows_mat;
                 __amdgpu_buffer_rsrc_t yr;
                 if constexpr (kCursor) {
@@ -590,8 +594,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
         };
         const int rows_w = r_end - r_begin;
         const int passes = (rows_w + NBUF - 1) / NBUF;
-        for (int ps = 0; ps + 1 < passes; ++ps) pass(std::true_type{}, NBUF);
-        if (passes > 0) pass(std::false_type{}, rows_w - (passes - 1) * NBUF);
+        using Full = std::integral_constant<int, NBUF>;
+        for (int ps = 0; ps + 1 < passes; ++ps) pass(std::true_type{}, Full{});
+        if (passes == 0) return;
+        // 1..NBUF rows left (wave-uniform); gate/up pairs leave an even count
+        const int left = rows_w - (passes - 1) * NBUF;
+        if constexpr (!PAIR) {
+            if (left == 1) return pass(std::false_type{}, std::integral_constant<int, 1>{});
+        }
+        if constexpr (NBUF > 2) {
+            if (left == 2) return pass(std::false_type{}, std::integral_constant<int, 2>{});
+        }
+        if constexpr (NBUF > 3 && !PAIR) {
+            if (left == 3) return pass(std::false_type{}, std::integral_constant<int, 3>{});
+        }
+        pass(std::false_type{}, Full{});
         return;
     } else {
         // ---- one or two members: records in VGPRs; the ring is reduced one
