@@ -307,6 +307,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
     constexpr int NBW = (NBMAX + WAVES - 1) / WAVES;  // staging blocks per wave
     extern __shared__ float xs[];                     // [MT][slices][64 records][STRIDE]
     __shared__ float ssq_s[NORM ? MT : 1][NORM ? NBMAX : 1];
+    __shared__ __attribute__((aligned(16))) float epi[XREG ? 4 : WAVES * 128];  // many-member pass epilogue, 512 B per wave
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -531,10 +532,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
         auto xf = [&](int m, int i) { return *reinterpret_cast<const float4*>(rec_base + m * 64 * STRIDE + 4 * i); };
         auto sf = [&](int m, int g) { return rec_base[m * 64 * STRIDE + 64 + g]; };
         int crow = r_begin;
+        float* const ep = epi + wave * 128;  // [4 lane rows][32 values]
+        const int vl = lane & 31;
+        float inv_l = inv[0];  // the RMSNorm factor of this lane's member
+#pragma unroll
+        for (int m = 1; m < MT; ++m)
+            if (vl % MT == m) inv_l = inv[m];
         auto pass = [&](auto refill_const, auto nr_const) {
             constexpr bool REFILL = decltype(refill_const)::value;
             constexpr int NR = decltype(nr_const)::value;
             static_assert(NR >= 1 && NR <= NBUF && (REFILL ? NR == NBUF : true), "full passes reduce the whole ring");
+            static_assert(NR * MT <= 32 && MT % 4 == 0, "a pass's values fit lanes 0-31 in whole float4s");
             // The records never change, but keeping all of them in registers
             // across passes would spill: re-read them every pass.
             asm volatile("" ::: "memory");
@@ -544,50 +552,61 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
 #pragma unroll
                 for (int r = 0; r < NBUF; ++r) load_next(ring[r], r);
             }
-            float gk[MT];
+            // Epilogue. Each (row r, member m) value's 16-lane row sums (the
+            // DPP steps of wave_sum_uniform) go through this wave's LDS
+            // scratch, and lane v = r * MT + m finishes value v: the row sums
+            // added (r0 + r1) + (r2 + r3), the RMSNorm factor, SwiGLU, the
+            // store. Every value sees wave_sum_uniform's operations in its
+            // order, so the bits equal the single-member launch's, and the
+            // per-value work runs once across lanes instead of once per value.
 #pragma unroll
-            for (int r = 0; r < NR; ++r) {
-                const int row = crow + r;
-                const bool live = row < r_end;
-                int mat, local, rows_mat;
-                __amdgpu_buffer_rsrc_t yr;
-                if constexpr (kCursor) {
-                    if (live) seek(ccur, row, true);
-                    yr = ccur.rs;
-                    local = row - ccur.start;
-                    rows_mat = ccur.rows_mat;
-                } else if constexpr (PAIR) {
-                    yr = pair_y;
-                    local = row >> 1;
-                    rows_mat = pair_rows;
-                } else {
-                    locate(live ? row : r_begin, mat, local);
-                    yr = pick_y(mat, rows_mat);
-                }
+            for (int r = 0; r < NR; ++r)
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
-                    if constexpr (SPLIT) {
-                        const float ps = wave_sum_uniform(part[r][m]);
-                        const uint32_t off =
-                            (live && lane == 0 && m < members)
-                                ? (uint32_t)((slice0 * members + m) * args.total_rows + row) * 4u
-                                : kOutOfRange;
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ps), partial_r, (int)off, 0, 0);
-                        continue;
-                    }
-                    const float total = wave_sum_uniform(part[r][m]) * inv[m];
-                    const uint32_t off = (live && lane == 0 && m < members)
-                                             ? (uint32_t)(m * rows_mat + local) * 4u
-                                             : kOutOfRange;
-                    if constexpr (PAIR) {
-                        if (r % 2 == 0) {
-                            gk[m] = total;
-                        } else {
-                            put(swiglu(gk[m], total), yr, off);
-                        }
-                    } else {
-                        put(total, yr, off);
-                    }
+                    float v = part[r][m];
+                    v = dpp_step<0xb1>(v);   // quad_perm [1,0,3,2]
+                    v = dpp_step<0x4e>(v);   // quad_perm [2,3,0,1]
+                    v = dpp_step<0x141>(v);  // row_half_mirror
+                    v = dpp_step<0x140>(v);  // row_mirror
+                    part[r][m] = v;
+                }
+            if ((lane & 15) == 0) {
+                float* dst = ep + 32 * (lane >> 4);
+#pragma unroll
+                for (int i = 0; i < NR * MT; i += 4)
+                    *reinterpret_cast<float4*>(dst + i) =
+                        float4{part[(i + 0) / MT][(i + 0) % MT], part[(i + 1) / MT][(i + 1) % MT],
+                               part[(i + 2) / MT][(i + 2) % MT], part[(i + 3) / MT][(i + 3) % MT]};
+            }
+            // (one wave's LDS operations complete in order: no barrier)
+            auto total_of = [&](int i) { return (ep[i] + ep[32 + i]) + (ep[64 + i] + ep[96 + i]); };
+            const int vr = vl / MT, vm = vl % MT;  // this lane's value: row crow + vr, member vm
+            const int row = crow + vr;
+            // lanes 32-63 repeat lanes 0-31's values and store nothing
+            const bool mine = lane < 32 && vl < NR * MT && row < r_end && vm < members;
+            if constexpr (SPLIT) {
+                const float ps = total_of(vl);
+                const uint32_t off = mine ? (uint32_t)((slice0 * members + vm) * args.total_rows + row) * 4u : kOutOfRange;
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ps), partial_r, (int)off, 0, 0);
+            } else if constexpr (PAIR) {
+                // gate rows are even, each followed by its up row: lane v
+                // (gate) also adds value v + MT (up)
+                const bool gate = (vr & 1) == 0 && vl + MT < 32;
+                const float g = total_of(vl) * inv_l;
+                const float u = total_of(gate ? vl + MT : vl) * inv_l;
+                const uint32_t off = (mine && gate) ? (uint32_t)(vm * pair_rows + (row >> 1)) * 4u : kOutOfRange;
+                put(swiglu(g, u), pair_y, off);
+            } else {
+                const float total = total_of(vl) * inv_l;
+                // rows move forward; the output resource can change at a
+                // matrix boundary inside the pass, so one store per row
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    const int rr = crow + r;
+                    if (rr < r_end) seek(ccur, rr, true);
+                    const uint32_t off =
+                        (mine && vr == r) ? (uint32_t)(vm * ccur.rows_mat + (rr - ccur.start)) * 4u : kOutOfRange;
+                    put(total, ccur.rs, off);
                 }
             }
             crow += NBUF;
