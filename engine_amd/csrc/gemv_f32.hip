@@ -834,7 +834,8 @@ hipError_t launch_few(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
 template <int T, int PRO, bool PAIR>
 hipError_t launch_many(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
     if (a.members <= 4) return F32Instance<T, 4, PRO, true, 4, 8, 1, PAIR>::launch(a, cu_count, 1, stream);
-    return F32Instance<T, 8, PRO, true, (T == kQ4K ? 4 : 2), 8, 1, PAIR>::launch(a, cu_count, 1, stream);
+    // ring depth: 4 rows where the registers allow (Q6_K rows need 22 VGPRs)
+    return F32Instance<T, 8, PRO, true, (T != kQ6K ? 4 : PAIR ? 2 : 3), 8, 1, PAIR>::launch(a, cu_count, 1, stream);
 }
 
 template <int T, int PRO>
@@ -885,7 +886,7 @@ template <int T>
 hipError_t launch_split(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
     hipError_t e = (a.members <= 4)
                        ? F32Instance<T, 4, kProPlain, true, 4, 8, 1, false, true>::launch(a, cu_count, 1, stream)
-                       : F32Instance<T, 8, kProPlain, true, (T == kQ4K ? 4 : 2), 8, 1, false, true>::launch(
+                       : F32Instance<T, 8, kProPlain, true, (T != kQ6K ? 4 : 3), 8, 1, false, true>::launch(
                              a, cu_count, 1, stream);
     if (e != hipSuccess) return e;
     const int slices = ((a.K >> 8) + 15) >> 4;
