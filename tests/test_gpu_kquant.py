@@ -473,6 +473,31 @@ def test_eight_members_bit_identical_at_qwen3_shapes(env, t, k, ns, members, nor
             assert max_rel_err(got[m][rows], ref) <= RTOL
 
 
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n", [10247, 14341])
+def test_eight_member_last_passes_bit_identical(env, t, n):
+    """Eight members over 4096-wide rows: the workgroups' 2048 waves (256 CUs)
+    take 5-6 (n = 10247) or 7-8 (n = 14341) rows each, so a wave's last pass
+    over its ring (4 rows for Q4_K / Q5_K, 3 for Q6_K) reduces 1, 2, 3 or all
+    of its rows. Every row of members 0 and 7 bit-identical to the
+    single-member call, and a row sample within the bar of the oracle."""
+    k, members = 4096, 8
+    print_case(test="last_passes", t=t, n=n)
+    enc = synth.kquant_numpy(t, k, n, seed=n + t)
+    w = upload(env, t, k, n, enc)
+    x = synth.activations_numpy(k, members, seed=n)
+    y = empty_dev(members * n)
+    env["k"][t].execute_warp_batch(w, to_dev(x.reshape(-1)), y, members)
+    got = to_host(y, env["ctx"]).reshape(members, n)
+    rows = _row_sample(n, 300, seed=t)
+    for m in (0, members - 1):
+        single = empty_dev(n)
+        env["k"][t].execute_warp(w, to_dev(x[m]), single)
+        assert np.array_equal(to_host(single, env["ctx"]).view(np.uint32), got[m].view(np.uint32)), m
+        assert max_rel_err(got[m][rows], _oracle_rows(t, enc, k, n, x[m], rows)) <= RTOL
+    del w, y
+
+
 @pytest.mark.parametrize("t,k,n,members", [(12, 4096, 4096, 1), (13, 12288, 4096, 2), (14, 4096, 1024, 4),
                                            (12, 2048, 333, 3)])
 def test_fixed16_wave_gemv_against_oracle(env, t, k, n, members):
