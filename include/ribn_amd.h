@@ -208,8 +208,9 @@ uint32_t ribn_amd_gemv_value_type(const ribn_amd_gemv *gemv);
  * (crates/nvidia/src/decode.rs:285-307).
  *   RIBN_AMD_GEMV_WARP (default; GemvMode::Warp): f32 activations against
  *     weights dequantised in registers, f32 accumulation. Up to 8 members
- *     (2 when K > 4096) share one weight stream; every row is bit-identical
- *     to the single-member call.
+ *     share one weight stream (from 3 members, K > 4096 is split by
+ *     4096-wide slice and the slice totals added in order); every row is
+ *     bit-identical to the single-member call.
  *   RIBN_AMD_GEMV_FIXED16 (opt-in, lossy; no reference twin, used like
  *     GemvMode::IntegerDot for throughput comparison): activations rounded to
  *     block fixed point (16-bit per scale group in the wave kernel, 15-bit per
@@ -566,8 +567,9 @@ ribn_amd_status ribn_amd_qwen3_prefill_step(ribn_amd_qwen3_decode *decode, ribn_
  * position + count - 1, 2 <= count <= max_members) as the members of one
  * step without the output head, so the weights are read once for the chunk.
  * Every attention input equals the serial prefill_step sequence's; GEMV
- * results are the batched GEMV's (bit-equal to serial on the wave path,
- * within the GEMV tolerance on the matrix-core path). Stream-ordered. */
+ * results are the batched GEMV's: bit-equal to serial in
+ * RIBN_AMD_GEMV_WARP, within the GEMV tolerance in RIBN_AMD_GEMV_FIXED16
+ * from 5 members (matrix cores). Stream-ordered. */
 ribn_amd_status ribn_amd_qwen3_prefill_chunk(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
                                              const uint32_t *tokens, size_t count, uint32_t position);
 /* CudaQwen35Decode::decode_step (decode.rs:508-516): one forward pass and the
