@@ -935,7 +935,9 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, void* worksp
 // measured calls: about 3 us per super-block step plus 0.05 us per MFMA
 // tile block, plus the split's partial tiles (written, read, reduced).
 // Q6_K shapes with M > 128 that the 192-row grid does not fill take 256-row
-// tiles with split K where those fill one round (q6k_wide_splits).
+// tiles with split K where those fill one round (q6k_wide_splits); other
+// M > 128 shapes take 192-row tiles with split K in one round at least half
+// full (wide_tile_splits).
 constexpr int kTileRb = 3;
 constexpr int kTileTb = 8;
 
@@ -1003,6 +1005,38 @@ static hipError_t launch_tile_t(void* workspace, const uint8_t* w, uint32_t wbyt
     return hipGetLastError();
 }
 
+// M > 128 where neither rule above applies: 192-row x 128-token tiles with
+// K split so the grid fits one round, at least half full, by the estimate of
+// choose_tile_small. The 32x32 kernel is far slower at these sizes even
+// against a partly idle round (Q4_K 4096 -> 12288: M = 192 65.1 -> 43.6 us
+// with split 2, M = 256 75.2 -> 48.9 us with split 2, M = 384 85.0 -> 64.8 us
+// at 75% fill; Q5_K 12288 -> 4096 at M = 256 level, 59.8 / 59.4 us).
+// Returns the split count, or 0 when no grid fits.
+static int wide_tile_splits(int M, int N, int K, size_t room_bytes, int cu_count) {
+    const long long cus = std::max(1, cu_count);
+    const int nb = K >> 8;
+    const size_t tile_bytes = (size_t)M * N * 4;
+    const long long tiles =
+        (long long)((N + 64 * kTileRb - 1) / (64 * kTileRb)) * ((M + 16 * kTileTb - 1) / (16 * kTileTb));
+    int best = 0;
+    double best_t = 1e30;
+    for (int s = 1; s <= kMaxSplits && s <= nb; ++s) {
+        const int split_sb = (nb + s - 1) / s;
+        const int splits = (nb + split_sb - 1) / split_sb;
+        if (splits > 1 && (size_t)splits * tile_bytes > room_bytes) break;
+        const long long wgs = tiles * splits;
+        if (wgs > cus) break;
+        if (wgs * 2 < cus) continue;
+        double t = split_sb * (3.0 + 0.05 * kTileRb * kTileTb);
+        if (splits > 1) t += 1.0 + (double)(2 * splits + 1) * (double)tile_bytes / 4.0e6;
+        if (t < best_t - 1e-9) {
+            best_t = t;
+            best = splits;
+        }
+    }
+    return best;
+}
+
 // Q6_K with M > 128 where the 192-row tiles do not fill the CUs (e.g.
 // 12288 -> 4096): 256-row x 128-token tiles of four 64-row waves with K
 // split so that the grid fills 90-100% of one round. 64-row waves read a
@@ -1060,13 +1094,15 @@ static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, void* worksp
     if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
     if (tile_ok && M > 128 && use_tile(M, N, cu_count))
         return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, kTileRb, kTileTb, 1, cu_count, stream);
-    if constexpr (T == kQ6K) {
-        if (tile_ok && M > 128) {
-            const size_t part_off = align256((size_t)M * K * 2) + align256((size_t)M * 4);
-            const int s =
-                q6k_wide_splits(M, N, K, workspace_bytes > part_off ? workspace_bytes - part_off : 0, cu_count);
+    if (tile_ok && M > 128) {
+        const size_t part_off = align256((size_t)M * K * 2) + align256((size_t)M * 4);
+        const size_t room = workspace_bytes > part_off ? workspace_bytes - part_off : 0;
+        if constexpr (T == kQ6K) {
+            const int s = q6k_wide_splits(M, N, K, room, cu_count);
             if (s) return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, 4, 8, s, cu_count, stream);
         }
+        const int s = wide_tile_splits(M, N, K, room, cu_count);
+        if (s) return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, kTileRb, kTileTb, s, cu_count, stream);
     }
     return launch_qgemm_t<T, 4, 8>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
 }
