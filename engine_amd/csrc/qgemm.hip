@@ -925,19 +925,19 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, void* worksp
 }
 
 // Wide tiles. M > 128 runs 192-row x 128-token workgroups when their grid
-// fills at least 90% of its last round of CUs (e.g. Q4_K 4096 -> 12288 at
-// M = 512: 64 x 4 = 256 workgroups); other shapes keep qgemm_kernel, whose
-// split K and 256-row tiles balance them better. Each wave's 48 rows keep its
+// fills at least 70% of its last round of CUs (e.g. Q4_K 4096 -> 12288 at
+// M = 512: 64 x 4 = 256 workgroups; at M = 768, 384 of 512: 127.6 against
+// 164.6 us on qgemm_kernel). Each wave's 48 rows keep its
 // B reads (the whole x tile per wave) within the LDS bandwidth (about 90
 // B/clk per CU measured); 32-row waves over 128 tokens are LDS-bound.
 // 32 < M <= 128 picks (rows per wave, tokens per workgroup, K split) among
 // the grids that fill 90-100% of one round, by an estimate fitted to
 // measured calls: about 3 us per super-block step plus 0.05 us per MFMA
 // tile block, plus the split's partial tiles (written, read, reduced).
-// Q6_K shapes with M > 128 that the 192-row grid does not fill take 256-row
-// tiles with split K where those fill one round (q6k_wide_splits); other
-// M > 128 shapes take 192-row tiles with split K in one round at least half
-// full (wide_tile_splits).
+// Q5_K and Q6_K shapes with M > 128 that the 192-row grid does not fill take
+// 256-row tiles with split K in one round at least 60% full (wide256_splits);
+// other M > 128 shapes take 192-row tiles with split K in one round at least
+// 60% full (wide_tile_splits); the rest keep qgemm_kernel.
 constexpr int kTileRb = 3;
 constexpr int kTileTb = 8;
 
@@ -945,7 +945,7 @@ static bool use_tile(int M, int N, int cu_count) {
     const long long wgs = (long long)((N + 64 * kTileRb - 1) / (64 * kTileRb)) * ((M + 16 * kTileTb - 1) / (16 * kTileTb));
     const long long cus = std::max(1, cu_count);
     const long long rounds = (wgs + cus - 1) / cus;
-    return wgs * 10 >= rounds * cus * 9;
+    return wgs * 10 >= rounds * cus * 7;
 }
 
 struct TileChoice {
@@ -1006,11 +1006,11 @@ static hipError_t launch_tile_t(void* workspace, const uint8_t* w, uint32_t wbyt
 }
 
 // M > 128 where neither rule above applies: 192-row x 128-token tiles with
-// K split so the grid fits one round, at least half full, by the estimate of
+// K split so the grid fits one round, at least 60% full, by the estimate of
 // choose_tile_small. The 32x32 kernel is far slower at these sizes even
 // against a partly idle round (Q4_K 4096 -> 12288: M = 192 65.1 -> 43.6 us
 // with split 2, M = 256 75.2 -> 48.9 us with split 2, M = 384 85.0 -> 64.8 us
-// at 75% fill; Q5_K 12288 -> 4096 at M = 256 level, 59.8 / 59.4 us).
+// at 75% fill; Q4_K 4096 -> 4096 at M = 512 44.2 against 46.9 us).
 // Returns the split count, or 0 when no grid fits.
 static int wide_tile_splits(int M, int N, int K, size_t room_bytes, int cu_count) {
     const long long cus = std::max(1, cu_count);
@@ -1026,7 +1026,7 @@ static int wide_tile_splits(int M, int N, int K, size_t room_bytes, int cu_count
         if (splits > 1 && (size_t)splits * tile_bytes > room_bytes) break;
         const long long wgs = tiles * splits;
         if (wgs > cus) break;
-        if (wgs * 2 < cus) continue;
+        if (wgs * 5 < cus * 3) continue;
         double t = split_sb * (3.0 + 0.05 * kTileRb * kTileTb);
         if (splits > 1) t += 1.0 + (double)(2 * splits + 1) * (double)tile_bytes / 4.0e6;
         if (t < best_t - 1e-9) {
@@ -1037,27 +1037,37 @@ static int wide_tile_splits(int M, int N, int K, size_t room_bytes, int cu_count
     return best;
 }
 
-// Q6_K with M > 128 where the 192-row tiles do not fill the CUs (e.g.
-// 12288 -> 4096): 256-row x 128-token tiles of four 64-row waves with K
-// split so that the grid fills 90-100% of one round. 64-row waves read a
-// quarter less LDS per MFMA than 48-row ones; measured at 12288 -> 4096
-// against the 32x32 kernel with split K: 104.5 against 110.3 us at M = 512
-// (split 4), 60.1 against 65.3 us at M = 256 (split 8). Q5_K measured level
-// (88.4 us both) and stays on the 32x32 kernel. Returns 0 when none fits.
-static int q6k_wide_splits(int M, int N, int K, size_t room_bytes, int cu_count) {
+// Q5_K and Q6_K with M > 128 where the 192-row tiles do not fill the CUs
+// (e.g. 12288 -> 4096): 256-row x 128-token tiles of four 64-row waves with
+// K split so that the grid fills 60-100% of one round, the split count by
+// the estimate of choose_tile_small. 64-row waves read a quarter less LDS
+// per MFMA than 48-row ones, which matters for the costlier 5- and 6-bit
+// dequantisation. Measured at 12288 -> 4096 against the 32x32 kernel with
+// split K: Q6_K 104.5 against 110.3 us at M = 512, 158.2 against 209.2 at
+// M = 768; Q5_K 54.9 against 59.0 us at M = 256, 82.9 against 88.6 at
+// M = 512, 141.4 against 213.1 at M = 1024. Returns 0 when none fits.
+static int wide256_splits(int M, int N, int K, size_t room_bytes, int cu_count) {
     const long long cus = std::max(1, cu_count);
     const int nb = K >> 8;
     const size_t tile_bytes = (size_t)M * N * 4;
     const long long tiles = (long long)((N + 255) / 256) * ((M + 127) / 128);
+    int best = 0;
+    double best_t = 1e30;
     for (int s = 1; s <= kMaxSplits && s <= nb; ++s) {
         const int split_sb = (nb + s - 1) / s;
         const int splits = (nb + split_sb - 1) / split_sb;
         if (splits > 1 && (size_t)splits * tile_bytes > room_bytes) break;
         const long long wgs = tiles * splits;
         if (wgs > cus) break;
-        if (wgs * 10 >= cus * 9) return splits;
+        if (wgs * 5 < cus * 3) continue;
+        double t = split_sb * (3.0 + 0.05 * 4 * 8);
+        if (splits > 1) t += 1.0 + (double)(2 * splits + 1) * (double)tile_bytes / 4.0e6;
+        if (t < best_t - 1e-9) {
+            best_t = t;
+            best = splits;
+        }
     }
-    return 0;
+    return best;
 }
 
 template <int T>
@@ -1067,7 +1077,7 @@ static hipError_t launch_qgemm_tile(void* workspace, const uint8_t* w, uint32_t 
     if (rb == 3 && tb == 4) return launch_tile_t<T, 3, 4>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
     if (rb == 2 && tb == 8) return launch_tile_t<T, 2, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
     if (rb == 2 && tb == 4) return launch_tile_t<T, 2, 4>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
-    if constexpr (T == kQ6K) {
+    if constexpr (T == kQ5K || T == kQ6K) {
         if (rb == 4 && tb == 8) return launch_tile_t<T, 4, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
     }
     return hipErrorInvalidValue;
@@ -1097,8 +1107,8 @@ static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, void* worksp
     if (tile_ok && M > 128) {
         const size_t part_off = align256((size_t)M * K * 2) + align256((size_t)M * 4);
         const size_t room = workspace_bytes > part_off ? workspace_bytes - part_off : 0;
-        if constexpr (T == kQ6K) {
-            const int s = q6k_wide_splits(M, N, K, room, cu_count);
+        if constexpr (T == kQ5K || T == kQ6K) {
+            const int s = wide256_splits(M, N, K, room, cu_count);
             if (s) return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, 4, 8, s, cu_count, stream);
         }
         const int s = wide_tile_splits(M, N, K, room, cu_count);

@@ -117,8 +117,12 @@ def test_prefill_config3_full_size(env, t, k, n):
     (14, 6144, 4000, 200, "f32"),     # Q6_K 256-row tiles: 16 x 2, K split in 8 (3 blocks each), last row tile 160 of 256
     (12, 4096, 12288, 256, "bf16"),   # 64 x 2 tiles, K split in 2 (one round)
     (12, 4096, 12288, 384, "f32"),    # 64 x 3 tiles, no split (three quarters of the CUs)
-    (13, 12288, 4096, 256, "bf16"),   # 22 x 2 tiles, K split in 5 (10, 10, 10, 10, 8 blocks)
+    (13, 12288, 4096, 256, "bf16"),   # Q5_K 256-row tiles: 16 x 2, K split in 8
+    (13, 12288, 4096, 640, "f32"),    # Q5_K 256-row tiles: 16 x 5, K split in 3 (one round, 94%)
+    (13, 4096, 4000, 300, "bf16"),    # Q5_K 256-row tiles: 16 x 3, K split in 5; last row tile 160, last token tile 44
     (12, 2048, 6000, 160, "f32"),     # 32 x 2 tiles, K split in 4; last row tile 48 of 192, last token tile 32 of 128
+    (12, 4096, 12288, 768, "bf16"),   # 64 x 6 tiles, no split: two rounds, the second three quarters full
+    (14, 12288, 4096, 768, "f32"),    # Q6_K 256-row tiles: 16 x 6, K split in 2
 ])
 def test_prefill_wide_tiles(env, t, k, n, m, dtype):
     """Shapes whose wide-tile grid fills a 256-CU MI355X (the wide-tile
