@@ -486,16 +486,47 @@ __global__ __launch_bounds__(WAVES * 64) void qgemm_kernel(const uint8_t* __rest
     }
 }
 
-// y[m][n] = unscale[m] * sum over splits z (in order) of partial[z][m][n]
+// y[m][n] = unscale[m] * sum over splits z (in order) of partial[z][m][n].
+// V = 4: four outputs per thread (16-byte loads and stores; N a multiple of
+// 4 and y 16-byte aligned), V = 1 otherwise. Every split's load is issued
+// before the first add; each element sees the same operations in the same
+// order in either form, so the results are identical.
+constexpr int kMaxReduceSplits = 16;
+
+template <int V>
 __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restrict__ partial,
                                                            const float* __restrict__ unscale, float* __restrict__ y,
                                                            int M, int N, int splits) {
+    typedef float vec_t __attribute__((ext_vector_type(V)));
     const size_t total = (size_t)M * N;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
-        float acc = partial[i];
-        for (int z = 1; z < splits; ++z) acc += partial[(size_t)z * total + i];
-        y[i] = acc * unscale[i / N];
+    const size_t units = total / V;
+    const size_t per_row = (size_t)N / V;
+    const vec_t* __restrict__ pv = reinterpret_cast<const vec_t*>(partial);
+    vec_t* __restrict__ yv = reinterpret_cast<vec_t*>(y);
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < units; i += (size_t)gridDim.x * 256) {
+        vec_t v[kMaxReduceSplits];
+#pragma unroll
+        for (int z = 0; z < kMaxReduceSplits; ++z)
+            if (z < splits) v[z] = pv[(size_t)z * units + i];
+        vec_t acc = v[0];
+#pragma unroll
+        for (int z = 1; z < kMaxReduceSplits; ++z)
+            if (z < splits) acc += v[z];
+        yv[i] = acc * unscale[i / per_row];
     }
+}
+
+static hipError_t launch_reduce(const float* part, const float* us, float* y, int M, int N, int splits, int cu_count,
+                                hipStream_t stream) {
+    if (splits < 2 || splits > kMaxReduceSplits) return hipErrorInvalidValue;
+    const bool wide = N % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    const size_t units = (size_t)M * N / (wide ? 4 : 1);
+    const int rgrid = (int)std::min<size_t>((units + 255) / 256, (size_t)std::max(1, cu_count) * 8);
+    if (wide)
+        hipLaunchKernelGGL(qgemm_reduce_kernel<4>, dim3(rgrid), dim3(256), 0, stream, part, us, y, M, N, splits);
+    else
+        hipLaunchKernelGGL(qgemm_reduce_kernel<1>, dim3(rgrid), dim3(256), 0, stream, part, us, y, M, N, splits);
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------------- wide tiles
@@ -918,10 +949,7 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, void* worksp
                        splits > 1 ? part : nullptr, M, N, K, split_steps);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
-    const size_t total = (size_t)M * N;
-    const int rgrid = (int)std::min<size_t>((total + 255) / 256, (size_t)cu_count * 8);
-    hipLaunchKernelGGL(qgemm_reduce_kernel, dim3(rgrid), dim3(256), 0, stream, part, us, y, M, N, splits);
-    return hipGetLastError();
+    return launch_reduce(part, us, y, M, N, splits, cu_count, stream);
 }
 
 // Wide tiles. M > 128 runs 192-row x 128-token workgroups when their grid
@@ -999,10 +1027,7 @@ static hipError_t launch_tile_t(void* workspace, const uint8_t* w, uint32_t wbyt
                        splits > 1 ? part : nullptr, M, N, K, split_sb);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
-    const size_t total = (size_t)M * N;
-    const int rgrid = (int)std::min<size_t>((total + 255) / 256, (size_t)std::max(1, cu_count) * 8);
-    hipLaunchKernelGGL(qgemm_reduce_kernel, dim3(rgrid), dim3(256), 0, stream, part, us, y, M, N, splits);
-    return hipGetLastError();
+    return launch_reduce(part, us, y, M, N, splits, cu_count, stream);
 }
 
 // M > 128 where neither rule above applies: 192-row x 128-token tiles with

@@ -48,7 +48,7 @@ def oracle_rows(t, enc, k, n, x, threads=1):
 
 
 @pytest.mark.parametrize("t", (12, 13, 14))
-@pytest.mark.parametrize("k,n,m", [(256, 32, 1), (512, 96, 40), (1024, 200, 130), (2304, 128, 257)])
+@pytest.mark.parametrize("k,n,m", [(256, 32, 1), (512, 96, 40), (1024, 200, 130), (2304, 128, 257), (1024, 75, 40)])
 @pytest.mark.parametrize("dtype", ("f32", "bf16"))
 def test_prefill_against_oracle(env, t, k, n, m, dtype):
     print("CASE prefill", t, k, n, m, dtype, flush=True)
@@ -123,6 +123,7 @@ def test_prefill_config3_full_size(env, t, k, n):
     (12, 2048, 6000, 160, "f32"),     # 32 x 2 tiles, K split in 4; last row tile 48 of 192, last token tile 32 of 128
     (12, 4096, 12288, 768, "bf16"),   # 64 x 6 tiles, no split: two rounds, the second three quarters full
     (14, 12288, 4096, 768, "f32"),    # Q6_K 256-row tiles: 16 x 6, K split in 2
+    (14, 12288, 4094, 384, "bf16"),   # as (14, 12288, 4096, 384) with N not a multiple of 4: one-wide split reduce
 ])
 def test_prefill_wide_tiles(env, t, k, n, m, dtype):
     """Shapes whose wide-tile grid fills a 256-CU MI355X (the wide-tile
