@@ -20,7 +20,8 @@
 //  - qgemm_tile_kernel: 192-row x 128-token workgroups of four waves on
 //    v_mfma_f32_16x16x32_f16 with packed-f16 dequantisation, for grids that
 //    fill the CUs (described where it is defined); 256-row tiles with split K
-//    for Q6_K shapes whose 192-row grid does not fill them.
+//    for Q5_K / Q6_K shapes whose 192-row grid does not fill them.
+//  - qgemm_reduce_kernel: adds the K splits' partial tiles in split order.
 //
 // MFMA 32x32x16 operand layout (measured on gfx950): lane l holds
 // A[l%32][8*(l/32)+j], B[8*(l/32)+j][l%32] (j = 0..7) and
