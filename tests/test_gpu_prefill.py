@@ -124,6 +124,8 @@ def test_prefill_config3_full_size(env, t, k, n):
     (12, 4096, 12288, 768, "bf16"),   # 64 x 6 tiles, no split: two rounds, the second three quarters full
     (14, 12288, 4096, 768, "f32"),    # Q6_K 256-row tiles: 16 x 6, K split in 2
     (14, 12288, 4094, 384, "bf16"),   # as (14, 12288, 4096, 384) with N not a multiple of 4: one-wide split reduce
+    (12, 4096, 12288, 129, "f32"),    # 64 x 2 tiles, K split in 2; the last token tile holds one token
+    (12, 4096, 12288, 640, "bf16"),   # 320 tiles: two rounds, the second a quarter full, and no split fits: the 32x32 kernel
 ])
 def test_prefill_wide_tiles(env, t, k, n, m, dtype):
     """Shapes whose wide-tile grid fills a 256-CU MI355X (the wide-tile
