@@ -6,6 +6,8 @@ gpu_helpers.RTOL) of the f32-accumulated oracle on the same inputs. bf16
 inputs are generated as bf16 values and handed to the oracle as the same
 values in f32, so the comparison isolates the kernel's own rounding.
 """
+import random
+
 import numpy as np
 import pytest
 
@@ -267,3 +269,37 @@ def test_prefill_validation(env):
         kern2.gemm_prefill(w, x, empty_dev(4 * n), 4)
     assert e.value.kind == "WorkspaceTooSmall" and e.value.actual == 0
     assert e.value.expected == E._lib.load().ribn_amd_gemm_workspace_bytes(4, k, 0)
+
+
+def _random_prefill_shapes(count, seed):
+    rng = random.Random(seed)
+    shapes = []
+    while len(shapes) < count:
+        t = rng.choice((12, 13, 14))
+        k = rng.choice((256, 1024, 2048, 4096, 6144, 12288))
+        n = rng.choice((75, 1000, 2050, 4096, 6000, 11000, 12288))
+        m = rng.choice((33, 48, 64, 100, 128, 129, 160, 200, 256, 300, 384, 511, 512))
+        shapes.append((t, k, n, m))
+    return shapes
+
+
+@pytest.mark.parametrize("i,t,k,n,m", [(i, *s) for i, s in enumerate(_random_prefill_shapes(24, 7))])
+def test_prefill_random_shapes(env, i, t, k, n, m):
+    """Seeded random shapes across every route (32x32 kernel, small-M tiles,
+    wide tiles with and without split K, ragged row and token tiles, N not a
+    multiple of 4): sampled rows against the oracle, every output finite."""
+    import torch
+    print("CASE prefill random", i, t, k, n, m, flush=True)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(1000 + i)
+    enc_dev = synth.kquant_torch(t, k, n, gen, torch.device("cuda:0"))
+    w = upload(env, t, k, n, enc_dev)
+    xd, x = bf16_values(synth.activations_numpy(k, m, seed=2000 + i))
+    y = empty_dev(m * n)
+    env["k"][t].gemm_prefill(w, xd, y, m)
+    got = to_host(y, env["ctx"]).reshape(m, n)
+    enc = enc_dev.cpu().numpy()
+    sample = sorted({0, m // 3, m - 1})
+    ref = np.stack([O.quant_gemv(t, enc, k, n, x[r], threads=16) for r in sample])
+    assert max_rel_err(got[sample], ref) <= RTOL
+    assert np.all(np.isfinite(got))
