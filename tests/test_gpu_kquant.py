@@ -531,3 +531,39 @@ def test_gemv_mode_errors(env):
         env["k"][12].set_mode(7)
     assert e.value.kind == "InvalidArgument" and e.value.actual == 7
     assert env["k"][12].mode() == E.GEMV_WARP
+
+
+def _random_gemv_shapes(count, seed):
+    import random
+    rng = random.Random(seed)
+    shapes = []
+    for _ in range(count):
+        t = rng.choice(TYPES)
+        k = 256 * rng.choice((1, 2, 3, 5, 8, 12, 16, 17, 24, 48, 64))
+        n = rng.choice((1, 7, 64, 75, 300, 1000, 2050, 4096, 6000, 12288, 32768))
+        members = rng.choice((1, 2, 3, 4, 5, 6, 7, 8, 9, 13, 16, 24, 33, 64))
+        shapes.append((t, k, n, members))
+    return shapes
+
+
+@pytest.mark.parametrize("i,t,k,n,members", [(i, *s) for i, s in enumerate(_random_gemv_shapes(24, 11))])
+def test_random_shapes_batch_matches_oracle_and_single_bitwise(env, i, t, k, n, members):
+    """Seeded random (type, K, N, members) through the default f32 GEMV: the
+    batch within 1e-3 of the oracle on sampled members, and every sampled
+    member's row bit-identical to its single-member launch
+    (cuda_reference.rs:5322-5334)."""
+    print_case(test="random gemv", i=i, t=t, k=k, n=n, members=members)
+    enc = synth.kquant_numpy(t, k, n, seed=300 + i)
+    x = synth.activations_numpy(k, members, seed=400 + i)
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(members * n)
+    env["k"][t].execute_warp_batch(w, to_dev(x.reshape(-1)), y, members)
+    got = to_host(y, env["ctx"]).reshape(members, n)
+    assert np.all(np.isfinite(got))
+    sample = sorted({0, members // 2, members - 1})
+    ref = np.stack([O.quant_gemv(t, enc, k, n, x[m], threads=16) for m in sample])
+    assert max_rel_err(got[sample], ref) <= RTOL
+    for m in sample:
+        ys = empty_dev(n)
+        env["k"][t].execute_warp(w, to_dev(x[m]), ys)
+        assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
