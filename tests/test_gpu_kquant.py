@@ -567,3 +567,29 @@ def test_random_shapes_batch_matches_oracle_and_single_bitwise(env, i, t, k, n, 
         ys = empty_dev(n)
         env["k"][t].execute_warp(w, to_dev(x[m]), ys)
         assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", ("warp", "fixed16"))
+@pytest.mark.parametrize("i,t,k,n,members", [(i, *s) for i, s in enumerate(_random_gemv_shapes(12, 23))])
+def test_random_shapes_fused_rms_norm(env, mode, i, t, k, n, members):
+    """Seeded random shapes through the RMSNorm-fused GEMV in the default f32
+    mode and the opt-in fixed-point mode: sampled members within 1e-3 of the
+    oracle's RMSNorm followed by its GEMV."""
+    E = env["E"]
+    kern = env["k"][t]
+    print_case(test="random fused", mode=mode, i=i, t=t, k=k, n=n, members=members)
+    enc = synth.kquant_numpy(t, k, n, seed=500 + i)
+    x = synth.activations_numpy(k, members, seed=600 + i) * 2.0
+    gam = synth.gamma_numpy(k, seed=700 + i)
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(members * n)
+    kern.set_mode(E.GEMV_FIXED16 if mode == "fixed16" else E.GEMV_WARP)
+    try:
+        kern.execute_rms_norm(w, to_dev(x.reshape(-1)), to_dev(gam), 1e-6, y, members)
+    finally:
+        kern.set_mode(E.GEMV_WARP)
+    got = to_host(y, env["ctx"]).reshape(members, n)
+    assert np.all(np.isfinite(got))
+    for m in sorted({0, members // 2, members - 1}):
+        normed = O.rms_norm_raw(x[m], gam, 1e-6)
+        assert max_rel_err(got[m], O.quant_gemv(t, enc, k, n, normed, threads=16)) <= RTOL
