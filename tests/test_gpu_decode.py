@@ -587,3 +587,19 @@ def test_decoder_errors(env):
     with pytest.raises(E.AmdKernelError) as err:
         build_decoder(env, TINY, bad)
     assert err.value.kind == "InvalidPlan"
+
+
+def _random_positions(seed):
+    import random
+    rng = random.Random(seed)
+    members = rng.choice((1, 2, 3, 5, 8))
+    edges = [0, 1, 62, 63, 64, 65, 127, 128, 255, 256, 1023, 1024, 2047, 2048, 2175, 2199]
+    return [rng.choice(edges) if rng.random() < 0.5 else rng.randrange(2200) for _ in range(members)]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_attention_random_positions(env, seed):
+    """Seeded random member counts and positions (chunk edges at multiples of
+    64 among them) against the oracle's attention, with the K/V append."""
+    qh, kvh = ((32, 8), (16, 4), (8, 2))[seed % 3]
+    _check_attention(env, qh, kvh, _random_positions(seed), 500 + seed)
