@@ -541,15 +541,20 @@ ribn_amd_status ribn_amd_kv_cache_create(ribn_amd_context* ctx, const ribn_amd_q
     c->partials = reinterpret_cast<float*>(p + 2 * cache_bytes);
     // nothing is cleared: a position is written before it is read, and every
     // partial is written before the merge reads it
+    context_retain(ctx);  // released by ribn_amd_kv_cache_destroy, like every other handle's
     *out = c;
     return ok();
 }
 
 void ribn_amd_kv_cache_destroy(ribn_amd_kv_cache* cache) {
     if (!cache) return;
-    DeviceGuard guard(cache->device);
-    hipFree(cache->block);  // waits for outstanding work on the device
+    ribn_amd_context* ctx = cache->ctx;
+    {
+        DeviceGuard guard(cache->device);
+        hipFree(cache->block);  // waits for outstanding work on the device
+    }
     delete cache;
+    context_release(ctx);
 }
 
 uint32_t ribn_amd_kv_cache_capacity(const ribn_amd_kv_cache* cache) { return cache ? cache->capacity : 0; }

@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <functional>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -220,12 +221,15 @@ ribn_amd_status check_epsilon(float epsilon) {
 // ---- device scratch of the allocation-free prefill (ribn_amd_gemm_prefill_static)
 //
 // One file-scope array per device, resolved to its device address once per
-// device when a context is created there. Every call on a device shares it.
+// device (when a context is created there, else on the entry point's first
+// call). Every call on a device shares it; calls on different streams are
+// ordered through a per-device event (see order_static_call).
 constexpr size_t kStaticScratchBytes = (size_t)8 << 20;
 constexpr int kStaticScratchDevices = 64;
 static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 static std::mutex g_scratch_mutex;
 static void* g_scratch_ptr[kStaticScratchDevices];  // device address of `scratch` per device
+static hipEvent_t g_scratch_done[kStaticScratchDevices];  // the last uncaptured call's completion per device
 
 // With `device` current: looks up the device address of `scratch` (once).
 ribn_amd_status resolve_static_scratch(int device) {
@@ -250,6 +254,39 @@ void* static_scratch(int device) {
     return g_scratch_ptr[device];
 }
 
+// With `device` current, ahead of a call's launches on `stream`: makes the
+// stream wait for the previous uncaptured call on this device (whatever its
+// stream), then records this call's completion after `launch` has enqueued
+// its kernels, so calls from several streams or contexts take the array in
+// turn. A stream under graph capture is left alone: the graph's own order
+// (and the caller's order of its replays against other calls) decides.
+// The event wait and record allocate nothing.
+ribn_amd_status order_static_call(int device, hipStream_t stream, const std::function<hipError_t()>& launch) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(stream, &cap);
+    if (e != hipSuccess) return driver(e, "hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone) {
+        e = launch();
+        return e == hipSuccess ? RIBN_AMD_OK : driver(e, "launch allocation-free prefill");
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    hipEvent_t& done = g_scratch_done[device];
+    if (done == nullptr) {
+        e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            done = nullptr;
+            return driver(e, "hipEventCreateWithFlags");
+        }
+    } else {
+        e = hipStreamWaitEvent(stream, done, 0);
+        if (e != hipSuccess) return driver(e, "hipStreamWaitEvent");
+    }
+    e = launch();
+    if (e != hipSuccess) return driver(e, "launch allocation-free prefill");
+    e = hipEventRecord(done, stream);
+    return e == hipSuccess ? RIBN_AMD_OK : driver(e, "hipEventRecord");
+}
+
 ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_context** out) {
     hipDeviceProp_t prop;
     hipError_t e = hipGetDeviceProperties(&prop, device);
@@ -258,8 +295,9 @@ ribn_amd_status new_context(int device, hipStream_t stream, bool owns, ribn_amd_
     const size_t act_bytes = (ribn_amd::gemv_act_scratch_bytes() + 255) / 256 * 256;
     {
         DeviceGuard guard(device);
-        ribn_amd_status st = resolve_static_scratch(device);
-        if (st != RIBN_AMD_OK) return st;
+        // Resolved here when it can be; a failure only concerns the
+        // allocation-free entry point, which tries again and reports it.
+        (void)resolve_static_scratch(device);
         e = hipMalloc(&ctx_scratch, act_bytes + RIBN_AMD_MAX_BATCH_MEMBERS * sizeof(ribn_amd::AttnMember));
         if (e != hipSuccess) return driver(e, "hipMalloc context scratch");
     }
@@ -1051,16 +1089,24 @@ ribn_amd_status ribn_amd_gemm_prefill_static(ribn_amd_gemv* g, const ribn_amd_qu
                     "holds %zu (use ribn_amd_gemm_prefill with a reserved workspace)",
                     members, (unsigned long long)k, need, kStaticScratchBytes);
     }
-    void* ptr = static_scratch(g->ctx->device);
-    if (ptr == nullptr) return fail(RIBN_AMD_DRIVER, 0, 0, "static scratch of device %d is unresolved", g->ctx->device);
-    DeviceGuard guard(g->ctx->device);
-    hipError_t e = ribn_amd::launch_act_f16(input_dtype == RIBN_AMD_BF16, input, gamma, epsilon, (int)members, (int)k,
-                                            ptr, g->ctx->stream);
-    if (e != hipSuccess) return driver(e, "launch prefill activation stage");
-    e = ribn_amd::launch_qgemm((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, ptr, kStaticScratchBytes,
-                               output, (int)members, (int)n, (int)k, g->ctx->cu_count, g->ctx->stream);
-    if (e != hipSuccess) return driver(e, "launch prefill matmul");
-    return ok();
+    const int device = g->ctx->device;
+    DeviceGuard guard(device);
+    void* ptr = static_scratch(device);
+    if (ptr == nullptr) {
+        st = resolve_static_scratch(device);  // with the device current
+        if (st != RIBN_AMD_OK) return st;
+        ptr = static_scratch(device);
+    }
+    hipStream_t stream = g->ctx->stream;
+    st = order_static_call(device, stream, [&]() {
+        hipError_t e = ribn_amd::launch_act_f16(input_dtype == RIBN_AMD_BF16, input, gamma, epsilon, (int)members,
+                                                (int)k, ptr, stream);
+        if (e != hipSuccess) return e;
+        return ribn_amd::launch_qgemm((int)g->value_type, w->data, (uint32_t)w->encoded_bytes, ptr,
+                                      kStaticScratchBytes, output, (int)members, (int)n, (int)k, g->ctx->cu_count,
+                                      stream);
+    });
+    return st == RIBN_AMD_OK ? ok() : st;
 }
 
 // ------------------------------------------------------------ embedding

@@ -215,7 +215,13 @@ uint32_t ribn_amd_gemv_value_type(const ribn_amd_gemv *gemv);
  *     GemvMode::IntegerDot for throughput comparison): activations rounded to
  *     block fixed point (16-bit per scale group in the wave kernel, 15-bit per
  *     super-block on the int8 matrix cores from 5 members) with integer dot
- *     products. Never bit-identical to WARP. */
+ *     products. Never bit-identical to WARP.
+ * The reference's third mode, GemvMode::Scalar (one thread per row, its
+ * decode correctness oracle), is not a mode here: its per-operator form is
+ * ribn_amd_gemv_execute (bit-identical to the host decoder + sequential
+ * dot), and decoder-level correctness is checked against a CPU oracle of the
+ * whole step instead. Mapping GemvMode::Scalar to a decoder mode is
+ * therefore InvalidArgument by design. */
 #define RIBN_AMD_GEMV_WARP 0u
 #define RIBN_AMD_GEMV_FIXED16 1u
 /* set_gemv_mode / gemv_mode (decode.rs:711-741) at the operator level: an
@@ -426,8 +432,14 @@ ribn_amd_status ribn_amd_gemm_prefill(ribn_amd_gemv *gemv, const ribn_amd_quanti
  * must fit 8 MiB (e.g. 1024 tokens at K = 4096, 256 at K = 16384); larger
  * calls return WorkspaceTooSmall { expected: 8 MiB, actual: bytes needed }
  * before any launch. Split K uses what is left. Every call on a GPU shares
- * that GPU's array (whatever the context or stream): calls that overlap in
- * time on one GPU race; order them on one stream or synchronise. */
+ * that GPU's array (whatever the context or stream). Calls made outside graph
+ * capture are ordered through a per-GPU event: each call's stream waits for
+ * the previous such call on that GPU, from any stream or context. Under
+ * capture nothing is added to the graph: replays of a captured call race
+ * with other calls on the GPU unless the caller orders them (one stream, or
+ * a synchronisation between them). The array's address is resolved at
+ * context creation, or on the first call if that failed; a GPU index past
+ * 63 is InvalidArgument here only. */
 ribn_amd_status ribn_amd_gemm_prefill_static(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
                                              const void *input, uint32_t input_dtype, size_t input_len,
                                              size_t members, const float *gamma, size_t gamma_len, float epsilon,
@@ -553,8 +565,9 @@ void ribn_amd_qwen3_decode_destroy(ribn_amd_qwen3_decode *decode);
 ribn_amd_status ribn_amd_qwen3_decode_set_graphs(ribn_amd_qwen3_decode *decode, int32_t enabled);
 /* CudaQwen35Decode::set_gemv_mode / gemv_mode (decode.rs:711-741): the
  * arithmetic of every projection of later steps (RIBN_AMD_GEMV_WARP by
- * default, or RIBN_AMD_GEMV_FIXED16); an unknown mode is InvalidArgument.
- * Captured graphs of the other mode are dropped. */
+ * default, or RIBN_AMD_GEMV_FIXED16); an unknown mode, GemvMode::Scalar's
+ * included (see the GEMV modes above), is InvalidArgument. Captured graphs
+ * of the other mode are dropped. */
 ribn_amd_status ribn_amd_qwen3_decode_set_gemv_mode(ribn_amd_qwen3_decode *decode, uint32_t mode);
 uint32_t ribn_amd_qwen3_decode_gemv_mode(const ribn_amd_qwen3_decode *decode);
 /* CudaQwen35Decode::prefill_step (decode.rs:489-499): advances `cache` by
