@@ -28,6 +28,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 / f16 MFMA
 HIDDEN, FFN, Q_OUT, KV_OUT, VOCAB = 4096, 12288, 4096, 1024, 151936
 EPS = 1e-6
 METRIC = "Q4_K GEMV HBM GB/s (% of peak) + batch-1 decode tok/s, Qwen3-8B shapes"
@@ -330,9 +331,13 @@ def _graph_time_us(torch, stream, fn, reps):
 
 def bench_batched(E, synth, torch, args):
     """the Qwen3-8B FFN (gate/up Q4_K 4096->12288, down Q5_K 12288->4096)
-    for M tokens. M <= 16 runs the decode step's batched GEMV entry points (gate/up as one
-    grouped launch), which take the wave GEMV below 5 members (4 for down's long K) and the
-    matrix-core GEMV above; M = 64 the prefill matmul. Activations are synthetic f32 ~N(0,1)."""
+    for M tokens with f32 activations ~N(0,1), through the decode step's batched GEMV entry
+    points (gate/up as one grouped launch). The default f32 arithmetic (GEMV_WARP) runs the f32
+    wave GEMV up to 8 members (weights read once per launch group, every row bit-identical to
+    the single call) and the f32-faithful matrix-core GEMV from 9 to 64 members (activations
+    split exactly into three bf16 pieces, f32 accumulation, weights read once for the batch).
+    For comparison: the opt-in block fixed-point mode at M <= 16 and the f16 prefill matmul at
+    M = 64."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream()
     ctx = E.AmdContext(0, stream=stream)
@@ -353,47 +358,50 @@ def bench_batched(E, synth, torch, args):
         x = torch.randn(m, HIDDEN, device=dev, generator=gen)
         h = torch.randn(m, FFN, device=dev, generator=gen)
         g, u, d = (torch.empty(m * n, device=dev) for n in (FFN, FFN, HIDDEN))
-        runs = []
-        if m <= 16:
-            for mode in ("warp", "fixed16"):
-                if mode == "warp":
-                    path = ("f32 wave GEMV, weights read once per 8 members (down's K = 12288 split by "
-                            "slice from 3 members, with an ordered slice reduction)")
-                else:
-                    path = ("block fixed-point " + ("wave GEMV" if m < 4 else
-                            "wave GEMV gate/up, matrix-core GEMV down" if m < 5 else "matrix-core GEMV") +
-                            ", weights read once per launch")
 
-                def fn():
-                    for ly in layers:
-                        k4.execute_group([ly["gate"], ly["up"]], x, [g, u], m)
-                        k5.execute_warp_batch(ly["down"], h, d, m)
-                runs.append((mode, path, fn))
+        def gemv_ffn():
+            for ly in layers:
+                k4.execute_group([ly["gate"], ly["up"]], x, [g, u], m)
+                k5.execute_warp_batch(ly["down"], h, d, m)
+        runs = [("warp", "f32 wave GEMV, weights read once per launch group of up to 8 members (down's K = 12288 "
+                         "split by slice from 3 members, with an ordered slice reduction)" if m <= 8 else
+                 "f32-faithful matrix-core GEMV (x split exactly into three bf16 pieces, bf16 MFMA with f32 "
+                 "accumulation, f32 scale epilogue), weights read once for the batch", gemv_ffn)]
+        if m <= 16:
+            runs.append(("fixed16", "block fixed-point " + ("wave GEMV" if m < 4 else
+                         "wave GEMV gate/up, matrix-core GEMV down" if m < 5 else "matrix-core GEMV") +
+                         ", weights read once per launch", gemv_ffn))
         else:
-            def fn():
+            def prefill_ffn():
                 for ly in layers:
                     k4.gemm_prefill(ly["gate"], x, g, m)
                     k4.gemm_prefill(ly["up"], x, u, m)
                     k5.gemm_prefill(ly["down"], h, d, m)
-            runs.append(("f16-mfma", "matrix-core matmul (f16 MFMA, f32 accumulation)", fn))
+            runs.append(("f16-mfma", "prefill matmul (activations rounded to f16, f16 MFMA, f32 accumulation)",
+                         prefill_ffn))
         per_m[m] = {}
         for mode, path, fn in runs:
             for kern in (k4, k5):
                 kern.set_mode(GEMV_MODES.get(mode, 0))
             us = _graph_time_us(torch, stream, fn, max(2, args.steps // 10)) / n_layers
+            flops = 2.0 * m * 3 * FFN * HIDDEN
             per_m[m][mode] = {"us_per_ffn": round(us, 2), "tokens_per_s": round(m * 1e6 / us, 1),
-                              "weight_GBps": round(wbytes / us / 1e3, 1),
-                              "tflops": round(2.0 * m * 3 * FFN * HIDDEN / us / 1e6, 2), "path": path}
+                              "weight_GBps": round(wbytes / us / 1e3, 1), "hbm_frac": round(wbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+                              "tflops": round(flops / us / 1e6, 2), "path": path}
+            if mode == "warp" and m > 8:
+                # executed on the matrix cores as three bf16 products per f32 one
+                per_m[m][mode]["bf16_mfma_frac"] = round(3 * flops / us / 1e6 / PEAK_BF16_TFLOPS, 4)
             log(f"bench batched: M={m} {mode}: {us:.2f} us per FFN ({path})")
         for kern in (k4, k5):
             kern.set_mode(0)
-    top = per_m[64]["f16-mfma"]
+    top = per_m[64]["warp"]
     return {
-        "metric": "batched decode FFN throughput (BASELINE config 2), tokens/s at M=64",
+        "metric": "batched decode FFN throughput (BASELINE config 2), tokens/s at M=64, f32 activations",
         "value": top["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(top["us_per_ffn"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16-mfma-f32 (M=64); per_m also holds f32 (warp) and i8dot4 / i8-mfma (fixed16) for M<=16",
+        "dtype": "f32 (M>=9 on bf16 MFMA with exact three-piece activations, f32 accumulation); per_m also holds "
+                 "i8dot4 / i8-mfma (fixed16) for M<=16 and f16-mfma at M=64",
         "data": "synthetic",
         "config": {"workload": "qwen3-8b-ffn-batched", "ffn_weight_bytes": wbytes, "layers_cycled": n_layers,
                    "per_m": per_m},

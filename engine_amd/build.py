@@ -31,7 +31,7 @@ HIPCC_FLAGS = [
     "-Wall", "-Wno-unused-function",
 ]
 
-SOURCES = ["kquant_kernels.hip", "gemv_wave.hip", "gemv_f32.hip", "gemv_mfma.hip", "q8_1.hip", "qgemm.hip", "decode_kernels.hip", "ribn_amd.cpp", "qwen3_decode.cpp", "gguf.cpp", "serving.cpp"]
+SOURCES = ["kquant_kernels.hip", "gemv_wave.hip", "gemv_f32.hip", "gemv_mfma.hip", "gemv_f32mma.hip", "q8_1.hip", "qgemm.hip", "decode_kernels.hip", "ribn_amd.cpp", "qwen3_decode.cpp", "gguf.cpp", "serving.cpp"]
 
 
 def hipcc() -> str:

@@ -1,0 +1,837 @@
+// f32-faithful batched k-quant GEMV on the bf16 matrix cores (gfx950 /
+// CDNA4, wave64): the default GEMV_WARP arithmetic for 9..64 members, with
+// the weights read once for the whole batch (the reference's batch GEMV reads
+// them once per launch of at most 8 members: q4_k.cu:161-258,
+// quantized.rs:445-487). Up to 8 members the f32 wave GEMV stays in charge:
+// its rows are bit-identical to the single-member call, as the reference
+// qualifies its batch lane (cuda_reference.rs:5322-5334).
+//
+// Why this is f32 arithmetic
+//  - Activations: each f32 value x is split exactly into three bf16 pieces,
+//    x = hi + mid + lo: hi keeps the top 8 significand bits (truncation),
+//    mid the top 8 of the exact remainder x - hi, lo the remaining <= 8 bits
+//    (x - hi - mid is exactly representable in bf16). Nothing is rounded.
+//  - Quants are small integers: Q4_K / Q5_K quants enter as 128 + q (0..31
+//    plus 128 is exact in bf16 and takes one byte permute per two quants),
+//    Q6_K as q - 32 (signed, exact).
+//  - v_mfma_f32_16x16x32_bf16 multiplies exactly (8 x 8 significand bits)
+//    and accumulates in f32. Three MFMAs per 32-element group (one per
+//    piece, chained through the accumulator) give S'_g = sum_i (128 + q_i) x_i
+//    = S_g + 128 X_g for 16 members x 16 weight rows, rounded only by the f32
+//    accumulation.
+//  - The epilogue is the f32 wave path's: part += (d*sc_g) * S'_g (f32 FMA
+//    per value) and, for Q4_K / Q5_K, the minimum term
+//    sum_g (dmin*m_g + 128 d*sc_g) * X_g (X_g the f32 group sums of x) on
+//    v_mfma_f32_16x16x4_f32 ([member][group] x [group][row]), which also
+//    takes the 128 X_g back out. Q6_K scale groups are 16 elements: the B
+//    operand is masked to each half of the 32-element MFMA group (S_g of each
+//    half), and Q6_K has no minimum term.
+//  So the products are the dequantised weights times x, regrouped per scale
+//  group like the wave path's, with f32 rounding in the sums; the order
+//  differs, so results agree with the sequential f32 GEMV to f32 rounding
+//  (within 5e-5 normwise on wide-dynamic-range activations), not bit for bit.
+//
+// Layout (pack_f32mma_kernel, one launch per product)
+//  - Member tile mt of 16, super-block b, 32-element group g, piece s: 64
+//    lanes x 16 bytes in the MFMA A-operand order: lane l = member (l % 16)
+//    of the tile, 8 bf16 of elements 8 (l / 16) .. + 7 of the group.
+//  - X sums (Q4_K / Q5_K minimum term): per (tile, block) 64 lanes x 2 f32,
+//    lane mi + 16 q holding X of groups q and 4 + q of member mi (the A
+//    operand of the two f32 MFMAs per block).
+//  - Per-member partial sums of x^2 per pack workgroup, for RMSNorm: the
+//    product divides its outputs by rms(x) (the wave GEMV's factorisation
+//    y = (W (x * gamma)) / rms).
+//
+// Product (f32mma_gemv_kernel)
+//  - One launch serves up to two member tiles (32 members): their fragments
+//    of a super-block, double-buffered, fill 98 KB of LDS. 33..64 members
+//    take two launches over the same packed activations.
+//  - A workgroup of W waves shares each super-block's fragments, loaded
+//    straight into LDS a block ahead; each wave owns R tiles of 16 weight
+//    rows (gate/up pairs: R/2 gate tiles and the up tiles of the same rows)
+//    over the workgroup's super-blocks and streams their weights through a
+//    two-block register ring.
+//  - Row groups short of the CUs split K across workgroups: raw row sums go
+//    to a partial buffer and f32mma_reduce_kernel adds the splits in order
+//    (deterministic) and applies the epilogue.
+//  - Lane l holds output row (l % 16) of each tile for members
+//    4 (l / 16) .. + 3 of each member tile (the MFMA C layout).
+// A member's output depends only on its own activations: its bits do not
+// change with the other members' values or count (from 9 members on).
+#include "kquant_device.hpp"
+#include "kquant_launch.hpp"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace ribn_amd {
+
+namespace {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kOOR = 0xffffff00u;  // buffer offset past any tensor: loads return 0, stores drop
+constexpr int kPackBlocks = 2;          // super-blocks per pack workgroup (one wave)
+constexpr int kPieces = 3;
+constexpr uint32_t kPieceBytes = 64 * 16;                               // one piece of one group
+constexpr uint32_t kFragBlockBytes = 8 * kPieces * kPieceBytes;         // 24 KiB per (member tile, block)
+constexpr uint32_t kXsumBlockBytes = 64 * 2 * 4;                        // per (member tile, block)
+
+__device__ __forceinline__ uint32_t top16(float f) { return __builtin_bit_cast(uint32_t, f) & 0xffff0000u; }
+
+// Two bf16 (the top halves of two f32 bit patterns) in one word, the first
+// in the low half.
+__device__ __forceinline__ uint32_t pack2(uint32_t lo_f32_bits, uint32_t hi_f32_bits) {
+    return __builtin_amdgcn_perm(hi_f32_bits, lo_f32_bits, 0x07060302u);
+}
+
+struct PackArgs {
+    const float* x;      // [members][K]
+    const float* x2;     // SwiGLU: silu(x) * x2, or null
+    const float* gamma;  // RMSNorm weight [K], or null
+    uint8_t* act;
+    F32MmaLayout L;
+    int K;
+};
+
+__global__ __launch_bounds__(64) void pack_f32mma_kernel(PackArgs a) {
+    const int m = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x * kPackBlocks + (tid >> 5);
+    const int c = tid & 31;
+    const int g = c >> 2, kq = c & 3;
+    const int nb = a.L.nb;
+    const bool live = b < nb;
+    float v[8];
+    float ssq = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = 0.f;
+    if (live) {
+        const size_t e0 = (size_t)m * a.K + (size_t)b * 256 + 32 * g + 8 * kq;
+        const float4 x0 = *reinterpret_cast<const float4*>(a.x + e0);
+        const float4 x1 = *reinterpret_cast<const float4*>(a.x + e0 + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+        if (a.x2 != nullptr) {
+            const float4 u0 = *reinterpret_cast<const float4*>(a.x2 + e0);
+            const float4 u1 = *reinterpret_cast<const float4*>(a.x2 + e0 + 4);
+            const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            // silu(gate) * up, in the reference's operation order (model_ops.rs:316-328)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = (v[j] / (1.0f + expf(-v[j]))) * u[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ssq += v[j] * v[j];
+            if (a.gamma != nullptr) {
+                const size_t k0 = (size_t)b * 256 + 32 * g + 8 * kq;
+                const float4 g0 = *reinterpret_cast<const float4*>(a.gamma + k0);
+                const float4 g1 = *reinterpret_cast<const float4*>(a.gamma + k0 + 4);
+                v[0] *= g0.x; v[1] *= g0.y; v[2] *= g0.z; v[3] *= g0.w;
+                v[4] *= g1.x; v[5] *= g1.y; v[6] *= g1.z; v[7] *= g1.w;
+            }
+        }
+    }
+    // x = hi + mid + lo, each piece the top 16 bits of an f32 (a bf16)
+    uint32_t hw[8], mw[8], lw[8];
+    float xs = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        hw[j] = top16(v[j]);
+        const float r1 = v[j] - __builtin_bit_cast(float, hw[j]);
+        mw[j] = top16(r1);
+        const float r2 = r1 - __builtin_bit_cast(float, mw[j]);
+        lw[j] = top16(r2);  // r2 has at most 8 significant bits: exact
+        xs += v[j];
+    }
+    xs += __shfl_xor(xs, 1, 64);
+    xs += __shfl_xor(xs, 2, 64);  // X_g over the four 8-element chunks of group g
+    if (live) {
+        const int mt = m >> 4, mi = m & 15;
+        const uint32_t blk = (uint32_t)(mt * nb + b);
+        uint8_t* fr = a.act + a.L.frag + (blk * 8u + (uint32_t)g) * kPieces * kPieceBytes + (uint32_t)(mi + 16 * kq) * 16u;
+        const uint32_t* pieces[3] = {hw, mw, lw};
+#pragma unroll
+        for (int s = 0; s < kPieces; ++s) {
+            const uint32_t* p = pieces[s];
+            *reinterpret_cast<uint4*>(fr + s * kPieceBytes) =
+                make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7]));
+        }
+        if (kq == 0) {
+            float* xsum = reinterpret_cast<float*>(a.act + a.L.xsum);
+            xsum[(blk * 64u + (uint32_t)(mi + 16 * (g & 3))) * 2u + (uint32_t)(g >> 2)] = xs;
+        }
+    }
+    // this workgroup's share of sum(x^2), for RMSNorm (summed in part order by the product)
+    const float ws = wave_sum(ssq);
+    if (tid == 0) reinterpret_cast<float*>(a.act + a.L.ssq)[m * a.L.parts + blockIdx.x] = ws;
+}
+
+// ------------------------------------------------------------------ product
+
+struct F32MmaArgs {
+    const uint8_t* w[kMaxGroup];
+    uint32_t wbytes[kMaxGroup];
+    float* y[kMaxGroup];
+    int rows_end[kMaxGroup];
+    int count;
+    int total_rows;
+    const uint8_t* act;
+    uint32_t act_bytes;
+    F32MmaLayout L;
+    int K;
+    int members;   // of the whole call (output and activation extents)
+    int member0;   // first member of this launch (a multiple of 16)
+    int count_here;  // members of this launch (at most 16 * MT)
+    int has_norm;
+    float eps;
+    int accumulate;
+    int pair_swiglu;
+    // K split across workgroups (blockIdx.y): each covers split_blocks
+    // super-blocks and stores raw row sums to partial[split][member][vrow]
+    // (vrow: the row in the launch's virtual row space; pairs: gate rows,
+    // then up rows), which f32mma_reduce_kernel adds in split order
+    float* partial;
+    int splits;
+    int split_blocks;
+};
+
+template <int T> struct WRaw;
+template <> struct WRaw<kQ4K> { uint4 h; uint2 q[4]; };
+template <> struct WRaw<kQ5K> { uint4 h; uint2 qh; uint2 q[4]; };
+// Q6_K: the 16 int8 scales, d, and for each half n the 8 low-nibble bytes of
+// both 32-byte quadrant pairs and the 8 qh bytes.
+template <> struct WRaw<kQ6K> { uint4 sc; uint32_t d16; uint2 ql[4]; uint2 qh[2]; };
+
+__device__ __forceinline__ uint2 load_b64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+
+// One lane's bytes of a 16-row tile's super-block (row l % 16, elements
+// 8 kq .. 8 kq + 7 of every group; crates/gguf/src/lib.rs:596-661 layouts).
+template <int T>
+__device__ __forceinline__ void load_w(WRaw<T>& d, __amdgpu_buffer_rsrc_t r, bool live, uint32_t base, int kq) {
+    if constexpr (T == kQ6K) {
+        // ql[128] at 0, qh[64] at 128, scales[16] at 192, d at 208
+        d.sc = load_b128(r, live ? base + 192u : kOOR);
+        d.d16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, live ? (int)(base + 208u) : (int)kOOR, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d.ql[i] = load_b64(r, live ? base + 32u * i + 8u * kq : kOOR);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) d.qh[n] = load_b64(r, live ? base + 128u + 32u * n + 8u * kq : kOOR);
+    } else {
+        d.h = load_b128(r, live ? base : kOOR);
+        if constexpr (T == kQ5K) {
+            d.qh = load_b64(r, live ? base + 16u + 8u * kq : kOOR);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) d.q[p] = load_b64(r, live ? base + 48u + 32u * p + 8u * kq : kOOR);
+        } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) d.q[p] = load_b64(r, live ? base + 16u + 32u * p + 8u * kq : kOOR);
+        }
+    }
+}
+
+// Eight unsigned byte quants q < 128 (two words) as the eight bf16 values
+// 128 + q, exactly: bf16 0x4300 is 128.0 with a 7-bit mantissa, so 0x43qq is
+// 128 + q. One byte permute per two quants.
+__device__ __forceinline__ v8bf bf16_128_plus(uint32_t w0, uint32_t w1) {
+    // bytes of the result: q, 0x43 for each half (selector 0-3: w, 4: the constant)
+    const uint32_t c = 0x43434343u;
+    const uint4 b = make_uint4(__builtin_amdgcn_perm(c, w0, 0x04010400u), __builtin_amdgcn_perm(c, w0, 0x04030402u),
+                               __builtin_amdgcn_perm(c, w1, 0x04010400u), __builtin_amdgcn_perm(c, w1, 0x04030402u));
+    return __builtin_bit_cast(v8bf, b);
+}
+
+// Eight signed byte quants as eight bf16 (exact).
+__device__ __forceinline__ v8bf bf16_of_sbytes(uint32_t w0, uint32_t w1) {
+    uint32_t f[8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        // signed byte t of each word (v_cvt_f32_i32 of the sign-extended byte)
+        f[t] = __builtin_bit_cast(uint32_t, (float)(int)(int8_t)(w0 >> (8 * t)));
+        f[4 + t] = __builtin_bit_cast(uint32_t, (float)(int)(int8_t)(w1 >> (8 * t)));
+    }
+    const uint4 b = make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
+    return __builtin_bit_cast(v8bf, b);
+}
+
+// Q6_K quants of 32-element group g minus 32, as signed bytes (half n = g / 4,
+// quadrant t = g % 4, elements 8 kq .. 8 kq + 7 of the quadrant; lib.rs:635-661):
+// low (t < 2) or high nibble of ql[64 n + 32 (t & 1) + l] and bits 2t, 2t + 1 of
+// qh[32 n + l]. x = q ^ 32 is q - 32 for q >= 32 and q + 32 otherwise, which
+// setting bits 6-7 turns into q - 32.
+__device__ __forceinline__ void q6_group(const WRaw<kQ6K>& d, int g, uint32_t& o0, uint32_t& o1) {
+    const int n = g >> 2, t = g & 3;
+    const uint2 lo = d.ql[2 * n + (t & 1)];
+    const uint2 hi = d.qh[n];
+    const int sl = (t >> 1) * 4, sh = 2 * t;
+    const uint32_t w[2] = {lo.x, lo.y}, h2[2] = {hi.x, hi.y};
+    uint32_t out[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t q = ((w[i] >> sl) & 0x0f0f0f0fu) | (((h2[i] >> sh) & 0x03030303u) << 4);
+        const uint32_t x = q ^ 0x20202020u;
+        out[i] = x | ((x & 0x20202020u) * 6u);
+    }
+    o0 = out[0];
+    o1 = out[1];
+}
+
+// One workgroup: W waves, wave w owning R tiles of 16 weight rows (gate/up
+// pairs: R/2 gate tiles and the up tiles of the same rows), all of them over
+// the workgroup's super-blocks [sb0, sb1) (a K split across workgroups when
+// blockIdx.y > 0 exists). Per super-block the MT member tiles' activation
+// fragments and X sums are loaded straight into LDS (double-buffered, a
+// block ahead) once for the W waves; weights stream through a two-block
+// register ring.
+template <int T, int R, int MT, bool PAIR, int W>
+__global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
+    constexpr int BB = BlockTraits<T>::bytes;
+    constexpr int FRAGS = MT * 8 * kPieces;  // 1 KB fragment loads per block
+    constexpr int XS = T == kQ6K ? 0 : 2 * MT;  // 256 B X-sum loads per block
+    static_assert(!PAIR || R % 2 == 0, "pairs split the tiles into gate and up halves");
+    // two slots as separate objects: the compiler can then tell that reads of
+    // one do not alias the loads into the other in flight
+    __shared__ __attribute__((aligned(16))) uint4 fa0[FRAGS * 64];
+    __shared__ __attribute__((aligned(16))) uint4 fa1[FRAGS * 64];
+    __shared__ __attribute__((aligned(16))) float2 xa0[XS ? MT * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float2 xa1[XS ? MT * 64 : 1];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kq = lane >> 4, rl = lane & 15;
+    const int nb = A.K >> 8;
+    const uint32_t row_bytes = (uint32_t)nb * BB;
+    const int sb0 = (int)blockIdx.y * A.split_blocks;
+    const int sb1 = min(nb, sb0 + A.split_blocks);
+    const int tile0 = A.member0 >> 4;
+
+    // this wave's tiles: (matrix, first local row); tiles never straddle matrices
+    __amdgpu_buffer_rsrc_t wr[R];
+    int mat[R], local0[R], rows_mat[R], vrow0[R];
+    bool live_row[R];
+    uint32_t rowoff[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        if constexpr (PAIR) {
+            mat[i] = i / (R / 2);
+            local0[i] = (((int)blockIdx.x * W + wave) * (R / 2) + i % (R / 2)) * 16;
+            rows_mat[i] = A.rows_end[0];
+            vrow0[i] = (mat[i] ? A.rows_end[0] : 0) + local0[i];
+        } else {
+            const int row0 = (((int)blockIdx.x * W + wave) * R + i) * 16;
+            int mm = 0, start = 0;
+#pragma unroll
+            for (int j = 0; j < kMaxGroup - 1; ++j) {
+                if (j + 1 < A.count && row0 >= A.rows_end[j]) {
+                    mm = j + 1;
+                    start = A.rows_end[j];
+                }
+            }
+            mat[i] = mm;
+            local0[i] = row0 < A.total_rows ? row0 - start : 1 << 30;
+            rows_mat[i] = A.rows_end[mm] - start;
+            vrow0[i] = row0;
+        }
+        const int mm = mat[i];
+        const uint8_t* w = A.w[0];
+        uint32_t wb = A.wbytes[0];
+#pragma unroll
+        for (int j = 1; j < kMaxGroup; ++j) {
+            if (mm == j) {
+                w = A.w[j];
+                wb = A.wbytes[j];
+            }
+        }
+        wr[i] = make_rsrc(w, wb);
+        const int lrow = local0[i] + rl;
+        live_row[i] = lrow < rows_mat[i];
+        rowoff[i] = live_row[i] ? (uint32_t)lrow * row_bytes : 0u;
+    }
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A.act, A.act_bytes);
+
+    // ---- activation fragments of block b into an LDS slot: load j of the
+    // block (fragment (member tile j / 24, group and piece j % 24), 1 KB) is
+    // issued by wave j % W; past the range the loads read zeros
+    auto stage = [&](auto slot_const, int b) {
+        constexpr int SL = decltype(slot_const)::value;
+        uint4* const fa = SL ? fa1 : fa0;
+        float2* const xa = SL ? xa1 : xa0;
+        const bool lb = b < sb1;
+#pragma unroll
+        for (int j = 0; j < FRAGS; ++j) {
+            if (j % W != wave) continue;
+            const int mt = j / (8 * kPieces);
+            const uint32_t off = A.L.frag + ((uint32_t)((tile0 + mt) * nb + b) * (8u * kPieces) +
+                                             (uint32_t)(j % (8 * kPieces))) * kPieceBytes + (uint32_t)lane * 16u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (__attribute__((address_space(3))) void*)&fa[j * 64], 16,
+                                                     (int)(lb ? off : kOOR), 0, 0, 0);
+        }
+#pragma unroll
+        for (int h = 0; h < XS; ++h) {
+            if ((FRAGS + h) % W != wave) continue;
+            const int mt = h >> 1;
+            const uint32_t off = A.L.xsum + (uint32_t)((tile0 + mt) * nb + b) * kXsumBlockBytes +
+                                 (uint32_t)(h & 1) * 256u + (uint32_t)lane * 4u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ar, (__attribute__((address_space(3))) void*)(reinterpret_cast<float*>(xa) + h * 64), 4,
+                (int)(lb ? off : kOOR), 0, 0, 0);
+        }
+        // written behind the compiler's back: LDS reads must not move across
+        asm volatile("" ::: "memory");
+    };
+
+    v4f acc[R][MT], macc[R][MT];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            acc[i][mt] = (v4f){0.f, 0.f, 0.f, 0.f};
+            macc[i][mt] = (v4f){0.f, 0.f, 0.f, 0.f};
+        }
+    WRaw<T> ring[2][R];
+    auto fill_w = [&](int s, int b) {
+        const bool lb = b < sb1;
+#pragma unroll
+        for (int i = 0; i < R; ++i) load_w<T>(ring[s][i], wr[i], lb && live_row[i], rowoff[i] + (uint32_t)b * BB, kq);
+    };
+
+    // ---- one super-block from weight slot s and LDS slot (fa, xa)
+    auto block = [&](auto slot_const) {
+        constexpr int s = decltype(slot_const)::value;  // weight ring slot = LDS slot
+        const uint4* const fa = s ? fa1 : fa0;
+        const float2* const xa = s ? xa1 : xa0;
+        float dd[R], bmin0[R], bmin1[R];
+        uint32_t scw_lo[R], scw_hi[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            if constexpr (T == kQ6K) {
+                dd[i] = half_bits_to_float(ring[s][i].d16 & 0xffffu);
+            } else {
+                const uint4 h = ring[s][i].h;
+                dd[i] = half_bits_to_float(h.x & 0xffffu);
+                const float dmn = half_bits_to_float(h.x >> 16);
+                // six-bit scales / minima of the 8 groups, four per word (lib.rs:573-587)
+                scw_lo[i] = h.y & 0x3f3f3f3fu;
+                scw_hi[i] = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+                const uint32_t mnw_lo = h.z & 0x3f3f3f3fu;
+                const uint32_t mnw_hi = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+                // the quants enter the MFMAs as 128 + q (see bf16_128_plus),
+                // so group g's sum is S'_g = S_g + 128 X_g; the minimum-term
+                // operand takes the 128 (d sc_g) X_g back out:
+                //   (d sc_g) S'_g - (dmin m_g + 128 d sc_g) X_g = (d sc_g) S_g - (dmin m_g) X_g
+                // (exact up to f32 rounding of the two products and sums)
+                const float sc0 = (float)((scw_lo[i] >> (8 * kq)) & 0xffu);
+                const float sc1 = (float)((scw_hi[i] >> (8 * kq)) & 0xffu);
+                bmin0[i] = dmn * (float)((mnw_lo >> (8 * kq)) & 0xffu) + 128.0f * (dd[i] * sc0);
+                bmin1[i] = dmn * (float)((mnw_hi >> (8 * kq)) & 0xffu) + 128.0f * (dd[i] * sc1);
+            }
+        }
+        if constexpr (T != kQ6K) {
+            // minimum term of groups kq and 4 + kq (the lane's k slot):
+            // A = X [member][group], B = dmin m [group][row]
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const float2 xs = xa[mt * 64 + lane];
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    macc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs.x, bmin0[i], macc[i][mt], 0, 0, 0);
+                    macc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs.y, bmin1[i], macc[i][mt], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            v8bf bq[R], bq1[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                if constexpr (T == kQ6K) {
+                    uint32_t q0, q1;
+                    q6_group(ring[s][i], g, q0, q1);
+                    // scale groups 2g (elements 0-15: lanes kq 0-1) and 2g + 1 (kq 2-3)
+                    const bool low = kq < 2;
+                    bq[i] = bf16_of_sbytes(low ? q0 : 0u, low ? q1 : 0u);
+                    bq1[i] = bf16_of_sbytes(low ? 0u : q0, low ? 0u : q1);
+                } else {
+                    const int p = g >> 1, sh = 4 * (g & 1);
+                    uint32_t q0 = (ring[s][i].q[p].x >> sh) & 0x0f0f0f0fu;
+                    uint32_t q1 = (ring[s][i].q[p].y >> sh) & 0x0f0f0f0fu;
+                    if constexpr (T == kQ5K) {
+                        // fifth bit of element j of group g: bit g of qh[j]
+                        q0 |= ((ring[s][i].qh.x >> g) & 0x01010101u) << 4;
+                        q1 |= ((ring[s][i].qh.y >> g) & 0x01010101u) << 4;
+                    }
+                    bq[i] = bf16_128_plus(q0, q1);
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int f = (mt * 8 + g) * kPieces;
+                const v8bf a0 = __builtin_bit_cast(v8bf, fa[(f + 0) * 64 + lane]);
+                const v8bf a1 = __builtin_bit_cast(v8bf, fa[(f + 1) * 64 + lane]);
+                const v8bf a2 = __builtin_bit_cast(v8bf, fa[(f + 2) * 64 + lane]);
+                const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    if constexpr (T == kQ6K) {
+                        v4f c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[i], zero, 0, 0, 0);
+                        v4f c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq1[i], zero, 0, 0, 0);
+                        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[i], c0, 0, 0, 0);
+                        c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq1[i], c1, 0, 0, 0);
+                        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bq[i], c0, 0, 0, 0);
+                        c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bq1[i], c1, 0, 0, 0);
+                        // scale index 2g and 2g + 1: bytes 2g, 2g + 1 of the 16 int8 scales
+                        const uint32_t scv[4] = {ring[s][i].sc.x, ring[s][i].sc.y, ring[s][i].sc.z, ring[s][i].sc.w};
+                        const uint32_t sw = scv[g >> 1] >> (16 * (g & 1));
+                        const float s0 = dd[i] * (float)(int8_t)(sw & 0xffu);
+                        const float s1 = dd[i] * (float)(int8_t)((sw >> 8) & 0xffu);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            acc[i][mt][t] = __builtin_fmaf(s1, c1[t], __builtin_fmaf(s0, c0[t], acc[i][mt][t]));
+                    } else {
+                        v4f c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[i], zero, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[i], c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bq[i], c, 0, 0, 0);
+                        const uint32_t scw = g < 4 ? scw_lo[i] : scw_hi[i];
+                        const float a_g = dd[i] * (float)((scw >> (8 * (g & 3))) & 0xffu);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) acc[i][mt][t] = __builtin_fmaf(a_g, c[t], acc[i][mt][t]);
+                    }
+                }
+            }
+            // one group's conversions and MFMA chains at a time (bounds the
+            // registers live across groups)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // ---- prologue: block sb0 in LDS slot 0, weights of sb0 and sb0 + 1
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    stage(S0{}, sb0);
+    fill_w(0, sb0);
+    fill_w(1, sb0 + 1);
+    __syncthreads();
+    // Pairs of blocks: the next block's fragments go to the other LDS slot
+    // (every wave finished reading it before the last barrier) ahead of the
+    // weights of the block after it, so the barrier's wait for the fragments
+    // leaves the weight loads in flight.
+    int b = sb0;
+    for (; b + 1 < sb1; b += 2) {
+        stage(S1{}, b + 1);
+        block(S0{});
+        fill_w(0, b + 2);
+        __syncthreads();
+        stage(S0{}, b + 2);
+        block(S1{});
+        fill_w(1, b + 3);
+        __syncthreads();
+    }
+    if (b < sb1) block(S0{});
+
+    // ---- epilogue: each wave owns its rows over the whole range
+    float v[R][MT][4];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[i][mt][t] = acc[i][mt][t] - macc[i][mt][t];
+    if (A.splits > 1) {
+        // raw row sums of this split ([split][member of the launch][vrow]);
+        // the reduce launch finishes them
+        const int vrows = PAIR ? 2 * A.rows_end[0] : A.total_rows;
+        const __amdgpu_buffer_rsrc_t pr =
+            make_rsrc(A.partial, (uint32_t)A.splits * (uint32_t)A.count_here * (uint32_t)vrows * 4u);
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int ml = 16 * mt + 4 * kq + t;  // member within the launch
+                    const bool ok = live_row[i] && ml < A.count_here;
+                    const uint32_t off =
+                        ok ? (uint32_t)(((int)blockIdx.y * A.count_here + ml) * vrows + vrow0[i] + rl) * 4u : kOOR;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[i][mt][t]), pr, (int)off, 0, 0);
+                }
+        return;
+    }
+    float inv[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            inv[mt][t] = 1.f;
+            const int mem = A.member0 + 16 * mt + 4 * kq + t;
+            if (A.has_norm && mem < A.members) {
+                const float* ssq = reinterpret_cast<const float*>(A.act + A.L.ssq);
+                float total = 0.f;
+                for (int p = 0; p < A.L.parts; ++p) total += ssq[mem * A.L.parts + p];
+                // RMSNorm (qwen_reference.rs:550-556): 1/sqrt(sum(x^2)/K + eps)
+                inv[mt][t] = 1.0f / sqrtf(total / (float)A.K + A.eps);
+            }
+        }
+    const bool accumulate = A.accumulate != 0;
+    auto put = [&](float value, __amdgpu_buffer_rsrc_t yr, uint32_t off) {
+        if (accumulate) {
+            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(value, yr, (int)off, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), yr, (int)off, 0, 0);
+        }
+    };
+    if constexpr (PAIR) {
+        const int ffn = A.rows_end[0];
+        const __amdgpu_buffer_rsrc_t yr = make_rsrc(A.y[0], (uint32_t)A.members * (uint32_t)ffn * 4u);
+#pragma unroll
+        for (int i = 0; i < R / 2; ++i)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int mem = A.member0 + 16 * mt + 4 * kq + t;
+                    const float gt = v[i][mt][t] * inv[mt][t];
+                    const float up = v[i + R / 2][mt][t] * inv[mt][t];
+                    // silu(gate) * up, in the reference's operation order (model_ops.rs:316-328)
+                    const float out = (gt / (1.0f + expf(-gt))) * up;
+                    const bool ok = live_row[i] && mem < A.members && 16 * mt + 4 * kq + t < A.count_here;
+                    put(out, yr, ok ? (uint32_t)(mem * ffn + local0[i] + rl) * 4u : kOOR);
+                }
+    } else {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int mm = mat[i];
+            float* y = A.y[0];
+#pragma unroll
+            for (int j = 1; j < kMaxGroup; ++j) {
+                if (mm == j) y = A.y[j];
+            }
+            const __amdgpu_buffer_rsrc_t yr = make_rsrc(y, (uint32_t)A.members * (uint32_t)rows_mat[i] * 4u);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int mem = A.member0 + 16 * mt + 4 * kq + t;
+                    const bool ok = live_row[i] && mem < A.members && 16 * mt + 4 * kq + t < A.count_here;
+                    put(v[i][mt][t] * inv[mt][t], yr, ok ? (uint32_t)(mem * rows_mat[i] + local0[i] + rl) * 4u : kOOR);
+                }
+        }
+    }
+}
+
+// Adds the splits' raw row sums in split order and applies the epilogue of
+// the one-split form (RMSNorm factor, SwiGLU pair, residual accumulate). One
+// thread per (member, output row).
+__global__ __launch_bounds__(256) void f32mma_reduce_kernel(F32MmaArgs A) {
+    const int pair = A.pair_swiglu;
+    const int rows = pair ? A.rows_end[0] : A.total_rows;
+    const int vrows = pair ? 2 * rows : A.total_rows;
+    const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (idx >= A.count_here * rows) return;
+    const int ml = idx / rows, row = idx - ml * rows;  // member within the launch
+    const int mem = A.member0 + ml;
+    float g = 0.f, u = 0.f;
+    for (int sp = 0; sp < A.splits; ++sp) {
+        const float* p = A.partial + ((size_t)sp * A.count_here + ml) * vrows;
+        g += p[row];
+        if (pair) u += p[rows + row];
+    }
+    float inv = 1.f;
+    if (A.has_norm) {
+        const float* ssq = reinterpret_cast<const float*>(A.act + A.L.ssq);
+        float total = 0.f;
+        for (int q = 0; q < A.L.parts; ++q) total += ssq[mem * A.L.parts + q];
+        // RMSNorm (qwen_reference.rs:550-556): 1/sqrt(sum(x^2)/K + eps)
+        inv = 1.0f / sqrtf(total / (float)A.K + A.eps);
+    }
+    float* y;
+    int local, rows_mat;
+    float out;
+    if (pair) {
+        const float gt = g * inv, up = u * inv;
+        // silu(gate) * up, in the reference's operation order (model_ops.rs:316-328)
+        out = (gt / (1.0f + expf(-gt))) * up;
+        y = A.y[0];
+        local = row;
+        rows_mat = rows;
+    } else {
+        int mm = 0, start = 0;
+        for (int j = 0; j + 1 < A.count; ++j) {
+            if (row >= A.rows_end[j]) {
+                mm = j + 1;
+                start = A.rows_end[j];
+            }
+        }
+        y = A.y[mm];
+        local = row - start;
+        rows_mat = A.rows_end[mm] - start;
+        out = g * inv;
+    }
+    float* dst = y + (size_t)mem * rows_mat + local;
+    if (A.accumulate) {
+        *dst += out;  // one thread per output: a plain read-modify-write
+    } else {
+        *dst = out;
+    }
+}
+
+// Row tiles per wave. Measured on MI355X at the Qwen3-8B FFN shapes (M = 16
+// and 32): two tiles run 10-20% faster than four, whose registers leave one
+// wave per SIMD.
+template <int T> constexpr int tiles_per_wave() { return 2; }
+// waves per workgroup (they share the LDS fragments): eight for one member
+// tile, four for two (whose registers allow one wave per SIMD)
+template <int MT> constexpr int waves_per_group() { return MT == 1 ? 8 : 4; }
+
+template <int T, int R, int MT, bool PAIR>
+hipError_t launch_shape(const F32MmaArgs& a, int groups, hipStream_t stream) {
+    constexpr int W = waves_per_group<MT>();
+    hipLaunchKernelGGL((f32mma_gemv_kernel<T, R, MT, PAIR, W>), dim3((unsigned)groups, (unsigned)a.splits),
+                       dim3(64 * W), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.splits == 1) return e;
+    const int rows = a.pair_swiglu ? a.rows_end[0] : a.total_rows;
+    const int threads = a.count_here * rows;
+    hipLaunchKernelGGL(f32mma_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+// Grid: row groups x K splits. A grid of row groups short of the CUs splits
+// K (at least two super-blocks per split, as far as the partial space
+// allows); the split depends on the shape and member count only, never on
+// the members' values.
+template <int T, int MT>
+hipError_t launch_mt(const F32MmaArgs& a0, size_t partial_bytes, int cu_count, hipStream_t stream) {
+    constexpr int R = tiles_per_wave<T>();
+    F32MmaArgs a = a0;
+    const int nb = a.K >> 8;
+    const bool pair = a.pair_swiglu != 0;
+    const int tiles = pair ? (a.rows_end[0] + 15) / 16 : (a.total_rows + 15) / 16;
+    const int per = waves_per_group<MT>() * (pair ? R / 2 : R);
+    const int groups = (tiles + per - 1) / per;
+    int splits = 1;
+    if (groups < cu_count) splits = std::min((cu_count + groups - 1) / groups, std::max(1, nb / 2));
+    const int vrows = pair ? 2 * a.rows_end[0] : a.total_rows;
+    const size_t split_bytes = (size_t)a.count_here * vrows * 4;
+    if (a.partial == nullptr) splits = 1;
+    else splits = std::max(1, std::min<int>(splits, (int)(partial_bytes / split_bytes)));
+    a.split_blocks = (nb + splits - 1) / splits;
+    a.splits = (nb + a.split_blocks - 1) / a.split_blocks;
+    if (pair) return launch_shape<T, R, MT, true>(a, groups, stream);
+    return launch_shape<T, R, MT, false>(a, groups, stream);
+}
+
+// One launch per 32 members (two member tiles: their fragments of a block,
+// double-buffered, fill 98 KB of LDS).
+template <int T>
+hipError_t launch_t(const F32MmaArgs& a, size_t partial_bytes, int cu_count, hipStream_t stream) {
+    for (int m0 = 0; m0 < a.members; m0 += 2 * 16) {
+        F32MmaArgs c = a;
+        c.member0 = m0;
+        c.count_here = std::min(2 * 16, a.members - m0);
+        const hipError_t e = c.count_here <= 16 ? launch_mt<T, 1>(c, partial_bytes, cu_count, stream)
+                                                : launch_mt<T, 2>(c, partial_bytes, cu_count, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+bool rows_tile_aligned(const WaveGemvArgs& a) {
+    if (a.pair_swiglu) return a.count == 2 && a.rows_end[1] == 2 * a.rows_end[0] && a.rows_end[0] % 16 == 0;
+    for (int i = 0; i + 1 < a.count; ++i) {
+        if (a.rows_end[i] % 16 != 0) return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+F32MmaLayout f32mma_layout(int members, int K) {
+    F32MmaLayout L{};
+    const int nb = K / 256;
+    L.nb = nb;
+    L.tiles = (members + 15) / 16;
+    L.parts = (nb + kPackBlocks - 1) / kPackBlocks;
+    const uint32_t blocks = (uint32_t)L.tiles * (uint32_t)nb;
+    L.frag = 0;
+    L.xsum = L.frag + blocks * kFragBlockBytes;
+    L.ssq = L.xsum + blocks * kXsumBlockBytes;
+    L.total = L.ssq + (uint32_t)members * (uint32_t)L.parts * 4u;
+    return L;
+}
+
+bool f32mma_supported(int value_type, const WaveGemvArgs& a) {
+    return (value_type == kQ4K || value_type == kQ5K || value_type == kQ6K) && a.members >= kF32MmaMinMembers &&
+           a.members <= kF32MmaMaxMembers && a.K >= 256 && a.K % 256 == 0 && a.K <= kWaveMaxK &&
+           (a.pair_swiglu == 0 || rows_tile_aligned(a)) && !(a.gamma != nullptr && a.x2 != nullptr);
+}
+
+hipError_t launch_gemv_f32mma(int value_type, const WaveGemvArgs& a, void* scratch, size_t scratch_bytes,
+                              int cu_count, hipStream_t stream) {
+    if (!f32mma_supported(value_type, a) || scratch == nullptr || a.count < 1 || a.count > kMaxGroup) {
+        return hipErrorInvalidValue;
+    }
+    const F32MmaLayout L = f32mma_layout(a.members, a.K);
+    if (L.total > scratch_bytes) return hipErrorInvalidValue;
+    PackArgs p{};
+    p.x = a.x;
+    p.x2 = a.x2;
+    p.gamma = a.gamma;
+    p.act = static_cast<uint8_t*>(scratch);
+    p.L = L;
+    p.K = a.K;
+    hipLaunchKernelGGL(pack_f32mma_kernel, dim3((unsigned)L.parts, (unsigned)a.members), dim3(64), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    F32MmaArgs m{};
+    for (int i = 0; i < kMaxGroup; ++i) {
+        m.w[i] = a.w[i];
+        m.wbytes[i] = a.wbytes[i];
+        m.y[i] = a.y[i];
+        m.rows_end[i] = a.rows_end[i];
+    }
+    m.count = a.count;
+    m.total_rows = a.total_rows;
+    m.act = static_cast<const uint8_t*>(scratch);
+    m.act_bytes = L.total;
+    m.L = L;
+    m.K = a.K;
+    m.members = a.members;
+    m.has_norm = a.gamma != nullptr ? 1 : 0;
+    m.eps = a.eps;
+    m.accumulate = a.accumulate;
+    m.pair_swiglu = a.pair_swiglu;
+    // split-K partials follow the packed activations in the scratch
+    const size_t part_off = ((size_t)L.total + 255) / 256 * 256;
+    m.partial = part_off < scratch_bytes ? reinterpret_cast<float*>(static_cast<uint8_t*>(scratch) + part_off) : nullptr;
+    const size_t part_bytes = part_off < scratch_bytes ? scratch_bytes - part_off : 0;
+    m.splits = 1;
+    m.split_blocks = a.K >> 8;
+    auto run = [&](const F32MmaArgs& args) -> hipError_t {
+        switch (value_type) {
+        case kQ4K: return launch_t<kQ4K>(args, part_bytes, cu_count, stream);
+        case kQ5K: return launch_t<kQ5K>(args, part_bytes, cu_count, stream);
+        case kQ6K: return launch_t<kQ6K>(args, part_bytes, cu_count, stream);
+        default: return hipErrorInvalidValue;
+        }
+    };
+    if (rows_tile_aligned(a)) return run(m);
+    // a group whose matrices do not end on whole tiles: one launch per matrix
+    // over the shared packed activations, each as its single-matrix call
+    for (int i = 0; i < a.count; ++i) {
+        F32MmaArgs one = m;
+        const int start = i > 0 ? a.rows_end[i - 1] : 0;
+        one.w[0] = a.w[i];
+        one.wbytes[0] = a.wbytes[i];
+        one.y[0] = a.y[i];
+        one.rows_end[0] = a.rows_end[i] - start;
+        one.total_rows = one.rows_end[0];
+        one.count = 1;
+        e = run(one);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace ribn_amd

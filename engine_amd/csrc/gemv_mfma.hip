@@ -697,13 +697,19 @@ hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& a, int /*cu_coun
 // GEMV or the slice totals of a split f32 launch (never both in one call).
 constexpr size_t kF32SplitScratchBytes = (size_t)2 << 20;
 size_t gemv_act_scratch_bytes() {
-    return std::max<size_t>(act16_layout(kMfmaMaxMembers, kWaveMaxK).total, kF32SplitScratchBytes);
+    const size_t f32mma = ((size_t)f32mma_layout(kF32MmaMaxMembers, kWaveMaxK).total + 255) / 256 * 256 +
+                          kF32MmaPartialBytes;
+    return std::max<size_t>(std::max<size_t>(act16_layout(kMfmaMaxMembers, kWaveMaxK).total, kF32SplitScratchBytes),
+                            f32mma);
 }
 
 int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith) {
     if (arith == kArithF32) {
         if (K < 256 || K > kWaveMaxK) return 0;
-        // launch_gemv splits larger calls into the launch groups each form stages
+        // the whole batch: launch_gemv takes 9..64 members to the matrix
+        // cores and splits smaller calls into the launch groups each wave
+        // form stages
+        if (gemv_mfma_supported(value_type) && K % 256 == 0) return kF32MmaMaxMembers;
         return swiglu_prologue ? kSwigluMaxMembers : kWaveMaxMembers;
     }
     if (!swiglu_prologue && gemv_mfma_supported(value_type) && K % 256 == 0 && K <= kWaveMaxK) {
@@ -716,6 +722,10 @@ int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith) 
 
 hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch, int cu_count, hipStream_t stream) {
     if (a.arith == kArithF32) {
+        if (act_scratch != nullptr && f32mma_supported(value_type, a) &&
+            f32mma_layout(a.members, a.K).total <= gemv_act_scratch_bytes()) {
+            return launch_gemv_f32mma(value_type, a, act_scratch, gemv_act_scratch_bytes(), cu_count, stream);
+        }
         // the f32 wave GEMV, in launch groups of as many members as it stages;
         // 3..8 members over a K of several slices split by slice when the
         // context scratch holds their slice totals

@@ -112,6 +112,37 @@ hipError_t launch_pack_act16(const float* x, const float* gamma, int members, in
                              hipStream_t stream);
 hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& args, int cu_count, hipStream_t stream);
 
+// ---- f32-faithful batched GEMV on the bf16 matrix cores (gemv_f32mma.hip)
+//
+// The default f32 arithmetic for 9..64 members: activations split exactly
+// into three bf16 pieces, quants exact in bf16, f32 accumulation, so results
+// agree with the f32 wave GEMV to f32 rounding (not bit for bit); the
+// weights are read once for the whole batch. Up to 8 members stay on the
+// wave GEMV, whose rows are bit-identical to the single-member call.
+constexpr int kF32MmaMinMembers = 9;
+constexpr int kF32MmaMaxMembers = 64;
+constexpr int kF32MmaMaxWaves = 4;  // K-split waves per workgroup
+// Byte offsets of the packed activations of `members` x K (K a multiple of
+// 256): bf16-piece MFMA fragments, f32 group sums, per-workgroup partial sums
+// of squares.
+struct F32MmaLayout {
+    uint32_t frag, xsum, ssq, total;
+    int nb;     // super-blocks of K
+    int tiles;  // member tiles of 16
+    int parts;  // pack workgroups per member
+};
+F32MmaLayout f32mma_layout(int members, int K);
+// Whether launch_gemv_f32mma serves this call (type, 9..64 members, K, pairs
+// of whole tiles, not both RMSNorm and SwiGLU prologues).
+bool f32mma_supported(int value_type, const WaveGemvArgs& args);
+// Split-K partial room a context keeps after the packed activations.
+constexpr size_t kF32MmaPartialBytes = (size_t)16 << 20;
+// Pack (RMSNorm or SwiGLU prologue fused) + product (+ an ordered split-K
+// reduce when the row groups alone do not fill the CUs); `scratch` holds
+// f32mma_layout(members, K).total bytes, then the partials.
+hipError_t launch_gemv_f32mma(int value_type, const WaveGemvArgs& args, void* scratch, size_t scratch_bytes,
+                              int cu_count, hipStream_t stream);
+
 // ---- Q8_1 activations and the integer-dot GEMV (q8_1.hip)
 
 constexpr int kQ8MaxMembers = 8;
@@ -127,7 +158,8 @@ hipError_t launch_gemv_q8_1(int value_type, const uint8_t* w, uint32_t wbytes, c
 size_t gemv_act_scratch_bytes();
 // Members one launch_gemv call may carry for this shape and arithmetic.
 int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith);
-// kArithF32: the f32 wave GEMV, split into the launch groups it stages.
+// kArithF32: 9..64 members on the bf16 matrix cores (launch_gemv_f32mma),
+// else the f32 wave GEMV, split into the launch groups it stages.
 // kArithFixed16: the block fixed-point wave GEMV, or from kMfmaMinMembers
 // (kMfmaMinMembersLongK for K spanning several slices) up to 16 members
 // without the SwiGLU prologue, packed activations through the matrix-core

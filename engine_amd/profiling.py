@@ -37,8 +37,10 @@ import sys
 from collections import defaultdict
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-# The decode GEMV's sources (the kernel the roofline and traffic figures are about).
-KERNEL_SOURCES = ("csrc/gemv_f32.hip", "csrc/wave_rows.hpp", "csrc/kquant_device.hpp", "csrc/kquant_launch.hpp")
+# The decode GEMV's sources (the kernel the roofline and traffic figures are
+# about), including the dispatcher that routes member counts to launch groups.
+KERNEL_SOURCES = ("csrc/gemv_f32.hip", "csrc/wave_rows.hpp", "csrc/kquant_device.hpp", "csrc/kquant_launch.hpp",
+                  "csrc/gemv_mfma.hip")
 
 
 def source_hash() -> str:

@@ -4,6 +4,14 @@ import numpy as np
 # Max relative error bound for GEMV/GEMM outputs against the f32-accumulated
 # oracle, measured normwise: max|y - ref| <= RTOL * max|ref|.
 RTOL = 1e-3
+# The bar of the f32 GEMV arithmetic on its own (the f32 wave GEMV on
+# wide-dynamic-range activations, and the f32-faithful matrix-core GEMV for
+# 9..64 members): normwise as RTOL.
+F32_RTOL = 5e-5
+# Batches up to this many members run the f32 wave GEMV, whose rows are
+# bit-identical to the single-member call (cuda_reference.rs:5322-5334);
+# larger ones run the f32-faithful matrix-core GEMV (within F32_RTOL).
+F32_BITWISE_MEMBERS = 8
 
 
 def mfma_path(t, k, members):

@@ -403,11 +403,12 @@ def test_batch_members_equal_single_sequences(env, members):
         pos = [p + 1 for p in pos]
 
 
-@pytest.mark.parametrize("members", [5, 8])
+@pytest.mark.parametrize("members", [5, 8, 12, 16, 33])
 def test_batch_step_matches_oracle(env, members):
-    """A batched decode step of 5 and 8 members (the batch sizes whose
-    projections took the matrix cores before GEMV_WARP) against the CPU
-    oracle's decode step per member, teacher-forced, at the 1e-3 bar."""
+    """A batched decode step of 5 and 8 members (the f32 wave GEMV) and of
+    12, 16 and 33 members (projections on the f32-faithful matrix-core GEMV)
+    against the CPU oracle's decode step per member, teacher-forced, at the
+    1e-3 bar."""
     print_case(test="batch_vs_oracle", members=members)
     E = env["E"]
     w = small_weights(TINY, 41 + members)
@@ -455,10 +456,12 @@ def test_prefill_chunk_equals_serial_prefill(env, chunk, mode):
     """A prefill chunk (consecutive tokens of one sequence as one step's
     members, K/V appended before attention) against serial prefill_step.
     GEMV_WARP (default): bit-equal caches and next-step logits at every chunk
-    size, including the reference's default chunk of 8 (serving.rs:357-371;
+    up to 8, the reference's default chunk (serving.rs:357-371;
     cuda_reference.rs:5322-5334: batched rows equal batch-1 rows bit for bit);
-    12 members run two launch groups. GEMV_FIXED16: within the GEMV bar where
-    the matrix cores serve the FFN down (4) or every GEMV (8)."""
+    a chunk of 12 runs the f32-faithful matrix-core GEMV, so its caches and
+    logits agree with serial prefill to f32 rounding (f16 cache values within
+    one rounding step, logits within 1e-4 normwise). GEMV_FIXED16: within the
+    GEMV bar where the matrix cores serve the FFN down (4) or every GEMV (8)."""
     print_case(test="prefill_chunk", chunk=chunk, mode=mode)
     E = env["E"]
     w = small_weights(TINY, 310)
@@ -482,11 +485,18 @@ def test_prefill_chunk_equals_serial_prefill(env, chunk, mode):
     lb = dec.copy_logits(0)
     ca = _cache_bytes(env, a, TINY["layers"], TINY["kv_heads"])
     cb = _cache_bytes(env, b, TINY["layers"], TINY["kv_heads"])
-    if mode == "warp":
+    if mode == "warp" and chunk <= 8:
         for x, y in zip(ca, cb):
             assert np.array_equal(x[:, :len(prompt)], y[:, :len(prompt)])
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
         assert sel_a == sel_b
+    elif mode == "warp":
+        for x, y in zip(ca, cb):
+            assert _f16_err(x[:, :len(prompt)], y[:, :len(prompt)]) <= 1e-3
+        assert max_rel_err(la, lb) <= 1e-4
+        top = np.sort(lb)[-2:]
+        if top[1] - top[0] > 4e-4 * np.abs(lb).max():
+            assert sel_a == sel_b
     else:
         for x, y in zip(ca, cb):
             assert _f16_err(x[:, :len(prompt)], y[:, :len(prompt)]) <= 4e-3
