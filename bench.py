@@ -761,22 +761,36 @@ def measured_traffic():
 
 
 def _cpu_model():
-    """`lscpu` model name of the host (falls back to /proc/cpuinfo)."""
+    """The host CPU as `lscpu` reports it: model name, vendor family / model /
+    stepping (identifying the part where a VM shortens the name, e.g. family 26
+    is AMD Zen 5, 25 Zen 3/4), sockets, cores, threads and L3. Falls back to
+    /proc/cpuinfo for the name."""
+    keys = {"Model name": "name", "Vendor ID": "vendor", "CPU family": "family", "Model": "model",
+            "Stepping": "stepping", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core", "L3": "l3", "L3 cache": "l3", "CPU max MHz": "max_mhz",
+            "Hypervisor vendor": "hypervisor"}
+    info = {}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
         for line in out.splitlines():
-            if line.startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in keys and keys[k] not in info and v.strip():
+                info[keys[k]] = v.strip()
     except (OSError, subprocess.SubprocessError):
         pass
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+    if "name" not in info:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        info["name"] = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    info.setdefault("name", "unknown")
+    info["cpus_usable"] = len(os.sched_getaffinity(0))
+    return info
 
 
 def main():

@@ -11,7 +11,10 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libribn_amd.so")
+# RIBN_AMD_LIBRARY names another build of the same ABI (the host-sanitized
+# test library of `python -m engine_amd.build --sanitize`); default: the
+# in-tree product library.
+LIB_PATH = os.environ.get("RIBN_AMD_LIBRARY") or os.path.join(HERE, "libribn_amd.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "ribn_amd.h")
 
 STATUS_NAMES = {

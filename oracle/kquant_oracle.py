@@ -1,6 +1,8 @@
 """ctypes front end of the CPU oracle -- TEST INFRASTRUCTURE ONLY.
 
-Loads oracle/build/libkquant_oracle.so (built by `make -C oracle`). Only tests/,
+Loads oracle/build/libkquant_oracle.so (built by `make -C oracle`), or the
+library KQUANT_ORACLE_LIBRARY names (the ASan + UBSan build of
+`make -C oracle asan`, for tests/test_sanitizers.py). Only tests/,
 __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module;
 the product package engine_amd never does.
 """
@@ -12,7 +14,7 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "build", "libkquant_oracle.so")
+LIB_PATH = os.environ.get("KQUANT_ORACLE_LIBRARY") or os.path.join(_HERE, "build", "libkquant_oracle.so")
 
 OK = 0
 UNSUPPORTED_TYPE = 1

@@ -163,3 +163,92 @@ def test_writer_round_trip(tmp_path):
             r = g.tensor_data_range(name)
             assert data[r.start:r.stop] == payload
             assert r.start % align == 0
+
+
+# Damaged files: every prefix of a well-formed file and seeded byte mutations
+# of its header and directory. Each must open cleanly or fail with a
+# GgufError; whatever opens is read back through every accessor. Run under
+# ASan + UBSan by tests/test_sanitizers.py, these are the parser's memory-safety
+# checks on untrusted input.
+
+def _rich_file() -> bytes:
+    rng = np.random.default_rng(7)
+    md = [("general.architecture", W.STRING, "qwen3"), ("u8", W.U8, 250), ("i16", W.I16, -30000),
+          ("u32", W.U32, 4_000_000_000), ("f32", W.F32, 1.5), ("b", W.BOOL, True), ("u64", W.U64, 2 ** 60),
+          ("f64", W.F64, -2.25), ("s", W.STRING, "héllo"), ("strs", W.ARRAY, (W.STRING, ["a", "bc", ""])),
+          ("nested", W.ARRAY, (W.ARRAY, [(W.I32, [1, -2]), (W.STRING, ["x"])])),
+          ("fl", W.ARRAY, (W.F32, [0.5, -1.0]))]
+    payloads = [("blk.0.w", [256, 3], 12, rng.integers(0, 256, 3 * 144, dtype=np.uint8).tobytes()),
+                ("blk.0.n", [256], 0, W.f32_payload(rng.standard_normal(256))),
+                ("blk.1.w", [512, 2], 14, rng.integers(0, 256, 2 * 2 * 210, dtype=np.uint8).tobytes())]
+    return W.build(md, payloads, alignment=64)
+
+
+def _read_all(g) -> None:
+    g.version()
+    g.tensor_data_offset()
+    g.metadata_map()
+    for t in g.tensors():
+        try:
+            g.tensor_data_range(t.name)
+        except E().GgufError:
+            pass
+        g.tensor(t.name)
+    g.close()
+
+
+def _open_or_error(path, data: bytes):
+    path.write_bytes(data)
+    try:
+        g = E().GgufFile.open(str(path))
+    except E().GgufError as e:
+        return e.kind
+    _read_all(g)
+    return None
+
+
+def test_rich_file_opens_and_nested_arrays_read_back(tmp_path):
+    data = _rich_file()
+    g = open_bytes(tmp_path, data)
+    assert g.metadata("nested") == [[1, -2], ["x"]]
+    assert len(g.tensors()) == 3
+    _read_all(g)
+
+
+def test_every_truncation_fails_cleanly(tmp_path):
+    data = _rich_file()
+    g = open_bytes(tmp_path, data, "whole.gguf")
+    data_start = g.tensor_data_offset()
+    g.close()
+    p = tmp_path / "cut.gguf"
+    kinds = {}
+    for n in range(len(data)):
+        kind = _open_or_error(p, data[:n])
+        if n < data_start:
+            # header, metadata and directory are all required
+            assert kind is not None, n
+        kinds[kind] = kinds.get(kind, 0) + 1
+    assert _open_or_error(p, data) is None
+    assert {"Io", "Truncated"} & set(kinds), kinds
+
+
+def test_mutated_headers_and_directories_fail_cleanly(tmp_path):
+    data = _rich_file()
+    g = open_bytes(tmp_path, data, "whole.gguf")
+    data_start = g.tensor_data_offset()
+    g.close()
+    rng = np.random.default_rng(2024)
+    p = tmp_path / "mut.gguf"
+    failures = 0
+    for i in range(1500):
+        b = bytearray(data)
+        if i % 3 == 0:
+            # one 8-byte field overwritten with a large or boundary count
+            pos = int(rng.integers(4, data_start - 8))
+            v = [2 ** 64 - 1, 2 ** 63, 2 ** 32, 2 ** 32 - 1, 0x7FFF_FFFF, 17, 0][int(rng.integers(7))]
+            b[pos:pos + 8] = struct.pack("<Q", v)
+        else:
+            for _ in range(int(rng.integers(1, 5))):
+                b[int(rng.integers(4, data_start))] = int(rng.integers(0, 256))
+        failures += _open_or_error(p, bytes(b)) is not None
+    assert failures > 100  # the mutations reach the parser's checks

@@ -72,3 +72,29 @@ def test_decode_steps_end_at_the_final_selection_launch(tmp_path):
     _write_trace(tmp_path / "x_kernel_trace.csv", rows)
     (w,) = P.decode_steps_summary(str(tmp_path), steps=1)
     assert w["argmax_grid"] == 64 and w["dispatches"] == 3 and w["busy_us"] == 3.0
+
+
+def test_resource_remarks_parse():
+    """The build's resource report reads the compiler's kernel-resource-usage
+    remarks (engine_amd/build.py --resource-report)."""
+    from engine_amd import build as B
+    tag = " [-Rpass-analysis=kernel-resource-usage]"
+    text = "\n".join([
+        "engine_amd/csrc/q8_1.hip:39:1: remark: Function Name: _ZN8ribn_amd4kernEv" + tag,
+        "   39 |   uint32_t blocks) {",
+        "engine_amd/csrc/q8_1.hip:39:1: remark:     TotalSGPRs: 16" + tag,
+        "engine_amd/csrc/q8_1.hip:39:1: remark:     VGPRs: 14" + tag,
+        "engine_amd/csrc/q8_1.hip:39:1: remark:     AGPRs: 0" + tag,
+        "engine_amd/csrc/q8_1.hip:39:1: remark:     ScratchSize [bytes/lane]: 8" + tag,
+        "engine_amd/csrc/q8_1.hip:39:1: remark:     Occupancy [waves/SIMD]: 8" + tag,
+        "engine_amd/csrc/q8_1.hip:39:1: remark:     SGPRs Spill: 0" + tag,
+        "engine_amd/csrc/q8_1.hip:39:1: remark:     VGPRs Spill: 2" + tag,
+        "engine_amd/csrc/q8_1.hip:39:1: remark:     LDS Size [bytes/block]: 4096" + tag,
+        "engine_amd/csrc/q8_1.hip:90:1: remark: Function Name: _ZN8ribn_amd5otherEv" + tag,
+        "engine_amd/csrc/q8_1.hip:90:1: remark:     VGPRs: 40" + tag,
+    ])
+    k = B.parse_resource_remarks(text)
+    assert k[0] == {"source": "q8_1.hip", "kernel": "_ZN8ribn_amd4kernEv", "sgpr": 16, "vgpr": 14, "agpr": 0,
+                    "scratch": 8, "occupancy": 8, "sgpr_spill": 0, "vgpr_spill": 2, "lds": 4096}
+    assert k[1] == {"source": "q8_1.hip", "kernel": "_ZN8ribn_amd5otherEv", "vgpr": 40}
+    assert B._short_name("void ribn_amd::(anonymous namespace)::k<1, (x)2>(ribn_amd::A)") == "k<1, (x)2>"
