@@ -256,22 +256,34 @@ def build_decoder(E, synth, torch, ctx, step, out_gamma, layers, seed, members):
     return dec, cfg
 
 
-def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed):
+def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed, prompt_chunk=512):
     """Prefills `context` prompt tokens per member, then times `gen_tokens`
     greedy steps of the graph-replayed generation loop (wall clock, which
     includes the step's host work). Member m's prompt depends on the seed and
-    m only, so member 0 has the same prompt at every batch size. Returns the
-    result line, the generated tokens and member 0's last logits."""
+    m only, so member 0 has the same prompt at every batch size. The first
+    context - 1 tokens of each prompt run through prefill_prompt (the prefill
+    matmul, chunks of `prompt_chunk`; timed with the workspace already
+    reserved, `prompt_tok_s` = prompt tokens per second over all members),
+    or with prompt_chunk = 0 as serial single-token steps (the reference's
+    prefill_step). Returns the result line, the generated tokens and member
+    0's last logits."""
     import numpy as np
     rng = np.random.default_rng(seed)
     prompts = rng.integers(0, VOCAB, size=(8, context))[:members]
     caches = [E.AmdKvCache(ctx, cfg, context + gen_tokens) for _ in range(members)]
+    if prompt_chunk:
+        dec.reserve_prompt(prompt_chunk)
+    ctx.synchronize()
     t0 = time.perf_counter()
-    for p in range(context - 1):
-        if members == 1:
-            dec.prefill_step(caches[0], int(prompts[0, p]), p)
-        else:
-            dec.decode_step_batch(caches, prompts[:, p], [p] * members)
+    if prompt_chunk:
+        for m in range(members):
+            dec.prefill_prompt(caches[m], prompts[m, :context - 1], 0, prompt_chunk)
+    else:
+        for p in range(context - 1):
+            if members == 1:
+                dec.prefill_step(caches[0], int(prompts[0, p]), p)
+            else:
+                dec.decode_step_batch(caches, prompts[:, p], [p] * members)
     ctx.synchronize()
     prefill_s = time.perf_counter() - t0
     last = prompts[:, context - 1]
@@ -283,7 +295,8 @@ def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed):
     kv_read = sum((context + s) * KV_BYTES_PER_TOKEN * cfg.layers // 36 for s in range(gen_tokens)) / gen_tokens
     line = {"members": members, "context": context, "generated": gen_tokens,
             "tok_s": round(members * gen_tokens / dt, 1), "ms_per_step": round(dt * 1e3 / gen_tokens, 4),
-            "prefill_s": round(prefill_s, 2), "kv_bytes_per_step": int(kv_read * members),
+            "prefill_s": round(prefill_s, 3), "prompt_chunk": prompt_chunk,
+            "prompt_tok_s": round(members * (context - 1) / prefill_s, 1), "kv_bytes_per_step": int(kv_read * members),
             "distinct_tokens": int(len(set(out.reshape(-1).tolist())))}
     return line, out, dec.copy_logits(0)
 
@@ -297,9 +310,10 @@ def model_decode_results(E, synth, torch, ctx, step, out_gamma, args):
     dec, cfg = build_decoder(E, synth, torch, ctx, step, out_gamma, args.layers, args.seed, 8)
     res, runs = {}, {}
     for members in (1, 8):
-        r, toks, logits = time_model_decode(E, dec, cfg, ctx, members, args.context, args.gen_tokens, args.seed)
+        r, toks, logits = time_model_decode(E, dec, cfg, ctx, members, args.context, args.gen_tokens, args.seed,
+                                            args.prompt_chunk)
         log(f"bench model: batch {members}: {r['tok_s']} tok/s ({r['ms_per_step']} ms/step, "
-            f"prefill {r['prefill_s']} s)")
+            f"prompt {r['prompt_tok_s']} tok/s in {r['prefill_s']} s)")
         res[members] = r
         runs[members] = (toks[0], logits)
     res["b8_member0_bitwise_equal_b1"] = bool(np.array_equal(runs[1][0], runs[8][0]) and
@@ -814,6 +828,8 @@ def main():
                          "open + staging of a Qwen3-8B-shaped file (--layers layers)")
     ap.add_argument("--context", type=int, default=2048, help="config 4: prompt tokens before generation")
     ap.add_argument("--gen-tokens", type=int, default=128, help="config 4: greedy tokens timed")
+    ap.add_argument("--prompt-chunk", type=int, default=512,
+                    help="config 4: prompt tokens per prefill-matmul chunk (0: serial single-token prefill)")
     ap.add_argument("--no-model", action="store_true", help="skip the config-4 full-decoder measurement")
     ap.add_argument("--concurrency", type=int, default=8, help="serving: requests in the burst")
     ap.add_argument("--prompt-tokens", type=int, default=257, help="serving: prompt tokens per request")

@@ -15,7 +15,7 @@ from .kquant import (  # noqa: F401
     validate_quantized_geometry,
 )
 from .gguf import GgufError, GgufFile, TensorInfo, load_qwen3_decode, qwen3_config_from_gguf  # noqa: F401
-from .qwen3 import AmdKvCache, AmdQwen3Config, AmdQwen3Decode, QWEN3_8B, attention_decode  # noqa: F401
+from .qwen3 import AmdKvCache, AmdQwen3Config, AmdQwen3Decode, QWEN3_8B, attention_decode, attention_prefill  # noqa: F401
 from .serving import AmdBackend, AmdDispatcher, AmdServingDispatcher, BackendError, plan_memory  # noqa: F401
 
 __all__ = [

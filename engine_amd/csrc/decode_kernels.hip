@@ -560,6 +560,242 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const uint2* part, int
     }
 }
 
+// ------------------------------------------------------------ prompt prefill
+//
+// kv_append_seq_kernel: the K/V of a prompt chunk's tokens, as kv_append_kernel
+// computes them for one token (K RMSNorm + rope, f16 round to nearest even),
+// at positions p0 + t. Grid (KV head, token).
+__global__ __launch_bounds__(128) void kv_append_seq_kernel(PrefillAttnArgs a) {
+    const int kvh = blockIdx.x;
+    const int t = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const float* src = (wave == 0 ? a.k : a.v) + ((size_t)t * a.kv_heads + kvh) * kHeadDim;
+    float x0 = src[lane];
+    float x1 = src[lane + 64];
+    const int pos = a.p0 + t;
+    if (wave == 0) {
+        norm_rope(x0, x1, a.k_norm[lane], a.k_norm[lane + 64], a.eps, rope_rot((float)pos, rope_freq(a.rope_base, lane)));
+    }
+    const size_t head_elems = (size_t)a.mem.capacity * kHeadDim;
+    uint16_t* dst = (wave == 0 ? a.mem.keys : a.mem.values) + (size_t)a.layer * a.mem.layer_elems +
+                    (size_t)kvh * head_elems + (size_t)pos * kHeadDim;
+    dst[lane] = __builtin_bit_cast(uint16_t, (_Float16)x0);
+    dst[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16)x1);
+}
+
+// attn_prefill_kernel: causal attention of a prompt chunk on the matrix cores
+// (v_mfma_f32_16x16x32_f16, f32 accumulation), after kv_append_seq_kernel
+// stored the chunk's K/V. Token t (position p0 + t) attends positions
+// 0 .. p0 + t: the reference's attention (model_ops.rs:430-566) for every
+// token of the chunk, as the serial prefill computes it one token at a time.
+//
+// A wave owns one query head and kPrefillTileTokens tokens; a workgroup holds
+// the QPK query heads of one KV head (and, for QPK < 4, 4 / QPK token tiles),
+// so every K/V byte it stages serves all of them. Keys advance in blocks of
+// 64 through LDS (K as [key][dim], V transposed to [dim][key]); the next
+// block's loads are in flight while a block is reduced.
+//
+// Per block and wave, with S^T = K Q^T (M = 16 keys, N = 16 tokens, K = 128
+// dims in 4 steps) the MFMA output puts token l%16 in lane l's column and keys
+// 4(l/16)+i in its rows, so the online softmax state of a token lives in its
+// four lanes (l%16 + 16g): maxima and denominators combine across them with
+// two lane exchanges. The probabilities, rounded to f16, are already the B
+// operand of O^T += V^T P^T (M = 16 dims, K = 32 keys): a dot product does not
+// depend on the order of its terms, so key slot 8g+j of a 32-key step is key
+// 16(j/4) + 4g + (j%4), and the A operand (V^T) reads the same keys.
+// Scores are scaled by log2(e)/sqrt(128) in f32 after the product. q is
+// normalised and roped in f32 (the decode kernel's operations) and enters the
+// products as two f16 pieces, hi = f16(q) and lo = f16(q - hi), and so do the
+// f32 probabilities: each product is two MFMAs and carries 22 significant
+// bits of the f32 operand (K and V are the cache's f16 values, exact), so the
+// attention follows the f32 reference to accumulation-order rounding.
+typedef _Float16 pf_half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pf_half4 __attribute__((ext_vector_type(4)));
+typedef float pf_float4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPfKeys = 64;              // keys per block
+constexpr int kPfKRow = kHeadDim + 8;    // LDS K row (halfs): 272 B
+constexpr int kPfVRow = kPfKeys + 8;     // LDS V^T row (halfs): 144 B
+
+template <int QPK>
+__global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(PrefillAttnArgs a) {
+    constexpr int W = QPK < 4 ? 4 : QPK;  // waves
+    constexpr int NT = 64 * W;
+    constexpr int TT = W / QPK;           // token tiles per workgroup
+    constexpr int PIECES = kPfKeys * (kHeadDim / 8) / NT;  // 16-byte K (and V) pieces per thread and block
+    __shared__ __attribute__((aligned(16))) _Float16 ks[kPfKeys][kPfKRow];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[kHeadDim][kPfVRow];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kvh = blockIdx.y;
+    const int hq = kvh * QPK + wave % QPK;
+    const int t0 = ((int)blockIdx.x * TT + wave / QPK) * kPrefillTileTokens;
+    const int tl = lane & 15;
+    const int g = lane >> 4;
+    const int t = t0 + tl;
+    const bool live = t < a.tokens;
+    const int pos = a.p0 + t;
+    const int qdim = a.q_heads * kHeadDim;
+    // the last position any token of the workgroup attends
+    const int wg_end = min(((int)blockIdx.x + 1) * TT * kPrefillTileTokens, a.tokens);
+    const int last = a.p0 + wg_end - 1;
+
+    // ---- K/V block loads (positions past `last` read as zero)
+    const size_t head_elems = (size_t)a.mem.capacity * kHeadDim;
+    const size_t base = (size_t)a.layer * a.mem.layer_elems + (size_t)kvh * head_elems;
+    const uint32_t span = (uint32_t)(last + 1) * (uint32_t)(kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.mem.keys + base, span);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.mem.values + base, span);
+    uint4 kp[PIECES], vp[PIECES];
+    auto issue = [&](int kb) {
+#pragma unroll
+        for (int r = 0; r < PIECES; ++r) {
+            const int idx = tid + NT * r;
+            const uint32_t off = ((uint32_t)(kb * kPfKeys + (idx >> 4)) * kHeadDim + 8u * (uint32_t)(idx & 15)) * 2u;
+            kp[r] = load_b128(kr, off);
+            vp[r] = load_b128(vr, off);
+        }
+    };
+    issue(0);
+
+    // ---- this lane's query dims 32s + 8g + j (s = 0..3, j = 0..7): RMSNorm
+    // over the head's 128 dims (the four lanes of the token add their parts),
+    // NEOX rope of the pairs (d, d + 64) = (s, s + 2), f16
+    float x[4][8];
+    const float* qrow = a.q + (size_t)t * qdim + (size_t)hq * kHeadDim;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int d = 32 * s + 8 * g;
+        float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
+        if (live) {
+            lo = *reinterpret_cast<const float4*>(qrow + d);
+            hi = *reinterpret_cast<const float4*>(qrow + d + 4);
+        }
+        x[s][0] = lo.x; x[s][1] = lo.y; x[s][2] = lo.z; x[s][3] = lo.w;
+        x[s][4] = hi.x; x[s][5] = hi.y; x[s][6] = hi.z; x[s][7] = hi.w;
+    }
+    float ssq = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ssq = __builtin_fmaf(x[s][j], x[s][j], ssq);
+    ssq += __shfl_xor(ssq, 16, 64);
+    ssq += __shfl_xor(ssq, 32, 64);
+    const float inv = 1.0f / sqrtf(ssq / (float)kHeadDim + a.eps);
+    pf_half8 qb[4], ql[4];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int d = 32 * s + 8 * g + j;
+            const float y0 = x[s][j] * inv * a.q_norm[d];
+            const float y1 = x[s + 2][j] * inv * a.q_norm[d + 64];
+            const Rot r = rope_rot((float)pos, rope_freq(a.rope_base, d));
+            const float q0 = y0 * r.c - y1 * r.s;
+            const float q1 = y0 * r.s + y1 * r.c;
+            qb[s][j] = (_Float16)q0;
+            ql[s][j] = (_Float16)(q0 - (float)qb[s][j]);
+            qb[s + 2][j] = (_Float16)q1;
+            ql[s + 2][j] = (_Float16)(q1 - (float)qb[s + 2][j]);
+        }
+    }
+
+    // ---- online softmax over the key blocks
+    float m_run = -FLT_MAX, l_run = 0.f;
+    pf_float4 o[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[d] = pf_float4{0.f, 0.f, 0.f, 0.f};
+    const int blocks = last / kPfKeys + 1;
+    for (int kb = 0; kb < blocks; ++kb) {
+#pragma unroll
+        for (int r = 0; r < PIECES; ++r) {
+            const int idx = tid + NT * r;
+            const int key = idx >> 4, c = idx & 15;
+            *reinterpret_cast<uint4*>(&ks[key][8 * c]) = kp[r];
+            const uint32_t w[4] = {vp[r].x, vp[r].y, vp[r].z, vp[r].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                vt[8 * c + 2 * j][key] = __builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffffu));
+                vt[8 * c + 2 * j + 1][key] = __builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
+            }
+        }
+        __syncthreads();
+        if (kb + 1 < blocks) issue(kb + 1);
+
+        // S^T for the block's four 16-key tiles
+        pf_float4 sc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            sc[kt] = pf_float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const pf_half8 ka = *reinterpret_cast<const pf_half8*>(&ks[16 * kt + tl][32 * s + 8 * g]);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sc[kt], 0, 0, 0);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[s], sc[kt], 0, 0, 0);
+            }
+        }
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kb * kPfKeys + 16 * kt + 4 * g + i;
+                const float v = key <= pos ? sc[kt][i] * a.scale : -INFINITY;
+                sc[kt][i] = v;
+                bmax = fmaxf(bmax, v);
+            }
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        const float m_new = fmaxf(m_run, bmax);
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= corr;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) o[d] *= corr;
+        pf_half8 pb[2], pl[2];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pv = __builtin_amdgcn_exp2f(sc[kt][i] - m_new);
+                l_run += pv;
+                const _Float16 ph = (_Float16)pv;
+                pb[kt >> 1][4 * (kt & 1) + i] = ph;
+                pl[kt >> 1][4 * (kt & 1) + i] = (_Float16)(pv - (float)ph);
+            }
+        }
+        // O^T += V^T P^T over the block's two 32-key steps
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const _Float16* row = &vt[16 * d + tl][32 * u + 4 * g];
+                const pf_half4 v0 = *reinterpret_cast<const pf_half4*>(row);
+                const pf_half4 v1 = *reinterpret_cast<const pf_half4*>(row + 16);
+                const pf_half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[u], o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[u], o[d], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- the token's denominator over its four lanes, then O / l
+    float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+    if (!live) return;
+    float* dst = a.out + (size_t)t * qdim + (size_t)hq * kHeadDim + 4 * g;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        *reinterpret_cast<float4*>(dst + 16 * d) =
+            make_float4(o[d][0] / l_tot, o[d][1] / l_tot, o[d][2] / l_tot, o[d][3] / l_tot);
+    }
+}
+
 }  // namespace
 
 size_t attn_partials_floats(int q_heads) { return (size_t)q_heads * kAttnChunks * kPartStride; }
@@ -600,6 +836,27 @@ hipError_t launch_kv_append(const AttnArgs& args, int members, hipStream_t strea
     }
     hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)args.kv_heads, (unsigned)members), dim3(128), 0, stream,
                        args);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream) {
+    if (a.tokens < 1 || a.kv_heads < 1 || a.q_heads % a.kv_heads != 0 || a.p0 < 0 ||
+        (long long)a.p0 + a.tokens > a.mem.capacity || a.mem.keys == nullptr || a.mem.values == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(kv_append_seq_kernel, dim3((unsigned)a.kv_heads, (unsigned)a.tokens), dim3(128), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.out == nullptr) return e;
+    const int qpk = a.q_heads / a.kv_heads;
+    const int tile = kPrefillTileTokens * (qpk < 4 ? 4 / qpk : 1);
+    const dim3 grid((unsigned)((a.tokens + tile - 1) / tile), (unsigned)a.kv_heads);
+    switch (qpk) {
+    case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(256), 0, stream, a); break;
+    case 8: hipLaunchKernelGGL(attn_prefill_kernel<8>, grid, dim3(512), 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -87,6 +87,34 @@ struct StepInputs {
 };
 hipError_t launch_step_inputs(const StepInputs& in, hipStream_t stream);
 
+// Prompt prefill: `tokens` consecutive tokens of one sequence at positions
+// p0 .. p0 + tokens - 1, their q/k/v projections computed for the whole chunk.
+struct PrefillAttnArgs {
+    AttnMember mem;        // the sequence's cache (partials unused)
+    int layer;
+    int p0;                // position of the chunk's first token
+    int tokens;            // tokens in the chunk
+    const float* q;        // [tokens][q_heads * 128], raw projection
+    const float* k;        // [tokens][kv_heads * 128]
+    const float* v;
+    const float* q_norm;   // [128]
+    const float* k_norm;
+    float* out;            // [tokens][q_heads * 128]; null: K/V append only
+    int q_heads;
+    int kv_heads;
+    float eps;
+    float rope_base;
+    float scale;           // log2(e) / sqrt(head_dim)
+};
+
+// Tokens one prompt-attention workgroup tile covers per query head.
+constexpr int kPrefillTileTokens = 16;
+
+// The chunk's K (RMSNorm + rope) and V stored as f16 at their positions, then
+// (when `out` is set) causal attention of every token over positions
+// 0 .. its own on the matrix cores. q_heads / kv_heads in {1, 2, 4, 8}.
+hipError_t launch_prefill_attention(const PrefillAttnArgs& args, hipStream_t stream);
+
 // Slice results a two-stage greedy selection keeps per member.
 constexpr int kArgmaxSlices = 64;
 

@@ -196,6 +196,13 @@ hipError_t launch_act_f16(bool bf16_in, const void* x, const float* gamma, float
                           hipStream_t stream);
 hipError_t launch_qgemm(int value_type, const uint8_t* w, uint32_t wbytes, void* workspace, size_t workspace_bytes,
                         float* y, int M, int N, int K, int cu_count, hipStream_t stream);
+// Activation stages of the decoder's prompt prefill (f32 [M][K], K a multiple
+// of 8): x += r (stored back to x), then RMSNorm with gamma, into the f16
+// workspace; or silu(gate) * up into it.
+hipError_t launch_act_f16_residual(float* x, const float* r, const float* gamma, float eps, int M, int K,
+                                   void* workspace, hipStream_t stream);
+hipError_t launch_act_f16_swiglu(const float* gate, const float* up, int M, int K, void* workspace,
+                                 hipStream_t stream);
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* y, int length, int members, float eps,
                            hipStream_t stream);

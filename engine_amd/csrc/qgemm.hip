@@ -44,6 +44,9 @@ typedef float float2_v __attribute__((ext_vector_type(2)));
 typedef float float16_v __attribute__((ext_vector_type(16)));
 
 constexpr int kActThreads = 256;
+constexpr int kActPlain = 0;   // activation prologues of act_f16_kernel
+constexpr int kActAdd = 1;
+constexpr int kActSwiglu = 2;
 constexpr int kStepK = 128;                                // K per pipeline step (half a super-block)
 constexpr int kXRow = kStepK + 8;                          // padded LDS row (halfs): 272 B, bank-conflict free
 constexpr uint32_t kGemmOutOfRange = 0xffffff00u;
@@ -69,10 +72,14 @@ __device__ __forceinline__ float block_max_256(float v, float* red) {
     return t;
 }
 
-template <bool BF16_IN, bool NORM>
+// PRO selects a prologue on f32 inputs (the decoder's prompt prefill):
+// kActAdd adds r into x first and stores the sum back to x (the residual
+// stream), kActSwiglu stages silu(x) * r (model_ops.rs:316-328).
+template <bool BF16_IN, bool NORM, int PRO = kActPlain>
 __global__ __launch_bounds__(kActThreads) void act_f16_kernel(const void* __restrict__ xin,
                                                                const float* __restrict__ gamma, float eps, int K,
-                                                               _Float16* __restrict__ xh, float* __restrict__ unscale) {
+                                                               _Float16* __restrict__ xh, float* __restrict__ unscale,
+                                                               const float* __restrict__ r = nullptr) {
     // Thread t owns chunks of 8 consecutive elements, 8*(t + 256c): one
     // 16-byte load (bf16) or two (f32) in, one 16-byte f16 store out.
     constexpr int kChunks = kGemmMaxK / 8 / kActThreads;  // 8
@@ -96,6 +103,25 @@ __global__ __launch_bounds__(kActThreads) void act_f16_kernel(const void* __rest
                 const float4 a = src[0], b = src[1];
                 v[c][0] = a.x; v[c][1] = a.y; v[c][2] = a.z; v[c][3] = a.w;
                 v[c][4] = b.x; v[c][5] = b.y; v[c][6] = b.z; v[c][7] = b.w;
+                if constexpr (PRO != kActPlain) {
+                    const float4* rs = reinterpret_cast<const float4*>(r + (size_t)m * K + e);
+                    const float4 ra = rs[0], rb = rs[1];
+                    const float rv[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        if constexpr (PRO == kActAdd) {
+                            v[c][j] = v[c][j] + rv[j];
+                        } else {
+                            v[c][j] = (v[c][j] / (1.0f + expf(-v[c][j]))) * rv[j];
+                        }
+                    }
+                    if constexpr (PRO == kActAdd) {
+                        float4* out = reinterpret_cast<float4*>(const_cast<float*>(static_cast<const float*>(xin)) +
+                                                                (size_t)m * K + e);
+                        out[0] = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+                        out[1] = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+                    }
+                }
             }
         } else {
 #pragma unroll
@@ -903,6 +929,26 @@ size_t gemm_workspace_bytes(size_t tokens, size_t K, size_t N) {
     // f16 activations, one f32 unscale per token, and room for kMaxSplits
     // partial [tokens][N] tiles (split K)
     return align256(tokens * K * 2) + align256(tokens * 4) + align256((size_t)kMaxSplits * tokens * N * 4);
+}
+
+hipError_t launch_act_f16_residual(float* x, const float* r, const float* gamma, float eps, int M, int K,
+                                   void* workspace, hipStream_t stream) {
+    if (M < 1 || K < 8 || K > kGemmMaxK || K % 8 != 0 || r == nullptr || gamma == nullptr) return hipErrorInvalidValue;
+    _Float16* xh = static_cast<_Float16*>(workspace);
+    float* us = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + align256((size_t)M * K * 2));
+    hipLaunchKernelGGL((act_f16_kernel<false, true, kActAdd>), dim3(M), dim3(kActThreads), 0, stream, x, gamma, eps,
+                       K, xh, us, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_act_f16_swiglu(const float* gate, const float* up, int M, int K, void* workspace,
+                                 hipStream_t stream) {
+    if (M < 1 || K < 8 || K > kGemmMaxK || K % 8 != 0 || up == nullptr) return hipErrorInvalidValue;
+    _Float16* xh = static_cast<_Float16*>(workspace);
+    float* us = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + align256((size_t)M * K * 2));
+    hipLaunchKernelGGL((act_f16_kernel<false, false, kActSwiglu>), dim3(M), dim3(kActThreads), 0, stream, gate,
+                       nullptr, 0.f, K, xh, us, up);
+    return hipGetLastError();
 }
 
 hipError_t launch_act_f16(bool bf16_in, const void* x, const float* gamma, float eps, int M, int K, void* workspace,

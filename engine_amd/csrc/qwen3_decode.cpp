@@ -157,6 +157,22 @@ struct ribn_amd_qwen3_decode {
     bool graphs;
     uint32_t gemv_mode;   // RIBN_AMD_GEMV_WARP (f32 activations) or RIBN_AMD_GEMV_FIXED16
     std::vector<GraphEntry> graph_cache;
+    // Prompt prefill on the prefill matmul (ribn_amd_qwen3_prefill_prompt):
+    // one allocation for chunks of up to prompt_tokens tokens, grown on demand.
+    void* prompt_block;
+    size_t prompt_bytes;
+    uint32_t prompt_tokens;
+    uint32_t* p_tokens;   // [chunk] token ids
+    float* p_hidden;      // [chunk][hidden] residual stream
+    float* p_q;           // [chunk][q_heads*128]
+    float* p_k;           // [chunk][kv_heads*128]
+    float* p_v;
+    float* p_attn;        // [chunk][q_heads*128]
+    float* p_gate;        // [chunk][ffn]
+    float* p_up;
+    float* p_y;           // [chunk][hidden] o / down projection, added by the next activation stage
+    void* p_gemm;         // f16 activations, unscales and split-K partials of the prefill matmul
+    size_t p_gemm_bytes;
 };
 
 namespace {
@@ -453,6 +469,137 @@ ribn_amd_status upload_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* 
     return ok();
 }
 
+// Prompt workspace for chunks of `tokens` tokens (grows, never shrinks;
+// synchronises the context stream when it replaces the block).
+ribn_amd_status reserve_prompt(ribn_amd_qwen3_decode* d, uint32_t tokens) {
+    if (d->prompt_block != nullptr && d->prompt_tokens >= tokens) return ok();
+    const ribn_amd_qwen3_config& c = d->cfg;
+    const size_t T = tokens;
+    const size_t qdim = (size_t)c.q_heads * c.head_dim, kvdim = (size_t)c.kv_heads * c.head_dim;
+    const size_t max_k = std::max<size_t>({c.hidden, qdim, c.ffn});
+    const size_t max_n = std::max<size_t>({c.hidden, qdim, c.ffn});
+    const size_t f32_counts[8] = {T * c.hidden, T * qdim, T * kvdim, T * kvdim, T * qdim, T * c.ffn, T * c.ffn,
+                                  T * c.hidden};
+    size_t bytes = align_up(T * sizeof(uint32_t));
+    size_t offsets[8];
+    for (int i = 0; i < 8; ++i) {
+        offsets[i] = bytes;
+        bytes += align_up(f32_counts[i] * sizeof(float));
+    }
+    const size_t gemm_offset = bytes;
+    // activations at the widest K, and split-K room for two partial tiles
+    const size_t gemm_bytes = ribn_amd::gemm_workspace_bytes(T, max_k, 0) + align_up(2 * T * max_n * sizeof(float));
+    bytes += gemm_bytes;
+    hipError_t e = hipStreamSynchronize(d->ctx->stream);
+    if (e != hipSuccess) return driver(e, "synchronize before replacing the prompt workspace");
+    if (d->prompt_block != nullptr) {
+        hipFree(d->prompt_block);
+        d->prompt_block = nullptr;
+        d->prompt_tokens = 0;
+    }
+    void* block = nullptr;
+    e = hipMalloc(&block, bytes);
+    if (e != hipSuccess) return driver(e, "hipMalloc prompt workspace");
+    char* p = static_cast<char*>(block);
+    d->prompt_block = block;
+    d->prompt_bytes = bytes;
+    d->prompt_tokens = tokens;
+    d->p_tokens = reinterpret_cast<uint32_t*>(p);
+    float** f32s[8] = {&d->p_hidden, &d->p_q, &d->p_k, &d->p_v, &d->p_attn, &d->p_gate, &d->p_up, &d->p_y};
+    for (int i = 0; i < 8; ++i) *f32s[i] = reinterpret_cast<float*>(p + offsets[i]);
+    d->p_gemm = p + gemm_offset;
+    d->p_gemm_bytes = gemm_bytes;
+    return ok();
+}
+
+// One prefill-matmul projection of the prompt chunk: y[T][N] = x W^T from the
+// f16 activations the last activation stage left in the workspace.
+hipError_t prompt_gemm(ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight* w, float* y, int tokens,
+                       hipStream_t stream) {
+    return ribn_amd::launch_qgemm((int)w->value_type, w->data, (uint32_t)w->encoded_bytes, d->p_gemm, d->p_gemm_bytes,
+                                  y, tokens, (int)w->output_size, (int)w->input_size, d->ctx->cu_count, stream);
+}
+
+// The launches of one prompt chunk: `tokens` tokens at positions p0.. of
+// `cache`, their ids already in p_tokens.
+hipError_t enqueue_prompt_chunk(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* cache, int tokens, int p0,
+                                hipStream_t stream) {
+    const ribn_amd_qwen3_config& c = d->cfg;
+    const int qdim = (int)(c.q_heads * c.head_dim);
+    hipError_t e = ribn_amd::launch_embedding((int)d->token_embd->value_type, d->token_embd->data,
+                                              (uint32_t)d->token_embd->encoded_bytes, d->p_tokens, 0, d->p_hidden,
+                                              c.hidden / 256, c.vocab, (uint32_t)tokens, stream);
+    for (uint32_t l = 0; l < c.layers && e == hipSuccess; ++l) {
+        const ribn_amd_qwen3_layer& L = d->layers[l];
+        // The last layer's attention output, o projection and FFN reach no
+        // cache (there is no output head here): only its K/V are computed.
+        const bool last = l + 1 == c.layers;
+        e = l == 0 ? ribn_amd::launch_act_f16(false, d->p_hidden, L.attn_norm, c.epsilon, tokens, (int)c.hidden,
+                                              d->p_gemm, stream)
+                   : ribn_amd::launch_act_f16_residual(d->p_hidden, d->p_y, L.attn_norm, c.epsilon, tokens,
+                                                       (int)c.hidden, d->p_gemm, stream);
+        if (e == hipSuccess && !last) e = prompt_gemm(d, L.attn_q, d->p_q, tokens, stream);
+        if (e == hipSuccess) e = prompt_gemm(d, L.attn_k, d->p_k, tokens, stream);
+        if (e == hipSuccess) e = prompt_gemm(d, L.attn_v, d->p_v, tokens, stream);
+        if (e != hipSuccess) break;
+        ribn_amd::PrefillAttnArgs a{};
+        a.mem = descriptor(cache, nullptr);
+        a.layer = (int)l;
+        a.p0 = p0;
+        a.tokens = tokens;
+        a.q = d->p_q;
+        a.k = d->p_k;
+        a.v = d->p_v;
+        a.q_norm = L.attn_q_norm;
+        a.k_norm = L.attn_k_norm;
+        a.out = last ? nullptr : d->p_attn;
+        a.q_heads = (int)c.q_heads;
+        a.kv_heads = (int)c.kv_heads;
+        a.eps = c.epsilon;
+        a.rope_base = c.rope_base;
+        a.scale = 1.4426950408889634f / sqrtf((float)c.head_dim);
+        e = ribn_amd::launch_prefill_attention(a, stream);
+        if (e != hipSuccess || last) break;
+        e = ribn_amd::launch_act_f16(false, d->p_attn, nullptr, 0.f, tokens, qdim, d->p_gemm, stream);
+        if (e == hipSuccess) e = prompt_gemm(d, L.attn_output, d->p_y, tokens, stream);
+        if (e == hipSuccess) {
+            e = ribn_amd::launch_act_f16_residual(d->p_hidden, d->p_y, L.ffn_norm, c.epsilon, tokens, (int)c.hidden,
+                                                  d->p_gemm, stream);
+        }
+        if (e == hipSuccess) e = prompt_gemm(d, L.ffn_gate, d->p_gate, tokens, stream);
+        if (e == hipSuccess) e = prompt_gemm(d, L.ffn_up, d->p_up, tokens, stream);
+        if (e == hipSuccess) e = ribn_amd::launch_act_f16_swiglu(d->p_gate, d->p_up, tokens, (int)c.ffn, d->p_gemm, stream);
+        if (e == hipSuccess) e = prompt_gemm(d, L.ffn_down, d->p_y, tokens, stream);
+    }
+    return e;
+}
+
+constexpr uint32_t kPromptChunkDefault = 512;
+constexpr uint32_t kPromptChunkMin = 16;
+constexpr uint32_t kPromptChunkMax = 2048;
+
+ribn_amd_status check_prompt_chunk(uint32_t chunk) {
+    if (chunk < kPromptChunkMin || chunk > kPromptChunkMax) {
+        return fail(RIBN_AMD_INVALID_ARGUMENT, kPromptChunkMax, chunk, "prompt chunks take %u..%u tokens, not %u",
+                    kPromptChunkMin, kPromptChunkMax, chunk);
+    }
+    return RIBN_AMD_OK;
+}
+
+// Dimensions the prefill matmul serves (K up to kGemmMaxK, multiples of 256).
+ribn_amd_status check_prompt_geometry(const ribn_amd_qwen3_config& c) {
+    const uint64_t qdim = (uint64_t)c.q_heads * c.head_dim;
+    const uint64_t ks[3] = {c.hidden, qdim, c.ffn};
+    for (uint64_t k : ks) {
+        if (k > (uint64_t)ribn_amd::kGemmMaxK || k % 256 != 0) {
+            return fail(RIBN_AMD_INVALID_PLAN, ribn_amd::kGemmMaxK, k,
+                        "the prompt prefill matmul takes K <= %d in whole super-blocks, not %llu", ribn_amd::kGemmMaxK,
+                        (unsigned long long)k);
+        }
+    }
+    return RIBN_AMD_OK;
+}
+
 }  // namespace
 
 namespace ribn_amd_decode {
@@ -568,6 +715,58 @@ ribn_amd_status ribn_amd_kv_cache_layer(ribn_amd_kv_cache* cache, uint32_t layer
     *keys = cache->keys + (size_t)layer * cache->layer_elems;
     *values = cache->values + (size_t)layer * cache->layer_elems;
     return ok();
+}
+
+ribn_amd_status ribn_amd_attention_prefill(ribn_amd_context* ctx, const ribn_amd_qwen3_config* config,
+                                           ribn_amd_kv_cache* cache, uint32_t layer, const float* q, const float* k,
+                                           const float* v, const float* q_norm, const float* k_norm, size_t tokens,
+                                           uint32_t position, float* output, size_t output_len) {
+    if (!ctx || !cache) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    ribn_amd_status st = check_config(config);
+    if (st != RIBN_AMD_OK) return st;
+    const void* ptrs[6] = {q, k, v, q_norm, k_norm, output};
+    const char* names[6] = {"q", "k", "v", "q_norm", "k_norm", "output"};
+    for (int i = 0; i < 6; ++i) {
+        st = check_device_ptr(ctx, ptrs[i], names[i], 16);
+        if (st != RIBN_AMD_OK) return st;
+    }
+    if (cache->device != ctx->device) {
+        return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)ctx->device, (uint64_t)cache->device,
+                    "the cache lives on device %d", cache->device);
+    }
+    if (!same_geometry(cache->cfg, *config) || layer >= cache->cfg.layers) {
+        return fail(RIBN_AMD_INVALID_PLAN, cache->cfg.layers, layer, "the cache does not hold layer %u", layer);
+    }
+    if (tokens == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "a prompt chunk needs at least one token");
+    if ((uint64_t)position + tokens > cache->capacity) {
+        return fail(RIBN_AMD_POSITION_OVERFLOW, cache->capacity, (uint64_t)position + tokens - 1,
+                    "token position %llu exceeds KV capacity %u", (unsigned long long)position + tokens - 1,
+                    cache->capacity);
+    }
+    const size_t want = tokens * config->q_heads * config->head_dim;
+    if (output_len != want) {
+        return fail(RIBN_AMD_OUTPUT_LENGTH, want, output_len, "attention output has %zu values, expected %zu",
+                    output_len, want);
+    }
+    DeviceGuard guard(ctx->device);
+    ribn_amd::PrefillAttnArgs a{};
+    a.mem = descriptor(cache, nullptr);
+    a.layer = (int)layer;
+    a.p0 = (int)position;
+    a.tokens = (int)tokens;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.out = output;
+    a.q_heads = (int)config->q_heads;
+    a.kv_heads = (int)config->kv_heads;
+    a.eps = config->epsilon;
+    a.rope_base = config->rope_base;
+    a.scale = 1.4426950408889634f / sqrtf((float)config->head_dim);
+    hipError_t e = ribn_amd::launch_prefill_attention(a, ctx->stream);
+    return e == hipSuccess ? ok() : driver(e, "prompt attention launch");
 }
 
 ribn_amd_status ribn_amd_attention_decode(ribn_amd_context* ctx, const ribn_amd_qwen3_config* config,
@@ -777,6 +976,7 @@ void ribn_amd_qwen3_decode_destroy(ribn_amd_qwen3_decode* d) {
     hipStreamDestroy(d->capture);
     hipFree(d->history);
     hipFree(d->block);
+    if (d->prompt_block) hipFree(d->prompt_block);
     ribn_amd_context* ctx = d->ctx;
     delete d;
     context_release(ctx);
@@ -847,6 +1047,58 @@ ribn_amd_status ribn_amd_qwen3_prefill_step(ribn_amd_qwen3_decode* d, ribn_amd_k
 ribn_amd_status ribn_amd_qwen3_prefill_chunk(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* cache,
                                              const uint32_t* tokens, size_t count, uint32_t position) {
     return ribn_amd_decode::enqueue_prefill_chunk(d, cache, tokens, count, position);
+}
+
+ribn_amd_status ribn_amd_qwen3_reserve_prompt(ribn_amd_qwen3_decode* d, uint32_t chunk_tokens) {
+    if (!d) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null decoder");
+    if (chunk_tokens == 0) chunk_tokens = kPromptChunkDefault;
+    ribn_amd_status st = check_prompt_chunk(chunk_tokens);
+    if (st == RIBN_AMD_OK) st = check_prompt_geometry(d->cfg);
+    if (st != RIBN_AMD_OK) return st;
+    DeviceGuard guard(d->ctx->device);
+    return reserve_prompt(d, chunk_tokens);
+}
+
+ribn_amd_status ribn_amd_qwen3_prefill_prompt(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* cache,
+                                              const uint32_t* tokens, size_t count, uint32_t position,
+                                              uint32_t chunk_tokens) {
+    if (!d || !cache || !tokens) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null argument");
+    if (count == 0) return fail(RIBN_AMD_INPUT_LENGTH, 1, 0, "a prompt prefill needs at least one token");
+    if (chunk_tokens == 0) chunk_tokens = kPromptChunkDefault;
+    ribn_amd_status st = check_prompt_chunk(chunk_tokens);
+    if (st == RIBN_AMD_OK) st = check_prompt_geometry(d->cfg);
+    if (st != RIBN_AMD_OK) return st;
+    if (cache->device != d->ctx->device) {
+        return fail(RIBN_AMD_CONTEXT_MISMATCH, (uint64_t)d->ctx->device, (uint64_t)cache->device,
+                    "the cache lives on device %d", cache->device);
+    }
+    if (!same_geometry(cache->cfg, d->cfg)) {
+        return fail(RIBN_AMD_INVALID_PLAN, 0, 0, "the cache has another layer or head geometry");
+    }
+    if ((uint64_t)position + count > cache->capacity) {
+        return fail(RIBN_AMD_POSITION_OVERFLOW, cache->capacity, (uint64_t)position + count - 1,
+                    "token position %llu exceeds KV capacity %u", (unsigned long long)position + count - 1,
+                    cache->capacity);
+    }
+    for (size_t i = 0; i < count; ++i) {
+        if (tokens[i] >= d->cfg.vocab) {
+            return fail(RIBN_AMD_INVALID_PLAN, d->cfg.vocab, tokens[i], "token %u is outside vocabulary %u",
+                        tokens[i], d->cfg.vocab);
+        }
+    }
+    DeviceGuard guard(d->ctx->device);
+    const uint32_t chunk = (uint32_t)std::min<size_t>(chunk_tokens, count);
+    st = reserve_prompt(d, chunk);
+    if (st != RIBN_AMD_OK) return st;
+    hipStream_t stream = d->ctx->stream;
+    for (size_t c0 = 0; c0 < count; c0 += chunk) {
+        const int n = (int)std::min<size_t>(chunk, count - c0);
+        hipError_t e = hipMemcpyAsync(d->p_tokens, tokens + c0, (size_t)n * sizeof(uint32_t), hipMemcpyHostToDevice,
+                                      stream);
+        if (e == hipSuccess) e = enqueue_prompt_chunk(d, cache, n, (int)(position + c0), stream);
+        if (e != hipSuccess) return driver(e, "prompt prefill chunk");
+    }
+    return ok();
 }
 
 ribn_amd_status ribn_amd_qwen3_generate(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* caches,

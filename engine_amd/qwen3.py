@@ -89,6 +89,16 @@ def attention_decode(ctx, config: AmdQwen3Config, caches, layer: int, q, k, v, q
                                               _ptr(output), output.numel()), AmdModelKernelError)
 
 
+def attention_prefill(ctx, config: AmdQwen3Config, cache, layer: int, q, k, v, q_norm, k_norm, tokens: int,
+                      position: int, output):
+    """One layer's causal attention for a prompt chunk of `tokens` tokens at
+    `position` (the K/V appended first)."""
+    cfg = config.to_c()
+    _check(ctx._lib.ribn_amd_attention_prefill(ctx.handle, ctypes.byref(cfg), cache.handle, layer, _ptr(q), _ptr(k),
+                                               _ptr(v), _ptr(q_norm), _ptr(k_norm), tokens, position, _ptr(output),
+                                               output.numel()), AmdModelKernelError)
+
+
 class AmdQwen3Decode:
     """Decode-step executor (CudaQwen35Decode + CudaQwen35BatchDecode).
 
@@ -139,6 +149,22 @@ class AmdQwen3Decode:
         tok = (ctypes.c_uint32 * n)(*[int(t) for t in tokens])
         _check(self.ctx._lib.ribn_amd_qwen3_prefill_chunk(self.handle, cache.handle, tok, n, position),
                AmdModelKernelError)
+
+    def prefill_prompt(self, cache: AmdKvCache, tokens, position: int, chunk_tokens: int = 0):
+        """A whole prompt (consecutive tokens of one sequence from `position`)
+        on the prefill matmul, in chunks of `chunk_tokens` (0: 512): the
+        projections as matmuls over the chunk, causal chunk attention on the
+        matrix cores, K/V written to the cache, no output head. Stands where
+        the reference runs run_prefill_chunk (decode.rs:2149-2267)."""
+        import numpy as np
+        tok = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
+        ptr = tok.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+        _check(self.ctx._lib.ribn_amd_qwen3_prefill_prompt(self.handle, cache.handle, ptr, tok.size, position,
+                                                           chunk_tokens), AmdModelKernelError)
+
+    def reserve_prompt(self, chunk_tokens: int = 0):
+        """Allocates the prompt workspace for chunks of `chunk_tokens` tokens ahead of prefill_prompt."""
+        _check(self.ctx._lib.ribn_amd_qwen3_reserve_prompt(self.handle, chunk_tokens), AmdModelKernelError)
 
     def decode_step(self, cache: AmdKvCache, token: int, position: int) -> int:
         out = ctypes.c_uint32()

@@ -23,8 +23,9 @@ def _f16_bits(values: np.ndarray) -> np.ndarray:
     return values.astype(np.float16).view(np.uint16)  # round-to-nearest-even
 
 
-def kquant_numpy(value_type: int, k: int, n: int, seed: int) -> np.ndarray:
-    """[n rows x k/256 blocks] encoded tensor as a flat uint8 array (numpy generator)."""
+def kquant_numpy(value_type: int, k: int, n: int, seed: int, centered: bool = False) -> np.ndarray:
+    """[n rows x k/256 blocks] encoded tensor as a flat uint8 array (numpy
+    generator). centered: as kquant_torch's (zero-mean Q4_K / Q5_K weights)."""
     if k % 256:
         raise ValueError("k must be a multiple of 256")
     rng = np.random.default_rng(seed)
@@ -34,6 +35,8 @@ def kquant_numpy(value_type: int, k: int, n: int, seed: int) -> np.ndarray:
     if value_type in (Q4_K, Q5_K):
         d = _f16_bits(rng.uniform(0.001, 0.02, size=nb))
         dmin = _f16_bits(rng.uniform(0.001, 0.02, size=nb))
+        if centered:
+            dmin = _f16_bits(d.view(np.float16).astype(np.float32) * _MEAN_Q[value_type])
         blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         blocks[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
     else:

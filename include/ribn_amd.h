@@ -547,6 +547,20 @@ ribn_amd_status ribn_amd_attention_decode(ribn_amd_context *ctx, const ribn_amd_
                                           const float *k_norm, const int32_t *positions, float *output,
                                           size_t output_len);
 
+/* One layer's attention for a prompt chunk of one sequence, as the reference's
+ * full_attention_layer_prefill_chunk runs it (decode.rs:2508-2640): the K
+ * (per-head RMSNorm + NEOX rope) and V of `tokens` consecutive tokens stored
+ * as f16 at positions position .. position + tokens - 1 first, then token t
+ * attends positions 0 .. position + t. q is [tokens][q_heads*128], k and v
+ * [tokens][kv_heads*128] (raw projections), output [tokens][q_heads*128].
+ * The attention runs on the matrix cores, q and the probabilities each as
+ * two f16 pieces (22 significant bits), K / V f16, f32 sums; the prompt
+ * prefill's attention. */
+ribn_amd_status ribn_amd_attention_prefill(ribn_amd_context *ctx, const ribn_amd_qwen3_config *config,
+                                           ribn_amd_kv_cache *cache, uint32_t layer, const float *q, const float *k,
+                                           const float *v, const float *q_norm, const float *k_norm, size_t tokens,
+                                           uint32_t position, float *output, size_t output_len);
+
 /* CudaQwen35Ops::argmax_into / argmax_into_batch (model_ops.rs:1583-1674):
  * selected[m] = the first index of the largest non-NaN value of
  * logits[m*length .. (m+1)*length) (device u32 array), 0 when every value is
@@ -591,6 +605,29 @@ ribn_amd_status ribn_amd_qwen3_prefill_step(ribn_amd_qwen3_decode *decode, ribn_
  * from 5 members (matrix cores). Stream-ordered. */
 ribn_amd_status ribn_amd_qwen3_prefill_chunk(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
                                              const uint32_t *tokens, size_t count, uint32_t position);
+/* Prompt prefill on the prefill matmul. It stands where the reference runs
+ * run_prefill_chunk (decode.rs:2149-2267: the prompt's projections through
+ * gemv_batch, `members` tokens at a time) and takes whole prompts: `count`
+ * consecutive tokens of one sequence at positions position ..
+ * position + count - 1, in chunks of up to `chunk_tokens` (16..2048; 0 means
+ * 512). Per chunk every projection runs on ribn_amd_gemm_prefill's kernels
+ * over all its tokens (f16 MFMA, f32 accumulation), attention is causal over
+ * the cache on the matrix cores (ribn_amd_attention_prefill's arithmetic),
+ * and the chunk's K/V are written to the cache; no
+ * output head. The cache then matches the serial prefill_step sequence's
+ * within the prefill matmul's tolerance (not bit for bit). Needs K <= 16384
+ * for every projection. The workspace for `chunk_tokens` is allocated on the
+ * first call (or by ribn_amd_qwen3_reserve_prompt) and grown when a call
+ * needs more, synchronising the context stream then; otherwise
+ * stream-ordered. Tokens are read from host memory before the call returns. */
+ribn_amd_status ribn_amd_qwen3_prefill_prompt(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
+                                              const uint32_t *tokens, size_t count, uint32_t position,
+                                              uint32_t chunk_tokens);
+/* Allocates (grows) the prompt workspace for chunks of `chunk_tokens` tokens
+ * (0 means 512) ahead of ribn_amd_qwen3_prefill_prompt. No reference
+ * counterpart (the reference sizes its batch scratch at construction,
+ * decode.rs:1582-1617). */
+ribn_amd_status ribn_amd_qwen3_reserve_prompt(ribn_amd_qwen3_decode *decode, uint32_t chunk_tokens);
 /* CudaQwen35Decode::decode_step (decode.rs:508-516): one forward pass and the
  * greedy token (blocking, as the reference). */
 ribn_amd_status ribn_amd_qwen3_decode_step(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,

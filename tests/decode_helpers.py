@@ -7,8 +7,9 @@ SMALL = dict(layers=2, hidden=512, q_heads=4, kv_heads=2, head_dim=128, ffn=768,
              rope_base=1.0e6, epsilon=1.0e-6)
 
 
-def small_weights(cfg, seed, types=None):
-    """Seeded model tensors; types maps tensor kind -> GGML type."""
+def small_weights(cfg, seed, types=None, centered=False):
+    """Seeded model tensors; types maps tensor kind -> GGML type; centered:
+    zero-mean Q4_K / Q5_K weights (synth.kquant_numpy)."""
     types = types or {}
     h, f, q, kv = cfg["hidden"], cfg["ffn"], cfg["q_heads"] * 128, cfg["kv_heads"] * 128
     w = {}
@@ -17,7 +18,7 @@ def small_weights(cfg, seed, types=None):
     def add(name, t, k, n):
         nonlocal s
         s += 1
-        w[name] = (t, k, n, synth.kquant_numpy(t, k, n, s))
+        w[name] = (t, k, n, synth.kquant_numpy(t, k, n, s, centered))
 
     add("token_embd", types.get("token_embd", 12), h, cfg["vocab"])
     add("output", types.get("output", 14), h, cfg["vocab"])
