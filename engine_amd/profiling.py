@@ -4,6 +4,7 @@
     python -m engine_amd.profiling pmc <dir-or-counter_collection.csv> [--copy-bytes N]
     python -m engine_amd.profiling source-hash
     python -m engine_amd.profiling decode-steps <dir-or-kernel_trace.csv> [--steps N]
+    python -m engine_amd.profiling prompt <dir-or-kernel_trace.csv> [--prompts N]
 
 `trace` groups dispatches by (kernel, grid size), since one kernel instance can
 serve launches of different shapes (the q/k/v and gate/up groups share one),
@@ -21,6 +22,11 @@ a trace of the decoder: a step ends with its greedy-selection dispatch
 in traces of the one-launch form), whose grid tells the batch sizes apart. Per kernel and
 grid it prints launches per step, mean duration and time per step, and per
 batch size the span and busy time of the window.
+
+`prompt` summarises the prompt-prefill dispatches of a trace (the prefill
+matmul, its activation stages, the chunk K/V append and the chunk attention:
+kernels no decode step launches) per kernel and grid: launches, mean duration
+and time per prompt (`--prompts N`: the trace holds N prompt prefills).
 
 `source-hash` prints the hash of the decode GEMV's sources, recorded in
 profile summaries so a stale measurement is recognisable.
@@ -149,6 +155,23 @@ def decode_steps_summary(path: str, steps: int = 32) -> list[dict]:
     return out
 
 
+# Kernels only the prompt prefill launches (ribn_amd_qwen3_prefill_prompt).
+PROMPT_KERNELS = ("act_f16_kernel", "qgemm", "attn_prefill_kernel", "kv_append_seq_kernel")
+
+
+def prompt_summary(path: str, prompts: int = 1) -> dict:
+    """Prompt-prefill kernels per (kernel, grid): launches per prompt, mean
+    duration and time per prompt, plus their busy time per prompt."""
+    groups: dict[tuple, list[int]] = defaultdict(list)
+    for name, grid, t0, t1 in _dispatches(path):
+        if name.startswith(PROMPT_KERNELS):
+            groups[(name, grid)].append(t1 - t0)
+    kernels = sorted(((k[0], k[1], len(v) / prompts, statistics.mean(v) / 1e3, sum(v) / prompts / 1e3)
+                      for k, v in groups.items()), key=lambda r: -r[4])
+    busy = sum(r[4] for r in kernels)
+    return {"prompts": prompts, "busy_us": busy, "kernels": kernels}
+
+
 def pmc_summary(path: str) -> dict[tuple, dict[str, float]]:
     """{(kernel, grid): {counter: mean value per dispatch}}."""
     acc: dict[tuple, dict[str, list[float]]] = defaultdict(lambda: defaultdict(list))
@@ -172,7 +195,7 @@ def copy_scale(summary: dict, counter: str, copy_bytes: int) -> float | None:
 
 
 def _main(argv: list[str]) -> int:
-    if not argv or argv[0] not in ("trace", "pmc", "source-hash", "decode-steps"):
+    if not argv or argv[0] not in ("trace", "pmc", "source-hash", "decode-steps", "prompt"):
         print(__doc__)
         return 2
     if argv[0] == "source-hash":
@@ -186,6 +209,14 @@ def _main(argv: list[str]) -> int:
             print(f"{'kernel':60s} {'grid':>9s} {'per_step':>8s} {'mean_us':>9s} {'us/step':>9s}")
             for name, grid, n, mean, per in w["kernels"]:
                 print(f"{name:60s} {grid:9d} {n:8.1f} {mean:9.3f} {per:9.1f}")
+        return 0
+    if argv[0] == "prompt":
+        prompts = int(argv[argv.index("--prompts") + 1]) if "--prompts" in argv else 1
+        w = prompt_summary(argv[1], prompts)
+        print(f"== {w['prompts']} prompt(s): prompt-prefill kernels busy {w['busy_us']:.1f} us per prompt")
+        print(f"{'kernel':66s} {'grid':>9s} {'n/prompt':>8s} {'mean_us':>9s} {'us/prompt':>10s} {'share':>6s}")
+        for name, grid, n, mean, per in w["kernels"]:
+            print(f"{name:66s} {grid:9d} {n:8.1f} {mean:9.3f} {per:10.1f} {per / w['busy_us']:6.1%}")
         return 0
     if argv[0] == "trace":
         match = argv[2] if len(argv) > 2 else ""

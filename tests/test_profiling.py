@@ -98,3 +98,24 @@ def test_resource_remarks_parse():
                     "scratch": 8, "occupancy": 8, "sgpr_spill": 0, "vgpr_spill": 2, "lds": 4096}
     assert k[1] == {"source": "q8_1.hip", "kernel": "_ZN8ribn_amd5otherEv", "vgpr": 40}
     assert B._short_name("void ribn_amd::(anonymous namespace)::k<1, (x)2>(ribn_amd::A)") == "k<1, (x)2>"
+
+
+def test_prompt_summary_keeps_prompt_kernels_only(tmp_path):
+    # two prompts of (act 1 us, qgemm 10 us, attention 4 us), with decode
+    # kernels around them that the summary leaves out
+    rows, t = [], 0
+    for _ in range(2):
+        for name, dur in (("void ribn_amd::act_f16_kernel<false, true, 0>(void const*)", 1000),
+                          ("void ribn_amd::qgemm_tile_kernel<12, 3, 8>(int)", 10000),
+                          ("void ribn_amd::(anonymous namespace)::attn_prefill_kernel<4>(ribn_amd::PrefillAttnArgs)",
+                           4000),
+                          ("void ribn_amd::gemv_f32_kernel<12>(int)", 3000)):
+            rows.append((name, (256, 1, 1), t, t + dur))
+            t += dur + 100
+    f = tmp_path / "run_kernel_trace.csv"
+    _write_trace(f, rows)
+    w = P.prompt_summary(str(tmp_path), prompts=2)
+    names = [k[0] for k in w["kernels"]]
+    assert names == ["qgemm_tile_kernel<12, 3, 8>", "attn_prefill_kernel<4>", "act_f16_kernel<false, true, 0>"]
+    assert w["kernels"][0][2:] == (1.0, 10.0, 10.0)
+    assert abs(w["busy_us"] - 15.0) < 1e-9
