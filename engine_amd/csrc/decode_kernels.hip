@@ -593,8 +593,11 @@ __global__ __launch_bounds__(128) void kv_append_seq_kernel(PrefillAttnArgs a) {
 // A wave owns one query head and kPrefillTileTokens tokens; a workgroup holds
 // the QPK query heads of one KV head (and, for QPK < 4, 4 / QPK token tiles),
 // so every K/V byte it stages serves all of them. Keys advance in blocks of
-// 64 through LDS (K as [key][dim], V transposed to [dim][key]); the next
-// block's loads are in flight while a block is reduced.
+// 64 through double-buffered LDS (K as [key][dim], V transposed to
+// [dim][key]): a block's global loads are issued before the previous block is
+// reduced and written to the other buffer after it, one barrier per block.
+// V is transposed in registers: a thread loads four consecutive keys of 8
+// dims and stores 8-byte rows of V^T.
 //
 // Per block and wave, with S^T = K Q^T (M = 16 keys, N = 16 tokens, K = 128
 // dims in 4 steps) the MFMA output puts token l%16 in lane l's column and keys
@@ -623,9 +626,10 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
     constexpr int W = QPK < 4 ? 4 : QPK;  // waves
     constexpr int NT = 64 * W;
     constexpr int TT = W / QPK;           // token tiles per workgroup
-    constexpr int PIECES = kPfKeys * (kHeadDim / 8) / NT;  // 16-byte K (and V) pieces per thread and block
-    __shared__ __attribute__((aligned(16))) _Float16 ks[kPfKeys][kPfKRow];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[kHeadDim][kPfVRow];
+    constexpr int KP = kPfKeys * (kHeadDim / 8) / NT;  // 16-byte K pieces per thread and block
+    // V: 256 units of 4 keys x 8 dims, one per thread of the first 256
+    __shared__ __attribute__((aligned(16))) _Float16 ks[2][kPfKeys][kPfKRow];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][kHeadDim][kPfVRow];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -649,14 +653,39 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
     const uint32_t span = (uint32_t)(last + 1) * (uint32_t)(kHeadDim * 2);
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.mem.keys + base, span);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.mem.values + base, span);
-    uint4 kp[PIECES], vp[PIECES];
+    const bool v_unit = tid < 256;
+    const int va = tid & 15;        // V unit: keys 4va .. 4va + 3
+    const int vc = (tid >> 4) & 15; // dims 8vc .. 8vc + 7
+    uint4 kp[KP], vp[4];
     auto issue = [&](int kb) {
 #pragma unroll
-        for (int r = 0; r < PIECES; ++r) {
+        for (int r = 0; r < KP; ++r) {
             const int idx = tid + NT * r;
-            const uint32_t off = ((uint32_t)(kb * kPfKeys + (idx >> 4)) * kHeadDim + 8u * (uint32_t)(idx & 15)) * 2u;
-            kp[r] = load_b128(kr, off);
-            vp[r] = load_b128(vr, off);
+            kp[r] = load_b128(kr, ((uint32_t)(kb * kPfKeys + (idx >> 4)) * kHeadDim + 8u * (uint32_t)(idx & 15)) * 2u);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t off = ((uint32_t)(kb * kPfKeys + 4 * va + r) * kHeadDim + 8u * (uint32_t)vc) * 2u;
+            vp[r] = load_b128(vr, v_unit ? off : kOOR);
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < KP; ++r) {
+            const int idx = tid + NT * r;
+            *reinterpret_cast<uint4*>(&ks[buf][idx >> 4][8 * (idx & 15)]) = kp[r];
+        }
+        if (v_unit) {
+            // row j of the unit: dim 8vc + j of keys 4va .. 4va + 3
+            const uint32_t w[4][4] = {{vp[0].x, vp[0].y, vp[0].z, vp[0].w}, {vp[1].x, vp[1].y, vp[1].z, vp[1].w},
+                                      {vp[2].x, vp[2].y, vp[2].z, vp[2].w}, {vp[3].x, vp[3].y, vp[3].z, vp[3].w}};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int sh = 16 * (j & 1);
+                const uint32_t e0 = (w[0][j >> 1] >> sh) & 0xffffu, e1 = (w[1][j >> 1] >> sh) & 0xffffu;
+                const uint32_t e2 = (w[2][j >> 1] >> sh) & 0xffffu, e3 = (w[3][j >> 1] >> sh) & 0xffffu;
+                *reinterpret_cast<uint2*>(&vt[buf][8 * vc + j][4 * va]) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+            }
         }
     };
     issue(0);
@@ -709,20 +738,10 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[d] = pf_float4{0.f, 0.f, 0.f, 0.f};
     const int blocks = last / kPfKeys + 1;
+    stage(0);
+    __syncthreads();
     for (int kb = 0; kb < blocks; ++kb) {
-#pragma unroll
-        for (int r = 0; r < PIECES; ++r) {
-            const int idx = tid + NT * r;
-            const int key = idx >> 4, c = idx & 15;
-            *reinterpret_cast<uint4*>(&ks[key][8 * c]) = kp[r];
-            const uint32_t w[4] = {vp[r].x, vp[r].y, vp[r].z, vp[r].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                vt[8 * c + 2 * j][key] = __builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffffu));
-                vt[8 * c + 2 * j + 1][key] = __builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
-            }
-        }
-        __syncthreads();
+        const int buf = kb & 1;
         if (kb + 1 < blocks) issue(kb + 1);
 
         // S^T for the block's four 16-key tiles
@@ -732,7 +751,7 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
             sc[kt] = pf_float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const pf_half8 ka = *reinterpret_cast<const pf_half8*>(&ks[16 * kt + tl][32 * s + 8 * g]);
+                const pf_half8 ka = *reinterpret_cast<const pf_half8*>(&ks[buf][16 * kt + tl][32 * s + 8 * g]);
                 sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sc[kt], 0, 0, 0);
                 sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[s], sc[kt], 0, 0, 0);
             }
@@ -773,14 +792,17 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
         for (int d = 0; d < 8; ++d) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const _Float16* row = &vt[16 * d + tl][32 * u + 4 * g];
+                const _Float16* row = &vt[buf][16 * d + tl][32 * u + 4 * g];
                 const pf_half4 v0 = *reinterpret_cast<const pf_half4*>(row);
                 const pf_half4 v1 = *reinterpret_cast<const pf_half4*>(row + 16);
-                const pf_half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[u], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[u], o[d], 0, 0, 0);
+                const pf_half8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[u], o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[u], o[d], 0, 0, 0);
             }
         }
+        // the next block into the other buffer: every wave finished reading
+        // it before the previous barrier
+        if (kb + 1 < blocks) stage(buf ^ 1);
         __syncthreads();
     }
 
