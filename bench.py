@@ -256,7 +256,7 @@ def build_decoder(E, synth, torch, ctx, step, out_gamma, layers, seed, members):
     return dec, cfg
 
 
-def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed, prompt_chunk=512):
+def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed, prompt_chunk=2048):
     """Prefills `context` prompt tokens per member, then times `gen_tokens`
     greedy steps of the graph-replayed generation loop (wall clock, which
     includes the step's host work). Member m's prompt depends on the seed and
@@ -828,7 +828,7 @@ def main():
                          "open + staging of a Qwen3-8B-shaped file (--layers layers)")
     ap.add_argument("--context", type=int, default=2048, help="config 4: prompt tokens before generation")
     ap.add_argument("--gen-tokens", type=int, default=128, help="config 4: greedy tokens timed")
-    ap.add_argument("--prompt-chunk", type=int, default=512,
+    ap.add_argument("--prompt-chunk", type=int, default=2048,
                     help="config 4: prompt tokens per prefill-matmul chunk (0: serial single-token prefill)")
     ap.add_argument("--no-model", action="store_true", help="skip the config-4 full-decoder measurement")
     ap.add_argument("--concurrency", type=int, default=8, help="serving: requests in the burst")

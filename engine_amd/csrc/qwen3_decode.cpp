@@ -487,8 +487,10 @@ ribn_amd_status reserve_prompt(ribn_amd_qwen3_decode* d, uint32_t tokens) {
         bytes += align_up(f32_counts[i] * sizeof(float));
     }
     const size_t gemm_offset = bytes;
-    // activations at the widest K, and split-K room for two partial tiles
-    const size_t gemm_bytes = ribn_amd::gemm_workspace_bytes(T, max_k, 0) + align_up(2 * T * max_n * sizeof(float));
+    // activations at the widest K, and split-K room for two partial tiles of
+    // up to 512 tokens (grids of more tokens fill the CUs without a split)
+    const size_t gemm_bytes = ribn_amd::gemm_workspace_bytes(T, max_k, 0) +
+                              align_up(2 * std::min<size_t>(T, 512) * max_n * sizeof(float));
     bytes += gemm_bytes;
     hipError_t e = hipStreamSynchronize(d->ctx->stream);
     if (e != hipSuccess) return driver(e, "synchronize before replacing the prompt workspace");
@@ -574,7 +576,7 @@ hipError_t enqueue_prompt_chunk(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* cac
     return e;
 }
 
-constexpr uint32_t kPromptChunkDefault = 512;
+constexpr uint32_t kPromptChunkDefault = 2048;
 constexpr uint32_t kPromptChunkMin = 16;
 constexpr uint32_t kPromptChunkMax = 2048;
 

@@ -152,7 +152,7 @@ class AmdQwen3Decode:
 
     def prefill_prompt(self, cache: AmdKvCache, tokens, position: int, chunk_tokens: int = 0):
         """A whole prompt (consecutive tokens of one sequence from `position`)
-        on the prefill matmul, in chunks of `chunk_tokens` (0: 512): the
+        on the prefill matmul, in chunks of `chunk_tokens` (0: 2048): the
         projections as matmuls over the chunk, causal chunk attention on the
         matrix cores, K/V written to the cache, no output head. Stands where
         the reference runs run_prefill_chunk (decode.rs:2149-2267)."""

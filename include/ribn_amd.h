@@ -610,7 +610,7 @@ ribn_amd_status ribn_amd_qwen3_prefill_chunk(ribn_amd_qwen3_decode *decode, ribn
  * gemv_batch, `members` tokens at a time) and takes whole prompts: `count`
  * consecutive tokens of one sequence at positions position ..
  * position + count - 1, in chunks of up to `chunk_tokens` (16..2048; 0 means
- * 512). Per chunk every projection runs on ribn_amd_gemm_prefill's kernels
+ * 2048). Per chunk every projection runs on ribn_amd_gemm_prefill's kernels
  * over all its tokens (f16 MFMA, f32 accumulation), attention is causal over
  * the cache on the matrix cores (ribn_amd_attention_prefill's arithmetic),
  * and the chunk's K/V are written to the cache; no
@@ -624,7 +624,7 @@ ribn_amd_status ribn_amd_qwen3_prefill_prompt(ribn_amd_qwen3_decode *decode, rib
                                               const uint32_t *tokens, size_t count, uint32_t position,
                                               uint32_t chunk_tokens);
 /* Allocates (grows) the prompt workspace for chunks of `chunk_tokens` tokens
- * (0 means 512) ahead of ribn_amd_qwen3_prefill_prompt. No reference
+ * (0 means 2048) ahead of ribn_amd_qwen3_prefill_prompt. No reference
  * counterpart (the reference sizes its batch scratch at construction,
  * decode.rs:1582-1617). */
 ribn_amd_status ribn_amd_qwen3_reserve_prompt(ribn_amd_qwen3_decode *decode, uint32_t chunk_tokens);
