@@ -1016,12 +1016,21 @@ static hipError_t launch_qgemm_t(const uint8_t* w, uint32_t wbytes, void* worksp
 constexpr int kTileRb = 3;
 constexpr int kTileTb = 8;
 
-static bool use_tile(int M, int N, int cu_count) {
-    const long long wgs = (long long)((N + 64 * kTileRb - 1) / (64 * kTileRb)) * ((M + 16 * kTileTb - 1) / (16 * kTileTb));
+// The wide-tile grid of RB row blocks per wave fills at least `tenths`
+// tenths of its last round of CUs.
+static bool use_tile(int M, int N, int cu_count, int rb = kTileRb, int tenths = 7) {
+    const long long wgs = (long long)((N + 64 * rb - 1) / (64 * rb)) * ((M + 16 * kTileTb - 1) / (16 * kTileTb));
     const long long cus = std::max(1, cu_count);
     const long long rounds = (wgs + cus - 1) / cus;
-    return wgs * 10 >= rounds * cus * 7;
+    return wgs * 10 >= rounds * cus * tenths;
 }
+
+// From this many tokens, 256-row tiles (RB = 4) take every type whose grid
+// fills its last round 90%: each B fragment read from LDS then feeds four
+// MFMAs instead of three. Measured at M = 2047: Q4_K 4096 -> 12288 244 us
+// against 262 (192-row tiles), 4096 -> 4096 87 against 100 (32x32 kernel);
+// at M = 1024 (4096 -> 12288, last round half full) 159 against 140.
+constexpr int kTileWideM = 1024;
 
 struct TileChoice {
     int rb = 0, tb = 0, splits = 0;  // rb == 0: none fits
@@ -1149,9 +1158,7 @@ static hipError_t launch_qgemm_tile(void* workspace, const uint8_t* w, uint32_t 
     if (rb == 3 && tb == 4) return launch_tile_t<T, 3, 4>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
     if (rb == 2 && tb == 8) return launch_tile_t<T, 2, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
     if (rb == 2 && tb == 4) return launch_tile_t<T, 2, 4>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
-    if constexpr (T == kQ5K || T == kQ6K) {
-        if (rb == 4 && tb == 8) return launch_tile_t<T, 4, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
-    }
+    if (rb == 4 && tb == 8) return launch_tile_t<T, 4, 8>(workspace, w, wbytes, y, M, N, K, splits, cu_count, stream);
     return hipErrorInvalidValue;
 }
 
@@ -1174,6 +1181,8 @@ static hipError_t launch_qgemm_m(const uint8_t* w, uint32_t wbytes, void* worksp
         if (c.rb) return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, c.rb, c.tb, c.splits, cu_count, stream);
     }
     if (M <= 64) return launch_qgemm_t<T, 2, 2>(w, wbytes, workspace, workspace_bytes, y, M, N, K, cu_count, stream);
+    if (tile_ok && M >= kTileWideM && use_tile(M, N, cu_count, 4, 9))
+        return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, 4, kTileTb, 1, cu_count, stream);
     if (tile_ok && M > 128 && use_tile(M, N, cu_count))
         return launch_qgemm_tile<T>(workspace, w, wbytes, y, M, N, K, kTileRb, kTileTb, 1, cu_count, stream);
     if (tile_ok && M > 128) {

@@ -14,7 +14,8 @@ import pytest
 from engine_amd import synth
 from oracle import kquant_oracle as O
 
-from .gpu_helpers import RTOL, empty_dev, max_rel_err, to_dev, to_host, wide_range_activations
+from .gpu_helpers import (F32_BITWISE_MEMBERS, F32_RTOL, RTOL, empty_dev, max_rel_err, to_dev, to_host,
+                          wide_range_activations)
 
 pytestmark = pytest.mark.gpu
 
@@ -128,6 +129,9 @@ def test_prefill_config3_full_size(env, t, k, n):
     (14, 12288, 4094, 384, "bf16"),   # as (14, 12288, 4096, 384) with N not a multiple of 4: one-wide split reduce
     (12, 4096, 12288, 129, "f32"),    # 64 x 2 tiles, K split in 2; the last token tile holds one token
     (12, 4096, 12288, 640, "bf16"),   # 320 tiles: two rounds, the second a quarter full, and no split fits: the 32x32 kernel
+    (12, 4096, 12288, 2047, "f32"),   # many tokens: 256-row tiles, 48 x 16 (three whole rounds), last token tile 127
+    (12, 4096, 4096, 2000, "bf16"),   # many tokens: 256-row tiles, 16 x 16, last token tile 80 of 128
+    (13, 12288, 4096, 2047, "f32"),   # many tokens: Q5_K 256-row tiles without a split
 ])
 def test_prefill_wide_tiles(env, t, k, n, m, dtype):
     """Shapes whose wide-tile grid fills a 256-CU MI355X (the wide-tile
@@ -197,8 +201,9 @@ def test_batched_ffn_m64_full_size(env, t, k, n):
     """BASELINE config 2 at M = 64 on the Qwen3-8B FFN shapes (gate/up Q4_K
     4096 -> 12288, down Q5_K 12288 -> 4096, f32 activations, RMSNorm fused on
     gate/up): the f16 matrix-core matmul and the batched GEMV (GEMV_WARP,
-    launch groups of 8 or 2 members) against the oracle on a token sample,
-    and batched rows bit-identical to single-member calls."""
+    which runs 64 members on the f32-faithful matrix-core GEMV) against the
+    oracle on a token sample, and batched rows within F32_RTOL of
+    single-member calls (bit-identical only up to F32_BITWISE_MEMBERS)."""
     m = 64
     print("CASE batched m64", t, k, n, flush=True)
     enc = synth.kquant_numpy(t, k, n, seed=640 + t)
@@ -227,7 +232,8 @@ def test_batched_ffn_m64_full_size(env, t, k, n):
             env["k"][t].execute_rms_norm(w, to_dev(x[i]), to_dev(gamma), 1e-6, one, 1)
         else:
             env["k"][t].execute_warp(w, to_dev(x[i]), one)
-        assert np.array_equal(to_host(one, env["ctx"]).view(np.uint32), batched[i].view(np.uint32))
+        assert m > F32_BITWISE_MEMBERS
+        assert max_rel_err(batched[i], to_host(one, env["ctx"])) <= F32_RTOL, i
 
 
 def test_prefill_matches_wave_gemv_rows(env):
