@@ -191,6 +191,7 @@ SIGNATURES = {
     "ribn_amd_serving_create": (_i32, [_vp, _u32, _u64, _pvp]),
     "ribn_amd_serving_destroy": (None, [_vp]),
     "ribn_amd_serving_set_prefill_chunk": (_i32, [_vp, _u32]),
+    "ribn_amd_serving_set_prompt_prefill": (_i32, [_vp, _u32]),
     "ribn_amd_serving_set_grouped_decode": (_i32, [_vp, _i32]),
     "ribn_amd_serving_dispatch_batch": (_i32, [_vp, ctypes.POINTER(ServingRow), _sz, ctypes.POINTER(ServingOutcome)]),
     "ribn_amd_serving_submit_batch": (_i32, [_vp, _u64, ctypes.POINTER(ServingRow), _sz]),

@@ -385,6 +385,16 @@ __global__ __launch_bounds__(128) void kv_append_kernel(AttnArgs a) {
     dst[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16)x1);
 }
 
+struct TokenArgs {
+    uint32_t tokens[kTokenArgs];
+    uint32_t* dst;
+    int count;
+};
+
+__global__ __launch_bounds__(256) void token_upload_kernel(TokenArgs in) {
+    for (int i = threadIdx.x; i < in.count; i += 256) in.dst[i] = in.tokens[i];
+}
+
 __global__ __launch_bounds__(64) void step_inputs_kernel(StepInputs in) {
     const int i = threadIdx.x;
     if (i >= in.count) return;
@@ -880,6 +890,20 @@ hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t stream
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_token_upload(const uint32_t* tokens, size_t count, uint32_t* dst, hipStream_t stream) {
+    if (tokens == nullptr || dst == nullptr) return hipErrorInvalidValue;
+    for (size_t i0 = 0; i0 < count; i0 += kTokenArgs) {
+        TokenArgs a;
+        a.count = (int)std::min<size_t>(kTokenArgs, count - i0);
+        for (int i = 0; i < a.count; ++i) a.tokens[i] = tokens[i0 + i];
+        a.dst = dst + i0;
+        hipLaunchKernelGGL(token_upload_kernel, dim3(1), dim3(256), 0, stream, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_step_inputs(const StepInputs& in, hipStream_t stream) {

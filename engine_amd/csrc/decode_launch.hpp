@@ -87,6 +87,12 @@ struct StepInputs {
 };
 hipError_t launch_step_inputs(const StepInputs& in, hipStream_t stream);
 
+// Stream-ordered upload of `count` token ids from host memory to dst through
+// kernel arguments (launches of up to kTokenArgs ids): the host array is not
+// read after the call returns and nothing waits for the stream.
+constexpr int kTokenArgs = 960;
+hipError_t launch_token_upload(const uint32_t* tokens, size_t count, uint32_t* dst, hipStream_t stream);
+
 // Prompt prefill: `tokens` consecutive tokens of one sequence at positions
 // p0 .. p0 + tokens - 1, their q/k/v projections computed for the whole chunk.
 struct PrefillAttnArgs {

@@ -1095,8 +1095,7 @@ ribn_amd_status ribn_amd_qwen3_prefill_prompt(ribn_amd_qwen3_decode* d, ribn_amd
     hipStream_t stream = d->ctx->stream;
     for (size_t c0 = 0; c0 < count; c0 += chunk) {
         const int n = (int)std::min<size_t>(chunk, count - c0);
-        hipError_t e = hipMemcpyAsync(d->p_tokens, tokens + c0, (size_t)n * sizeof(uint32_t), hipMemcpyHostToDevice,
-                                      stream);
+        hipError_t e = ribn_amd::launch_token_upload(tokens + c0, (size_t)n, d->p_tokens, stream);
         if (e == hipSuccess) e = enqueue_prompt_chunk(d, cache, n, (int)(position + c0), stream);
         if (e != hipSuccess) return driver(e, "prompt prefill chunk");
     }

@@ -8,8 +8,10 @@
 // its rows without waiting on the device:
 //   - an all-decode batch (or, with grouped decode, each compatible group of a
 //     mixed batch) runs as one batched decode step; other rows run one by one
-//     (prefill: leading whole chunks as prefill-chunk steps, the rest as
-//     single steps, the sampling token through the output head);
+//     (prefill: with prompt prefill set, a prefix of at least
+//     kPromptMinTokens on the prefill matmul; else leading whole chunks as
+//     prefill-chunk steps; the rest as single steps, the sampling token
+//     through the output head);
 //   - each sampling row's greedy token is copied, stream-ordered, into its own
 //     pinned host slot (hipHostMalloc) leased for the submission's lifetime;
 //   - one event recorded after the rows covers every kernel and copy.
@@ -52,6 +54,9 @@ using namespace ribn_amd_abi;
 namespace {
 
 constexpr int32_t kNoSlot = -1;
+// Shortest prefill prefix the prompt-prefill lane takes (shorter ones keep
+// the chunk / serial path, where a matmul launch per projection buys little).
+constexpr uint32_t kPromptMinTokens = 16;
 
 // CudaHybridState with its KV family (Qwen3 has no recurrent layers).
 struct PhysicalState {
@@ -132,6 +137,7 @@ struct ribn_amd_serving {
     ribn_amd_qwen3_config cfg;
     uint32_t lane_max;       // widest batched decode lane
     uint32_t prefill_chunk;  // 0: serial prefill
+    uint32_t prompt_chunk;   // 0: off; else prompt prefixes on the prefill matmul in chunks of this many tokens
     bool grouped;
     uint64_t kv_budget;      // 0: unbounded
     uint64_t kv_in_use;
@@ -355,7 +361,21 @@ ribn_amd_status run_row(ribn_amd_serving* s, const ribn_amd_serving_row& row, bo
         }
         const bool sampling = row.requests_sampling != 0;
         const uint32_t chunk = s->prefill_chunk;
-        const uint32_t chunked = chunked_prefix_len(row.token_count, chunk, sampling);
+        uint32_t chunked = chunked_prefix_len(row.token_count, chunk, sampling);
+        const uint32_t prefix = sampling ? row.token_count - 1 : row.token_count;
+        if (s->prompt_chunk != 0 && prefix >= kPromptMinTokens) {
+            // the prompt-prefill lane: every token but the sampling one
+            if ((uint64_t)row.state_position + prefix > 0x7fffffffull) {
+                return fail(RIBN_AMD_POSITION_OVERFLOW, 0x7fffffffull, (uint64_t)row.state_position + prefix,
+                            "prefill position overflowed");
+            }
+            st = ribn_amd_qwen3_prefill_prompt(s->decode, p->cache, row.tokens, prefix, row.state_position,
+                                               s->prompt_chunk);
+            if (st == RIBN_AMD_OK) st = advance(p, (uint64_t)row.state_position + prefix);
+            if (st != RIBN_AMD_OK) return st;
+            chunked = 0;
+        }
+        const uint32_t serial_from = s->prompt_chunk != 0 && prefix >= kPromptMinTokens ? prefix : chunked;
         for (uint32_t off = 0; off < chunked; off += chunk) {
             const uint64_t position = (uint64_t)row.state_position + off;
             if (position + chunk > 0x7fffffffull) {
@@ -366,7 +386,7 @@ ribn_amd_status run_row(ribn_amd_serving* s, const ribn_amd_serving_row& row, bo
             if (st == RIBN_AMD_OK) st = advance(p, position + chunk);
             if (st != RIBN_AMD_OK) return st;
         }
-        for (uint32_t off = chunked; off < row.token_count; ++off) {
+        for (uint32_t off = serial_from; off < row.token_count; ++off) {
             const uint64_t position = (uint64_t)row.state_position + off;
             if (position >= 0x7fffffffull) {
                 return fail(RIBN_AMD_POSITION_OVERFLOW, 0x7fffffffull, position, "prefill position overflowed");
@@ -578,6 +598,19 @@ void ribn_amd_serving_destroy(ribn_amd_serving* s) {
     ribn_amd_context* ctx = s->ctx;
     delete s;
     context_release(ctx);
+}
+
+ribn_amd_status ribn_amd_serving_set_prompt_prefill(ribn_amd_serving* s, uint32_t chunk_tokens) {
+    if (!s) return fail(RIBN_AMD_INVALID_ARGUMENT, 0, 0, "null dispatcher");
+    if (chunk_tokens == 0) {
+        s->prompt_chunk = 0;
+        return ok();
+    }
+    // the workspace now, so no submission allocates or waits for the device
+    const ribn_amd_status st = ribn_amd_qwen3_reserve_prompt(s->decode, chunk_tokens);
+    if (st != RIBN_AMD_OK) return st;
+    s->prompt_chunk = chunk_tokens;
+    return ok();
 }
 
 ribn_amd_status ribn_amd_serving_set_prefill_chunk(ribn_amd_serving* s, uint32_t members) {

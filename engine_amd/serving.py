@@ -225,6 +225,13 @@ class AmdServingDispatcher(AmdDispatcher):
         _call(self._lib.ribn_amd_serving_set_prefill_chunk(self.handle, members))
         return self
 
+    def with_prompt_prefill(self, chunk_tokens: int) -> "AmdServingDispatcher":
+        """Prefill prefixes of at least 16 tokens on the prefill matmul
+        (AmdQwen3Decode.prefill_prompt) in chunks of `chunk_tokens`; 0 turns
+        it off. No reference counterpart; reserves the workspace now."""
+        _call(self._lib.ribn_amd_serving_set_prompt_prefill(self.handle, chunk_tokens))
+        return self
+
     def with_grouped_decode(self, enabled: bool) -> "AmdServingDispatcher":
         _call(self._lib.ribn_amd_serving_set_grouped_decode(self.handle, 1 if enabled else 0))
         return self

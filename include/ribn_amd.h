@@ -619,7 +619,8 @@ ribn_amd_status ribn_amd_qwen3_prefill_chunk(ribn_amd_qwen3_decode *decode, ribn
  * for every projection. The workspace for `chunk_tokens` is allocated on the
  * first call (or by ribn_amd_qwen3_reserve_prompt) and grown when a call
  * needs more, synchronising the context stream then; otherwise
- * stream-ordered. Tokens are read from host memory before the call returns. */
+ * stream-ordered (tokens travel in kernel arguments: the host array is read
+ * before the call returns, and nothing waits for the stream). */
 ribn_amd_status ribn_amd_qwen3_prefill_prompt(ribn_amd_qwen3_decode *decode, ribn_amd_kv_cache *cache,
                                               const uint32_t *tokens, size_t count, uint32_t position,
                                               uint32_t chunk_tokens);
@@ -714,6 +715,15 @@ void ribn_amd_serving_destroy(ribn_amd_serving *serving);
  * prompt tokens run as one prefill-chunk step (2 <= members <= the decoder's
  * max_members); 0 restores serial prefill. */
 ribn_amd_status ribn_amd_serving_set_prefill_chunk(ribn_amd_serving *serving, uint32_t members);
+/* No reference counterpart (the reference prefills through prefill_chunk
+ * and prefill_step, serving.rs:136-160,357-371): with chunk_tokens != 0 a
+ * prefill segment's tokens other than the sampling one, when at least 16,
+ * run as one ribn_amd_qwen3_prefill_prompt call in chunks of chunk_tokens
+ * (16..2048); shorter prefixes keep the prefill-chunk / serial path. Results
+ * are within the prefill matmul's tolerance of serial prefill, not bit-equal.
+ * Allocates the decoder's prompt workspace now (synchronising its stream),
+ * so submissions neither allocate nor wait. 0 turns the lane off. */
+ribn_amd_status ribn_amd_serving_set_prompt_prefill(ribn_amd_serving *serving, uint32_t chunk_tokens);
 /* with_grouped_decode (serving.rs:337-341): compatible decode rows of mixed
  * batches are gathered into lanes (opt-in, as in the reference). */
 ribn_amd_status ribn_amd_serving_set_grouped_decode(ribn_amd_serving *serving, int32_t enabled);

@@ -231,6 +231,44 @@ def test_prefill_chunk_lane_equals_serial_prefill(env):
         S.AmdServingDispatcher(env["dec"], 4).with_prefill_chunk(9)  # the decoder serves 8 members
 
 
+def test_prompt_prefill_lane_equals_direct_prompt_prefill(env):
+    """The prompt-prefill lane (no reference counterpart): a 40-token prompt's
+    first 39 tokens through prefill_prompt (chunks of 16: 16 + 16 + 7), the
+    last through the output head, then decode steps, as a submission and
+    eagerly; equal token for token to direct prefill_prompt + decode_step
+    calls. A 10-token prompt (prefix under 16) keeps the serial path: equal
+    to direct serial prefill. Bad chunk sizes are rejected."""
+    print_case(test="serving_prompt_prefill")
+    dec = env["dec"]
+    prompt = [(71 * i + 5) % TINY["vocab"] for i in range(40)]
+    c = cache(env)
+    dec.prefill_prompt(c, prompt[:-1], 0, 16)
+    want = [dec.decode_step(c, prompt[-1], len(prompt) - 1)]
+    for s in range(3):
+        want.append(dec.decode_step(c, want[-1], len(prompt) + s))
+    for submission in (1, None):
+        disp = S.AmdServingDispatcher(dec, 4).with_prompt_prefill(16)
+        r = Request(prompt)
+        run(disp, [r], [r.prefill()], submission=submission)
+        for s in range(3):
+            run(disp, [r], [r.decode()], submission=None if submission is None else 2 + s)
+        assert r.generated == want, (submission, r.generated, want)
+        disp.close()
+    short = [(31 * i + 9) % TINY["vocab"] for i in range(10)]
+    disp = S.AmdServingDispatcher(dec, 4).with_prompt_prefill(16)
+    r = Request(short)
+    run(disp, [r], [r.prefill()], submission=1)
+    for s in range(2):
+        run(disp, [r], [r.decode()], submission=2 + s)
+    want_short, _ = direct(env, short, 2)
+    assert r.generated == want_short
+    disp.close()
+    with pytest.raises(S.BackendError):
+        S.AmdServingDispatcher(dec, 4).with_prompt_prefill(8)
+    with pytest.raises(S.BackendError):
+        S.AmdServingDispatcher(dec, 4).with_prompt_prefill(4096)
+
+
 def test_grouped_decode_of_a_mixed_batch(env):
     print_case(test="serving_grouped")
     dec = env["dec"]
