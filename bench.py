@@ -653,6 +653,8 @@ def bench_serving(E, synth, torch, ctx, step, out_gamma, args):
     disp = S.AmdServingDispatcher(dec, args.concurrency, kv_budget_bytes=per_seq * args.concurrency)
     if args.prefill_chunk:
         disp.with_prefill_chunk(args.prefill_chunk)
+    if args.prompt_prefill:
+        disp.with_prompt_prefill(args.prompt_prefill)
     caps = S.BackendCapabilities("rocm", 0, "rocm", torch.cuda.get_device_properties(0).total_memory)
     plan = S.ExecutionPlan("qwen3-8b-shaped", "rocm", 0, 1, frozenset((S.Phase.PREFILL, S.Phase.DECODE)))
     backend = S.AmdBackend(caps, disp)
@@ -707,7 +709,7 @@ def bench_serving(E, synth, torch, ctx, step, out_gamma, args):
     log(f"bench serving: warm-up burst ({args.concurrency} x {args.prompt_tokens} prompt tokens, 2 tokens)")
     run_burst(2)
     log(f"bench serving: timed burst ({args.concurrency} x {args.prompt_tokens} prompt, {args.tokens} tokens, "
-        f"prefill chunk {args.prefill_chunk or 'off'})")
+        f"prefill chunk {args.prefill_chunk or 'off'}, prompt prefill {args.prompt_prefill or 'off'})")
     reqs, wall, batches = run_burst(args.tokens)
     ttft = [r["times"][0] for r in reqs]
     itl = [b - a for r in reqs for a, b in zip(r["times"], r["times"][1:])]
@@ -730,7 +732,8 @@ def bench_serving(E, synth, torch, ctx, step, out_gamma, args):
         "dtype": ("f32" if args.gemv_mode == "warp" else "i8dot4-f32") + " GEMV, f16 KV, f32 attention",
         "config": {"workload": "qwen3-8b-serving-burst", "layers": args.layers, "concurrency": args.concurrency,
                    "prompt_tokens": args.prompt_tokens, "output_tokens": args.tokens,
-                   "prefill_chunk": args.prefill_chunk, "batch_tokens": args.batch_tokens,
+                   "prefill_chunk": args.prefill_chunk, "prompt_prefill": args.prompt_prefill,
+                   "batch_tokens": args.batch_tokens,
                    "grouped_decode": False},
         "serving": {"wall_s": round(wall, 3), "batches": batches,
                     "prefill_tok_s": round(prompt_total / first_all, 1),
@@ -836,6 +839,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=32, help="serving: output tokens per request")
     ap.add_argument("--prefill-chunk", type=int, default=8, help="serving: prefill chunk members (0: serial)")
     ap.add_argument("--batch-tokens", type=int, default=128, help="serving: prompt tokens per scheduler batch")
+    ap.add_argument("--prompt-prefill", type=int, default=2048,
+                    help="serving: prefill prefixes of 16+ tokens on the prefill matmul in chunks of this many "
+                         "tokens (0: off, the prefill-chunk / serial path)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the timed work, copy a MIB-MiB device buffer three times: a kernel of known "
                          "traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE onto bytes")
