@@ -756,6 +756,39 @@ def bench_serving(E, synth, torch, ctx, step, out_gamma, args):
     return result
 
 
+def bench_mfma_peak(E, synth, torch, args):
+    """The measured dense peak of the matrix-core instructions (SURVEY's
+    roofline note: confirm the 2.5 PFLOP/s f16 / bf16 figure with a
+    microbenchmark): ribn_amd_probe_mfma_peak, a full grid of four waves per
+    SIMD issuing independent MFMAs on register operands, median of 5 runs."""
+    import ctypes
+    ctx = E.AmdContext(0)
+    kinds = {0: "v_mfma_f32_16x16x32_f16", 1: "v_mfma_f32_32x32x16_f16", 2: "v_mfma_f32_16x16x32_bf16",
+             3: "v_mfma_f32_16x16x4_f32"}
+    published = {0: 2500.0, 1: 2500.0, 2: 2500.0, 3: 157.3}
+    res = {}
+    for kind, name in kinds.items():
+        runs = []
+        for _ in range(5):
+            out = ctypes.c_double()
+            st = ctx._lib.ribn_amd_probe_mfma_peak(ctx.handle, kind, 20000, ctypes.byref(out))
+            if st != 0:
+                raise RuntimeError(f"MFMA probe failed with status {st}")
+            runs.append(out.value)
+        runs.sort()
+        res[name] = {"tflops": round(runs[2], 1), "published_tflops": published[kind],
+                     "of_published": round(runs[2] / published[kind], 4)}
+        log(f"bench mfma-peak: {name}: {runs[2]:.1f} TFLOP/s ({runs[2] / published[kind]:.1%} of {published[kind]})")
+    f16 = res["v_mfma_f32_16x16x32_f16"]["tflops"]
+    return {"metric": "MI355X dense f16 MFMA peak, measured (v_mfma_f32_16x16x32_f16)", "value": f16,
+            "unit": "TFLOP/s", "n_gpus": 1, "steps": 5, "warmup": 1, "ms_per_step": None, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+            "config": {"workload": "mfma-peak", "iterations": 20000, "waves_per_simd": 4, "kinds": res},
+            "roofline": {"bound": "mfma", "achieved": f16, "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(f16 / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None},
+            "cpu_baseline": None}
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_f32_q4k_gate_up_traffic.md")
 
 
@@ -822,13 +855,15 @@ def main():
     ap.add_argument("--gemv-mode", choices=tuple(GEMV_MODES), default="warp",
                     help="GEMV arithmetic: warp (f32 activations, default) or fixed16 (opt-in block fixed point)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1", "gguf", "serving"),
+    ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1", "gguf", "serving",
+                                           "mfma-peak"),
                     default="decode",
                     help="decode: BASELINE config 1 (the headline line, default, which also carries the "
                          "config-4 tok/s); batched: config 2 (FFN at M = 1, 4, 16, 64); prefill: config 3 "
                          "(M = 512 bf16 matmuls); model: config 4 alone (full decoder, batch 1 and 8); q8_1: "
                          "the Q8_1 integer-dot projections (pack + GEMV) at batch 1 and 8; gguf: GGUF "
-                         "open + staging of a Qwen3-8B-shaped file (--layers layers)")
+                         "open + staging of a Qwen3-8B-shaped file (--layers layers); mfma-peak: the "
+                         "measured dense peak of the matrix-core instructions the prefill uses")
     ap.add_argument("--context", type=int, default=2048, help="config 4: prompt tokens before generation")
     ap.add_argument("--gen-tokens", type=int, default=128, help="config 4: greedy tokens timed")
     ap.add_argument("--prompt-chunk", type=int, default=2048,
@@ -860,9 +895,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    if args.workload in ("batched", "prefill", "q8_1", "gguf"):
+    if args.workload in ("batched", "prefill", "q8_1", "gguf", "mfma-peak"):
         result = {"batched": bench_batched, "prefill": bench_prefill, "q8_1": bench_q8_1,
-                  "gguf": bench_gguf}[args.workload](
+                  "gguf": bench_gguf, "mfma-peak": bench_mfma_peak}[args.workload](
             E, synth, torch, args)
         print(json.dumps(result), flush=True)
         return

@@ -179,6 +179,7 @@ SIGNATURES = {
     "ribn_amd_qwen3_prefill_chunk": (_i32, [_vp, _vp, ctypes.POINTER(_u32), _sz, _u32]),
     "ribn_amd_attention_prefill": (_i32, [_vp, ctypes.POINTER(Qwen3Config), _vp, _u32, _vp, _vp, _vp, _vp, _vp, _sz,
                                        _u32, _vp, _sz]),
+    "ribn_amd_probe_mfma_peak": (_i32, [_vp, _u32, _u32, ctypes.POINTER(ctypes.c_double)]),
     "ribn_amd_qwen3_prefill_prompt": (_i32, [_vp, _vp, ctypes.POINTER(_u32), _sz, _u32, _u32]),
     "ribn_amd_qwen3_reserve_prompt": (_i32, [_vp, _u32]),
     "ribn_amd_qwen3_decode_step": (_i32, [_vp, _vp, _u32, _u32, ctypes.POINTER(_u32)]),

@@ -60,7 +60,7 @@ SANITIZE_FLAGS = [
 SANITIZE_LINK = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
                  "-Xarch_host", "-shared-libsan"]
 
-SOURCES = ["kquant_kernels.hip", "gemv_wave.hip", "gemv_f32.hip", "gemv_mfma.hip", "gemv_f32mma.hip", "q8_1.hip", "qgemm.hip", "decode_kernels.hip", "ribn_amd.cpp", "qwen3_decode.cpp", "gguf.cpp", "serving.cpp"]
+SOURCES = ["kquant_kernels.hip", "gemv_wave.hip", "gemv_f32.hip", "gemv_mfma.hip", "gemv_f32mma.hip", "q8_1.hip", "qgemm.hip", "decode_kernels.hip", "probe.hip", "ribn_amd.cpp", "qwen3_decode.cpp", "gguf.cpp", "serving.cpp"]
 
 
 def hipcc() -> str:

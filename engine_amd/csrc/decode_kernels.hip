@@ -754,17 +754,21 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
         const int buf = kb & 1;
         if (kb + 1 < blocks) issue(kb + 1);
 
-        // S^T for the block's four 16-key tiles
+        // S^T for the block's four 16-key tiles, issued tile-interleaved:
+        // consecutive MFMAs feed different accumulators
         pf_float4 sc[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            sc[kt] = pf_float4{0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < 4; ++kt) sc[kt] = pf_float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const pf_half8 ka = *reinterpret_cast<const pf_half8*>(&ks[buf][16 * kt + tl][32 * s + 8 * g]);
-                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sc[kt], 0, 0, 0);
-                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[s], sc[kt], 0, 0, 0);
-            }
+        for (int s = 0; s < 4; ++s) {
+            pf_half8 ka[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+                ka[kt] = *reinterpret_cast<const pf_half8*>(&ks[buf][16 * kt + tl][32 * s + 8 * g]);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt], qb[s], sc[kt], 0, 0, 0);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt], ql[s], sc[kt], 0, 0, 0);
         }
         float bmax = -INFINITY;
 #pragma unroll
@@ -797,18 +801,22 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
                 pl[kt >> 1][4 * (kt & 1) + i] = (_Float16)(pv - (float)ph);
             }
         }
-        // O^T += V^T P^T over the block's two 32-key steps
+        // O^T += V^T P^T over the block's two 32-key steps, issued
+        // dim-tile-interleaved (eight accumulators between dependent MFMAs)
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
+        for (int u = 0; u < 2; ++u) {
+            pf_half8 vf[8];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int d = 0; d < 8; ++d) {
                 const _Float16* row = &vt[buf][16 * d + tl][32 * u + 4 * g];
                 const pf_half4 v0 = *reinterpret_cast<const pf_half4*>(row);
                 const pf_half4 v1 = *reinterpret_cast<const pf_half4*>(row + 16);
-                const pf_half8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[u], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[u], o[d], 0, 0, 0);
+                vf[d] = pf_half8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
             }
+#pragma unroll
+            for (int d = 0; d < 8; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[d], pb[u], o[d], 0, 0, 0);
+#pragma unroll
+            for (int d = 0; d < 8; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[d], pl[u], o[d], 0, 0, 0);
         }
         // the next block into the other buffer: every wave finished reading
         // it before the previous barrier

@@ -451,6 +451,18 @@ ribn_amd_status ribn_amd_gemm_prefill_static(ribn_amd_gemv *gemv, const ribn_amd
                                              size_t members, const float *gamma, size_t gamma_len, float epsilon,
                                              float *output, size_t output_len);
 
+/* ----------------------------------------------------------- measurement */
+
+/* Matrix-core peak probe (no reference counterpart; it confirms the MFMA peak
+ * the prefill roofline is priced against): a grid of four waves per SIMD
+ * issuing independent MFMAs on register operands for `iterations` rounds,
+ * timed with events on the context stream (blocking). kind 0
+ * v_mfma_f32_16x16x32_f16, 1 v_mfma_f32_32x32x16_f16, 2
+ * v_mfma_f32_16x16x32_bf16, 3 v_mfma_f32_16x16x4_f32. Writes the achieved
+ * dense TFLOP/s. */
+ribn_amd_status ribn_amd_probe_mfma_peak(ribn_amd_context *ctx, uint32_t kind, uint32_t iterations,
+                                         double *tflops);
+
 /* ------------------------------------------------------------- embedding */
 
 /* CudaQ4KEmbedding::from_context (quantized.rs:913-960): gather kernel for a
