@@ -216,12 +216,19 @@ def _short_name(name: str) -> str:
 
 
 def _demangle(names: list[str]) -> list[str]:
+    """c++filt where it knows the mangling; names it leaves mangled (binutils
+    does not know `DF16_`, the _Float16 parameter code) go through the kernel
+    name reader of engine_amd.profiling, which keeps the template arguments."""
+    from engine_amd.profiling import short_name
+
     tool = shutil.which("c++filt") or shutil.which("llvm-cxxfilt")
-    if not names or not tool:
-        return names
-    res = subprocess.run([tool], input="\n".join(names), capture_output=True, text=True)
-    out = [_short_name(n) for n in res.stdout.splitlines()]
-    return out if res.returncode == 0 and len(out) == len(names) else names
+    out = names
+    if names and tool:
+        res = subprocess.run([tool], input="\n".join(names), capture_output=True, text=True)
+        lines = res.stdout.splitlines()
+        if res.returncode == 0 and len(lines) == len(names):
+            out = lines
+    return [short_name(n) if n.startswith("_Z") else _short_name(n) for n in out]
 
 
 if __name__ == "__main__":

@@ -98,6 +98,10 @@ def test_resource_remarks_parse():
                     "scratch": 8, "occupancy": 8, "sgpr_spill": 0, "vgpr_spill": 2, "lds": 4096}
     assert k[1] == {"source": "q8_1.hip", "kernel": "_ZN8ribn_amd5otherEv", "vgpr": 40}
     assert B._short_name("void ribn_amd::(anonymous namespace)::k<1, (x)2>(ribn_amd::A)") == "k<1, (x)2>"
+    # _Float16 parameters (DF16_) that binutils' c++filt leaves mangled still read as names
+    assert B._demangle(["_ZN8ribn_amd12qgemm_kernelILi12ELi4ELi8EEEvPKhjPKDF16_PKfPfS7_iiii",
+                        "_ZN8ribn_amd14act_f16_kernelILb0ELb1ELi1EEEvPKvPKffiPDF16_PfS4_"]) == [
+        "qgemm_kernel<12, 4, 8>", "act_f16_kernel<false, true, 1>"]
 
 
 def test_prompt_summary_keeps_prompt_kernels_only(tmp_path):
