@@ -607,7 +607,12 @@ __global__ __launch_bounds__(128) void kv_append_seq_kernel(PrefillAttnArgs a) {
 // [dim][key]): a block's global loads are issued before the previous block is
 // reduced and written to the other buffer after it, one barrier per block.
 // V is transposed in registers: a thread loads four consecutive keys of 8
-// dims and stores 8-byte rows of V^T.
+// dims and stores 8-byte rows of V^T. LDS has 32 four-byte banks: K rows are
+// unpadded with 16-byte piece p of key k at slot p ^ (k & 15), and V^T rows
+// are 68 halfs (34 dwords), so the K and V^T stores and the fragment reads
+// of 16 lanes (8 for 16-byte accesses) fall in distinct banks (counted: no
+// conflict cycles). The rope angles of the workgroup's tokens are computed
+// once per workgroup, not once per query head.
 //
 // Per block and wave, with S^T = K Q^T (M = 16 keys, N = 16 tokens, K = 128
 // dims in 4 steps) the MFMA output puts token l%16 in lane l's column and keys
@@ -628,8 +633,8 @@ typedef _Float16 pf_half4 __attribute__((ext_vector_type(4)));
 typedef float pf_float4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPfKeys = 64;              // keys per block
-constexpr int kPfKRow = kHeadDim + 8;    // LDS K row (halfs): 272 B
-constexpr int kPfVRow = kPfKeys + 8;     // LDS V^T row (halfs): 144 B
+constexpr int kPfVRow = kPfKeys + 4;     // LDS V^T row (halfs): 136 B
+constexpr float kPfLazy = 15.0f;         // log2 headroom of the lazy softmax rescale
 
 template <int QPK>
 __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(PrefillAttnArgs a) {
@@ -638,7 +643,7 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
     constexpr int TT = W / QPK;           // token tiles per workgroup
     constexpr int KP = kPfKeys * (kHeadDim / 8) / NT;  // 16-byte K pieces per thread and block
     // V: 256 units of 4 keys x 8 dims, one per thread of the first 256
-    __shared__ __attribute__((aligned(16))) _Float16 ks[2][kPfKeys][kPfKRow];
+    __shared__ __attribute__((aligned(16))) _Float16 ks[2][kPfKeys][kHeadDim];
     __shared__ __attribute__((aligned(16))) _Float16 vt[2][kHeadDim][kPfVRow];
 
     const int tid = threadIdx.x;
@@ -683,7 +688,7 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
 #pragma unroll
         for (int r = 0; r < KP; ++r) {
             const int idx = tid + NT * r;
-            *reinterpret_cast<uint4*>(&ks[buf][idx >> 4][8 * (idx & 15)]) = kp[r];
+            *reinterpret_cast<uint4*>(&ks[buf][idx >> 4][8 * ((idx & 15) ^ ((idx >> 4) & 15))]) = kp[r];
         }
         if (v_unit) {
             // row j of the unit: dim 8vc + j of keys 4va .. 4va + 3
@@ -699,6 +704,30 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
         }
     };
     issue(0);
+
+    // ---- rope angles of the workgroup's tokens, shared by its QPK query
+    // heads: entry (row, d) = the rotation of pair (d, d + 64) at position
+    // p0 + first token + row, the same rope_rot / rope_freq values each lane
+    // would compute. The table lives in V^T buffer 1, which the first block
+    // writes only after every wave has passed the barrier before the loop.
+    // (One query head per workgroup token tile, QPK = 1, shares nothing: its
+    // lanes compute their own.)
+    constexpr int kRotRow = 65;  // float2 per token row (padded)
+    float2* const rot_tab = reinterpret_cast<float2*>(&vt[1][0][0]);
+    static_assert(QPK == 1 || TT * kPrefillTileTokens * kRotRow * sizeof(float2) <= sizeof(vt[1]),
+                  "rope table must fit one V^T buffer");
+    if constexpr (QPK > 1) {
+#pragma unroll
+        for (int r = 0; r < TT * kPrefillTileTokens * 64 / NT; ++r) {
+            const int e = tid + NT * r;
+            const int row = e >> 6, d = e & 63;
+            const Rot rr = rope_rot((float)(a.p0 + (int)blockIdx.x * TT * kPrefillTileTokens + row),
+                                    rope_freq(a.rope_base, d));
+            rot_tab[row * kRotRow + d] = make_float2(rr.c, rr.s);
+        }
+        __syncthreads();
+    }
+    const int rot_row = (wave / QPK) * kPrefillTileTokens + tl;
 
     // ---- this lane's query dims 32s + 8g + j (s = 0..3, j = 0..7): RMSNorm
     // over the head's 128 dims (the four lanes of the token add their parts),
@@ -732,7 +761,14 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
             const int d = 32 * s + 8 * g + j;
             const float y0 = x[s][j] * inv * a.q_norm[d];
             const float y1 = x[s + 2][j] * inv * a.q_norm[d + 64];
-            const Rot r = rope_rot((float)pos, rope_freq(a.rope_base, d));
+            Rot r;
+            if constexpr (QPK > 1) {
+                const float2 cs = rot_tab[rot_row * kRotRow + d];
+                r.c = cs.x;
+                r.s = cs.y;
+            } else {
+                r = rope_rot((float)pos, rope_freq(a.rope_base, d));
+            }
             const float q0 = y0 * r.c - y1 * r.s;
             const float q1 = y0 * r.s + y1 * r.c;
             qb[s][j] = (_Float16)q0;
@@ -764,41 +800,71 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
             pf_half8 ka[4];
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
-                ka[kt] = *reinterpret_cast<const pf_half8*>(&ks[buf][16 * kt + tl][32 * s + 8 * g]);
+                ka[kt] = *reinterpret_cast<const pf_half8*>(&ks[buf][16 * kt + tl][8 * ((4 * s + g) ^ tl)]);
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt], qb[s], sc[kt], 0, 0, 0);
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt], ql[s], sc[kt], 0, 0, 0);
         }
+        // keys past a token's position are masked; a block wholly at or below
+        // the wave's first position needs no mask (a wave-uniform test)
         float bmax = -INFINITY;
+        if (kb * kPfKeys + kPfKeys - 1 <= a.p0 + t0) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
+            for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kb * kPfKeys + 16 * kt + 4 * g + i;
-                const float v = key <= pos ? sc[kt][i] * a.scale : -INFINITY;
-                sc[kt][i] = v;
-                bmax = fmaxf(bmax, v);
+                for (int i = 0; i < 4; ++i) {
+                    sc[kt][i] *= a.scale;
+                    bmax = fmaxf(bmax, sc[kt][i]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = kb * kPfKeys + 16 * kt + 4 * g + i;
+                    const float v = key <= pos ? sc[kt][i] * a.scale : -INFINITY;
+                    sc[kt][i] = v;
+                    bmax = fmaxf(bmax, v);
+                }
             }
         }
         bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-        const float m_new = fmaxf(m_run, bmax);
-        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        l_run *= corr;
+        // Lazy rescaling: the reference point m_run moves (to the block's
+        // maximum) only when that maximum passes it by more than kPfLazy.
+        // Until then the probabilities exp2(s - m_run) stay below
+        // 2^kPfLazy, inside f16 range for the hi/lo split, and O and l keep
+        // their scale; O / l is the same softmax. The first block always
+        // moves it (from -FLT_MAX, with a zero correction).
+        const bool move = bmax > m_run + kPfLazy;
+        if (__any(move)) {
+            const float m_new = move ? bmax : m_run;
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= corr;
 #pragma unroll
-        for (int d = 0; d < 8; ++d) o[d] *= corr;
+            for (int d = 0; d < 8; ++d) o[d] *= corr;
+        }
+        // probabilities in pairs: hi = f16(p) and lo = f16(p - hi), each pair
+        // converted by one packed instruction (round toward zero: hi + lo
+        // still carries 22 bits of p, since p - hi is exact in f32)
         pf_half8 pb[2], pl[2];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float pv = __builtin_amdgcn_exp2f(sc[kt][i] - m_new);
-                l_run += pv;
-                const _Float16 ph = (_Float16)pv;
-                pb[kt >> 1][4 * (kt & 1) + i] = ph;
-                pl[kt >> 1][4 * (kt & 1) + i] = (_Float16)(pv - (float)ph);
+            for (int i = 0; i < 4; i += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(sc[kt][i] - m_run);
+                const float p1 = __builtin_amdgcn_exp2f(sc[kt][i + 1] - m_run);
+                l_run += p0;
+                l_run += p1;
+                const auto h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+                const auto r = __builtin_amdgcn_cvt_pkrtz(p0 - (float)h[0], p1 - (float)h[1]);
+                pb[kt >> 1][4 * (kt & 1) + i] = h[0];
+                pb[kt >> 1][4 * (kt & 1) + i + 1] = h[1];
+                pl[kt >> 1][4 * (kt & 1) + i] = r[0];
+                pl[kt >> 1][4 * (kt & 1) + i + 1] = r[1];
             }
         }
         // O^T += V^T P^T over the block's two 32-key steps, issued
