@@ -1,4 +1,4 @@
-// f32-faithful batched k-quant GEMV on the bf16 matrix cores (gfx950 /
+// f32-faithful batched k-quant GEMV on the matrix cores (gfx950 /
 // CDNA4, wave64): the default GEMV_WARP arithmetic for 9..64 members, with
 // the weights read once for the whole batch (the reference's batch GEMV reads
 // them once per launch of at most 8 members: q4_k.cu:161-258,
@@ -6,38 +6,46 @@
 // its rows are bit-identical to the single-member call, as the reference
 // qualifies its batch lane (cuda_reference.rs:5322-5334).
 //
-// Why this is f32 arithmetic
-//  - Activations: each f32 value x is split exactly into three bf16 pieces,
-//    x = hi + mid + lo: hi keeps the top 8 significand bits (truncation),
-//    mid the top 8 of the exact remainder x - hi, lo the remaining <= 8 bits
-//    (x - hi - mid is exactly representable in bf16). Nothing is rounded.
-//  - Quants are small integers: Q4_K / Q5_K quants enter as 128 + q (0..31
-//    plus 128 is exact in bf16 and takes one byte permute per two quants),
-//    Q6_K as q - 32 (signed, exact).
-//  - v_mfma_f32_16x16x32_bf16 multiplies exactly (8 x 8 significand bits)
-//    and accumulates in f32. Three MFMAs per 32-element group (one per
-//    piece, chained through the accumulator) give S'_g = sum_i (128 + q_i) x_i
-//    = S_g + 128 X_g for 16 members x 16 weight rows, rounded only by the f32
-//    accumulation.
-//  - The epilogue is the f32 wave path's: part += (d*sc_g) * S'_g (f32 FMA
-//    per value) and, for Q4_K / Q5_K, the minimum term
-//    sum_g (dmin*m_g + 128 d*sc_g) * X_g (X_g the f32 group sums of x) on
-//    v_mfma_f32_16x16x4_f32 ([member][group] x [group][row]), which also
-//    takes the 128 X_g back out. Q6_K scale groups are 16 elements: the B
-//    operand is masked to each half of the 32-element MFMA group (S_g of each
-//    half), and Q6_K has no minimum term.
-//  So the products are the dequantised weights times x, regrouped per scale
-//  group like the wave path's, with f32 rounding in the sums; the order
-//  differs, so results agree with the sequential f32 GEMV to f32 rounding
+// Why this is f32 arithmetic (two forms, by weight type)
+//  - Q4_K / Q5_K, f16 form. The quants times their six-bit group scale are
+//    exact f16 values: q sc <= 31 * 63 = 1953 < 2^11, built per pair as
+//    (1024 + q) sc - 1024 sc by one packed FMA with a single (exact)
+//    rounding. Activations are scaled per (member, super-block) by a power
+//    of two 2^e that puts the block's largest |x| in [2^14, 2^15), then split
+//    into two f16 pieces, hi = f16(x 2^e) and lo = f16(x 2^e - hi): 22
+//    significant bits for |x| down to 2^-29 of the block maximum.
+//    v_mfma_f32_16x16x32_f16 multiplies exactly (11 x 11 bits) and
+//    accumulates in f32, so one chain per piece runs through all 8 groups of
+//    a super-block: S = sum (sc_g q_i) (x_i 2^e). The block epilogue adds
+//    (d 2^-e) S per value, and the minimum term sum_g (dmin m_g) X_g (X_g the
+//    f32 group sums of x) runs on v_mfma_f32_16x16x4_f32 ([member][group] x
+//    [group][row]). Because each element carries its own scale, an MFMA step
+//    may mix groups: lane quarter kq reads the row's 16-byte quant pieces at
+//    16 kq and 64 + 16 kq (the four lanes of a row read 64 contiguous bytes
+//    per load), and step c = 4L + 2h + r takes nibble h of bytes 8r .. + 7 of
+//    its piece L; the pack writes the activations in that order.
+//  - Q6_K, bf16 form. (q - 32) sc needs up to 12 bits, more than f16 holds
+//    exactly, so the scale stays in an f32 epilogue per scale group. Each
+//    f32 value x is split exactly into three bf16 pieces, x = hi + mid + lo:
+//    hi keeps the top 8 significand bits (truncation), mid the top 8 of the
+//    exact remainder, lo the remaining <= 8 bits. Quants enter as q - 32
+//    (signed, exact). Three v_mfma_f32_16x16x32_bf16 per 32-element group
+//    give S_g of each 16-element scale group (the B operand masked to each
+//    half) for 16 members x 16 rows; the epilogue adds (d sc_g) S_g.
+//  So the products are the dequantised weights times x, with f32 rounding in
+//  the sums (and, in the f16 form, x rounded to 22 bits); the order differs
+//  from the sequential f32 GEMV, so results agree with it to f32 rounding
 //  (within 5e-5 normwise on wide-dynamic-range activations), not bit for bit.
 //
 // Layout (pack_f32mma_kernel, one launch per product)
-//  - Member tile mt of 16, super-block b, 32-element group g, piece s: 64
-//    lanes x 16 bytes in the MFMA A-operand order: lane l = member (l % 16)
-//    of the tile, 8 bf16 of elements 8 (l / 16) .. + 7 of the group.
+//  - Member tile mt of 16, super-block b, MFMA step c, piece s: 64 lanes x
+//    16 bytes in the MFMA A-operand order: lane l = member (l % 16) of the
+//    tile and its 8 values of lane quarter l / 16 (bf16 form: elements
+//    8 (l / 16) .. + 7 of group c; f16 form: the step order above).
 //  - X sums (Q4_K / Q5_K minimum term): per (tile, block) 64 lanes x 2 f32,
 //    lane mi + 16 q holding X of groups q and 4 + q of member mi (the A
-//    operand of the two f32 MFMAs per block).
+//    operand of the two f32 MFMAs per block); f16 form: the 16 members'
+//    2^-e per (tile, block).
 //  - Per-member partial sums of x^2 per pack workgroup, for RMSNorm: the
 //    product divides its outputs by rms(x) (the wave GEMV's factorisation
 //    y = (W (x * gamma)) / rms).
@@ -61,6 +69,8 @@
 #include "kquant_device.hpp"
 #include "kquant_launch.hpp"
 
+#include <float.h>
+
 #include <algorithm>
 #include <type_traits>
 
@@ -73,10 +83,11 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kOOR = 0xffffff00u;  // buffer offset past any tensor: loads return 0, stores drop
 constexpr int kPackBlocks = 2;          // super-blocks per pack workgroup (one wave)
-constexpr int kPieces = 3;
 constexpr uint32_t kPieceBytes = 64 * 16;                               // one piece of one group
-constexpr uint32_t kFragBlockBytes = 8 * kPieces * kPieceBytes;         // 24 KiB per (member tile, block)
 constexpr uint32_t kXsumBlockBytes = 64 * 2 * 4;                        // per (member tile, block)
+constexpr uint32_t kIscaleBlockBytes = 16 * 4;                          // per (member tile, block)
+// Activation pieces per element: three bf16 for Q6_K, two f16 for Q4_K / Q5_K.
+template <int T> constexpr int pieces_of() { return T == kQ6K ? 3 : 2; }
 
 __device__ __forceinline__ uint32_t top16(float f) { return __builtin_bit_cast(uint32_t, f) & 0xffff0000u; }
 
@@ -95,6 +106,7 @@ struct PackArgs {
     int K;
 };
 
+template <int PIECES>
 __global__ __launch_bounds__(64) void pack_f32mma_kernel(PackArgs a) {
     const int m = blockIdx.y;
     const int tid = threadIdx.x;
@@ -132,35 +144,73 @@ __global__ __launch_bounds__(64) void pack_f32mma_kernel(PackArgs a) {
             }
         }
     }
-    // x = hi + mid + lo, each piece the top 16 bits of an f32 (a bf16)
-    uint32_t hw[8], mw[8], lw[8];
     float xs = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        hw[j] = top16(v[j]);
-        const float r1 = v[j] - __builtin_bit_cast(float, hw[j]);
-        mw[j] = top16(r1);
-        const float r2 = r1 - __builtin_bit_cast(float, mw[j]);
-        lw[j] = top16(r2);  // r2 has at most 8 significant bits: exact
-        xs += v[j];
-    }
+    for (int j = 0; j < 8; ++j) xs += v[j];
     xs += __shfl_xor(xs, 1, 64);
     xs += __shfl_xor(xs, 2, 64);  // X_g over the four 8-element chunks of group g
-    if (live) {
-        const int mt = m >> 4, mi = m & 15;
-        const uint32_t blk = (uint32_t)(mt * nb + b);
-        uint8_t* fr = a.act + a.L.frag + (blk * 8u + (uint32_t)g) * kPieces * kPieceBytes + (uint32_t)(mi + 16 * kq) * 16u;
-        const uint32_t* pieces[3] = {hw, mw, lw};
+    const int mt = m >> 4, mi = m & 15;
+    const uint32_t blk = (uint32_t)(mt * nb + b);
+    // the bf16 form keeps group order (step g, lane quarter kq); the f16 form
+    // puts elements 8 kq .. + 7 of group g at step 4 (g >> 2) + 2 (g & 1) +
+    // (kq & 1), lane quarter 2 ((g >> 1) & 1) + (kq >> 1) (the product's
+    // weight piece order)
+    const uint32_t step = PIECES == 3 ? (uint32_t)g : (uint32_t)(4 * (g >> 2) + 2 * (g & 1) + (kq & 1));
+    const uint32_t quarter = PIECES == 3 ? (uint32_t)kq : (uint32_t)(2 * ((g >> 1) & 1) + (kq >> 1));
+    uint8_t* fr = a.act + a.L.frag + (blk * 8u + step) * PIECES * kPieceBytes + ((uint32_t)mi + 16u * quarter) * 16u;
+    if constexpr (PIECES == 3) {
+        // x = hi + mid + lo, each piece the top 16 bits of an f32 (a bf16)
+        uint32_t hw[8], mw[8], lw[8];
 #pragma unroll
-        for (int s = 0; s < kPieces; ++s) {
-            const uint32_t* p = pieces[s];
-            *reinterpret_cast<uint4*>(fr + s * kPieceBytes) =
-                make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7]));
+        for (int j = 0; j < 8; ++j) {
+            hw[j] = top16(v[j]);
+            const float r1 = v[j] - __builtin_bit_cast(float, hw[j]);
+            mw[j] = top16(r1);
+            const float r2 = r1 - __builtin_bit_cast(float, mw[j]);
+            lw[j] = top16(r2);  // r2 has at most 8 significant bits: exact
         }
-        if (kq == 0) {
-            float* xsum = reinterpret_cast<float*>(a.act + a.L.xsum);
-            xsum[(blk * 64u + (uint32_t)(mi + 16 * (g & 3))) * 2u + (uint32_t)(g >> 2)] = xs;
+        if (live) {
+            const uint32_t* pieces[3] = {hw, mw, lw};
+#pragma unroll
+            for (int s = 0; s < 3; ++s) {
+                const uint32_t* p = pieces[s];
+                *reinterpret_cast<uint4*>(fr + s * kPieceBytes) =
+                    make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7]));
+            }
         }
+    } else {
+        // The block's power-of-two scale 2^e puts its largest |x| in
+        // [2^14, 2^15): then x 2^e = hi + lo with hi = f16(x 2^e) and
+        // lo = f16(x 2^e - hi) (both RNE) keeps 22 significant bits of x
+        // for |x| down to 2^-29 of the block maximum. The product applies
+        // 2^-e per (member, block).
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        int ex = 0;
+        if (mx > 0.f && mx <= FLT_MAX) (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+        const int e = min(126, max(-126, 15 - ex));
+        const float sc = __builtin_ldexpf(1.0f, e);
+        uint32_t hp[4], lp[4];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const float x0 = v[j] * sc, x1 = v[j + 1] * sc;
+            const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+            const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+            hp[j / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            lp[j / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
+        if (live) {
+            *reinterpret_cast<uint4*>(fr) = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+            *reinterpret_cast<uint4*>(fr + kPieceBytes) = make_uint4(lp[0], lp[1], lp[2], lp[3]);
+            if (c == 0) reinterpret_cast<float*>(a.act + a.L.iscale)[blk * 16u + (uint32_t)mi] = __builtin_ldexpf(1.0f, -e);
+        }
+    }
+    if (live && kq == 0) {
+        float* xsum = reinterpret_cast<float*>(a.act + a.L.xsum);
+        xsum[(blk * 64u + (uint32_t)(mi + 16 * (g & 3))) * 2u + (uint32_t)(g >> 2)] = xs;
     }
     // this workgroup's share of sum(x^2), for RMSNorm (summed in part order by the product)
     const float ws = wave_sum(ssq);
@@ -197,8 +247,12 @@ struct F32MmaArgs {
 };
 
 template <int T> struct WRaw;
-template <> struct WRaw<kQ4K> { uint4 h; uint2 q[4]; };
-template <> struct WRaw<kQ5K> { uint4 h; uint2 qh; uint2 q[4]; };
+// Q4_K / Q5_K: the header and the lane's two 16-byte quant pieces, bytes
+// 16 kq .. + 15 and 64 + 16 kq .. + 15 of the 128 (elements 16 (kq & 1) .. + 15
+// of groups 2 (kq >> 1), + 1 and 4 + 2 (kq >> 1), + 1); Q5_K also the 16
+// high-bit bytes of those elements.
+template <> struct WRaw<kQ4K> { uint4 h, q0, q1; };
+template <> struct WRaw<kQ5K> { uint4 h, qh, q0, q1; };
 // Q6_K: the 16 int8 scales, d, and for each half n the 8 low-nibble bytes of
 // both 32-byte quadrant pairs and the 8 qh bytes.
 template <> struct WRaw<kQ6K> { uint4 sc; uint32_t d16; uint2 ql[4]; uint2 qh[2]; };
@@ -221,14 +275,12 @@ __device__ __forceinline__ void load_w(WRaw<T>& d, __amdgpu_buffer_rsrc_t r, boo
         for (int n = 0; n < 2; ++n) d.qh[n] = load_b64(r, live ? base + 128u + 32u * n + 8u * kq : kOOR);
     } else {
         d.h = load_b128(r, live ? base : kOOR);
-        if constexpr (T == kQ5K) {
-            d.qh = load_b64(r, live ? base + 16u + 8u * kq : kOOR);
-#pragma unroll
-            for (int p = 0; p < 4; ++p) d.q[p] = load_b64(r, live ? base + 48u + 32u * p + 8u * kq : kOOR);
-        } else {
-#pragma unroll
-            for (int p = 0; p < 4; ++p) d.q[p] = load_b64(r, live ? base + 16u + 32u * p + 8u * kq : kOOR);
-        }
+        // quants at 16 (Q4_K) or 48 (Q5_K, after the 32 high-bit bytes at 16)
+        const uint32_t qs = T == kQ5K ? 48u : 16u;
+        if constexpr (T == kQ5K) d.qh = load_b128(r, live ? base + 16u + 16u * (kq & 1) : kOOR);
+        // the four lanes of a row read 64 contiguous bytes per load
+        d.q0 = load_b128(r, live ? base + qs + 16u * kq : kOOR);
+        d.q1 = load_b128(r, live ? base + qs + 64u + 16u * kq : kOOR);
     }
 }
 
@@ -254,6 +306,23 @@ __device__ __forceinline__ v8bf bf16_of_sbytes(uint32_t w0, uint32_t w1) {
     }
     const uint4 b = make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
     return __builtin_bit_cast(v8bf, b);
+}
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+// Eight unsigned byte quants q < 32 times the group scale sc (< 64) as f16,
+// exactly: the byte permute makes 1024 + q (f16 0x6400 | q), and the packed
+// FMA (1024 + q) * sc - 1024 sc rounds once, to the exact q * sc <= 1953.
+__device__ __forceinline__ v8h f16_scaled_quants(uint32_t w0, uint32_t w1, h2v sc, h2v nsc) {
+    const uint32_t c = 0x64646464u;
+    const uint32_t p[4] = {__builtin_amdgcn_perm(c, w0, 0x04010400u), __builtin_amdgcn_perm(c, w0, 0x04030402u),
+                           __builtin_amdgcn_perm(c, w1, 0x04010400u), __builtin_amdgcn_perm(c, w1, 0x04030402u)};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        o[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2v, p[k]), sc, nsc));
+    return __builtin_bit_cast(v8h, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
 // Q6_K quants of 32-element group g minus 32, as signed bytes (half n = g / 4,
@@ -288,8 +357,10 @@ __device__ __forceinline__ void q6_group(const WRaw<kQ6K>& d, int g, uint32_t& o
 template <int T, int R, int MT, bool PAIR, int W>
 __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
     constexpr int BB = BlockTraits<T>::bytes;
-    constexpr int FRAGS = MT * 8 * kPieces;  // 1 KB fragment loads per block
+    constexpr int PC = pieces_of<T>();
+    constexpr int FRAGS = MT * 8 * PC;  // 1 KB fragment loads per block
     constexpr int XS = T == kQ6K ? 0 : 2 * MT;  // 256 B X-sum loads per block
+    constexpr int IS = T == kQ6K ? 0 : MT;      // inverse block scales (16 lanes x 4 B) per block
     static_assert(!PAIR || R % 2 == 0, "pairs split the tiles into gate and up halves");
     // two slots as separate objects: the compiler can then tell that reads of
     // one do not alias the loads into the other in flight
@@ -297,6 +368,8 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
     __shared__ __attribute__((aligned(16))) uint4 fa1[FRAGS * 64];
     __shared__ __attribute__((aligned(16))) float2 xa0[XS ? MT * 64 : 1];
     __shared__ __attribute__((aligned(16))) float2 xa1[XS ? MT * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float isa0[IS ? MT * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float isa1[IS ? MT * 64 : 1];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -362,9 +435,9 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
 #pragma unroll
         for (int j = 0; j < FRAGS; ++j) {
             if (j % W != wave) continue;
-            const int mt = j / (8 * kPieces);
-            const uint32_t off = A.L.frag + ((uint32_t)((tile0 + mt) * nb + b) * (8u * kPieces) +
-                                             (uint32_t)(j % (8 * kPieces))) * kPieceBytes + (uint32_t)lane * 16u;
+            const int mt = j / (8 * PC);
+            const uint32_t off = A.L.frag + ((uint32_t)((tile0 + mt) * nb + b) * (8u * PC) +
+                                             (uint32_t)(j % (8 * PC))) * kPieceBytes + (uint32_t)lane * 16u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (__attribute__((address_space(3))) void*)&fa[j * 64], 16,
                                                      (int)(lb ? off : kOOR), 0, 0, 0);
         }
@@ -377,6 +450,14 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ar, (__attribute__((address_space(3))) void*)(reinterpret_cast<float*>(xa) + h * 64), 4,
                 (int)(lb ? off : kOOR), 0, 0, 0);
+        }
+        float* const isa = SL ? isa1 : isa0;
+#pragma unroll
+        for (int mt = 0; mt < IS; ++mt) {
+            if ((FRAGS + XS + mt) % W != wave) continue;
+            const uint32_t off = A.L.iscale + (uint32_t)((tile0 + mt) * nb + b) * kIscaleBlockBytes + (uint32_t)lane * 4u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (__attribute__((address_space(3))) void*)(isa + mt * 64), 4,
+                                                     (int)(lb && lane < 16 ? off : kOOR), 0, 0, 0);
         }
         // written behind the compiler's back: LDS reads must not move across
         asm volatile("" ::: "memory");
@@ -417,15 +498,8 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
                 scw_hi[i] = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
                 const uint32_t mnw_lo = h.z & 0x3f3f3f3fu;
                 const uint32_t mnw_hi = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-                // the quants enter the MFMAs as 128 + q (see bf16_128_plus),
-                // so group g's sum is S'_g = S_g + 128 X_g; the minimum-term
-                // operand takes the 128 (d sc_g) X_g back out:
-                //   (d sc_g) S'_g - (dmin m_g + 128 d sc_g) X_g = (d sc_g) S_g - (dmin m_g) X_g
-                // (exact up to f32 rounding of the two products and sums)
-                const float sc0 = (float)((scw_lo[i] >> (8 * kq)) & 0xffu);
-                const float sc1 = (float)((scw_hi[i] >> (8 * kq)) & 0xffu);
-                bmin0[i] = dmn * (float)((mnw_lo >> (8 * kq)) & 0xffu) + 128.0f * (dd[i] * sc0);
-                bmin1[i] = dmn * (float)((mnw_hi >> (8 * kq)) & 0xffu) + 128.0f * (dd[i] * sc1);
+                bmin0[i] = dmn * (float)((mnw_lo >> (8 * kq)) & 0xffu);
+                bmin1[i] = dmn * (float)((mnw_hi >> (8 * kq)) & 0xffu);
             }
         }
         if constexpr (T != kQ6K) {
@@ -440,41 +514,93 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
                     macc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs.y, bmin1[i], macc[i][mt], 0, 0, 0);
                 }
             }
-        }
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            v8bf bq[R], bq1[R];
+            // S = sum over the block of (sc_g q) (2^e x): one chain per
+            // activation piece through the block's 8 MFMA steps, then
+            // acc += (d 2^-e) S. Step c = 4L + 2h + r takes, in lane quarter
+            // kq, nibble h of bytes 8r .. + 7 of the lane's piece L: elements
+            // 16 (kq & 1) + 8r .. + 7 of group 4L + 2 (kq >> 1) + h. Each step
+            // mixes four scale groups, every element carrying its own scale
+            // (the packed activations follow the same order).
+            const v4f zero = {0.f, 0.f, 0.f, 0.f};
+            v4f ch[R][MT], cl[R][MT];
+            h2v sc2[R][4], nsc2[R][4];
 #pragma unroll
             for (int i = 0; i < R; ++i) {
-                if constexpr (T == kQ6K) {
+#pragma unroll
+                for (int lh = 0; lh < 4; ++lh) {
+                    const uint32_t scw = (lh >> 1) ? scw_hi[i] : scw_lo[i];
+                    const float scf = (float)((scw >> (8 * (2 * (kq >> 1) + (lh & 1)))) & 0xffu);
+                    const _Float16 a = (_Float16)scf, na = (_Float16)(-1024.0f * scf);
+                    sc2[i][lh] = h2v{a, a};
+                    nsc2[i][lh] = h2v{na, na};
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const int L = c >> 2, hn = (c >> 1) & 1, r = c & 1;
+                v8h bq[R];
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    const uint4 qw = L ? ring[s][i].q1 : ring[s][i].q0;
+                    const uint32_t w0 = r ? qw.z : qw.x, w1 = r ? qw.w : qw.y;
+                    uint32_t q0 = (w0 >> (4 * hn)) & 0x0f0f0f0fu;
+                    uint32_t q1 = (w1 >> (4 * hn)) & 0x0f0f0f0fu;
+                    if constexpr (T == kQ5K) {
+                        // fifth bit of element e of group g: bit g of qh[e]
+                        const uint4 hw = ring[s][i].qh;
+                        const uint32_t h0 = r ? hw.z : hw.x, h1 = r ? hw.w : hw.y;
+                        const int gb = 4 * L + 2 * (kq >> 1) + hn;
+                        q0 |= ((h0 >> gb) & 0x01010101u) << 4;
+                        q1 |= ((h1 >> gb) & 0x01010101u) << 4;
+                    }
+                    bq[i] = f16_scaled_quants(q0, q1, sc2[i][2 * L + hn], nsc2[i][2 * L + hn]);
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int f = (mt * 8 + c) * PC;
+                    const v8h a0 = __builtin_bit_cast(v8h, fa[(f + 0) * 64 + lane]);
+                    const v8h a1 = __builtin_bit_cast(v8h, fa[(f + 1) * 64 + lane]);
+#pragma unroll
+                    for (int i = 0; i < R; ++i) {
+                        ch[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bq[i], c ? ch[i][mt] : zero, 0, 0, 0);
+                        cl[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bq[i], c ? cl[i][mt] : zero, 0, 0, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const float* const isa = s ? isa1 : isa0;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const float4 inv4 = *reinterpret_cast<const float4*>(isa + mt * 64 + 4 * kq);
+                const float inv[4] = {inv4.x, inv4.y, inv4.z, inv4.w};
+#pragma unroll
+                for (int i = 0; i < R; ++i)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        acc[i][mt][t] = __builtin_fmaf(dd[i] * inv[t], ch[i][mt][t] + cl[i][mt][t], acc[i][mt][t]);
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                v8bf bq[R], bq1[R];
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
                     uint32_t q0, q1;
                     q6_group(ring[s][i], g, q0, q1);
                     // scale groups 2g (elements 0-15: lanes kq 0-1) and 2g + 1 (kq 2-3)
                     const bool low = kq < 2;
                     bq[i] = bf16_of_sbytes(low ? q0 : 0u, low ? q1 : 0u);
                     bq1[i] = bf16_of_sbytes(low ? 0u : q0, low ? 0u : q1);
-                } else {
-                    const int p = g >> 1, sh = 4 * (g & 1);
-                    uint32_t q0 = (ring[s][i].q[p].x >> sh) & 0x0f0f0f0fu;
-                    uint32_t q1 = (ring[s][i].q[p].y >> sh) & 0x0f0f0f0fu;
-                    if constexpr (T == kQ5K) {
-                        // fifth bit of element j of group g: bit g of qh[j]
-                        q0 |= ((ring[s][i].qh.x >> g) & 0x01010101u) << 4;
-                        q1 |= ((ring[s][i].qh.y >> g) & 0x01010101u) << 4;
-                    }
-                    bq[i] = bf16_128_plus(q0, q1);
                 }
-            }
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const int f = (mt * 8 + g) * kPieces;
-                const v8bf a0 = __builtin_bit_cast(v8bf, fa[(f + 0) * 64 + lane]);
-                const v8bf a1 = __builtin_bit_cast(v8bf, fa[(f + 1) * 64 + lane]);
-                const v8bf a2 = __builtin_bit_cast(v8bf, fa[(f + 2) * 64 + lane]);
-                const v4f zero = {0.f, 0.f, 0.f, 0.f};
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int f = (mt * 8 + g) * PC;
+                    const v8bf a0 = __builtin_bit_cast(v8bf, fa[(f + 0) * 64 + lane]);
+                    const v8bf a1 = __builtin_bit_cast(v8bf, fa[(f + 1) * 64 + lane]);
+                    const v8bf a2 = __builtin_bit_cast(v8bf, fa[(f + 2) * 64 + lane]);
+                    const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int i = 0; i < R; ++i) {
-                    if constexpr (T == kQ6K) {
+                    for (int i = 0; i < R; ++i) {
                         v4f c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[i], zero, 0, 0, 0);
                         v4f c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq1[i], zero, 0, 0, 0);
                         c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[i], c0, 0, 0, 0);
@@ -489,20 +615,12 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
 #pragma unroll
                         for (int t = 0; t < 4; ++t)
                             acc[i][mt][t] = __builtin_fmaf(s1, c1[t], __builtin_fmaf(s0, c0[t], acc[i][mt][t]));
-                    } else {
-                        v4f c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[i], zero, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[i], c, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bq[i], c, 0, 0, 0);
-                        const uint32_t scw = g < 4 ? scw_lo[i] : scw_hi[i];
-                        const float a_g = dd[i] * (float)((scw >> (8 * (g & 3))) & 0xffu);
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) acc[i][mt][t] = __builtin_fmaf(a_g, c[t], acc[i][mt][t]);
                     }
                 }
+                // one group's conversions and MFMA chains at a time (bounds the
+                // registers live across groups)
+                __builtin_amdgcn_sched_barrier(0);
             }
-            // one group's conversions and MFMA chains at a time (bounds the
-            // registers live across groups)
-            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -747,7 +865,7 @@ bool rows_tile_aligned(const WaveGemvArgs& a) {
 
 }  // namespace
 
-F32MmaLayout f32mma_layout(int members, int K) {
+F32MmaLayout f32mma_layout(int members, int K, int pieces) {
     F32MmaLayout L{};
     const int nb = K / 256;
     L.nb = nb;
@@ -755,8 +873,9 @@ F32MmaLayout f32mma_layout(int members, int K) {
     L.parts = (nb + kPackBlocks - 1) / kPackBlocks;
     const uint32_t blocks = (uint32_t)L.tiles * (uint32_t)nb;
     L.frag = 0;
-    L.xsum = L.frag + blocks * kFragBlockBytes;
-    L.ssq = L.xsum + blocks * kXsumBlockBytes;
+    L.xsum = L.frag + blocks * 8u * (uint32_t)pieces * kPieceBytes;
+    L.iscale = L.xsum + blocks * kXsumBlockBytes;
+    L.ssq = L.iscale + blocks * kIscaleBlockBytes;
     L.total = L.ssq + (uint32_t)members * (uint32_t)L.parts * 4u;
     return L;
 }
@@ -772,7 +891,8 @@ hipError_t launch_gemv_f32mma(int value_type, const WaveGemvArgs& a, void* scrat
     if (!f32mma_supported(value_type, a) || scratch == nullptr || a.count < 1 || a.count > kMaxGroup) {
         return hipErrorInvalidValue;
     }
-    const F32MmaLayout L = f32mma_layout(a.members, a.K);
+    const int pieces = value_type == kQ6K ? 3 : 2;
+    const F32MmaLayout L = f32mma_layout(a.members, a.K, pieces);
     if (L.total > scratch_bytes) return hipErrorInvalidValue;
     PackArgs p{};
     p.x = a.x;
@@ -781,7 +901,11 @@ hipError_t launch_gemv_f32mma(int value_type, const WaveGemvArgs& a, void* scrat
     p.act = static_cast<uint8_t*>(scratch);
     p.L = L;
     p.K = a.K;
-    hipLaunchKernelGGL(pack_f32mma_kernel, dim3((unsigned)L.parts, (unsigned)a.members), dim3(64), 0, stream, p);
+    if (pieces == 3) {
+        hipLaunchKernelGGL(pack_f32mma_kernel<3>, dim3((unsigned)L.parts, (unsigned)a.members), dim3(64), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(pack_f32mma_kernel<2>, dim3((unsigned)L.parts, (unsigned)a.members), dim3(64), 0, stream, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     F32MmaArgs m{};

@@ -126,12 +126,13 @@ constexpr int kF32MmaMaxWaves = 4;  // K-split waves per workgroup
 // 256): bf16-piece MFMA fragments, f32 group sums, per-workgroup partial sums
 // of squares.
 struct F32MmaLayout {
-    uint32_t frag, xsum, ssq, total;
+    uint32_t frag, xsum, iscale, ssq, total;
     int nb;     // super-blocks of K
     int tiles;  // member tiles of 16
     int parts;  // pack workgroups per member
 };
-F32MmaLayout f32mma_layout(int members, int K);
+// pieces: 3 (bf16 pieces, Q6_K) or 2 (f16 pieces, Q4_K / Q5_K); 3 sizes both.
+F32MmaLayout f32mma_layout(int members, int K, int pieces = 3);
 // Whether launch_gemv_f32mma serves this call (type, 9..64 members, K, pairs
 // of whole tiles, not both RMSNorm and SwiGLU prologues).
 bool f32mma_supported(int value_type, const WaveGemvArgs& args);
