@@ -840,16 +840,29 @@ hipError_t launch_mt(const F32MmaArgs& a0, size_t partial_bytes, int cu_count, h
     return launch_shape<T, R, MT, false>(a, groups, stream);
 }
 
-// One launch per 32 members (two member tiles: their fragments of a block,
-// double-buffered, fill 98 KB of LDS).
+// Member tiles per launch: the f16 form's fragments of a block (16 KB per
+// tile, double-buffered) let four tiles (64 members) share one weight stream
+// in 128 KB of LDS; the bf16 form's (24 KB per tile) two.
+template <int T> constexpr int max_tiles() { return T == kQ6K ? 2 : 4; }
+
 template <int T>
 hipError_t launch_t(const F32MmaArgs& a, size_t partial_bytes, int cu_count, hipStream_t stream) {
-    for (int m0 = 0; m0 < a.members; m0 += 2 * 16) {
+    constexpr int kStep = 16 * max_tiles<T>();
+    for (int m0 = 0; m0 < a.members; m0 += kStep) {
         F32MmaArgs c = a;
         c.member0 = m0;
-        c.count_here = std::min(2 * 16, a.members - m0);
-        const hipError_t e = c.count_here <= 16 ? launch_mt<T, 1>(c, partial_bytes, cu_count, stream)
-                                                : launch_mt<T, 2>(c, partial_bytes, cu_count, stream);
+        c.count_here = std::min(kStep, a.members - m0);
+        const int tiles = (c.count_here + 15) / 16;
+        hipError_t e;
+        if constexpr (max_tiles<T>() == 4) {
+            e = tiles == 1   ? launch_mt<T, 1>(c, partial_bytes, cu_count, stream)
+                : tiles == 2 ? launch_mt<T, 2>(c, partial_bytes, cu_count, stream)
+                : tiles == 3 ? launch_mt<T, 3>(c, partial_bytes, cu_count, stream)
+                             : launch_mt<T, 4>(c, partial_bytes, cu_count, stream);
+        } else {
+            e = tiles == 1 ? launch_mt<T, 1>(c, partial_bytes, cu_count, stream)
+                           : launch_mt<T, 2>(c, partial_bytes, cu_count, stream);
+        }
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
