@@ -797,14 +797,15 @@ __global__ __launch_bounds__(256) void f32mma_reduce_kernel(F32MmaArgs A) {
 // Row tiles per wave. Measured on MI355X at the Qwen3-8B FFN shapes (M = 16
 // and 32): two tiles run 10-20% faster than four, whose registers leave one
 // wave per SIMD.
-template <int T> constexpr int tiles_per_wave() { return 2; }
+template <int MT, bool PAIR> constexpr int tiles_per_wave() { return MT >= 3 && !PAIR ? 1 : 2; }
 // waves per workgroup (they share the LDS fragments): eight for one member
-// tile, four for two (whose registers allow one wave per SIMD)
-template <int MT> constexpr int waves_per_group() { return MT == 1 ? 8 : 4; }
+// tile or one row tile per wave, four otherwise (whose registers allow one
+// wave per SIMD)
+template <int MT, int R> constexpr int waves_per_group() { return MT == 1 || R == 1 ? 8 : 4; }
 
 template <int T, int R, int MT, bool PAIR>
 hipError_t launch_shape(const F32MmaArgs& a, int groups, hipStream_t stream) {
-    constexpr int W = waves_per_group<MT>();
+    constexpr int W = waves_per_group<MT, R>();
     hipLaunchKernelGGL((f32mma_gemv_kernel<T, R, MT, PAIR, W>), dim3((unsigned)groups, (unsigned)a.splits),
                        dim3(64 * W), 0, stream, a);
     hipError_t e = hipGetLastError();
@@ -819,14 +820,23 @@ hipError_t launch_shape(const F32MmaArgs& a, int groups, hipStream_t stream) {
 // K (at least two super-blocks per split, as far as the partial space
 // allows); the split depends on the shape and member count only, never on
 // the members' values.
+template <int T, int R, int MT, bool PAIR>
+hipError_t launch_split(F32MmaArgs a, int nb, size_t partial_bytes, int cu_count, hipStream_t stream);
+
 template <int T, int MT>
 hipError_t launch_mt(const F32MmaArgs& a0, size_t partial_bytes, int cu_count, hipStream_t stream) {
-    constexpr int R = tiles_per_wave<T>();
     F32MmaArgs a = a0;
     const int nb = a.K >> 8;
     const bool pair = a.pair_swiglu != 0;
+    if (pair) return launch_split<T, tiles_per_wave<MT, true>(), MT, true>(a, nb, partial_bytes, cu_count, stream);
+    return launch_split<T, tiles_per_wave<MT, false>(), MT, false>(a, nb, partial_bytes, cu_count, stream);
+}
+
+template <int T, int R, int MT, bool PAIR>
+hipError_t launch_split(F32MmaArgs a, int nb, size_t partial_bytes, int cu_count, hipStream_t stream) {
+    const bool pair = PAIR;
     const int tiles = pair ? (a.rows_end[0] + 15) / 16 : (a.total_rows + 15) / 16;
-    const int per = waves_per_group<MT>() * (pair ? R / 2 : R);
+    const int per = waves_per_group<MT, R>() * (pair ? R / 2 : R);
     const int groups = (tiles + per - 1) / per;
     int splits = 1;
     if (groups < cu_count) splits = std::min((cu_count + groups - 1) / groups, std::max(1, nb / 2));
@@ -836,8 +846,7 @@ hipError_t launch_mt(const F32MmaArgs& a0, size_t partial_bytes, int cu_count, h
     else splits = std::max(1, std::min<int>(splits, (int)(partial_bytes / split_bytes)));
     a.split_blocks = (nb + splits - 1) / splits;
     a.splits = (nb + a.split_blocks - 1) / a.split_blocks;
-    if (pair) return launch_shape<T, R, MT, true>(a, groups, stream);
-    return launch_shape<T, R, MT, false>(a, groups, stream);
+    return launch_shape<T, R, MT, PAIR>(a, groups, stream);
 }
 
 // Member tiles per launch: the f16 form's fragments of a block (16 KB per
