@@ -51,21 +51,28 @@
 //    y = (W (x * gamma)) / rms).
 //
 // Product (f32mma_gemv_kernel)
-//  - One launch serves up to two member tiles (32 members): their fragments
-//    of a super-block, double-buffered, fill 98 KB of LDS. 33..64 members
-//    take two launches over the same packed activations.
-//  - A workgroup of W waves shares each super-block's fragments, loaded
-//    straight into LDS a block ahead; each wave owns R tiles of 16 weight
-//    rows (gate/up pairs: R/2 gate tiles and the up tiles of the same rows)
-//    over the workgroup's super-blocks and streams their weights through a
-//    two-block register ring.
-//  - Row groups short of the CUs split K across workgroups: raw row sums go
-//    to a partial buffer and f32mma_reduce_kernel adds the splits in order
-//    (deterministic) and applies the epilogue.
+//  - One launch serves up to four member tiles (64 members) in the f16 form
+//    and two in the bf16 form; more members take further launches over the
+//    same packed activations.
+//  - A workgroup is W compute waves and one loader wave. The loader streams
+//    each super-block's fragments, X sums and inverse block scales for all
+//    member tiles straight into LDS (2-4 slots, 1-3 blocks ahead) and waits
+//    only for its own loads before each barrier; the compute waves never wait
+//    on a load at a barrier. Each compute wave owns one tile of 16 weight rows
+//    (gate/up pairs: a gate tile and the up tile of the same rows) over the
+//    workgroup's super-blocks and streams its weights through a register ring
+//    2-4 blocks deep.
+//  - Launch shape: the grid fills the CUs in one round (every workgroup
+//    resident at once); among such shapes the one with the fewest (row tile x
+//    super-block) units per workgroup wins. Row groups short of the CUs split
+//    K across workgroups: raw row sums go to a partial buffer and
+//    f32mma_reduce_kernel adds the splits in order (deterministic) and applies
+//    the epilogue. The split depends on the weight shape alone.
 //  - Lane l holds output row (l % 16) of each tile for members
 //    4 (l / 16) .. + 3 of each member tile (the MFMA C layout).
-// A member's output depends only on its own activations: its bits do not
-// change with the other members' values or count (from 9 members on).
+// A member's output depends only on its own activations and the weight
+// shape: its bits do not change with the other members' values, their count
+// (from 9 members on) or its position in the batch.
 #include "kquant_device.hpp"
 #include "kquant_launch.hpp"
 
@@ -347,38 +354,152 @@ __device__ __forceinline__ void q6_group(const WRaw<kQ6K>& d, int g, uint32_t& o
     o1 = out[1];
 }
 
-// One workgroup: W waves, wave w owning R tiles of 16 weight rows (gate/up
-// pairs: R/2 gate tiles and the up tiles of the same rows), all of them over
-// the workgroup's super-blocks [sb0, sb1) (a K split across workgroups when
-// blockIdx.y > 0 exists). Per super-block the MT member tiles' activation
-// fragments and X sums are loaded straight into LDS (double-buffered, a
-// block ahead) once for the W waves; weights stream through a two-block
-// register ring.
-template <int T, int R, int MT, bool PAIR, int W>
-__global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [I0, N).
+template <int I, int N> struct StaticFor {
+    template <typename F> __device__ __forceinline__ static void run(F& f) {
+        if constexpr (I < N) {
+            f(std::integral_constant<int, I>{});
+            StaticFor<I + 1, N>::run(f);
+        }
+    }
+};
+
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
+// expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// A workgroup barrier that neither waits for this wave's outstanding loads
+// (the compiler's __syncthreads fence would) nor lets the compiler move
+// memory accesses across it.
+__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// The same after this wave's LDS reads have returned (the slot they read is
+// refilled after the barrier).
+__device__ __forceinline__ void lds_done_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One workgroup: W compute waves and one loader wave (the last). Compute wave
+// w owns R tiles of 16 weight rows (gate/up pairs: a gate tile and the up
+// tile of the same rows) over the workgroup's super-blocks [sb0, sb1) (a K
+// split across workgroups when gridDim.y > 1) and streams their weights
+// through an NS-block register ring. The loader wave streams every block's
+// activation fragments, X sums and inverse block scales for the MT member
+// tiles straight into NL LDS slots (NL - 1 blocks ahead), so no compute wave
+// ever waits on a load at a barrier: block b's fragments are complete when
+// the loader reaches barrier b, and the compute waves' weight loads run NS - 1
+// blocks ahead, independent of the barriers.
+template <int T, int R, int MT, bool PAIR, int NL, int NS>
+__global__ __launch_bounds__(512) void f32mma_gemv_kernel(F32MmaArgs A) {
     constexpr int BB = BlockTraits<T>::bytes;
     constexpr int PC = pieces_of<T>();
     constexpr int FRAGS = MT * 8 * PC;  // 1 KB fragment loads per block
     constexpr int XS = T == kQ6K ? 0 : 2 * MT;  // 256 B X-sum loads per block
     constexpr int IS = T == kQ6K ? 0 : MT;      // inverse block scales (16 lanes x 4 B) per block
+    constexpr int NDMA = FRAGS + XS + IS;       // the loader's loads per block
     static_assert(!PAIR || R % 2 == 0, "pairs split the tiles into gate and up halves");
-    // two slots as separate objects: the compiler can then tell that reads of
-    // one do not alias the loads into the other in flight
+    static_assert(NL >= 2 && NL <= 4 && NS % NL == 0, "the ring cycles through whole LDS slot rounds");
+    static_assert((NL - 2) * NDMA < 64, "the loader's wait count fits vmcnt");
+    // one object per slot: the compiler can then tell the slots apart
     __shared__ __attribute__((aligned(16))) uint4 fa0[FRAGS * 64];
     __shared__ __attribute__((aligned(16))) uint4 fa1[FRAGS * 64];
+    __shared__ __attribute__((aligned(16))) uint4 fa2[NL > 2 ? FRAGS * 64 : 1];
+    __shared__ __attribute__((aligned(16))) uint4 fa3[NL > 3 ? FRAGS * 64 : 1];
     __shared__ __attribute__((aligned(16))) float2 xa0[XS ? MT * 64 : 1];
     __shared__ __attribute__((aligned(16))) float2 xa1[XS ? MT * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float2 xa2[XS && NL > 2 ? MT * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float2 xa3[XS && NL > 3 ? MT * 64 : 1];
     __shared__ __attribute__((aligned(16))) float isa0[IS ? MT * 64 : 1];
     __shared__ __attribute__((aligned(16))) float isa1[IS ? MT * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float isa2[IS && NL > 2 ? MT * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float isa3[IS && NL > 3 ? MT * 64 : 1];
+    auto fa_of = [&](auto slot_c) -> uint4* {
+        constexpr int S = decltype(slot_c)::value;
+        if constexpr (S == 0) return fa0;
+        else if constexpr (S == 1) return fa1;
+        else if constexpr (S == 2) return fa2;
+        else return fa3;
+    };
+    auto xa_of = [&](auto slot_c) -> float2* {
+        constexpr int S = decltype(slot_c)::value;
+        if constexpr (S == 0) return xa0;
+        else if constexpr (S == 1) return xa1;
+        else if constexpr (S == 2) return xa2;
+        else return xa3;
+    };
+    auto isa_of = [&](auto slot_c) -> float* {
+        constexpr int S = decltype(slot_c)::value;
+        if constexpr (S == 0) return isa0;
+        else if constexpr (S == 1) return isa1;
+        else if constexpr (S == 2) return isa2;
+        else return isa3;
+    };
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6)) - 1;  // compute waves
     const int kq = lane >> 4, rl = lane & 15;
     const int nb = A.K >> 8;
     const uint32_t row_bytes = (uint32_t)nb * BB;
     const int sb0 = (int)blockIdx.y * A.split_blocks;
     const int sb1 = min(nb, sb0 + A.split_blocks);
     const int tile0 = A.member0 >> 4;
+
+    if (wave == W) {
+        // ---- loader: block b's fragments into LDS slot (b - sb0) % NL; past
+        // the range the loads read zeros into a slot nobody reads
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(A.act, A.act_bytes);
+        auto stage = [&](auto slot_c, int b) {
+            uint4* const fa = fa_of(slot_c);
+            float2* const xa = xa_of(slot_c);
+            float* const isa = isa_of(slot_c);
+            const bool lb = b < sb1;
+#pragma unroll
+            for (int j = 0; j < FRAGS; ++j) {
+                const int mt = j / (8 * PC);
+                const uint32_t off = A.L.frag + ((uint32_t)((tile0 + mt) * nb + b) * (8u * PC) +
+                                                 (uint32_t)(j % (8 * PC))) * kPieceBytes + (uint32_t)lane * 16u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (__attribute__((address_space(3))) void*)&fa[j * 64], 16,
+                                                         (int)(lb ? off : kOOR), 0, 0, 0);
+            }
+#pragma unroll
+            for (int h = 0; h < XS; ++h) {
+                const int mt = h >> 1;
+                const uint32_t off = A.L.xsum + (uint32_t)((tile0 + mt) * nb + b) * kXsumBlockBytes +
+                                     (uint32_t)(h & 1) * 256u + (uint32_t)lane * 4u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ar, (__attribute__((address_space(3))) void*)(reinterpret_cast<float*>(xa) + h * 64), 4,
+                    (int)(lb ? off : kOOR), 0, 0, 0);
+            }
+#pragma unroll
+            for (int mt = 0; mt < IS; ++mt) {
+                const uint32_t off =
+                    A.L.iscale + (uint32_t)((tile0 + mt) * nb + b) * kIscaleBlockBytes + (uint32_t)lane * 4u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (__attribute__((address_space(3))) void*)(isa + mt * 64),
+                                                         4, (int)(lb && lane < 16 ? off : kOOR), 0, 0, 0);
+            }
+        };
+        auto prologue = [&](auto u) { stage(u, sb0 + decltype(u)::value); };
+        StaticFor<0, NL - 1>::run(prologue);
+        wait_vmcnt<(NL - 2) * NDMA>();  // block sb0's loads are in
+        bare_barrier();
+        int b = sb0;
+        auto step = [&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            // the slot of block b + u - 1, which every compute wave finished
+            // before the last barrier
+            stage(std::integral_constant<int, (u + NL - 1) % NL>{}, b + u + NL - 1);
+            wait_vmcnt<(NL - 2) * NDMA>();  // block b + u + 1's loads are in
+            bare_barrier();
+        };
+        // whole ring rounds, then the last blocks (no loop back-edge after a
+        // partial round, so no path skips a step and loops again)
+        for (; b + NS <= sb1; b += NS) StaticFor<0, NS>::run(step);
+        auto tail = [&](auto uc) {
+            if (b + decltype(uc)::value < sb1) step(uc);
+        };
+        StaticFor<0, NS - 1>::run(tail);
+        return;
+    }
 
     // this wave's tiles: (matrix, first local row); tiles never straddle matrices
     __amdgpu_buffer_rsrc_t wr[R];
@@ -422,46 +543,6 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
         live_row[i] = lrow < rows_mat[i];
         rowoff[i] = live_row[i] ? (uint32_t)lrow * row_bytes : 0u;
     }
-    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A.act, A.act_bytes);
-
-    // ---- activation fragments of block b into an LDS slot: load j of the
-    // block (fragment (member tile j / 24, group and piece j % 24), 1 KB) is
-    // issued by wave j % W; past the range the loads read zeros
-    auto stage = [&](auto slot_const, int b) {
-        constexpr int SL = decltype(slot_const)::value;
-        uint4* const fa = SL ? fa1 : fa0;
-        float2* const xa = SL ? xa1 : xa0;
-        const bool lb = b < sb1;
-#pragma unroll
-        for (int j = 0; j < FRAGS; ++j) {
-            if (j % W != wave) continue;
-            const int mt = j / (8 * PC);
-            const uint32_t off = A.L.frag + ((uint32_t)((tile0 + mt) * nb + b) * (8u * PC) +
-                                             (uint32_t)(j % (8 * PC))) * kPieceBytes + (uint32_t)lane * 16u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (__attribute__((address_space(3))) void*)&fa[j * 64], 16,
-                                                     (int)(lb ? off : kOOR), 0, 0, 0);
-        }
-#pragma unroll
-        for (int h = 0; h < XS; ++h) {
-            if ((FRAGS + h) % W != wave) continue;
-            const int mt = h >> 1;
-            const uint32_t off = A.L.xsum + (uint32_t)((tile0 + mt) * nb + b) * kXsumBlockBytes +
-                                 (uint32_t)(h & 1) * 256u + (uint32_t)lane * 4u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ar, (__attribute__((address_space(3))) void*)(reinterpret_cast<float*>(xa) + h * 64), 4,
-                (int)(lb ? off : kOOR), 0, 0, 0);
-        }
-        float* const isa = SL ? isa1 : isa0;
-#pragma unroll
-        for (int mt = 0; mt < IS; ++mt) {
-            if ((FRAGS + XS + mt) % W != wave) continue;
-            const uint32_t off = A.L.iscale + (uint32_t)((tile0 + mt) * nb + b) * kIscaleBlockBytes + (uint32_t)lane * 4u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (__attribute__((address_space(3))) void*)(isa + mt * 64), 4,
-                                                     (int)(lb && lane < 16 ? off : kOOR), 0, 0, 0);
-        }
-        // written behind the compiler's back: LDS reads must not move across
-        asm volatile("" ::: "memory");
-    };
 
     v4f acc[R][MT], macc[R][MT];
 #pragma unroll
@@ -471,18 +552,19 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
             acc[i][mt] = (v4f){0.f, 0.f, 0.f, 0.f};
             macc[i][mt] = (v4f){0.f, 0.f, 0.f, 0.f};
         }
-    WRaw<T> ring[2][R];
-    auto fill_w = [&](int s, int b) {
+    WRaw<T> ring[NS][R];
+    auto fill_w = [&](auto ring_c, int b) {
+        constexpr int s = decltype(ring_c)::value;
         const bool lb = b < sb1;
 #pragma unroll
         for (int i = 0; i < R; ++i) load_w<T>(ring[s][i], wr[i], lb && live_row[i], rowoff[i] + (uint32_t)b * BB, kq);
     };
 
-    // ---- one super-block from weight slot s and LDS slot (fa, xa)
-    auto block = [&](auto slot_const) {
-        constexpr int s = decltype(slot_const)::value;  // weight ring slot = LDS slot
-        const uint4* const fa = s ? fa1 : fa0;
-        const float2* const xa = s ? xa1 : xa0;
+    // ---- one super-block from weight ring slot s and LDS slot (fa, xa, isa)
+    auto block = [&](auto ring_c, auto slot_c) {
+        constexpr int s = decltype(ring_c)::value;
+        const uint4* const fa = fa_of(slot_c);
+        const float2* const xa = xa_of(slot_c);
         float dd[R], bmin0[R], bmin1[R];
         uint32_t scw_lo[R], scw_hi[R];
 #pragma unroll
@@ -568,7 +650,7 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            const float* const isa = s ? isa1 : isa0;
+            const float* const isa = isa_of(slot_c);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const float4 inv4 = *reinterpret_cast<const float4*>(isa + mt * 64 + 4 * kq);
@@ -624,29 +706,23 @@ __global__ __launch_bounds__(W * 64) void f32mma_gemv_kernel(F32MmaArgs A) {
         }
     };
 
-    // ---- prologue: block sb0 in LDS slot 0, weights of sb0 and sb0 + 1
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    stage(S0{}, sb0);
-    fill_w(0, sb0);
-    fill_w(1, sb0 + 1);
-    __syncthreads();
-    // Pairs of blocks: the next block's fragments go to the other LDS slot
-    // (every wave finished reading it before the last barrier) ahead of the
-    // weights of the block after it, so the barrier's wait for the fragments
-    // leaves the weight loads in flight.
+    // ---- prologue: weights of the first NS - 1 blocks
+    auto prologue = [&](auto u) { fill_w(u, sb0 + decltype(u)::value); };
+    StaticFor<0, NS - 1>::run(prologue);
+    bare_barrier();  // the loader has block sb0's fragments in slot 0
     int b = sb0;
-    for (; b + 1 < sb1; b += 2) {
-        stage(S1{}, b + 1);
-        block(S0{});
-        fill_w(0, b + 2);
-        __syncthreads();
-        stage(S0{}, b + 2);
-        block(S1{});
-        fill_w(1, b + 3);
-        __syncthreads();
-    }
-    if (b < sb1) block(S0{});
+    auto step = [&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        // refill the ring slot of block b + u - 1 with block b + u + NS - 1
+        fill_w(std::integral_constant<int, (u + NS - 1) % NS>{}, b + u + NS - 1);
+        block(uc, std::integral_constant<int, u % NL>{});
+        lds_done_barrier();  // slot u % NL may be refilled from here on
+    };
+    for (; b + NS <= sb1; b += NS) StaticFor<0, NS>::run(step);
+    auto tail = [&](auto uc) {
+        if (b + decltype(uc)::value < sb1) step(uc);
+    };
+    StaticFor<0, NS - 1>::run(tail);
 
     // ---- epilogue: each wave owns its rows over the whole range
     float v[R][MT][4];
@@ -794,20 +870,73 @@ __global__ __launch_bounds__(256) void f32mma_reduce_kernel(F32MmaArgs A) {
     }
 }
 
-// Row tiles per wave. Measured on MI355X at the Qwen3-8B FFN shapes (M = 16
-// and 32): two tiles run 10-20% faster than four, whose registers leave one
-// wave per SIMD.
-template <int MT, bool PAIR> constexpr int tiles_per_wave() { return MT >= 3 && !PAIR ? 1 : 2; }
-// waves per workgroup (they share the LDS fragments): eight for one member
-// tile or one row tile per wave, four otherwise (whose registers allow one
-// wave per SIMD)
-template <int MT, int R> constexpr int waves_per_group() { return MT == 1 || R == 1 ? 8 : 4; }
+// Member tiles per launch: the f16 form's fragments of a block (16 KB per
+// tile) let four tiles (64 members) share one weight stream; the bf16 form's
+// (24 KB per tile) two.
+template <int T> constexpr int max_tiles() { return T == kQ6K ? 2 : 4; }
+// LDS slots (fragment look-ahead + 1): as many as 160 KB of LDS holds, at
+// most four, and few enough that the loader's in-flight loads fit its
+// six-bit vmcnt wait.
+template <int T, int MT> constexpr int lds_slots() {
+    return T == kQ6K ? (MT == 1 ? 4 : 3) : (MT == 1 ? 4 : MT <= 3 ? 3 : 2);
+}
+// Weight ring depth: the LDS slot count, or four blocks beside two slots
+// when the ring's registers leave room (one row tile per wave).
+template <int T, int R, int MT> constexpr int ring_depth() {
+    constexpr int nl = lds_slots<T, MT>();
+    return nl == 2 ? (R == 1 ? 4 : 2) : nl;
+}
+
+// Launch shape of one product: compute waves per workgroup, the K split and
+// the row groups. The split comes from the weight shape alone (row tiles,
+// super-blocks and the partial room a 64-member launch needs), never from the
+// member count, so a member's sums are added in the same order whatever the
+// batch: among the one-tile-per-wave shapes whose grid fits the CUs in one
+// round (all workgroups resident at once), the one with the fewest (row tile
+// x super-block) units per workgroup sets it (ties: more compute waves, which
+// share the LDS fragments, then fewer splits). Measured on MI355X at the
+// Qwen3-8B FFN shapes, two row tiles per wave (halving the LDS fragment
+// reads) ran M = 64 slower: 96.0 against 80.3 us per FFN.
+struct F32MmaShape {
+    int waves, splits, split_blocks, groups;
+};
+constexpr int kF32MmaMaxComputeWaves = 7;  // plus the loader: eight waves, two per SIMD
+F32MmaShape f32mma_split(int tiles, int nb, int max_splits, int cu_count) {
+    constexpr int kMaxWaves = kF32MmaMaxComputeWaves;
+    F32MmaShape best{kMaxWaves, 1, nb, (tiles + kMaxWaves - 1) / kMaxWaves};
+    long best_cost = -1;
+    for (int s = 1; s <= std::min(nb, std::max(1, max_splits)); ++s) {
+        const int sbk = (nb + s - 1) / s;
+        if ((nb + sbk - 1) / sbk != s) continue;  // the same split as a smaller s
+        for (int w = 1; w <= kMaxWaves; ++w) {
+            const int groups = (tiles + w - 1) / w;
+            if ((long)groups * s > cu_count) continue;
+            const long cost = (long)w * sbk;
+            const bool better = best_cost < 0 || cost < best_cost ||
+                                (cost == best_cost && (w > best.waves || (w == best.waves && s < best.splits)));
+            if (better) {
+                best = {w, s, sbk, groups};
+                best_cost = cost;
+            }
+        }
+    }
+    return best;
+}
+// The same split with R row tiles per wave (gate/up pairs: 2): the fewest
+// compute waves that still fit the grid in one round.
+F32MmaShape f32mma_shape_r(const F32MmaShape& one, int tiles, int R, int cu_count) {
+    const int units = (tiles + R - 1) / R;
+    const int max_groups = std::max(1, cu_count / one.splits);
+    const int w = std::min(kF32MmaMaxComputeWaves, std::max(1, (units + max_groups - 1) / max_groups));
+    return {w, one.splits, one.split_blocks, (units + w - 1) / w};
+}
 
 template <int T, int R, int MT, bool PAIR>
-hipError_t launch_shape(const F32MmaArgs& a, int groups, hipStream_t stream) {
-    constexpr int W = waves_per_group<MT, R>();
-    hipLaunchKernelGGL((f32mma_gemv_kernel<T, R, MT, PAIR, W>), dim3((unsigned)groups, (unsigned)a.splits),
-                       dim3(64 * W), 0, stream, a);
+hipError_t launch_shape(F32MmaArgs a, const F32MmaShape& sh, hipStream_t stream) {
+    a.splits = sh.splits;
+    a.split_blocks = sh.split_blocks;
+    hipLaunchKernelGGL((f32mma_gemv_kernel<T, R, MT, PAIR, lds_slots<T, MT>(), ring_depth<T, R, MT>()>),
+                       dim3((unsigned)sh.groups, (unsigned)sh.splits), dim3(64 * (sh.waves + 1)), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.splits == 1) return e;
     const int rows = a.pair_swiglu ? a.rows_end[0] : a.total_rows;
@@ -816,61 +945,36 @@ hipError_t launch_shape(const F32MmaArgs& a, int groups, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Grid: row groups x K splits. A grid of row groups short of the CUs splits
-// K (at least two super-blocks per split, as far as the partial space
-// allows); the split depends on the shape and member count only, never on
-// the members' values.
-template <int T, int R, int MT, bool PAIR>
-hipError_t launch_split(F32MmaArgs a, int nb, size_t partial_bytes, int cu_count, hipStream_t stream);
-
 template <int T, int MT>
-hipError_t launch_mt(const F32MmaArgs& a0, size_t partial_bytes, int cu_count, hipStream_t stream) {
-    F32MmaArgs a = a0;
-    const int nb = a.K >> 8;
-    const bool pair = a.pair_swiglu != 0;
-    if (pair) return launch_split<T, tiles_per_wave<MT, true>(), MT, true>(a, nb, partial_bytes, cu_count, stream);
-    return launch_split<T, tiles_per_wave<MT, false>(), MT, false>(a, nb, partial_bytes, cu_count, stream);
+hipError_t launch_mt(const F32MmaArgs& a, const F32MmaShape& one, int tiles, int cu_count, hipStream_t stream) {
+    if (a.pair_swiglu) return launch_shape<T, 2, MT, true>(a, f32mma_shape_r(one, tiles, 2, cu_count), stream);
+    return launch_shape<T, 1, MT, false>(a, one, stream);
 }
-
-template <int T, int R, int MT, bool PAIR>
-hipError_t launch_split(F32MmaArgs a, int nb, size_t partial_bytes, int cu_count, hipStream_t stream) {
-    const bool pair = PAIR;
-    const int tiles = pair ? (a.rows_end[0] + 15) / 16 : (a.total_rows + 15) / 16;
-    const int per = waves_per_group<MT, R>() * (pair ? R / 2 : R);
-    const int groups = (tiles + per - 1) / per;
-    int splits = 1;
-    if (groups < cu_count) splits = std::min((cu_count + groups - 1) / groups, std::max(1, nb / 2));
-    const int vrows = pair ? 2 * a.rows_end[0] : a.total_rows;
-    const size_t split_bytes = (size_t)a.count_here * vrows * 4;
-    if (a.partial == nullptr) splits = 1;
-    else splits = std::max(1, std::min<int>(splits, (int)(partial_bytes / split_bytes)));
-    a.split_blocks = (nb + splits - 1) / splits;
-    a.splits = (nb + a.split_blocks - 1) / a.split_blocks;
-    return launch_shape<T, R, MT, PAIR>(a, groups, stream);
-}
-
-// Member tiles per launch: the f16 form's fragments of a block (16 KB per
-// tile, double-buffered) let four tiles (64 members) share one weight stream
-// in 128 KB of LDS; the bf16 form's (24 KB per tile) two.
-template <int T> constexpr int max_tiles() { return T == kQ6K ? 2 : 4; }
 
 template <int T>
 hipError_t launch_t(const F32MmaArgs& a, size_t partial_bytes, int cu_count, hipStream_t stream) {
     constexpr int kStep = 16 * max_tiles<T>();
+    const int nb = a.K >> 8;
+    const bool pair = a.pair_swiglu != 0;
+    const int tiles = pair ? 2 * ((a.rows_end[0] + 15) / 16) : (a.total_rows + 15) / 16;
+    const int vrows = pair ? 2 * a.rows_end[0] : a.total_rows;
+    const size_t split_bytes = (size_t)kStep * (size_t)vrows * 4;
+    const int max_splits = a.partial == nullptr ? 1 : (int)std::min<size_t>(16, partial_bytes / split_bytes);
+    const F32MmaShape one = f32mma_split(tiles, nb, max_splits, cu_count);
     for (int m0 = 0; m0 < a.members; m0 += kStep) {
         F32MmaArgs c = a;
         c.member0 = m0;
         c.count_here = std::min(kStep, a.members - m0);
-        const int tiles = (c.count_here + 15) / 16;
+        const int mts = (c.count_here + 15) / 16;
         hipError_t e;
         if constexpr (max_tiles<T>() == 4) {
-            e = tiles == 1   ? launch_mt<T, 1>(c, partial_bytes, cu_count, stream)
-                : tiles == 2 ? launch_mt<T, 2>(c, partial_bytes, cu_count, stream)
-                : tiles == 3 ? launch_mt<T, 3>(c, partial_bytes, cu_count, stream)
-                             : launch_mt<T, 4>(c, partial_bytes, cu_count, stream);
+            e = mts == 1   ? launch_mt<T, 1>(c, one, tiles, cu_count, stream)
+                : mts == 2 ? launch_mt<T, 2>(c, one, tiles, cu_count, stream)
+                : mts == 3 ? launch_mt<T, 3>(c, one, tiles, cu_count, stream)
+                           : launch_mt<T, 4>(c, one, tiles, cu_count, stream);
         } else {
-            e = tiles == 1 ? launch_mt<T, 1>(c, partial_bytes, cu_count, stream)
-                           : launch_mt<T, 2>(c, partial_bytes, cu_count, stream);
+            e = mts == 1 ? launch_mt<T, 1>(c, one, tiles, cu_count, stream)
+                         : launch_mt<T, 2>(c, one, tiles, cu_count, stream);
         }
         if (e != hipSuccess) return e;
     }

@@ -114,14 +114,15 @@ hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& args, int cu_cou
 
 // ---- f32-faithful batched GEMV on the bf16 matrix cores (gemv_f32mma.hip)
 //
-// The default f32 arithmetic for 9..64 members: activations split exactly
-// into three bf16 pieces, quants exact in bf16, f32 accumulation, so results
-// agree with the f32 wave GEMV to f32 rounding (not bit for bit); the
-// weights are read once for the whole batch. Up to 8 members stay on the
-// wave GEMV, whose rows are bit-identical to the single-member call.
+// The default f32 arithmetic for 9..64 members: exact products on the
+// matrix cores (Q4_K / Q5_K: quants times group scale exact in f16 against
+// activations in two f16 pieces; Q6_K: quants exact in bf16 against three
+// bf16 pieces), f32 accumulation, so results agree with the f32 wave GEMV to
+// f32 rounding (not bit for bit); the weights are read once for the whole
+// batch. Up to 8 members stay on the wave GEMV, whose rows are bit-identical
+// to the single-member call.
 constexpr int kF32MmaMinMembers = 9;
 constexpr int kF32MmaMaxMembers = 64;
-constexpr int kF32MmaMaxWaves = 4;  // K-split waves per workgroup
 // Byte offsets of the packed activations of `members` x K (K a multiple of
 // 256): bf16-piece MFMA fragments, f32 group sums, per-workgroup partial sums
 // of squares.
