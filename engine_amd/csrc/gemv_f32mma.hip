@@ -224,6 +224,22 @@ __global__ __launch_bounds__(64) void pack_f32mma_kernel(PackArgs a) {
     if (tid == 0) reinterpret_cast<float*>(a.act + a.L.ssq)[m * a.L.parts + blockIdx.x] = ws;
 }
 
+// Sum of p[0..n) in index order, its loads issued eight at a time (a plain
+// loop waits for each load before the next add).
+__device__ __forceinline__ float sum_in_order(const float* p, int n) {
+    float total = 0.f;
+    for (int base = 0; base < n; base += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = base + j < n ? p[base + j] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (base + j < n) total += t[j];
+        }
+    }
+    return total;
+}
+
 // ------------------------------------------------------------------ product
 
 struct F32MmaArgs {
@@ -761,8 +777,7 @@ __global__ __launch_bounds__(512) void f32mma_gemv_kernel(F32MmaArgs A) {
             const int mem = A.member0 + 16 * mt + 4 * kq + t;
             if (A.has_norm && mem < A.members) {
                 const float* ssq = reinterpret_cast<const float*>(A.act + A.L.ssq);
-                float total = 0.f;
-                for (int p = 0; p < A.L.parts; ++p) total += ssq[mem * A.L.parts + p];
+                const float total = sum_in_order(ssq + mem * A.L.parts, A.L.parts);
                 // RMSNorm (qwen_reference.rs:550-556): 1/sqrt(sum(x^2)/K + eps)
                 inv[mt][t] = 1.0f / sqrtf(total / (float)A.K + A.eps);
             }
@@ -825,17 +840,27 @@ __global__ __launch_bounds__(256) void f32mma_reduce_kernel(F32MmaArgs A) {
     if (idx >= A.count_here * rows) return;
     const int ml = idx / rows, row = idx - ml * rows;  // member within the launch
     const int mem = A.member0 + ml;
-    float g = 0.f, u = 0.f;
-    for (int sp = 0; sp < A.splits; ++sp) {
+    // the splits' sums in split order (at most 16 splits: every load issued
+    // before the first add)
+    float gv[16], uv[16];
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp) {
         const float* p = A.partial + ((size_t)sp * A.count_here + ml) * vrows;
-        g += p[row];
-        if (pair) u += p[rows + row];
+        gv[sp] = sp < A.splits ? p[row] : 0.f;
+        uv[sp] = sp < A.splits && pair ? p[rows + row] : 0.f;
+    }
+    float g = 0.f, u = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp) {
+        if (sp < A.splits) {
+            g += gv[sp];
+            u += uv[sp];
+        }
     }
     float inv = 1.f;
     if (A.has_norm) {
         const float* ssq = reinterpret_cast<const float*>(A.act + A.L.ssq);
-        float total = 0.f;
-        for (int q = 0; q < A.L.parts; ++q) total += ssq[mem * A.L.parts + q];
+        const float total = sum_in_order(ssq + mem * A.L.parts, A.L.parts);
         // RMSNorm (qwen_reference.rs:550-556): 1/sqrt(sum(x^2)/K + eps)
         inv = 1.0f / sqrtf(total / (float)A.K + A.eps);
     }
@@ -881,12 +906,13 @@ template <int T, int MT> constexpr int lds_slots() {
     return T == kQ6K ? (MT == 1 ? 4 : 3) : (MT == 1 ? 4 : MT <= 3 ? 3 : 2);
 }
 // Weight ring depth: the LDS slot count, or four blocks beside two slots
-// when the ring's registers leave room (one row tile per wave).
+// when the ring's registers leave room (one row tile per wave). Measured on
+// MI355X at the Qwen3-8B FFN shapes, an eight-block ring at one member tile
+// ran M = 16 slower (49.8 against 46-47 us per FFN).
 template <int T, int R, int MT> constexpr int ring_depth() {
     constexpr int nl = lds_slots<T, MT>();
     return nl == 2 ? (R == 1 ? 4 : 2) : nl;
 }
-
 // Launch shape of one product: compute waves per workgroup, the K split and
 // the row groups. The split comes from the weight shape alone (row tiles,
 // super-blocks and the partial room a 64-member launch needs), never from the
