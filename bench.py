@@ -343,13 +343,14 @@ def _graph_time_us(torch, stream, fn, reps):
     return a.elapsed_time(b) * 1e3 / reps
 
 
-def bench_batched(E, synth, torch, args):
+def batched_ffn_times(E, synth, torch, args, ms=(1, 4, 8, 16, 64), compare=True):
     """the Qwen3-8B FFN (gate/up Q4_K 4096->12288, down Q5_K 12288->4096)
     for M tokens with f32 activations ~N(0,1), through the decode step's batched GEMV entry
     points (gate/up as one grouped launch). The default f32 arithmetic (GEMV_WARP) runs the f32
     wave GEMV up to 8 members (weights read once per launch group, every row bit-identical to
-    the single call) and the f32-faithful matrix-core GEMV from 9 to 64 members (activations
-    split exactly into three bf16 pieces, f32 accumulation, weights read once for the batch).
+    the single call) and the f32-faithful matrix-core GEMV from 9 to 64 members (Q4_K / Q5_K:
+    quants times group scale exact in f16 against activations in two f16 pieces with a per-block
+    power-of-two scale, f16 MFMA with f32 accumulation; weights read once for the batch).
     For comparison: the opt-in block fixed-point mode at M <= 16 and the f16 prefill matmul at
     M = 64."""
     dev = torch.device("cuda:0")
@@ -368,7 +369,7 @@ def bench_batched(E, synth, torch, args):
     k4, k5 = E.AmdQ4KGemv.from_context(ctx), E.AmdQ5KGemv.from_context(ctx)
     wbytes = 2 * (FFN * HIDDEN // 256 * 144) + HIDDEN * FFN // 256 * 176
     per_m = {}
-    for m in (1, 4, 8, 16, 64):
+    for m in ms:
         x = torch.randn(m, HIDDEN, device=dev, generator=gen)
         h = torch.randn(m, FFN, device=dev, generator=gen)
         g, u, d = (torch.empty(m * n, device=dev) for n in (FFN, FFN, HIDDEN))
@@ -379,13 +380,13 @@ def bench_batched(E, synth, torch, args):
                 k5.execute_warp_batch(ly["down"], h, d, m)
         runs = [("warp", "f32 wave GEMV, weights read once per launch group of up to 8 members (down's K = 12288 "
                          "split by slice from 3 members, with an ordered slice reduction)" if m <= 8 else
-                 "f32-faithful matrix-core GEMV (x split exactly into three bf16 pieces, bf16 MFMA with f32 "
-                 "accumulation, f32 scale epilogue), weights read once for the batch", gemv_ffn)]
-        if m <= 16:
+                 "f32-faithful matrix-core GEMV (quants x group scale exact in f16, x in two f16 pieces, f16 MFMA "
+                 "with f32 accumulation, f32 block epilogue), weights read once for the batch", gemv_ffn)]
+        if compare and m <= 16:
             runs.append(("fixed16", "block fixed-point " + ("wave GEMV" if m < 4 else
                          "wave GEMV gate/up, matrix-core GEMV down" if m < 5 else "matrix-core GEMV") +
                          ", weights read once per launch", gemv_ffn))
-        else:
+        elif compare:
             def prefill_ffn():
                 for ly in layers:
                     k4.gemm_prefill(ly["gate"], x, g, m)
@@ -403,18 +404,24 @@ def bench_batched(E, synth, torch, args):
                               "weight_GBps": round(wbytes / us / 1e3, 1), "hbm_frac": round(wbytes / us / 1e3 / PEAK_HBM_GBS, 4),
                               "tflops": round(flops / us / 1e6, 2), "path": path}
             if mode == "warp" and m > 8:
-                # executed on the matrix cores as three bf16 products per f32 one
-                per_m[m][mode]["bf16_mfma_frac"] = round(3 * flops / us / 1e6 / PEAK_BF16_TFLOPS, 4)
+                # executed on the matrix cores as two f16 products (the activation's two pieces) per f32 one
+                per_m[m][mode]["f16_mfma_frac"] = round(2 * flops / us / 1e6 / PEAK_BF16_TFLOPS, 4)
             log(f"bench batched: M={m} {mode}: {us:.2f} us per FFN ({path})")
         for kern in (k4, k5):
             kern.set_mode(0)
+    return per_m, wbytes, n_layers
+
+
+def bench_batched(E, synth, torch, args):
+    """BASELINE config 2 as its own bench line: every M in f32 mode, with the opt-in comparisons."""
+    per_m, wbytes, n_layers = batched_ffn_times(E, synth, torch, args)
     top = per_m[64]["warp"]
     return {
         "metric": "batched decode FFN throughput (BASELINE config 2), tokens/s at M=64, f32 activations",
         "value": top["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(top["us_per_ffn"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (M>=9 on bf16 MFMA with exact three-piece activations, f32 accumulation); per_m also holds "
+        "dtype": "f32 (M>=9 on f16 MFMA with exact two-piece activations, f32 accumulation); per_m also holds "
                  "i8dot4 / i8-mfma (fixed16) for M<=16 and f16-mfma at M=64",
         "data": "synthetic",
         "config": {"workload": "qwen3-8b-ffn-batched", "ffn_weight_bytes": wbytes, "layers_cycled": n_layers,
@@ -869,6 +876,7 @@ def main():
     ap.add_argument("--prompt-chunk", type=int, default=2048,
                     help="config 4: prompt tokens per prefill-matmul chunk (0: serial single-token prefill)")
     ap.add_argument("--no-model", action="store_true", help="skip the config-4 full-decoder measurement")
+    ap.add_argument("--no-batched", action="store_true", help="skip the config-2 M = 16 / 64 FFN figures")
     ap.add_argument("--concurrency", type=int, default=8, help="serving: requests in the burst")
     ap.add_argument("--prompt-tokens", type=int, default=257, help="serving: prompt tokens per request")
     ap.add_argument("--tokens", type=int, default=32, help="serving: output tokens per request")
@@ -992,6 +1000,16 @@ def main():
     if not args.no_model:
         model = model_decode_results(E, synth, torch, ctx, step, out_gamma, args)
 
+    batched = None
+    if not args.no_batched:
+        # BASELINE config 2 at the sizes the f32-faithful matrix-core GEMV serves (its own line:
+        # --workload batched)
+        per_m, _, _ = batched_ffn_times(E, synth, torch, args, ms=(16, 64), compare=False)
+        batched = {"us_per_ffn": {str(m): per_m[m]["warp"]["us_per_ffn"] for m in per_m},
+                   "tokens_per_s": {str(m): per_m[m]["warp"]["tokens_per_s"] for m in per_m},
+                   "dtype": "f32 (f16 MFMA on exact two-piece activations, f32 accumulation)",
+                   "workload": "qwen3-8b-ffn-batched (gate/up Q4_K grouped + down Q5_K, 8 layers cycled)"}
+
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: timing the CPU baseline")
@@ -1018,6 +1036,7 @@ def main():
         "decode_tok_s": model[1]["tok_s"] if model else None,
         "decode_tok_s_b8": model[8]["tok_s"] if model else None,
         "decode_model": model,
+        "batched_ffn": batched,
         "gemv_chain_tok_s": round(1000.0 / ms_step, 2),
         "gemv_mode": args.gemv_mode,
         "comparison_mode": {"gemv_mode": other, "dtype": "i8dot4-f32" if other == "fixed16" else "f32",
