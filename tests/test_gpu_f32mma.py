@@ -105,6 +105,24 @@ def test_member_bits_independent_of_batch(env, t):
     assert np.array_equal(mid9.view(np.uint32), full[37:46].view(np.uint32))
 
 
+@pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096)])
+def test_member_bits_independent_of_batch_ffn_shapes(env, t, k, n):
+    """The same at the Qwen3-8B FFN shapes, where launches of 16 and 64
+    members differ in member tiles per launch and waves per workgroup: the K
+    split follows the weight shape alone, so a member's sums are added in the
+    same order (a split that followed the member count would change the last
+    bits here)."""
+    case(test="f32mma batch invariance ffn", t=t, k=k, n=n)
+    enc = synth.kquant_numpy(t, k, n, seed=60 + t)
+    x = synth.activations_numpy(k, 64, seed=61).reshape(64, k)
+    w = upload(env, t, k, n, enc)
+    full = batch(env, t, w, x, n, 64)
+    assert np.all(np.isfinite(full))
+    for lo, hi in ((0, 16), (40, 49), (48, 64)):
+        part = batch(env, t, w, x[lo:hi], n, hi - lo)
+        assert np.array_equal(part.view(np.uint32), full[lo:hi].view(np.uint32)), (lo, hi)
+
+
 def test_fused_rms_norm(env):
     """RMSNorm fused into the pack stage (x * gamma packed, 1/rms applied per
     member at the output) against the oracle's RMSNorm then GEMV."""
