@@ -269,7 +269,8 @@ def time_model_decode(E, dec, cfg, ctx, members, context, gen_tokens, seed, prom
     0's last logits."""
     import numpy as np
     rng = np.random.default_rng(seed)
-    prompts = rng.integers(0, VOCAB, size=(8, context))[:members]
+    # rows are drawn in order, so member m's prompt is the same at every batch size
+    prompts = rng.integers(0, VOCAB, size=(max(8, members), context))[:members]
     caches = [E.AmdKvCache(ctx, cfg, context + gen_tokens) for _ in range(members)]
     if prompt_chunk:
         dec.reserve_prompt(prompt_chunk)
@@ -305,11 +306,14 @@ def model_decode_results(E, synth, torch, ctx, step, out_gamma, args):
     """Batch 1, then batch 8 whose member 0 has batch 1's prompt. In the f32
     GEMV mode member 0's tokens and last logits equal batch 1's bit for bit
     (`b8_member0_bitwise_equal_b1`): a check on the timed run itself, beside
-    `distinct_tokens` (the centered random weights give varied greedy tokens)."""
+    `distinct_tokens` (the centered random weights give varied greedy tokens).
+    Then batch 16, whose projections run on the f32-faithful matrix-core GEMV
+    (weights read once for the batch; rows agree with batch 1 to f32 rounding,
+    not bit for bit)."""
     import numpy as np
-    dec, cfg = build_decoder(E, synth, torch, ctx, step, out_gamma, args.layers, args.seed, 8)
+    dec, cfg = build_decoder(E, synth, torch, ctx, step, out_gamma, args.layers, args.seed, 16)
     res, runs = {}, {}
-    for members in (1, 8):
+    for members in (1, 8, 16):
         r, toks, logits = time_model_decode(E, dec, cfg, ctx, members, args.context, args.gen_tokens, args.seed,
                                             args.prompt_chunk)
         log(f"bench model: batch {members}: {r['tok_s']} tok/s ({r['ms_per_step']} ms/step, "
