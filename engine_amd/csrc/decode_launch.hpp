@@ -14,8 +14,10 @@ constexpr int kHeadDim = 128;
 // arithmetic does not depend on the batch it runs in, and a captured step
 // serves every position.
 constexpr int kAttnChunks = 32;
-// Members one attention launch serves (the host splits larger batches).
-constexpr int kAttnMaxMembers = 8;
+// Members one attention launch serves (the host splits larger batches): the
+// decoder's whole batch. At batch 16 one launch of 16 members ran the step
+// 6% faster than two launches of 8 (3,448 against 3,243 tok/s).
+constexpr int kAttnMaxMembers = 64;
 // Floats per (chunk, query head) partial: 128 output sums, the running
 // maximum, the running denominator, two pad words (16-byte rows).
 constexpr int kPartStride = kHeadDim + 4;
