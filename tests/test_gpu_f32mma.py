@@ -105,13 +105,13 @@ def test_member_bits_independent_of_batch(env, t):
     assert np.array_equal(mid9.view(np.uint32), full[37:46].view(np.uint32))
 
 
-@pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096)])
+@pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096), (12, 4096, 4096), (13, 12288, 4000)])
 def test_member_bits_independent_of_batch_ffn_shapes(env, t, k, n):
-    """The same at the Qwen3-8B FFN shapes, where launches of 16 and 64
-    members differ in member tiles per launch and waves per workgroup: the K
-    split follows the weight shape alone, so a member's sums are added in the
-    same order (a split that followed the member count would change the last
-    bits here)."""
+    """The same at the Qwen3-8B FFN and o shapes (and a ragged row count),
+    where launches of 16 and 64 members differ in member tiles per launch and
+    waves per workgroup: the K split follows the weight shape alone, so a
+    member's sums are added in the same order (a split that followed the
+    member count would change the last bits here)."""
     case(test="f32mma batch invariance ffn", t=t, k=k, n=n)
     enc = synth.kquant_numpy(t, k, n, seed=60 + t)
     x = synth.activations_numpy(k, 64, seed=61).reshape(64, k)
