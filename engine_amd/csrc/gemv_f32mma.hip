@@ -111,6 +111,10 @@ struct PackArgs {
     uint8_t* act;
     F32MmaLayout L;
     int K;
+    // a pending residual update of x (F32MmaFold): x += the splits' sums in
+    // split order, stored back to x, before packing
+    const float* fold_partial;
+    int fold_splits;
 };
 
 template <int PIECES>
@@ -132,6 +136,25 @@ __global__ __launch_bounds__(64) void pack_f32mma_kernel(PackArgs a) {
         const float4 x1 = *reinterpret_cast<const float4*>(a.x + e0 + 4);
         v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
         v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+        if (a.fold_splits > 0) {
+            // y += g with g = ((0 + p_0) + p_1) + ... (f32mma_reduce_kernel's
+            // sum and its unit RMSNorm factor), stored back as the residual
+            float gs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            const size_t split_elems = (size_t)gridDim.y * a.K;
+            for (int sp = 0; sp < a.fold_splits; ++sp) {
+                const float* p = a.fold_partial + (size_t)sp * split_elems + e0;
+                const float4 p0 = *reinterpret_cast<const float4*>(p);
+                const float4 p1 = *reinterpret_cast<const float4*>(p + 4);
+                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) gs[j] += pv[j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = v[j] + gs[j] * 1.0f;
+            float* xw = const_cast<float*>(a.x) + e0;
+            *reinterpret_cast<float4*>(xw) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4*>(xw + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
         if (a.x2 != nullptr) {
             const float4 u0 = *reinterpret_cast<const float4*>(a.x2 + e0);
             const float4 u1 = *reinterpret_cast<const float4*>(a.x2 + e0 + 4);
@@ -267,6 +290,7 @@ struct F32MmaArgs {
     float* partial;
     int splits;
     int split_blocks;
+    int skip_reduce;  // the caller takes the split sums (F32MmaFold) instead of a reduce launch
 };
 
 template <int T> struct WRaw;
@@ -964,7 +988,7 @@ hipError_t launch_shape(F32MmaArgs a, const F32MmaShape& sh, hipStream_t stream)
     hipLaunchKernelGGL((f32mma_gemv_kernel<T, R, MT, PAIR, lds_slots<T, MT>(), ring_depth<T, R, MT>()>),
                        dim3((unsigned)sh.groups, (unsigned)sh.splits), dim3(64 * (sh.waves + 1)), 0, stream, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.splits == 1) return e;
+    if (e != hipSuccess || a.splits == 1 || a.skip_reduce) return e;
     const int rows = a.pair_swiglu ? a.rows_end[0] : a.total_rows;
     const int threads = a.count_here * rows;
     hipLaunchKernelGGL(f32mma_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
@@ -978,7 +1002,7 @@ hipError_t launch_mt(const F32MmaArgs& a, const F32MmaShape& one, int tiles, int
 }
 
 template <int T>
-hipError_t launch_t(const F32MmaArgs& a, size_t partial_bytes, int cu_count, hipStream_t stream) {
+hipError_t launch_t(const F32MmaArgs& a, size_t partial_bytes, int cu_count, F32MmaFold* defer, hipStream_t stream) {
     constexpr int kStep = 16 * max_tiles<T>();
     const int nb = a.K >> 8;
     const bool pair = a.pair_swiglu != 0;
@@ -987,8 +1011,17 @@ hipError_t launch_t(const F32MmaArgs& a, size_t partial_bytes, int cu_count, hip
     const size_t split_bytes = (size_t)kStep * (size_t)vrows * 4;
     const int max_splits = a.partial == nullptr ? 1 : (int)std::min<size_t>(16, partial_bytes / split_bytes);
     const F32MmaShape one = f32mma_split(tiles, nb, max_splits, cu_count);
+    // an accumulating single-weight product of one launch may leave its split
+    // sums to the next call (F32MmaFold)
+    const bool deferred = defer != nullptr && one.splits > 1 && a.accumulate && !pair && a.count == 1 &&
+                          !a.has_norm && a.members <= kStep;
+    if (defer != nullptr) {
+        *defer = F32MmaFold{};
+        if (deferred) *defer = F32MmaFold{a.y[0], a.partial, one.splits, a.members, a.total_rows};
+    }
     for (int m0 = 0; m0 < a.members; m0 += kStep) {
         F32MmaArgs c = a;
+        c.skip_reduce = deferred ? 1 : 0;
         c.member0 = m0;
         c.count_here = std::min(kStep, a.members - m0);
         const int mts = (c.count_here + 15) / 16;
@@ -1016,6 +1049,28 @@ bool rows_tile_aligned(const WaveGemvArgs& a) {
 }
 
 }  // namespace
+
+namespace {
+
+// y[m][r] += ((0 + p_0) + p_1) + ... (a pending F32MmaFold finished on its own:
+// f32mma_reduce_kernel's sum and unit factor). One thread per element.
+__global__ __launch_bounds__(256) void f32mma_fold_flush_kernel(F32MmaFold f) {
+    const int idx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (idx >= f.members * f.rows) return;
+    float g = 0.f;
+    for (int sp = 0; sp < f.splits; ++sp) g += f.partial[(size_t)sp * f.members * f.rows + idx];
+    f.y[idx] += g * 1.0f;
+}
+
+}  // namespace
+
+hipError_t launch_f32mma_fold_flush(F32MmaFold* f, hipStream_t stream) {
+    if (f == nullptr || f->splits <= 0) return hipSuccess;
+    const int n = f->members * f->rows;
+    hipLaunchKernelGGL(f32mma_fold_flush_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, *f);
+    *f = F32MmaFold{};
+    return hipGetLastError();
+}
 
 F32MmaLayout f32mma_layout(int members, int K, int pieces) {
     F32MmaLayout L{};
@@ -1053,6 +1108,14 @@ hipError_t launch_gemv_f32mma(int value_type, const WaveGemvArgs& a, void* scrat
     p.act = static_cast<uint8_t*>(scratch);
     p.L = L;
     p.K = a.K;
+    if (a.fold != nullptr && a.fold->splits > 0) {
+        // the pending update must be of exactly this input
+        if (a.fold->y != a.x || a.fold->members != a.members || a.fold->rows != a.K || a.x2 != nullptr) {
+            return hipErrorInvalidValue;
+        }
+        p.fold_partial = a.fold->partial;
+        p.fold_splits = a.fold->splits;
+    }
     if (pieces == 3) {
         hipLaunchKernelGGL(pack_f32mma_kernel<3>, dim3((unsigned)L.parts, (unsigned)a.members), dim3(64), 0, stream, p);
     } else {
@@ -1084,15 +1147,16 @@ hipError_t launch_gemv_f32mma(int value_type, const WaveGemvArgs& a, void* scrat
     const size_t part_bytes = part_off < scratch_bytes ? scratch_bytes - part_off : 0;
     m.splits = 1;
     m.split_blocks = a.K >> 8;
-    auto run = [&](const F32MmaArgs& args) -> hipError_t {
+    auto run = [&](const F32MmaArgs& args, F32MmaFold* defer) -> hipError_t {
         switch (value_type) {
-        case kQ4K: return launch_t<kQ4K>(args, part_bytes, cu_count, stream);
-        case kQ5K: return launch_t<kQ5K>(args, part_bytes, cu_count, stream);
-        case kQ6K: return launch_t<kQ6K>(args, part_bytes, cu_count, stream);
+        case kQ4K: return launch_t<kQ4K>(args, part_bytes, cu_count, defer, stream);
+        case kQ5K: return launch_t<kQ5K>(args, part_bytes, cu_count, defer, stream);
+        case kQ6K: return launch_t<kQ6K>(args, part_bytes, cu_count, defer, stream);
         default: return hipErrorInvalidValue;
         }
     };
-    if (rows_tile_aligned(a)) return run(m);
+    if (rows_tile_aligned(a)) return run(m, a.count == 1 ? a.defer : nullptr);
+    if (a.defer != nullptr) *a.defer = F32MmaFold{};
     // a group whose matrices do not end on whole tiles: one launch per matrix
     // over the shared packed activations, each as its single-matrix call
     for (int i = 0; i < a.count; ++i) {
@@ -1104,7 +1168,7 @@ hipError_t launch_gemv_f32mma(int value_type, const WaveGemvArgs& a, void* scrat
         one.rows_end[0] = a.rows_end[i] - start;
         one.total_rows = one.rows_end[0];
         one.count = 1;
-        e = run(one);
+        e = run(one, nullptr);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

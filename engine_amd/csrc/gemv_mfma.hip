@@ -720,12 +720,23 @@ int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith) 
     return per;
 }
 
-hipError_t launch_gemv(int value_type, const WaveGemvArgs& a, void* act_scratch, int cu_count, hipStream_t stream) {
+hipError_t launch_gemv(int value_type, const WaveGemvArgs& a0, void* act_scratch, int cu_count, hipStream_t stream) {
+    WaveGemvArgs a = a0;
+    if (a.arith == kArithF32 && act_scratch != nullptr && f32mma_supported(value_type, a) &&
+        f32mma_layout(a.members, a.K).total <= gemv_act_scratch_bytes()) {
+        return launch_gemv_f32mma(value_type, a, act_scratch, gemv_act_scratch_bytes(), cu_count, stream);
+    }
+    // any other path: a pending residual update is added on its own first,
+    // and this call leaves nothing pending
+    if (a.fold != nullptr && a.fold->splits > 0) {
+        F32MmaFold f = *a.fold;
+        hipError_t e = launch_f32mma_fold_flush(&f, stream);
+        if (e != hipSuccess) return e;
+        a.fold = nullptr;
+    }
+    if (a.defer != nullptr) *a.defer = F32MmaFold{};
+    a.defer = nullptr;
     if (a.arith == kArithF32) {
-        if (act_scratch != nullptr && f32mma_supported(value_type, a) &&
-            f32mma_layout(a.members, a.K).total <= gemv_act_scratch_bytes()) {
-            return launch_gemv_f32mma(value_type, a, act_scratch, gemv_act_scratch_bytes(), cu_count, stream);
-        }
         // the f32 wave GEMV, in launch groups of as many members as it stages;
         // 3..8 members over a K of several slices split by slice when the
         // context scratch holds their slice totals

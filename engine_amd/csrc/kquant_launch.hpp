@@ -28,6 +28,19 @@ constexpr int kProSwiglu = 2;
 // Members one SwiGLU-prologue launch serves (the host splits larger batches).
 constexpr int kSwigluMaxMembers = 2;
 
+// A residual update the f32-faithful matrix-core GEMV left pending: the raw
+// split sums of an accumulating product, y[m][r] += sum over splits in split
+// order of partial[split][m][r] (what f32mma_reduce_kernel would have added).
+// The next f32-faithful call whose input x is that y adds them first
+// (identical bits) and stores y, so the reduce launch disappears.
+struct F32MmaFold {
+    float* y;              // [members][rows]
+    const float* partial;  // [splits][members][rows]
+    int splits;            // 0: nothing pending
+    int members;
+    int rows;
+};
+
 struct WaveGemvArgs {
     const uint8_t* w[kMaxGroup];
     uint32_t wbytes[kMaxGroup];
@@ -50,6 +63,12 @@ struct WaveGemvArgs {
     int arith;
     // f32 launches split by slice: [slices][members][total_rows] slice totals
     float* partial;
+    // f32-faithful matrix-core path only (9..64 members): `defer` (an
+    // accumulating single-weight product) receives its pending split sums
+    // instead of a reduce launch, or splits = 0 if it finished; `fold` (an
+    // input x equal to fold->y) adds pending sums into x first.
+    F32MmaFold* defer;
+    const F32MmaFold* fold;
 };
 
 constexpr int kArithF32 = 0;
@@ -144,6 +163,9 @@ constexpr size_t kF32MmaPartialBytes = (size_t)16 << 20;
 // f32mma_layout(members, K).total bytes, then the partials.
 hipError_t launch_gemv_f32mma(int value_type, const WaveGemvArgs& args, void* scratch, size_t scratch_bytes,
                               int cu_count, hipStream_t stream);
+// Adds a pending F32MmaFold into its y on its own (when no f32-faithful call
+// consumes it) and clears it; nothing when none is pending.
+hipError_t launch_f32mma_fold_flush(F32MmaFold* fold, hipStream_t stream);
 
 // ---- Q8_1 activations and the integer-dot GEMV (q8_1.hip)
 

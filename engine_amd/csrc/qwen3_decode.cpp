@@ -180,13 +180,24 @@ namespace {
 // GEMV over `count` weights of one value type sharing the activation x, in
 // launch groups of as many members as one launch serves (the wave GEMV, or the
 // matrix-core GEMV for 3..16 members of Q4_K / Q5_K).
+// `fold`: the residual update of x pending from the previous accumulating
+// product (the f32-faithful matrix-core GEMV adds it while packing x, or it
+// is added on its own first); `defer`: this accumulating product may leave
+// its own split sums pending there instead of a reduce launch.
 hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight* const* ws, int count,
                 const float* x, const float* x2, const float* gamma, float* const* ys, int members, bool accumulate,
-                hipStream_t stream, bool pair = false) {
+                hipStream_t stream, bool pair = false, ribn_amd::F32MmaFold* fold = nullptr,
+                ribn_amd::F32MmaFold* defer = nullptr) {
     const int K = (int)ws[0]->input_size;
     const int arith = arith_of_mode(d->gemv_mode);
     const int per = ribn_amd::gemv_launch_members((int)ws[0]->value_type, K, x2 != nullptr, arith);
     if (per <= 0) return hipErrorInvalidValue;
+    if (fold != nullptr && fold->splits > 0 && members > per) {
+        // several launch groups: the update goes in on its own first
+        hipError_t e = ribn_amd::launch_f32mma_fold_flush(fold, stream);
+        if (e != hipSuccess) return e;
+    }
+    if (members > per) defer = nullptr;
     for (int m0 = 0; m0 < members; m0 += per) {
         const int mc = std::min(per, members - m0);
         ribn_amd::WaveGemvArgs a{};
@@ -210,9 +221,12 @@ hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight*
         a.accumulate = accumulate ? 1 : 0;
         a.pair_swiglu = pair ? 1 : 0;
         a.arith = arith;
+        a.fold = fold != nullptr && fold->splits > 0 ? fold : nullptr;
+        a.defer = defer;
         hipError_t e = ribn_amd::launch_gemv((int)ws[0]->value_type, a, d->ctx->act_scratch, d->ctx->cu_count,
                                              stream);
         if (e != hipSuccess) return e;
+        if (fold != nullptr) *fold = ribn_amd::F32MmaFold{};  // consumed (or flushed) by this call
     }
     return hipSuccess;
 }
@@ -220,12 +234,14 @@ hipError_t wave(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight*
 // RMSNorm-fused GEMVs of weights sharing one input: one launch per run of
 // equal value types (q/k/v or gate/up of Q4_K_M files may mix types).
 hipError_t wave_shared(const ribn_amd_qwen3_decode* d, const ribn_amd_quantized_weight* const* ws, float* const* ys,
-                       int count, const float* x, const float* gamma, int members, hipStream_t stream) {
+                       int count, const float* x, const float* gamma, int members, hipStream_t stream,
+                       ribn_amd::F32MmaFold* fold = nullptr) {
     int i = 0;
     while (i < count) {
         int j = i + 1;
         while (j < count && ws[j]->value_type == ws[i]->value_type) ++j;
-        hipError_t e = wave(d, ws + i, j - i, x, nullptr, gamma, ys + i, members, false, stream);
+        // the first launch takes the pending update of x (and clears it)
+        hipError_t e = wave(d, ws + i, j - i, x, nullptr, gamma, ys + i, members, false, stream, false, fold);
         if (e != hipSuccess) return e;
         i = j;
     }
@@ -283,34 +299,44 @@ hipError_t enqueue_step(ribn_amd_qwen3_decode* d, const GraphKey& key, hipStream
                                               (uint32_t)d->token_embd->encoded_bytes, d->tokens, 0, d->hidden,
                                               c.hidden / 256, c.vocab, (uint32_t)members, stream);
     if (e != hipSuccess) return e;
+    // The o and down products add into the residual d->hidden. With split K
+    // on the f32-faithful matrix-core GEMV (9..64 members) they leave their
+    // split sums pending and the next RMSNorm-fused GEMV over d->hidden adds
+    // them while packing it (the same sums, so the same bits as a reduce
+    // launch).
+    ribn_amd::F32MmaFold pending{};
     for (uint32_t l = 0; l < c.layers; ++l) {
         const ribn_amd_qwen3_layer& L = d->layers[l];
         const ribn_amd_quantized_weight* qkv[3] = {L.attn_q, L.attn_k, L.attn_v};
         float* qkv_out[3] = {d->q, d->k, d->v};
-        e = wave_shared(d, qkv, qkv_out, 3, d->hidden, L.attn_norm, members, stream);
+        e = wave_shared(d, qkv, qkv_out, 3, d->hidden, L.attn_norm, members, stream, &pending);
         if (e != hipSuccess) return e;
         e = attention(c, d->members_dev, key.chunks, key.appended, members, l, d->q, d->k, d->v, L.attn_q_norm,
                       L.attn_k_norm, d->positions, d->attn, d->partials, stream);
         if (e != hipSuccess) return e;
-        e = wave(d, &L.attn_output, 1, d->attn, nullptr, nullptr, &d->hidden, members, true, stream);
+        e = wave(d, &L.attn_output, 1, d->attn, nullptr, nullptr, &d->hidden, members, true, stream, false, nullptr,
+                 &pending);
         if (e != hipSuccess) return e;
         const ribn_amd_quantized_weight* gu[2] = {L.ffn_gate, L.ffn_up};
         if (L.ffn_gate->value_type == L.ffn_up->value_type && c.hidden <= (uint32_t)ribn_amd::kSliceK) {
             // gate/up pairs store silu(gate) * up; down reads it as a plain input
             float* act[2] = {d->gate, d->gate};
-            e = wave(d, gu, 2, d->hidden, nullptr, L.ffn_norm, act, members, false, stream, true);
+            e = wave(d, gu, 2, d->hidden, nullptr, L.ffn_norm, act, members, false, stream, true, &pending);
             if (e != hipSuccess) return e;
-            e = wave(d, &L.ffn_down, 1, d->gate, nullptr, nullptr, &d->hidden, members, true, stream);
+            e = wave(d, &L.ffn_down, 1, d->gate, nullptr, nullptr, &d->hidden, members, true, stream, false, nullptr,
+                     &pending);
         } else {
             float* gu_out[2] = {d->gate, d->up};
-            e = wave_shared(d, gu, gu_out, 2, d->hidden, L.ffn_norm, members, stream);
+            e = wave_shared(d, gu, gu_out, 2, d->hidden, L.ffn_norm, members, stream, &pending);
             if (e != hipSuccess) return e;
-            e = wave(d, &L.ffn_down, 1, d->gate, d->up, nullptr, &d->hidden, members, true, stream);
+            e = wave(d, &L.ffn_down, 1, d->gate, d->up, nullptr, &d->hidden, members, true, stream, false, nullptr,
+                     &pending);
         }
         if (e != hipSuccess) return e;
     }
-    if (!key.head) return hipSuccess;
-    e = wave(d, &d->output, 1, d->hidden, nullptr, d->output_norm, &d->logits, members, false, stream);
+    if (!key.head) return ribn_amd::launch_f32mma_fold_flush(&pending, stream);
+    e = wave(d, &d->output, 1, d->hidden, nullptr, d->output_norm, &d->logits, members, false, stream, false,
+             &pending);
     if (e != hipSuccess) return e;
     return ribn_amd::launch_argmax(d->logits, (int)c.vocab, members, d->selected, d->tokens,
                                    key.advance ? d->positions : nullptr, d->steps, d->history,
