@@ -211,12 +211,13 @@ uint32_t ribn_amd_gemv_value_type(const ribn_amd_gemv *gemv);
  *     (the reference's batch cap) share one weight stream (from 3 members,
  *     K > 4096 is split by 4096-wide slice and the slice totals added in
  *     order); every row is bit-identical to the single-member call. From 9
- *     to 64 members the products run on the bf16 matrix cores at f32
- *     precision (activations split exactly into three bf16 pieces, f32
- *     accumulation) with the weights read once per 32 members: rows agree
- *     with the single call to f32 rounding (within 5e-5 normwise of the
- *     sequential f32 GEMV), and a member's bits do not depend on the rest of
- *     the batch.
+ *     to 64 members the products run on the matrix cores at f32 precision
+ *     (Q4_K / Q5_K: quants times group scale exact in f16, activations in
+ *     two f16 pieces; Q6_K: activations in three bf16 pieces; f32
+ *     accumulation) with the weights read once per 64 members (32 for
+ *     Q6_K): rows agree with the single call to f32 rounding (within 5e-5
+ *     normwise of the sequential f32 GEMV), and a member's bits do not
+ *     depend on the rest of the batch.
  *   RIBN_AMD_GEMV_FIXED16 (opt-in, lossy; no reference twin, used like
  *     GemvMode::IntegerDot for throughput comparison): activations rounded to
  *     block fixed point (16-bit per scale group in the wave kernel, 15-bit per
