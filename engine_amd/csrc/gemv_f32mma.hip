@@ -394,7 +394,7 @@ __device__ __forceinline__ void q6_group(const WRaw<kQ6K>& d, int g, uint32_t& o
     o1 = out[1];
 }
 
-// Compile-time loop: f(std::integral_constant<int, I>) for I in [I0, N).
+// Compile-time loop: f(std::integral_constant<int, J>) for J in [I, N).
 template <int I, int N> struct StaticFor {
     template <typename F> __device__ __forceinline__ static void run(F& f) {
         if constexpr (I < N) {

@@ -131,7 +131,7 @@ hipError_t launch_pack_act16(const float* x, const float* gamma, int members, in
                              hipStream_t stream);
 hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& args, int cu_count, hipStream_t stream);
 
-// ---- f32-faithful batched GEMV on the bf16 matrix cores (gemv_f32mma.hip)
+// ---- f32-faithful batched GEMV on the matrix cores (gemv_f32mma.hip)
 //
 // The default f32 arithmetic for 9..64 members: exact products on the
 // matrix cores (Q4_K / Q5_K: quants times group scale exact in f16 against
@@ -143,8 +143,8 @@ hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& args, int cu_cou
 constexpr int kF32MmaMinMembers = 9;
 constexpr int kF32MmaMaxMembers = 64;
 // Byte offsets of the packed activations of `members` x K (K a multiple of
-// 256): bf16-piece MFMA fragments, f32 group sums, per-workgroup partial sums
-// of squares.
+// 256): the pieces' MFMA fragments, f32 group sums, inverse block scales (f16
+// form), per-workgroup partial sums of squares.
 struct F32MmaLayout {
     uint32_t frag, xsum, iscale, ssq, total;
     int nb;     // super-blocks of K
@@ -182,7 +182,7 @@ hipError_t launch_gemv_q8_1(int value_type, const uint8_t* w, uint32_t wbytes, c
 size_t gemv_act_scratch_bytes();
 // Members one launch_gemv call may carry for this shape and arithmetic.
 int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith);
-// kArithF32: 9..64 members on the bf16 matrix cores (launch_gemv_f32mma),
+// kArithF32: 9..64 members on the matrix cores (launch_gemv_f32mma),
 // else the f32 wave GEMV, split into the launch groups it stages.
 // kArithFixed16: the block fixed-point wave GEMV, or from kMfmaMinMembers
 // (kMfmaMinMembersLongK for K spanning several slices) up to 16 members
