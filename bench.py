@@ -496,6 +496,110 @@ def bench_q8_1(E, synth, torch, args):
     }
 
 
+# The reference's own GEMV figures (`crates/nvidia/examples/int_dot_bench.rs`, shapes at :24,
+# weight bytes / median host-timed launch + synchronize at :493-525), RTX 4090, weight GB/s,
+# `benchmarks/qwen-prefill-qualification.md:515-523` ("after" columns): (batch 1, batch 8).
+PUBLISHED_SHAPES = ((5120, 5120), (5120, 17408), (17408, 5120))
+PUBLISHED_RTX4090 = {
+    12: ((1027.4, 276.1), (1454.1, 433.3), (1353.8, 296.2)),
+    13: ((975.0, 323.3), (1303.2, 504.1), (1178.5, 351.7)),
+    14: ((1157.6, 403.9), (1537.7, 597.1), (1417.0, 418.4)),
+}
+
+
+def bench_published(E, synth, torch, args):
+    """The reference's published GEMV shapes (Qwen3.x-27B: K x N = 5120x5120, 5120x17408,
+    17408x5120) for Q4_K / Q5_K / Q6_K, batch 1 (execute_warp) and 8 members
+    (execute_warp_batch), weight GB/s = encoded weight bytes / time per launch, three ways:
+    - host: the reference's method (one matrix, launch + synchronize timed on the host,
+      median of --steps iterations); the matrix stays cache-resident, like the RTX 4090
+      figures it sits beside (every one of these matrices fits that card's 72 MB L2);
+    - resident: the same matrix, back-to-back launches replayed as a HIP graph, device time
+      per launch (the matrix sits in the 256 MB Infinity Cache);
+    - hbm: launches rotate over distinct copies of the matrix totalling at least 1 GB, so
+      every launch streams its weights from HBM (the roofline figure)."""
+    import math
+    import statistics
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    ctx = E.AmdContext(0, stream=stream)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    iters = max(20, args.steps)
+    rows_out = []
+    for t in (12, 13, 14):
+        kern = E.QwenGemvKernel.from_value_type(ctx, t)
+        for si, (k, n) in enumerate(PUBLISHED_SHAPES):
+            wbytes = n * (k // 256) * BLOCK_BYTES[t]
+            base = synth.kquant_torch(t, k, n, gen, dev)
+            copies = max(2, math.ceil(1.0e9 / wbytes))
+            store = E.AmdWeightStore(ctx)
+            tensors = [base] + [base.clone() for _ in range(copies - 1)]
+            ws = []
+            for ci, enc in enumerate(tensors):
+                store.materialize_quantized(f"w{ci}", [k, n], t, enc)
+                ws.append(store.quantized_tensor(f"w{ci}"))
+            for members in (1, 8):
+                x = torch.randn(members * k, device=dev, generator=gen)
+                y = torch.empty(members * n, device=dev)
+
+                def one(w):
+                    if members == 1:
+                        kern.execute_warp(w, x, y)
+                    else:
+                        kern.execute_warp_batch(w, x, y, members)
+
+                with torch.cuda.stream(stream):
+                    for _ in range(5):
+                        one(ws[0])
+                torch.cuda.synchronize()
+                host = []
+                for _ in range(iters):
+                    t0 = time.perf_counter()
+                    with torch.cuda.stream(stream):
+                        one(ws[0])
+                    stream.synchronize()
+                    host.append(time.perf_counter() - t0)
+                host_us = statistics.median(host) * 1e6
+                reps = max(2, iters // 10)
+                resident_us = _graph_time_us(torch, stream, lambda: [one(ws[0]) for _ in range(32)], reps) / 32
+                hbm_us = _graph_time_us(torch, stream, lambda: [one(w) for w in ws], reps) / len(ws)
+                pub = PUBLISHED_RTX4090[t][si][0 if members == 1 else 1]
+                row = {"type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}[t], "k": k, "n": n, "members": members,
+                       "weight_bytes": wbytes, "copies_rotated": len(ws),
+                       "host_us": round(host_us, 2), "host_GBps": round(wbytes / host_us / 1e3, 1),
+                       "resident_us": round(resident_us, 2), "resident_GBps": round(wbytes / resident_us / 1e3, 1),
+                       "hbm_us": round(hbm_us, 2), "hbm_GBps": round(wbytes / hbm_us / 1e3, 1),
+                       "hbm_frac": round(wbytes / hbm_us / 1e3 / PEAK_HBM_GBS, 4),
+                       "rtx4090_published_GBps": pub}
+                rows_out.append(row)
+                log(f"bench published: {row['type']} {k}x{n} M={members}: host {row['host_GBps']} GB/s, "
+                    f"resident {row['resident_GBps']}, hbm {row['hbm_GBps']} ({row['hbm_frac']:.1%}); "
+                    f"RTX 4090 published {pub}")
+            for w in ws:
+                w.close()
+            del ws, tensors, base, store
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+        kern.close()
+    q4 = [r for r in rows_out if r["type"] == "Q4_K" and r["members"] == 1]
+    hbm = sum(r["weight_bytes"] for r in q4) / sum(r["hbm_us"] for r in q4) / 1e3
+    return {
+        "metric": "Q4_K warp GEMV weight GB/s at the reference's published shapes, batch 1, HBM-streamed",
+        "value": round(hbm, 1), "unit": "GB/s", "n_gpus": 1, "steps": iters, "warmup": 5,
+        "ms_per_step": round(sum(r["hbm_us"] for r in q4) / 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "reference-published-shapes", "rows": rows_out,
+                   "note": "rtx4090_published_GBps are the reference's cache-resident RTX 4090 figures; "
+                           "host_GBps follows the reference's timing method on this GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(hbm, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(hbm / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "gemv_f32_kernel, Q4_K, the three published shapes, batch 1"},
+        "cpu_baseline": None,
+    }
+
+
 def bench_gguf(E, synth, torch, args):
     """GGUF staging (the format step before the path): writes a Qwen3-8B-shaped
     GGUF (Q4_K token_embd and projections, Q5_K down, Q6_K output, f32 norms)
@@ -867,14 +971,16 @@ def main():
                     help="GEMV arithmetic: warp (f32 activations, default) or fixed16 (opt-in block fixed point)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", choices=("decode", "batched", "prefill", "model", "q8_1", "gguf", "serving",
-                                           "mfma-peak"),
+                                           "mfma-peak", "published"),
                     default="decode",
                     help="decode: BASELINE config 1 (the headline line, default, which also carries the "
                          "config-4 tok/s); batched: config 2 (FFN at M = 1, 4, 16, 64); prefill: config 3 "
                          "(M = 512 bf16 matmuls); model: config 4 alone (full decoder, batch 1 and 8); q8_1: "
                          "the Q8_1 integer-dot projections (pack + GEMV) at batch 1 and 8; gguf: GGUF "
                          "open + staging of a Qwen3-8B-shaped file (--layers layers); mfma-peak: the "
-                         "measured dense peak of the matrix-core instructions the prefill uses")
+                         "measured dense peak of the matrix-core instructions the prefill uses; published: the "
+                         "reference's own GEMV bench shapes (int_dot_bench), batch 1 and 8, beside its RTX 4090 "
+                         "figures")
     ap.add_argument("--context", type=int, default=2048, help="config 4: prompt tokens before generation")
     ap.add_argument("--gen-tokens", type=int, default=128, help="config 4: greedy tokens timed")
     ap.add_argument("--prompt-chunk", type=int, default=2048,
@@ -907,9 +1013,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    if args.workload in ("batched", "prefill", "q8_1", "gguf", "mfma-peak"):
+    if args.workload in ("batched", "prefill", "q8_1", "gguf", "mfma-peak", "published"):
         result = {"batched": bench_batched, "prefill": bench_prefill, "q8_1": bench_q8_1,
-                  "gguf": bench_gguf, "mfma-peak": bench_mfma_peak}[args.workload](
+                  "gguf": bench_gguf, "mfma-peak": bench_mfma_peak, "published": bench_published}[args.workload](
             E, synth, torch, args)
         print(json.dumps(result), flush=True)
         return

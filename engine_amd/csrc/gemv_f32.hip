@@ -691,7 +691,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_f32_kernel(WaveGemvArgs args)
                 const uint32_t off = (last && row < r_end && lane == 0 && m < members)
                                          ? (uint32_t)(m * rows_mat + local) * 4u
                                          : kOutOfRange;
-                if constexpr (PAIR) {
+                if constexpr (SPLIT) {
+                    // this workgroup's slice total P_s, as the several-member pass stores it
+                    const uint32_t poff = (row < r_end && lane == 0 && m < members)
+                                              ? (uint32_t)((slice0 * members + m) * args.total_rows + row) * 4u
+                                              : kOutOfRange;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ps), partial_r, (int)poff, 0, 0);
+                } else if constexpr (PAIR) {
                     if (r % 2 == 0) {
                         gk[m] = total;
                     } else {
@@ -880,11 +886,14 @@ hipError_t launch_type(const WaveGemvArgs& a, int cu_count, hipStream_t stream) 
     return launch_plain<T, kProPlain>(a, cu_count, stream);
 }
 
-// Three to eight members over a K of several slices: one workgroup per
-// (row range, slice), then the ordered slice reduction.
+// Members over a K of several slices: one workgroup per (row range, slice),
+// then the ordered slice reduction. One member (a K beyond kWaveMaxK) keeps
+// its records in VGPRs, as the one-launch form does.
 template <int T>
 hipError_t launch_split(const WaveGemvArgs& a, int cu_count, hipStream_t stream) {
-    hipError_t e = (a.members <= 4)
+    hipError_t e = (a.members == 1)
+                       ? F32Instance<T, 1, kProPlain, true, 3, 8, 1, false, true>::launch(a, cu_count, 1, stream)
+                   : (a.members <= 4)
                        ? F32Instance<T, 4, kProPlain, true, 4, 8, 1, false, true>::launch(a, cu_count, 1, stream)
                        : F32Instance<T, 8, kProPlain, true, (T != kQ6K ? 4 : 3), 8, 1, false, true>::launch(
                              a, cu_count, 1, stream);
@@ -904,8 +913,11 @@ size_t f32_split_partial_bytes(int members, int K, int total_rows) {
 }
 
 hipError_t launch_gemv_f32_split(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream) {
-    if (args.members < 3 || args.members > kWaveMaxMembers || args.K <= kSliceElems || args.K > kWaveMaxK ||
-        args.gamma != nullptr || args.x2 != nullptr || args.pair_swiglu || args.partial == nullptr) {
+    const int min_members = args.K > kWaveMaxK ? 1 : 3;
+    if (args.members < min_members || args.members > kWaveMaxMembers || args.K <= kSliceElems ||
+        args.K > kF32SplitMaxK || args.K % 256 != 0 || args.gamma != nullptr || args.x2 != nullptr ||
+        args.pair_swiglu || args.partial == nullptr ||
+        f32_split_partial_bytes(args.members, args.K, args.total_rows) > kF32SplitScratchBytes) {
         return hipErrorInvalidValue;
     }
     switch (value_type) {
@@ -914,6 +926,13 @@ hipError_t launch_gemv_f32_split(int value_type, const WaveGemvArgs& args, int c
     case kQ6K: return launch_split<kQ6K>(args, cu_count, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+int f32_long_k_members(int K, int total_rows) {
+    if (K <= kWaveMaxK || K > kF32SplitMaxK || K % 256 != 0 || total_rows < 1) return 0;
+    int m = kWaveMaxMembers;
+    while (m > 0 && f32_split_partial_bytes(m, K, total_rows) > kF32SplitScratchBytes) --m;
+    return m;
 }
 
 int f32_max_members(int K) {

@@ -695,7 +695,6 @@ hipError_t launch_gemv_mfma(int value_type, const MfmaGemvArgs& a, int /*cu_coun
 
 // The context scratch serves either the packed activations of the matrix-core
 // GEMV or the slice totals of a split f32 launch (never both in one call).
-constexpr size_t kF32SplitScratchBytes = (size_t)2 << 20;
 size_t gemv_act_scratch_bytes() {
     const size_t f32mma = ((size_t)f32mma_layout(kF32MmaMaxMembers, kWaveMaxK).total + 255) / 256 * 256 +
                           kF32MmaPartialBytes;
@@ -705,7 +704,10 @@ size_t gemv_act_scratch_bytes() {
 
 int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith) {
     if (arith == kArithF32) {
-        if (K < 256 || K > kWaveMaxK) return 0;
+        // a K beyond one launch's staging: launch_gemv runs the whole batch as
+        // slice-split groups
+        if (K > kWaveMaxK) return (!swiglu_prologue && K <= kF32SplitMaxK && K % 256 == 0) ? kF32MmaMaxMembers : 0;
+        if (K < 256) return 0;
         // the whole batch: launch_gemv takes 9..64 members to the matrix
         // cores and splits smaller calls into the launch groups each wave
         // form stages
@@ -736,6 +738,28 @@ hipError_t launch_gemv(int value_type, const WaveGemvArgs& a0, void* act_scratch
     }
     if (a.defer != nullptr) *a.defer = F32MmaFold{};
     a.defer = nullptr;
+    if (a.arith == kArithF32 && a.K > kWaveMaxK) {
+        // K beyond what one workgroup stages: groups of up to 8 members in the
+        // slice-split form (one slice staged per workgroup, the slice totals
+        // added in order by the reduce launch), plain or accumulating products
+        const int per = f32_long_k_members(a.K, a.total_rows);
+        if (per <= 0 || act_scratch == nullptr || a.x2 != nullptr || a.gamma != nullptr || a.pair_swiglu) {
+            return hipErrorInvalidValue;
+        }
+        for (int m0 = 0; m0 < a.members; m0 += per) {
+            WaveGemvArgs c = a;
+            c.members = std::min(per, a.members - m0);
+            c.x = a.x + (size_t)m0 * a.K;
+            for (int i = 0; i < a.count; ++i) {
+                const int n = a.rows_end[i] - (i > 0 ? a.rows_end[i - 1] : 0);
+                c.y[i] = a.y[i] + (size_t)m0 * n;
+            }
+            c.partial = static_cast<float*>(act_scratch);
+            hipError_t e = launch_gemv_f32_split(value_type, c, cu_count, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     if (a.arith == kArithF32) {
         // the f32 wave GEMV, in launch groups of as many members as it stages;
         // 3..8 members over a K of several slices split by slice when the

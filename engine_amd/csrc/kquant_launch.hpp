@@ -19,6 +19,12 @@ constexpr int kWaveMaxK = 16384;
 // K one wave covers per unit (16 super-blocks); the many-member and gate/up
 // pair forms need K within it.
 constexpr int kSliceK = 4096;
+// Largest K of the f32 GEMV's slice-split form, which stages one slice per
+// workgroup and so serves a K beyond kWaveMaxK (plain and accumulating
+// products, no fused prologue), and the bytes of slice totals it may keep
+// in the context scratch.
+constexpr int kF32SplitMaxK = 65536;
+constexpr size_t kF32SplitScratchBytes = (size_t)2 << 20;
 
 // Activation prologue of the wave GEMV: plain x, RMSNorm(x; gamma), or
 // SwiGLU silu(x) * x2.
@@ -78,11 +84,15 @@ constexpr int kArithFixed16 = 1;
 int f32_max_members(int K);
 // The f32-activation wave GEMV (gemv_f32.hip); members <= f32_max_members(K).
 hipError_t launch_gemv_f32(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
-// Its slice-split form for 3..8 members over K spanning several slices (plain
-// prologue, no pairs): args.partial holds f32_split_partial_bytes of slice
-// totals, which a second launch adds in slice order into y.
+// Its slice-split form over K spanning several slices (plain prologue, no
+// pairs): 3..8 members up to kWaveMaxK, 1..8 members beyond it (up to
+// kF32SplitMaxK); args.partial holds f32_split_partial_bytes of slice totals,
+// which a second launch adds in slice order into y.
 size_t f32_split_partial_bytes(int members, int K, int total_rows);
 hipError_t launch_gemv_f32_split(int value_type, const WaveGemvArgs& args, int cu_count, hipStream_t stream);
+// Members per slice-split launch for a K beyond kWaveMaxK (0: that form does
+// not serve this shape, whose slice totals would not fit the scratch).
+int f32_long_k_members(int K, int total_rows);
 
 // Largest member count one wave launch can stage for this K (0 if none).
 int wave_max_members(int K);

@@ -159,8 +159,19 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
     DeviceGuard guard(g->ctx->device);
     int per_launch = std::min(ribn_amd::wave_max_members((int)k), ribn_amd::kWaveMaxMembers);
     if (up != nullptr) per_launch = std::min(per_launch, ribn_amd::kSwigluMaxMembers);
+    int arith = arith_of_mode(g->mode);
+    uint64_t total_rows = 0;
+    for (size_t i = 0; i < count; ++i) total_rows += ws[i]->output_size;
+    if (per_launch <= 0 && gamma == nullptr && up == nullptr && total_rows <= (uint64_t)INT32_MAX &&
+        ribn_amd::f32_long_k_members((int)k, (int)total_rows) > 0) {
+        // K beyond what one workgroup stages (e.g. the 17408-wide down
+        // projection of the reference's 27B shapes): the f32 GEMV's
+        // slice-split form, in either mode
+        arith = ribn_amd::kArithF32;
+        per_launch = 1;
+    }
     if (per_launch <= 0) {
-        // K too large to stage in LDS: the exact-order kernel still serves it.
+        // K too large for every staged form: the exact-order kernel still serves it.
         if (gamma != nullptr || up != nullptr || accumulate) {
             return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kWaveMaxK, k, "fused GEMV forms support K up to %d",
                         ribn_amd::kWaveMaxK);
@@ -173,7 +184,7 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
         }
         return ok();
     }
-    per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, up != nullptr, arith_of_mode(g->mode));
+    per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, up != nullptr, arith);
     for (size_t m0 = 0; m0 < members; m0 += (size_t)per_launch) {
         const size_t mc = std::min<size_t>((size_t)per_launch, members - m0);
         ribn_amd::WaveGemvArgs a{};
@@ -195,7 +206,7 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
         a.eps = eps;
         a.K = (int)k;
         a.members = (int)mc;
-        a.arith = arith_of_mode(g->mode);
+        a.arith = arith;
         hipError_t e = ribn_amd::launch_gemv((int)g->value_type, a, g->ctx->act_scratch, g->ctx->cu_count,
                                              g->ctx->stream);
         if (e != hipSuccess) return driver(e, "launch GEMV");

@@ -243,7 +243,12 @@ uint32_t ribn_amd_gemv_mode(const ribn_amd_gemv *gemv);
 ribn_amd_status ribn_amd_gemv_execute(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
                                       const float *input, size_t input_len, float *output, size_t output_len);
 /* execute_warp (quantized.rs:401-435): the wave64 bandwidth kernel (default
- * decode path), in the kernel object's GEMV mode. */
+ * decode path), in the kernel object's GEMV mode. K up to 16384 stages in one
+ * launch; a K of 16640..65536 (e.g. the 17408-wide down projection of the
+ * reference's 27B shapes) runs the f32 slice-split form in either mode (one
+ * 4096-wide slice per workgroup, slice totals added in order by a second
+ * launch; plain, grouped and accumulating products); a larger K runs the
+ * exact-order kernel. */
 ribn_amd_status ribn_amd_gemv_execute_warp(ribn_amd_gemv *gemv, const ribn_amd_quantized_weight *weight,
                                            const float *input, size_t input_len, float *output,
                                            size_t output_len);

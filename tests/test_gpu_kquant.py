@@ -187,6 +187,84 @@ def test_batch_matches_oracle_and_single_bitwise(env, t, members):
         assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
 
 
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("k,n", [(5120, 5120), (5120, 17408), (17408, 5120)])
+def test_reference_bench_shapes(env, t, k, n):
+    """The shapes of the reference's own GEMV bench (int_dot_bench.rs:24, Qwen3.x-27B
+    projections; K = 17408 leaves a 4-block last slice): execute_warp within 1e-3 of the
+    oracle, and 8 members through execute_warp_batch bit-identical to their single
+    launches (cuda_reference.rs:5322-5334)."""
+    print_case(test="reference_bench_shape", t=t, k=k, n=n)
+    enc = synth.kquant_numpy(t, k, n, seed=k + 7 * n + t)
+    x = synth.activations_numpy(k, 8, seed=abs(k - n) + t)
+    w = upload(env, t, k, n, enc)
+    y = empty_dev(8 * n)
+    env["k"][t].execute_warp_batch(w, to_dev(x.reshape(-1)), y, 8)
+    got = to_host(y, env["ctx"]).reshape(8, n)
+    for m in (0, 5):
+        assert max_rel_err(got[m], O.quant_gemv(t, enc, k, n, x[m], threads=8)) <= RTOL
+    for m in range(8):
+        ys = empty_dev(n)
+        env["k"][t].execute_warp(w, to_dev(x[m]), ys)
+        assert np.array_equal(to_host(ys, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
+
+
+@pytest.mark.parametrize("t,k,n,members", [(13, 256 * 130, 75, 3), (14, 65536, 64, 1), (12, 65536, 40, 8),
+                                           (12, 16640, 333, 2)])
+def test_long_k_slice_split(env, t, k, n, members):
+    """K beyond one workgroup's staging (16384) runs the f32 GEMV's slice-split form
+    (one slice staged per workgroup, slice totals added in order): a grouped launch of
+    two weights against the oracle, members bit-identical to their single launches, and
+    the accumulating form (output += W x) equal to a store plus a host add."""
+    print_case(test="long_k", t=t, k=k, n=n, members=members)
+    encs = [synth.kquant_numpy(t, k, n, seed=k + n + j) for j in range(2)]
+    x = synth.activations_numpy(k, members, seed=n + members)
+    ws = [upload(env, t, k, n, e) for e in encs]
+    ys = [empty_dev(members * n) for _ in ws]
+    env["k"][t].execute_group(ws, to_dev(x.reshape(-1)), ys, members)
+    for j in range(2):
+        got = to_host(ys[j], env["ctx"]).reshape(members, n)
+        ref = O.quant_gemv(t, encs[j], k, n, x.reshape(-1), members=members).reshape(members, n)
+        assert max_rel_err(got, ref) <= RTOL
+        for m in range(members):
+            y1 = empty_dev(n)
+            env["k"][t].execute_warp(ws[j], to_dev(x[m]), y1)
+            assert np.array_equal(to_host(y1, env["ctx"]).view(np.uint32), got[m].view(np.uint32))
+    base = synth.activations_numpy(n, members, seed=7).reshape(-1)
+    acc = to_dev(base)
+    env["k"][t].execute_fused(ws[0], to_dev(x.reshape(-1)), acc, members, accumulate=True)
+    want = base + to_host(ys[0], env["ctx"])
+    assert np.array_equal(to_host(acc, env["ctx"]).view(np.uint32), want.view(np.uint32))
+
+
+def test_long_k_modes_and_exact_fallback(env):
+    """The opt-in fixed-point mode takes the same slice-split f32 form beyond K = 16384
+    (same bits as the default mode); past the split form's largest K (65536) a plain
+    product still runs on the exact-order kernel, bit-identical to the oracle's
+    sequential dot (qwen_reference.rs:31-40)."""
+    E = env["E"]
+    t, k, n = 12, 17408, 96
+    enc = synth.kquant_numpy(t, k, n, seed=5)
+    x = synth.activations_numpy(k, 1, seed=6)[0]
+    w = upload(env, t, k, n, enc)
+    outs = []
+    for mode in (E.GEMV_WARP, E.GEMV_FIXED16):
+        env["k"][t].set_mode(mode)
+        y = empty_dev(n)
+        env["k"][t].execute_warp(w, to_dev(x), y)
+        outs.append(to_host(y, env["ctx"]))
+    env["k"][t].set_mode(E.GEMV_WARP)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    k2, n2 = 65536 + 256, 24
+    enc2 = synth.kquant_numpy(t, k2, n2, seed=8)
+    x2 = synth.activations_numpy(k2, 1, seed=9)[0]
+    w2 = upload(env, t, k2, n2, enc2)
+    y2 = empty_dev(n2)
+    env["k"][t].execute_warp(w2, to_dev(x2), y2)
+    ref = O.quant_gemv(t, enc2, k2, n2, x2)
+    assert np.array_equal(to_host(y2, env["ctx"]).view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("t,k,n", [(12, 4096, 12288), (13, 12288, 4096), (14, 4096, 4096)])
 def test_linearity_full_size(env, t, k, n):
     # W(a x1 + b x2) = a W x1 + b W x2 (size-independent property)
