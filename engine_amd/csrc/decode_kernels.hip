@@ -10,7 +10,7 @@
 // Qwen3 has no q gate, so the attention output is not gated.
 //
 // Work split (split-T "flash decoding"): the grid is (chunk, KV head,
-// member). A workgroup takes one contiguous chunk (at least kMinChunkTokens,
+// member). A workgroup takes one contiguous chunk (at least min_chunk tokens,
 // at most the launch's grid chunks per context) of the member's tokens for one KV
 // head and all q_per_kv query heads that share it, so each K/V byte is read
 // once; workgroups past the context exit. Within the workgroup a 16-lane row
@@ -52,19 +52,29 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kRing = 4;                  // steps of K/V loads in flight per wave
 constexpr int kStepTokens = kWaves * 4;   // tokens a workgroup covers per step
 constexpr int kRows = kWaves * 4;         // 16-lane rows of a workgroup, one softmax state each
-// A chunk spans at least this many tokens (sweep on MI355X over workgroups of
-// 256/512 threads and 16-256-token minimum chunks: batch 1 at 2048 tokens is
-// fastest here, and short contexts need fewer chunks and merges).
+// A chunk spans at least this many tokens in launches of up to 8 members
+// (sweep on MI355X over workgroups of 256/512 threads and 16-256-token minimum
+// chunks: batch 1 at 2048 tokens is fastest here, and short contexts need
+// fewer chunks and merges), and kMinChunkTokensWide from 9 members, whose
+// grids of 64-token chunks run in several rounds (2,048 workgroups at 16
+// members and 2,048 tokens): batch-16 decode 3,550 -> 3,730 tok/s, where the
+// same chunks at batch 1 cost 1.2%. From 9 members the projections run on
+// the matrix cores and agree with single rows to f32 rounding, so the
+// bit-for-bit lane (up to 8 members) keeps the 64-token chunks.
 constexpr int kMinChunkTokens = 64;
-static_assert(kMinChunkTokens % kStepTokens == 0, "chunks are whole steps");
+constexpr int kMinChunkTokensWide = 128;
+static_assert(kMinChunkTokens % kStepTokens == 0 && kMinChunkTokensWide % kStepTokens == 0,
+              "chunks are whole steps");
 
+constexpr int kBitLaneMembers = 8;  // the batch GEMVs' bit-identity lane (f32 wave GEMV)
+int attn_min_chunk(int members) { return members > kBitLaneMembers ? kMinChunkTokensWide : kMinChunkTokens; }
 
 // Tokens per chunk for a context of `tokens` in a launch of `chunks` grid
-// chunks: kMinChunkTokens, or more when the context needs more than `chunks`
-// chunks of that size.
-__device__ __forceinline__ int chunk_tokens(int tokens, int chunks) {
+// chunks: min_chunk, or more when the context needs more than `chunks` chunks
+// of that size.
+__device__ __forceinline__ int chunk_tokens(int tokens, int chunks, int min_chunk) {
     int len = (tokens + chunks - 1) / chunks;
-    len = len < kMinChunkTokens ? kMinChunkTokens : len;
+    len = len < min_chunk ? min_chunk : len;
     return (len + kStepTokens - 1) / kStepTokens * kStepTokens;
 }
 
@@ -172,7 +182,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a) {
     uint16_t* const keys = mb.keys + (size_t)a.layer * mb.layer_elems;
     uint16_t* const values = mb.values + (size_t)a.layer * mb.layer_elems;
     const int tokens = pos + 1;
-    const int len = chunk_tokens(tokens, a.chunks);
+    const int len = chunk_tokens(tokens, a.chunks, a.min_chunk);
     const int t0 = chunk * len;
     if (t0 >= tokens) return;  // no tokens in this chunk (uniform over the workgroup)
     const int t1 = min(t0 + len, tokens);
@@ -436,7 +446,7 @@ __global__ __launch_bounds__(kHeadDim) __attribute__((amdgpu_waves_per_eu(1, 2))
         ml[c] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pr, (int)(row + kHeadDim * 4), 0, 0));
     }
     const int tokens = a.positions[m] + 1;
-    const int len = chunk_tokens(tokens, a.chunks);
+    const int len = chunk_tokens(tokens, a.chunks, a.min_chunk);
     const int chunks = (tokens + len - 1) / len;
     float mx = -FLT_MAX;
 #pragma unroll
@@ -906,9 +916,10 @@ __global__ __launch_bounds__(64 * (QPK < 4 ? 4 : QPK)) void attn_prefill_kernel(
 
 size_t attn_partials_floats(int q_heads) { return (size_t)q_heads * kAttnChunks * kPartStride; }
 
-int attn_grid_chunks(int max_capacity) {
-    // chunks a context can need: capacity / kMinChunkTokens, up to kAttnChunks
-    return std::max(1, std::min(kAttnChunks, (max_capacity + kMinChunkTokens - 1) / kMinChunkTokens));
+int attn_grid_chunks(int max_capacity, int members) {
+    // chunks a context can need: capacity / the minimum chunk, up to kAttnChunks
+    const int min_chunk = attn_min_chunk(members);
+    return std::max(1, std::min(kAttnChunks, (max_capacity + min_chunk - 1) / min_chunk));
 }
 
 hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t stream) {
@@ -916,11 +927,13 @@ hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t strea
         args.chunks < 1 || args.chunks > kAttnChunks || args.mem == nullptr) {
         return hipErrorInvalidValue;
     }
-    // The chunking depends on the caches' capacity only, never on the member
-    // count, so every member's bits equal its single-sequence step (the
-    // reference qualifies batched rows bit for bit against batch-1 rows,
-    // cuda_reference.rs:5322-5334).
-    const AttnArgs& b = args;
+    // The chunking depends on the caches' capacity and on the member count's
+    // range only, so up to 8 members every member's bits equal its
+    // single-sequence step (the reference qualifies batched rows bit for bit
+    // against batch-1 rows, cuda_reference.rs:5322-5334), and from 9 to 64
+    // they equal its step in any other batch of that range.
+    AttnArgs b = args;
+    b.min_chunk = attn_min_chunk(members);
     const dim3 grid((unsigned)b.chunks, (unsigned)b.kv_heads, (unsigned)members);
     switch (b.q_heads / b.kv_heads) {
     case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(kThreads), 0, stream, b); break;

@@ -10,9 +10,10 @@ namespace ribn_amd {
 // Head geometry the attention kernel is built for (Qwen3: 128-wide heads).
 constexpr int kHeadDim = 128;
 // Token chunks per (member, KV head): the work of one workgroup, at most
-// this many. The count depends on the caches' capacity only, so a member's
-// arithmetic does not depend on the batch it runs in, and a captured step
-// serves every position.
+// this many. The count depends on the caches' capacity and on whether the
+// launch holds more than 8 members (chunks of at least 64 tokens up to 8, 128
+// beyond): a member's arithmetic is the same at any batch size within each
+// range, and a captured step serves every position.
 constexpr int kAttnChunks = 32;
 // Members one attention launch serves (the host splits larger batches): the
 // decoder's whole batch. At batch 16 one launch of 16 members ran the step
@@ -36,7 +37,8 @@ struct AttnMember {
 struct AttnArgs {
     const AttnMember* mem;     // device [members] descriptors
     int layer;
-    int chunks;                // grid chunks: ceil(max capacity / 64), at most kAttnChunks
+    int chunks;                // grid chunks: attn_grid_chunks(max capacity, members)
+    int min_chunk;             // tokens a chunk spans at least (launch_attention sets it)
     int appended;              // 1: every member's K/V is already in its cache (launch_kv_append)
     const float* q;            // [members][q_heads * 128], raw projection
     const float* k;            // [members][kv_heads * 128], raw projection
@@ -58,8 +60,9 @@ struct AttnArgs {
 // Floats of one sequence's attention partials ([q_heads][kAttnChunks][kPartStride]).
 size_t attn_partials_floats(int q_heads);
 
-// Grid chunks of an attention launch over caches of at most `max_capacity` tokens.
-int attn_grid_chunks(int max_capacity);
+// Grid chunks of an attention launch of `members` over caches of at most
+// `max_capacity` tokens.
+int attn_grid_chunks(int max_capacity, int members);
 
 // Two launches: the chunked attention writing partials, then their merge into
 // `out`. members <= kAttnMaxMembers; q_heads / kv_heads in {1, 2, 4, 8}.

@@ -491,7 +491,7 @@ ribn_amd_status upload_step(ribn_amd_qwen3_decode* d, ribn_amd_kv_cache* const* 
         hipError_t e = ribn_amd::launch_step_inputs(in, d->ctx->stream);
         if (e != hipSuccess) return driver(e, "upload step inputs");
     }
-    d->chunks = ribn_amd::attn_grid_chunks(max_capacity);
+    d->chunks = ribn_amd::attn_grid_chunks(max_capacity, (int)members);
     return ok();
 }
 
@@ -853,8 +853,9 @@ ribn_amd_status ribn_amd_attention_decode(ribn_amd_context* ctx, const ribn_amd_
     }
     // Positions are device values: the kernel checks them against each cache
     // and drops an append past its capacity.
-    hipError_t e = attention(*config, mem, ribn_amd::attn_grid_chunks(max_capacity), false, (int)members, layer, q, k,
-                             v, q_norm, k_norm, positions, output, nullptr, ctx->stream);
+    const int chunks = ribn_amd::attn_grid_chunks(max_capacity, (int)members);
+    hipError_t e = attention(*config, mem, chunks, false, (int)members, layer, q, k, v, q_norm, k_norm, positions,
+                             output, nullptr, ctx->stream);
     return e == hipSuccess ? ok() : driver(e, "launch attention");
 }
 

@@ -209,6 +209,16 @@ def test_attention_eight_members_long_chunks(env, qh, kvh):
     _check_attention(env, qh, kvh, [2100, 0, 511, 512, 1000, 63, 2047, 64], 99)
 
 
+@pytest.mark.parametrize("qh,kvh", [(32, 8), (8, 2)])
+def test_attention_wide_batch_chunks(env, qh, kvh):
+    """From 9 members a chunk spans at least 128 tokens (at most 8 members: 64),
+    so 12 and 16 members over contexts up to 2,101 tokens (every chunk edge
+    from one to 17 chunks) run the wide chunking, against the oracle."""
+    _check_attention(env, qh, kvh, [2100, 0, 127, 128, 129, 255, 256, 511, 1000, 63, 2047, 64], 7)
+    _check_attention(env, qh, kvh, [1, 2, 130, 300, 383, 384, 700, 900, 1023, 1024, 1500, 1800, 2000, 2099, 5, 77],
+                     8)
+
+
 def _check_attention(env, qh, kvh, pos_list, seed):
     E = env["E"]
     cfg = dict(layers=1, hidden=qh * 128, q_heads=qh, kv_heads=kvh, head_dim=128, ffn=256, vocab=1,
@@ -374,7 +384,8 @@ def test_batch_members_equal_single_sequences(env, members):
     """decode_step_batch against decode_step per member: with the default
     GEMV_WARP arithmetic every member's logits and token equal its
     single-sequence step bit for bit, up to the reference's 8 batch members
-    (cuda_reference.rs:5322-5334; attention chunks depend on capacity only)."""
+    (cuda_reference.rs:5322-5334; up to 8 members the attention chunks
+    depend on the caches' capacity only)."""
     print_case(test="batch_vs_single", members=members)
     E = env["E"]
     w = small_weights(TINY, 31)
@@ -436,6 +447,36 @@ def test_batch_step_matches_oracle(env, members):
                 assert sel[m] == ref[m], (m, sel[m], ref[m])
         nxt = ref  # teacher forcing on the oracle's choices
         pos = [p + 1 for p in pos]
+
+
+def test_wide_batch_member_bits_independent_of_batch(env):
+    """From 9 members (projections on the f32-faithful matrix-core GEMV,
+    attention chunks of at least 128 tokens) a member's logits do not depend on
+    the batch it runs in: the same caches and tokens at 16 and at 9 members give
+    the same bits for the shared members, over contexts of several chunks."""
+    print_case(test="wide_batch_bits")
+    E = env["E"]
+    w = small_weights(TINY, 77)
+    dec = build_decoder(env, TINY, w, max_members=16)
+    rng = np.random.default_rng(5)
+    cap = 640
+    caches, pos = [], []
+    for m in range(16):
+        c = E.AmdKvCache(env["ctx"], config(env, TINY), cap)
+        p = int(rng.integers(100, cap - 8))
+        for layer in range(TINY["layers"]):
+            keys = rng.standard_normal((p, TINY["kv_heads"], 128)).astype(np.float16).view(np.uint16)
+            values = rng.standard_normal((p, TINY["kv_heads"], 128)).astype(np.float16).view(np.uint16)
+            _fill_cache(env, c, layer, keys, values)
+        caches.append(c)
+        pos.append(p)
+    toks = [int(t) for t in rng.integers(0, TINY["vocab"], 16)]
+    sel16 = dec.decode_step_batch(caches, toks, pos)
+    l16 = [dec.copy_logits(m) for m in range(9)]
+    sel9 = dec.decode_step_batch(caches[:9], toks[:9], pos[:9])
+    for m in range(9):
+        assert np.array_equal(dec.copy_logits(m).view(np.uint32), l16[m].view(np.uint32)), m
+        assert sel9[m] == sel16[m]
 
 
 def _cache_bytes(env, cache, layers, kv_heads):
