@@ -451,28 +451,38 @@ def test_batch_step_matches_oracle(env, members):
 
 def test_wide_batch_member_bits_independent_of_batch(env):
     """From 9 members (projections on the f32-faithful matrix-core GEMV,
-    attention chunks of at least 128 tokens) a member's logits do not depend on
-    the batch it runs in: the same caches and tokens at 16 and at 9 members give
-    the same bits for the shared members, over contexts of several chunks."""
+    attention chunks of at least 128 tokens) over contexts of several chunks:
+    every member's step against the
+    oracle's at the decoder bar, and a member's logits independent of the batch
+    it runs in (the same caches and tokens at 16 and at 9 members give the same
+    bits for the shared members)."""
     print_case(test="wide_batch_bits")
     E = env["E"]
     w = small_weights(TINY, 77)
     dec = build_decoder(env, TINY, w, max_members=16)
     rng = np.random.default_rng(5)
     cap = 640
-    caches, pos = [], []
+    caches, pos, orcs = [], [], []
     for m in range(16):
         c = E.AmdKvCache(env["ctx"], config(env, TINY), cap)
+        orc = OracleQwen3(TINY, w, cap)
         p = int(rng.integers(100, cap - 8))
         for layer in range(TINY["layers"]):
             keys = rng.standard_normal((p, TINY["kv_heads"], 128)).astype(np.float16).view(np.uint16)
             values = rng.standard_normal((p, TINY["kv_heads"], 128)).astype(np.float16).view(np.uint16)
             _fill_cache(env, c, layer, keys, values)
+            orc.keys[layer][:p] = keys
+            orc.values[layer][:p] = values
         caches.append(c)
+        orcs.append(orc)
         pos.append(p)
     toks = [int(t) for t in rng.integers(0, TINY["vocab"], 16)]
     sel16 = dec.decode_step_batch(caches, toks, pos)
     l16 = [dec.copy_logits(m) for m in range(9)]
+    for m in range(16):
+        orcs[m].step(toks[m], pos[m])
+        err = max_rel_err(dec.copy_logits(m), orcs[m].logits)
+        assert err <= RTOL, (m, pos[m], err)
     sel9 = dec.decode_step_batch(caches[:9], toks[:9], pos[:9])
     for m in range(9):
         assert np.array_equal(dec.copy_logits(m).view(np.uint32), l16[m].view(np.uint32)), m
