@@ -185,6 +185,10 @@ ribn_amd_status launch_wave_group(ribn_amd_gemv* g, const ribn_amd_quantized_wei
         return ok();
     }
     per_launch = ribn_amd::gemv_launch_members((int)g->value_type, (int)k, up != nullptr, arith);
+    if (per_launch <= 0) {
+        return fail(RIBN_AMD_SHAPE_OVERFLOW, (uint64_t)ribn_amd::kWaveMaxK, k, "no GEMV form serves K = %llu",
+                    (unsigned long long)k);
+    }
     for (size_t m0 = 0; m0 < members; m0 += (size_t)per_launch) {
         const size_t mc = std::min<size_t>((size_t)per_launch, members - m0);
         ribn_amd::WaveGemvArgs a{};
