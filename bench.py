@@ -872,10 +872,10 @@ def bench_serving(E, synth, torch, ctx, step, out_gamma, args):
 
 
 def bench_mfma_peak(E, synth, torch, args):
-    """The measured dense peak of the matrix-core instructions (SURVEY's
-    roofline note: confirm the 2.5 PFLOP/s f16 / bf16 figure with a
-    microbenchmark): ribn_amd_probe_mfma_peak, a full grid of four waves per
-    SIMD issuing independent MFMAs on register operands, median of 5 runs."""
+    """The measured dense peak of the matrix-core instructions (the published
+    2.5 PFLOP/s f16 / bf16 figure checked with a microbenchmark):
+    ribn_amd_probe_mfma_peak, a full grid of four waves per SIMD issuing
+    independent MFMAs on register operands, median of 5 runs."""
     import ctypes
     ctx = E.AmdContext(0)
     kinds = {0: "v_mfma_f32_16x16x32_f16", 1: "v_mfma_f32_32x32x16_f16", 2: "v_mfma_f32_16x16x32_bf16",
