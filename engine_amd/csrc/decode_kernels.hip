@@ -949,6 +949,22 @@ hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t strea
     return hipGetLastError();
 }
 
+namespace {
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* gate, const float* up, float* out, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const float g = gate[i];
+        out[i] = (g / (1.0f + expf(-g))) * up[i];
+    }
+}
+}  // namespace
+
+hipError_t launch_swiglu(const float* gate, const float* up, float* out, size_t n, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid), dim3(256), 0, stream, gate, up, out, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_kv_append(const AttnArgs& args, int members, hipStream_t stream) {
     if (members < 1 || members > kAttnMaxMembers || args.kv_heads < 1 || args.mem == nullptr) {
         return hipErrorInvalidValue;

@@ -77,6 +77,11 @@ hipError_t launch_attention(const AttnArgs& args, int members, hipStream_t strea
 // may share a cache (consecutive positions of one sequence).
 hipError_t launch_kv_append(const AttnArgs& args, int members, hipStream_t stream);
 
+// out[i] = silu(gate[i]) * up[i] over n values (model_ops.rs:316-328, the
+// same operations as the GEMVs' SwiGLU prologue and pair epilogue); out may
+// alias gate.
+hipError_t launch_swiglu(const float* gate, const float* up, float* out, size_t n, hipStream_t stream);
+
 // Stream-ordered upload of up to kStepInputs members' step inputs through
 // kernel arguments (no host buffer outlives the call): descriptors, token
 // ids and positions; a null destination is skipped.

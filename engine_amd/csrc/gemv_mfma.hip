@@ -703,10 +703,10 @@ size_t gemv_act_scratch_bytes() {
 }
 
 int gemv_launch_members(int value_type, int K, bool swiglu_prologue, int arith) {
+    // a K beyond one launch's staging: launch_gemv runs the whole batch as
+    // slice-split groups (f32 arithmetic in either mode)
+    if (K > kWaveMaxK) return (!swiglu_prologue && K <= kF32SplitMaxK && K % 256 == 0) ? kF32MmaMaxMembers : 0;
     if (arith == kArithF32) {
-        // a K beyond one launch's staging: launch_gemv runs the whole batch as
-        // slice-split groups
-        if (K > kWaveMaxK) return (!swiglu_prologue && K <= kF32SplitMaxK && K % 256 == 0) ? kF32MmaMaxMembers : 0;
         if (K < 256) return 0;
         // the whole batch: launch_gemv takes 9..64 members to the matrix
         // cores and splits smaller calls into the launch groups each wave
@@ -738,10 +738,11 @@ hipError_t launch_gemv(int value_type, const WaveGemvArgs& a0, void* act_scratch
     }
     if (a.defer != nullptr) *a.defer = F32MmaFold{};
     a.defer = nullptr;
-    if (a.arith == kArithF32 && a.K > kWaveMaxK) {
+    if (a.K > kWaveMaxK) {
         // K beyond what one workgroup stages: groups of up to 8 members in the
         // slice-split form (one slice staged per workgroup, the slice totals
-        // added in order by the reduce launch), plain or accumulating products
+        // added in order by the reduce launch), plain or accumulating
+        // products, f32 arithmetic in either mode
         const int per = f32_long_k_members(a.K, a.total_rows);
         if (per <= 0 || act_scratch == nullptr || a.x2 != nullptr || a.gamma != nullptr || a.pair_swiglu) {
             return hipErrorInvalidValue;

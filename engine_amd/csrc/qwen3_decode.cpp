@@ -103,13 +103,18 @@ ribn_amd_status check_config(const ribn_amd_qwen3_config* c) {
         return fail(RIBN_AMD_INVALID_PLAN, 8, group, "query heads per KV head must be 1, 2, 4 or 8 (got %u)", group);
     }
     const uint64_t qdim = (uint64_t)c->q_heads * c->head_dim;
-    const uint64_t dims[3] = {c->hidden, c->ffn, qdim};
+    const uint64_t dims[2] = {c->hidden, qdim};
     for (uint64_t d : dims) {
         if (d == 0 || d % 256 != 0 || d > (uint64_t)ribn_amd::kWaveMaxK) {
             return fail(RIBN_AMD_INVALID_PLAN, (uint64_t)ribn_amd::kWaveMaxK, d,
-                        "hidden, ffn and q_heads*head_dim must be multiples of 256 up to %d (got %llu)",
+                        "hidden and q_heads*head_dim must be multiples of 256 up to %d (got %llu)",
                         ribn_amd::kWaveMaxK, (unsigned long long)d);
         }
+    }
+    // the down projection's K: beyond kWaveMaxK it runs the slice-split GEMV
+    if (c->ffn == 0 || c->ffn % 256 != 0 || c->ffn > (uint64_t)ribn_amd::kF32SplitMaxK) {
+        return fail(RIBN_AMD_INVALID_PLAN, (uint64_t)ribn_amd::kF32SplitMaxK, c->ffn,
+                    "ffn must be a multiple of 256 up to %d (got %u)", ribn_amd::kF32SplitMaxK, c->ffn);
     }
     if (c->vocab == 0 || c->vocab > (uint32_t)std::numeric_limits<int>::max()) {
         return fail(RIBN_AMD_INVALID_PLAN, 1, c->vocab, "vocabulary size %u is out of range", c->vocab);
@@ -322,6 +327,16 @@ hipError_t enqueue_step(ribn_amd_qwen3_decode* d, const GraphKey& key, hipStream
             // gate/up pairs store silu(gate) * up; down reads it as a plain input
             float* act[2] = {d->gate, d->gate};
             e = wave(d, gu, 2, d->hidden, nullptr, L.ffn_norm, act, members, false, stream, true, &pending);
+            if (e != hipSuccess) return e;
+            e = wave(d, &L.ffn_down, 1, d->gate, nullptr, nullptr, &d->hidden, members, true, stream, false, nullptr,
+                     &pending);
+        } else if (c.ffn > (uint32_t)ribn_amd::kWaveMaxK) {
+            // a down projection wider than the SwiGLU prologue stages:
+            // silu(gate) * up on its own, then the plain slice-split product
+            float* gu_out[2] = {d->gate, d->up};
+            e = wave_shared(d, gu, gu_out, 2, d->hidden, L.ffn_norm, members, stream, &pending);
+            if (e != hipSuccess) return e;
+            e = ribn_amd::launch_swiglu(d->gate, d->up, d->gate, (size_t)members * c.ffn, stream);
             if (e != hipSuccess) return e;
             e = wave(d, &L.ffn_down, 1, d->gate, nullptr, nullptr, &d->hidden, members, true, stream, false, nullptr,
                      &pending);

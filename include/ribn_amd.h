@@ -504,7 +504,11 @@ typedef struct ribn_amd_kv_cache ribn_amd_kv_cache;
 typedef struct ribn_amd_qwen3_decode ribn_amd_qwen3_decode;
 
 /* Decoder geometry. Qwen3-8B: 36 layers, hidden 4096, 32 query / 8 KV heads
- * of 128, FFN 12288, vocab 151936, rope base 1e6, RMSNorm eps 1e-6. */
+ * of 128, FFN 12288, vocab 151936, rope base 1e6, RMSNorm eps 1e-6. hidden
+ * and q_heads * head_dim are multiples of 256 up to 16384; ffn a multiple of
+ * 256 up to 65536 (beyond 16384 the down projection runs the slice-split
+ * GEMV, as for the reference's 17408-wide FFN; the prompt prefill matmul
+ * still needs every K <= 16384). */
 typedef struct ribn_amd_qwen3_config {
     uint32_t layers;
     uint32_t hidden;

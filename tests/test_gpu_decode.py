@@ -489,6 +489,52 @@ def test_wide_batch_member_bits_independent_of_batch(env):
         assert sel9[m] == sel16[m]
 
 
+LONG_FFN = dict(layers=2, hidden=1024, q_heads=8, kv_heads=2, head_dim=128, ffn=16640, vocab=2048,
+                rope_base=1.0e6, epsilon=1.0e-6)
+WIDE_LONG_FFN = dict(layers=1, hidden=4352, q_heads=8, kv_heads=2, head_dim=128, ffn=17408, vocab=512,
+                     rope_base=1.0e6, epsilon=1.0e-6)
+
+
+@pytest.mark.parametrize("cfg_name,members", [("long", 1), ("long", 3), ("long", 12), ("wide", 1), ("wide", 2)])
+def test_decoder_ffn_beyond_staging(env, cfg_name, members):
+    """An FFN wider than one GEMV launch stages (16640 and 17408, the latter the
+    reference's 27B down projection): the down projection runs the slice-split
+    GEMV, after the gate/up pairs (hidden 1024) or after separate gate and up
+    launches and an elementwise SwiGLU (hidden 4352). Teacher-forced steps
+    against the oracle at the decoder bar, and up to 8 members every member's
+    logits bit-identical to its single-sequence step."""
+    print_case(test="ffn_beyond_staging", cfg=cfg_name, members=members)
+    E = env["E"]
+    cfg = LONG_FFN if cfg_name == "long" else WIDE_LONG_FFN
+    w = small_weights(cfg, 91 + members, centered=True)
+    dec = build_decoder(env, cfg, w, max_members=members)
+    prompts = [[(131 * m + 17 * i + 3) % cfg["vocab"] for i in range(2 + m % 2)] for m in range(members)]
+    caches = [E.AmdKvCache(env["ctx"], config(env, cfg), 16) for _ in range(members)]
+    orcs = [OracleQwen3(cfg, w, 16) for _ in range(members)]
+    nxt, pos = [], []
+    for m, p in enumerate(prompts):
+        for i, t in enumerate(p[:-1]):
+            dec.prefill_step(caches[m], t, i)
+            orcs[m].step(t, i, head=False)
+        nxt.append(p[-1])
+        pos.append(len(p) - 1)
+    for step in range(2):
+        dec.decode_step_batch(caches, nxt, pos)
+        logits = [dec.copy_logits(m) for m in range(members)]
+        ref = [orcs[m].step(nxt[m], pos[m]) for m in range(members)]
+        for m in range(members):
+            assert max_rel_err(logits[m], orcs[m].logits) <= RTOL, (step, m)
+        if step == 0 and 1 < members <= 8:
+            for m in range(members):
+                single = E.AmdKvCache(env["ctx"], config(env, cfg), 16)
+                for i, t in enumerate(prompts[m][:-1]):
+                    dec.prefill_step(single, t, i)
+                dec.decode_step(single, nxt[m], pos[m])
+                assert np.array_equal(dec.copy_logits(0).view(np.uint32), logits[m].view(np.uint32)), m
+        nxt = ref  # teacher forcing on the oracle's choices
+        pos = [p + 1 for p in pos]
+
+
 def _cache_bytes(env, cache, layers, kv_heads):
     lib, ctx = env["ctx"]._lib, env["ctx"]
     out = []
@@ -643,6 +689,15 @@ def test_decoder_errors(env):
     with pytest.raises(E.AmdKernelError) as err:
         E.AmdKvCache(env["ctx"], config(env, dict(TINY, head_dim=64)), 8)
     assert err.value.kind == "InvalidPlan"
+    # hidden up to 16384, ffn up to 65536 (its down projection on the slice-split GEMV)
+    for bad_cfg, limit in ((dict(TINY, hidden=16640), 16384), (dict(TINY, ffn=65536 + 256), 65536)):
+        with pytest.raises(E.AmdKernelError) as err:
+            E.AmdKvCache(env["ctx"], config(env, bad_cfg), 8)
+        assert err.value.kind == "InvalidPlan" and err.value.expected == limit
+    long_dec = build_decoder(env, LONG_FFN, small_weights(LONG_FFN, 6))
+    with pytest.raises(E.AmdKernelError) as err:
+        long_dec.prefill_prompt(E.AmdKvCache(env["ctx"], config(env, LONG_FFN), 8), [1, 2], 0)
+    assert err.value.kind == "InvalidPlan"  # the prefill matmul takes K <= 16384
     bad = dict(w)
     bad["blk.1.ffn_up"] = (12, 1024, 4352, synth.kquant_numpy(12, 1024, 4352, 3))
     with pytest.raises(E.AmdKernelError) as err:
